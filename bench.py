@@ -1,0 +1,237 @@
+"""FFI fwd + bwd + SR-SGD step throughput on one MI355X (BASELINE.json metric).
+
+One step = forward logits (incl. the X -> X^T copy), backward to features
+(deterministic, fused SR to bf16 with seed 123), backward to weights (fp32) +
+bias gradient (fp32), and the fused SR-SGD update of weights and bias
+(lr 0.05, wd 1e-4, momentum 0, seed 42 + step).  Inputs are synthetic and
+resident in HBM before timing; the grad of the logits dY = bf16(sigmoid(z) - Y)
+is computed once from the initial logits (Y binary,
+~5 positives per row, Zipf(1.1) over labels).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1]
+                       [--no-cpu-baseline] [--phases]
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "FFI fwd+bwd+SR-step samples/sec at O=131K/670K/3M; %HBM & %MFMA roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+CONFIGS = {
+    0: dict(B=64, D=768, O=4096, G=32, F=32, pos=5),
+    1: dict(B=512, D=768, O=131073, G=64, F=128, pos=5),
+    2: dict(B=512, D=768, O=670091, G=64, F=64, pos=5),
+    3: dict(B=256, D=4096, O=500000, G=32, F=256, pos=5),
+    4: dict(B=1024, D=768, O=3000000, G=128, F=128, pos=10),
+}
+
+
+def phase_bytes(B, D, O, G, F):
+    """Algorithmic HBM bytes per phase (bf16 tensors, fp32 weight/bias grads,
+    momentum 0): every tensor read or written once."""
+    Gc = (O + G - 1) // G
+    return {
+        "fwd": 2 * B * O + 2 * O * F + 4 * Gc * F + 2 * B * D + 2 * O,
+        "bwd_features": 2 * B * O + 2 * O * F + 4 * Gc * F + 2 * B * D,
+        "bwd_weights": 2 * B * O + 2 * B * D + 4 * Gc * F + 4 * O * F + 4 * O,
+        "sgd": (2 + 4 + 2) * O * F + (2 + 4 + 2) * O,
+    }
+
+
+def make_inputs(cfg, dev):
+    import numpy as np
+    import torch
+
+    B, D, O, G, F = cfg["B"], cfg["D"], cfg["O"], cfg["G"], cfg["F"]
+    Gc = (O + G - 1) // G
+    x = torch.randn(B, D, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    bound = 1.0 / math.sqrt(F)
+    W = ((torch.rand(O, F, generator=torch.Generator().manual_seed(1)) * 2 - 1) * bound).to(torch.bfloat16)
+    rng = np.random.default_rng(2)
+    idx = np.argsort(rng.random((Gc, D), dtype=np.float32), axis=1)[:, :F].astype(np.int32)
+    rng_y = np.random.default_rng(3)
+    n_pos = B * cfg["pos"]
+    lab = rng_y.zipf(1.1, size=4 * n_pos)
+    lab = lab[lab <= O][:n_pos] - 1
+    rows = np.repeat(np.arange(B), cfg["pos"])[: len(lab)]
+    Y = torch.zeros(B, O, dtype=torch.float32)
+    Y[torch.from_numpy(rows), torch.from_numpy(lab)] = 1.0
+    return (x.to(dev), W.to(dev), torch.zeros(O, dtype=torch.bfloat16, device=dev),
+            torch.from_numpy(idx).to(dev), Y.to(dev))
+
+
+def cpu_baseline(cfg, budget_s=20.0):
+    """Times the CPU oracle (PyTorch-CPU gather+bmm fwd/bwd + C SR-SGD) on a
+    slice of the label groups, scaled to the full label count."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    ncores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(ncores)
+    oracle.set_num_threads(ncores)
+    B, D, O, G, F = cfg["B"], cfg["D"], cfg["O"], cfg["G"], cfg["F"]
+    Gc = (O + G - 1) // G
+    frac = 1
+    while Gc // frac > 256 and frac < 64:
+        frac *= 2
+    Gs = max(1, Gc // frac)
+    Os = Gs * G
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, D, generator=g).to(torch.bfloat16)
+    W = ((torch.rand(Os, F, generator=g) * 2 - 1) / math.sqrt(F)).to(torch.bfloat16)
+    bias = torch.zeros(Os, dtype=torch.bfloat16)
+    idx = torch.randint(0, D, (Gs, F), generator=g, dtype=torch.int32)
+    dY = (torch.randn(B, Os, generator=g) * 0.1).to(torch.bfloat16)
+
+    def one_step(seed):
+        xT = x.t().contiguous()
+        oracle.ffi_forward(idx, xT, W, bias, G).to(torch.bfloat16)
+        dxt = oracle.ffi_backward_features(idx, W, dY, G, D)
+        oracle.sr_round_bf16(dxt.t().contiguous().numpy(), 123)
+        dW = oracle.ffi_backward_weights(idx, xT, dY, G)
+        db = oracle.bias_grad(dY)
+        wb = W.view(torch.int16).numpy().view(np.uint16)
+        oracle.sgd_sr_step(wb, dW.numpy(), None, 0.05, 1e-4, 0.0, False, True, seed)
+        oracle.sgd_sr_step(bias.view(torch.int16).numpy().view(np.uint16), db.numpy(), None,
+                           0.05, 1e-4, 0.0, False, True, seed)
+
+    one_step(0)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        one_step(len(times) + 1)
+        times.append(time.perf_counter() - t0)
+    t_med = sorted(times)[len(times) // 2]
+    t_full = t_med * (O / Os)
+    return {"value": B / t_full, "unit": "samples/s", "cores": ncores, "kind": "port",
+            "sample": (f"oracle (torch-CPU gather+bmm fwd/bwd + C/OpenMP SR-SGD) on {Gs} of {Gc} "
+                       f"label groups (O_s={Os}), median of {len(times)} steps after 1 warm-up, "
+                       f"step time scaled by O/O_s={O / Os:.1f}"),
+            "step_ms_full_scaled": t_full * 1e3}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phases", action="store_true",
+                    help="also print per-phase event timings to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the FFI path shards by label "
+                          "groups with one all-reduce of dX per step (see DESIGN.md); "
+                          "multi-GPU runs are not part of this build", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    from haste_amd.step import FFITrainStep
+
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    B, D, O, G, F = cfg["B"], cfg["D"], cfg["O"], cfg["G"], cfg["F"]
+    x, W, bias, idx, Y = make_inputs(cfg, dev)
+    st = FFITrainStep(W, bias, idx, B, D, G, lr=0.05, weight_decay=1e-4, seed=42)
+    logits = st.forward(x)
+    ldy = st.ldo
+    dY_buf = torch.zeros(B, ldy, dtype=torch.bfloat16, device=dev)
+    dY_buf[:, :O] = (torch.sigmoid(logits.float()) - Y).to(torch.bfloat16)
+    del Y
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    names = ["fwd", "bwd_features", "bwd_weights", "sgd"]
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        st.forward(x)
+        if ev is not None:
+            ev[1].record(stream)
+        st.backward(dY_buf, ldy) if ev is None else _timed_backward(st, dY_buf, ldy, ev, stream)
+        if ev is not None:
+            ev[3].record(stream)
+        st.sgd()
+        if ev is not None:
+            ev[4].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    wall0 = time.perf_counter()
+    for k in range(args.steps):
+        step(evs[k])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t0.elapsed_time(t1)
+    ms_per_step = total_ms / args.steps
+    phase_ms = {n: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / args.steps
+                for i, n in enumerate(names)}
+
+    pb = phase_bytes(B, D, O, G, F)
+    phase_gbs = {n: pb[n] / (phase_ms[n] * 1e-3) / 1e9 for n in names}
+    dom = max(names, key=lambda n: phase_ms[n])
+    step_bytes = sum(pb.values())
+    flops = 3 * 2 * B * O * F
+    result = {
+        "metric": METRIC,
+        "value": B / (ms_per_step * 1e-3),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"BASELINE config {args.config}: grouped FFI fwd + bwd_features + "
+                               f"bwd_weights + SR-SGD step", "B": B, "D": D, "O": O, "G": G,
+                   "fan_in": F, "grad_dtype": "fp32"},
+        "roofline": {"bound": "hbm", "achieved": phase_gbs[dom], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": phase_gbs[dom] / HBM_PEAK_GBS, "traffic": None,
+                     "kernel_phase": dom},
+        "step_roofline": {"bytes": step_bytes, "hbm_frac": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                          "mfma_frac": flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS},
+        "phases_us": {n: round(phase_ms[n] * 1e3, 2) for n in names},
+        "phases_hbm_frac": {n: round(phase_gbs[n] / HBM_PEAK_GBS, 4) for n in names},
+        "wall_s": wall,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg)
+    print(json.dumps(result), flush=True)
+
+
+def _timed_backward(st, dY, ldy, ev, stream):
+    st.backward_features(dY, ldy)
+    ev[2].record(stream)
+    st.backward_weights(dY, ldy)
+
+
+if __name__ == "__main__":
+    main()

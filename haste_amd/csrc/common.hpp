@@ -1,0 +1,154 @@
+// Shared device/host helpers for the HASTE FFI HIP library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <string>
+
+#include "../../include/haste_ffi.h"
+
+namespace haste {
+
+// ---------------------------------------------------------------- errors ----
+// Thread-local last error, returned by haste_last_error().
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define HASTE_CHECK_ARG(cond, ...)                 \
+    do {                                           \
+        if (!(cond)) {                             \
+            ::haste::set_error(__VA_ARGS__);       \
+            return HASTE_ERR_INVALID_ARG;          \
+        }                                          \
+    } while (0)
+
+#define HASTE_CHECK_LAUNCH(what)                                                  \
+    do {                                                                          \
+        hipError_t e_ = hipGetLastError();                                        \
+        if (e_ != hipSuccess) {                                                   \
+            ::haste::set_error("%s: launch failed: %s", what, hipGetErrorString(e_)); \
+            return HASTE_ERR_HIP;                                                 \
+        }                                                                         \
+    } while (0)
+
+#define HASTE_HIP_TRY(expr, what)                                                 \
+    do {                                                                          \
+        hipError_t e_ = (expr);                                                   \
+        if (e_ != hipSuccess) {                                                   \
+            ::haste::set_error("%s: %s", what, hipGetErrorString(e_));            \
+            return HASTE_ERR_HIP;                                                 \
+        }                                                                         \
+    } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// --------------------------------------------------------------- vectors ----
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 16-bit element type tags.
+struct BF16 {
+    static constexpr int code = HASTE_DTYPE_BF16;
+};
+struct F16 {
+    static constexpr int code = HASTE_DTYPE_F16;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+    return (float)v;
+}
+
+template <typename T>
+__device__ __forceinline__ float bits_to_f32(uint32_t h);
+template <>
+__device__ __forceinline__ float bits_to_f32<BF16>(uint32_t h) { return bf16_bits_to_f32(h); }
+template <>
+__device__ __forceinline__ float bits_to_f32<F16>(uint32_t h) { return f16_bits_to_f32(h); }
+
+// fp32 -> bf16 round-to-nearest-even (quiet NaN keeps the sign).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
+    _Float16 h = (_Float16)f;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t f32_to_bits(float f);
+template <>
+__device__ __forceinline__ uint32_t f32_to_bits<BF16>(float f) { return f32_to_bf16_rne(f); }
+template <>
+__device__ __forceinline__ uint32_t f32_to_bits<F16>(float f) { return f32_to_f16_rne(f); }
+
+// ---------------------------------------------------------------- MFMA ------
+// D(16x16 f32) += A(16x32) * B(32x16); lane L supplies A row L%16 and B column
+// L%16, eight K-elements each (the same K positions for A and B), and holds
+// D rows 4*(L/16)+0..3 of column L%16.
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16x16x32<F16>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// -------------------------------------------------------------- Philox ------
+// Philox4x32-10 (Salmon et al., SC'11) with the round function of Triton's
+// philox_impl; returns word 0 for counter (c0, c1, c2, 0) and key (k0, k1).
+// tl.randint(seed, off) == philox_w0(off_lo, off_hi, 0, seed_lo, seed_hi).
+__device__ __forceinline__ uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t k0,
+                                              uint32_t k1) {
+    uint32_t c3 = 0u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return c0;
+}
+
+// Stochastic rounding fp32 -> bf16 bits (random low 16 bits added to the fp32
+// pattern, upper half kept); NaN -> quiet NaN.
+__device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t r) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
+    return (u + (r & 0xFFFFu)) >> 16;
+}
+
+// Workgroup-id remap so that consecutive logical ids land on the same XCD
+// (the hardware dispatches workgroup i to XCD i % 8).  Returns -1 for the
+// padding ids of a grid rounded up to a multiple of 8.
+__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nlogical) {
+    const int64_t per = (nlogical + 7) / 8;
+    const int64_t w = (bid % 8) * per + bid / 8;
+    return w < nlogical ? w : -1;
+}
+
+}  // namespace haste

@@ -1,0 +1,129 @@
+// On-device rewire (prune + regrow) of a bf16 grouped FFI layer, gfx950.
+//
+// Restates GroupFixedFanIn.rewire (shared_ffi/rewire.py:143-239) as one kernel
+// with one workgroup per label group and no host synchronisation.  The
+// reference's random draws (torch.randint / uniform_ on the device generator)
+// and its topk(sorted=False) tie order cannot be reproduced, so the contract
+// is fixed here (and restated bit-for-bit by the CPU oracle):
+//   score[g, j] = (fp32 sum over rows l of g, ascending, of |W[l, j]|) / rows
+//   prune:  THRESHOLD -> score < threshold;  FRACTION -> k smallest (score, j)
+//   regrow: RANDOM -> d = (philox(seed; g*F+j, 1, 0).w0 * D) >> 32
+//           UNUSED -> attempts t = 0..63 with counter (g*F+j, 1, t); first
+//           candidate not used by the group (kept slots and slots regrown
+//           earlier in ascending j); else the last candidate
+//   weights at pruned slots, every row: ZERO -> 0; RANDOM ->
+//           RNE(fma((w0 >> 8) * 2^-24, 2*bound, -bound)), w0 = philox(seed; l*F+j, 2, 0).w0
+#include "common.hpp"
+
+namespace haste {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnusedTries = 64;
+
+__global__ __launch_bounds__(kThreads) void rewire_kernel(
+    uint16_t* __restrict__ W, int32_t* __restrict__ idx, float* __restrict__ scores_out,
+    int32_t* __restrict__ n_pruned, int64_t O, int F, int G, int D, int prune_mode, float thr,
+    int k, int regrow_mode, int init_mode, float bound, uint32_t k0, uint32_t k1) {
+    __shared__ float sc[256];
+    __shared__ int32_t sidx[256];
+    __shared__ int mask[256];
+
+    const int64_t g = blockIdx.x;
+    const int j = threadIdx.x;
+    const int64_t l0 = g * G;
+    const int64_t l1 = min(O, l0 + G);
+    const bool jv = j < F;
+
+    float score = 0.0f;
+    if (jv) {
+        for (int64_t l = l0; l < l1; ++l) score += fabsf(bf16_bits_to_f32(W[l * F + j]));
+        score = score / (float)(l1 - l0);
+        sc[j] = score;
+        sidx[j] = idx[g * F + j];
+        if (scores_out) scores_out[g * F + j] = score;
+    }
+    __syncthreads();
+
+    int m = 0;
+    if (jv) {
+        if (prune_mode == HASTE_PRUNE_THRESHOLD) {
+            m = score < thr;
+        } else {
+            int rank = 0;
+            for (int q = 0; q < F; ++q) {
+                const float u = sc[q];
+                rank += (u < score) || (u == score && q < j);
+            }
+            m = rank < k;
+        }
+        mask[j] = m;
+    }
+    const int count = __syncthreads_count(m);
+
+    if (regrow_mode == HASTE_REGROW_RANDOM) {
+        if (m) {
+            const uint32_t w0 = philox_w0((uint32_t)(g * F + j), 1u, 0u, k0, k1);
+            sidx[j] = (int32_t)(((uint64_t)w0 * (uint64_t)D) >> 32);
+        }
+    } else {
+        for (int jj = 0; jj < F; ++jj) {
+            if (!mask[jj]) continue;  // uniform
+            uint32_t cand = 0;
+            for (int t = 0; t < kUnusedTries; ++t) {
+                const uint32_t w0 = philox_w0((uint32_t)(g * F + jj), 1u, (uint32_t)t, k0, k1);
+                cand = (uint32_t)(((uint64_t)w0 * (uint64_t)D) >> 32);
+                const int used = jv && (!mask[j] || j < jj) && sidx[j] == (int32_t)cand;
+                if (!__syncthreads_or(used)) break;
+            }
+            if (j == 0) sidx[jj] = (int32_t)cand;
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+
+    if (m) {
+        idx[g * F + j] = sidx[j];
+        for (int64_t l = l0; l < l1; ++l) {
+            uint32_t h = 0u;
+            if (init_mode == HASTE_INIT_RANDOM) {
+                const uint32_t w0 = philox_w0((uint32_t)(l * F + j), 2u, 0u, k0, k1);
+                const float u01 = (float)(w0 >> 8) * 0x1p-24f;
+                h = f32_to_bf16_rne(__builtin_fmaf(u01, 2.0f * bound, -bound));
+            }
+            W[l * F + j] = (uint16_t)h;
+        }
+    }
+    if (j == 0 && n_pruned != nullptr && count > 0) atomicAdd(n_pruned, count);
+}
+
+}  // namespace
+}  // namespace haste
+
+extern "C" int haste_rewire(uint16_t* W, int32_t* idx, float* scores_out, int32_t* n_pruned,
+                            int64_t O, int64_t F, int64_t G, int64_t D, int32_t prune_mode,
+                            float threshold, int64_t k, int32_t regrow_mode, int32_t init_mode,
+                            float bound, uint64_t seed, void* stream) {
+    HASTE_CHECK_ARG(W && idx, "haste_rewire: null pointer");
+    HASTE_CHECK_ARG(F >= 1 && F <= 256, "haste_rewire: fan_in must be in [1, 256] (got %lld)",
+                    (long long)F);
+    HASTE_CHECK_ARG(G >= 1 && O >= 1 && D >= 1 && D <= 0x7FFFFFFF,
+                    "haste_rewire: invalid sizes O=%lld G=%lld D=%lld", (long long)O,
+                    (long long)G, (long long)D);
+    HASTE_CHECK_ARG(O * F < ((int64_t)1 << 32),
+                    "haste_rewire: O*F must be < 2^32 (Philox counter width)");
+    HASTE_CHECK_ARG(prune_mode == HASTE_PRUNE_THRESHOLD || prune_mode == HASTE_PRUNE_FRACTION,
+                    "haste_rewire: bad prune mode %d", (int)prune_mode);
+    HASTE_CHECK_ARG(regrow_mode == HASTE_REGROW_RANDOM || regrow_mode == HASTE_REGROW_UNUSED,
+                    "haste_rewire: bad regrow mode %d", (int)regrow_mode);
+    HASTE_CHECK_ARG(init_mode == HASTE_INIT_ZERO || init_mode == HASTE_INIT_RANDOM,
+                    "haste_rewire: bad init mode %d", (int)init_mode);
+    HASTE_CHECK_ARG(k >= 0 && k <= F, "haste_rewire: k must be in [0, F] (got %lld)", (long long)k);
+    const int64_t Gc = haste::ceil_div(O, G);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    haste::rewire_kernel<<<dim3((unsigned)Gc), dim3(haste::kThreads), 0, st>>>(
+        W, idx, scores_out, n_pruned, O, (int)F, (int)G, (int)D, prune_mode, threshold, (int)k,
+        regrow_mode, init_mode, bound, (uint32_t)seed, (uint32_t)(seed >> 32));
+    HASTE_CHECK_LAUNCH("haste_rewire");
+    return HASTE_OK;
+}

@@ -1,0 +1,94 @@
+"""SGD with momentum, weight decay and stochastic rounding (reference:
+shared_ffi/optim_sr.py:7-114, class ``SRSgd``; the north star calls it SGD_SR).
+
+Semantics kept from the reference:
+  * per param group, ``seed`` is read and then incremented by 1 on every
+    step (optim_sr.py:59-62); every tensor of the group uses that seed with
+    offsets restarting at 0 (so weights and bias share random streams);
+  * fp32 params take the plain torch path (optim_sr.py:73-84);
+  * low-precision params are updated in place by one fused kernel
+    (g' = fma(wd, w, g); m' = fma(mu, m, g'); w' = fma(-lr, m' or g', w);
+    SR to bf16 with tl.randint(seed, i), or RNE when SR is off);
+  * non-contiguous params are updated through a contiguous copy.
+Difference: the fp32 momentum buffer is allocated only once momentum is
+actually used (the reference always allocates it, optim_sr.py:35-44); a
+buffer created later starts at zero, which is what the reference's unused
+buffer holds.
+"""
+from __future__ import annotations
+
+import torch
+from torch.optim import Optimizer
+
+from .sr import sgd_update
+
+__all__ = ["SRSgd", "SGD_SR"]
+
+
+class SRSgd(Optimizer):
+    def __init__(self, params, lr: float = 1e-3, weight_decay: float = 0.0,
+                 momentum: float = 0.0, use_momentum: bool = True,
+                 stochastic_rounding: bool = True, seed: int = 123):
+        defaults = dict(lr=lr, weight_decay=weight_decay, momentum=momentum,
+                        use_momentum=use_momentum, stochastic_rounding=stochastic_rounding,
+                        seed=seed)
+        super().__init__(params, defaults)
+
+    @staticmethod
+    def _uses_momentum(group) -> bool:
+        return bool(group["use_momentum"]) and group["momentum"] != 0.0
+
+    def _momentum_buf(self, p: torch.Tensor) -> torch.Tensor:
+        state = self.state[p]
+        buf = state.get("momentum_buf")
+        if buf is None:
+            buf = torch.zeros_like(p.data, dtype=torch.float32, device=p.device)
+            state["momentum_buf"] = buf
+        return buf
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+
+        for group in self.param_groups:
+            lr = group["lr"]
+            wd = group["weight_decay"]
+            mu = group["momentum"]
+            use_mom = group["use_momentum"]
+            sr = group["stochastic_rounding"]
+            seed = group["seed"]
+            group["seed"] += 1
+            mom_on = self._uses_momentum(group)
+
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                grad = p.grad
+
+                if p.dtype == torch.float32:
+                    if wd != 0.0:
+                        grad = grad.add(p, alpha=wd)
+                    if mom_on:
+                        buf = self._momentum_buf(p)
+                        buf.mul_(mu).add_(grad)
+                        update = buf
+                    else:
+                        update = grad
+                    p.add_(update, alpha=-lr)
+                    continue
+
+                w = p.data
+                w_contig = w if w.is_contiguous() else w.contiguous()
+                g_contig = grad if grad.is_contiguous() else grad.contiguous()
+                sgd_update(w_contig, g_contig, self._momentum_buf(p) if mom_on else None,
+                           learning_rate=lr, weight_decay=wd, momentum=mu,
+                           use_momentum=use_mom, stochastic_rounding=sr, seed=seed)
+                if w_contig.data_ptr() != w.data_ptr():
+                    p.data.copy_(w_contig)
+        return loss
+
+
+SGD_SR = SRSgd

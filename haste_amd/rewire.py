@@ -1,0 +1,131 @@
+"""Grouped fixed-fan-in layer with on-device rewiring (reference:
+shared_ffi/rewire.py:36-239, ``GroupFixedFanIn``).
+
+Constructor arguments, parameter/buffer names and dtypes (``weights`` [O, F],
+``bias`` [O], persistent buffer ``group_locations`` int32 [ceil(O/G), F]) and
+initialisation follow the reference (rewire.py:64-127).  ``rewire()`` runs as
+one HIP kernel (libhaste_ffi.so ``haste_rewire``) with no host sync; its
+contract is deterministic (see include/haste_ffi.h): the reference's
+torch.randint / uniform_ draws and topk tie order are replaced by Philox
+streams keyed by a seed drawn from torch's default CPU generator, and ties in
+fraction mode go to the lower slot.  ``regrow_mode="unused"`` (new) draws only
+indices not already present in the group.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _C, _lib, ops
+
+GROWTH_MODES = ["random"]
+PRUNE_MODES = ["threshold", "fraction"]
+INIT_MODES = ["random", "zero"]
+REGROW_MODES = ["random", "unused"]
+GROUP_SIZES = [16, 32, 64, 128]
+
+__all__ = ["GroupFixedFanIn"]
+
+
+class GroupFixedFanIn(torch.nn.Module):
+    """Fixed fan-in sparse linear layer whose labels share index sets in groups
+    of ``group_size`` (see the reference docstring, rewire.py:37-58)."""
+
+    __constants__ = ["in_features", "out_features", "fan_in"]
+    in_features: int
+    out_features: int
+    fan_in: int
+
+    def __init__(self, in_features: int, out_features: int, fan_in: int, bias: bool = True,
+                 device=None, dtype=None, *, group_size=32, prune_mode="threshold",
+                 rewire_threshold=None, rewire_fraction=None, growth_mode="random",
+                 init_mode="random", regrow_mode="random", **kwargs):
+        super().__init__(**kwargs)
+        factory_kwargs = {"device": device, "dtype": dtype}
+        self.in_features = in_features
+        self.out_features = out_features
+        self.fan_in = fan_in
+
+        assert prune_mode in PRUNE_MODES, f"Invalid prune_mode={prune_mode}; supported: {PRUNE_MODES}"
+        assert growth_mode in GROWTH_MODES, f"Invalid growth_mode={growth_mode}; supported: {GROWTH_MODES}"
+        assert init_mode in INIT_MODES, f"Invalid init_mode={init_mode}; supported: {INIT_MODES}"
+        assert regrow_mode in REGROW_MODES, f"Invalid regrow_mode={regrow_mode}; supported: {REGROW_MODES}"
+        if prune_mode == "threshold" and rewire_threshold is None:
+            raise ValueError("rewire_threshold must be specified for prune_mode 'threshold'")
+        elif prune_mode == "fraction" and rewire_fraction is None:
+            raise ValueError("rewire_fraction must be specified for prune_mode 'fraction'")
+        self.prune_mode = prune_mode
+        self.growth_mode = growth_mode
+        self.init_mode = init_mode
+        self.regrow_mode = regrow_mode
+        if prune_mode == "fraction":
+            self.rewire_fraction = rewire_fraction
+            assert 0 <= rewire_fraction < 1, \
+                f"Invalid reware_fraction={rewire_fraction}; supported range [0,1)"
+        else:
+            self.rewire_threshold = rewire_threshold
+
+        self.weights = torch.nn.parameter.Parameter(torch.empty((out_features, fan_in), **factory_kwargs))
+        bound = 1 / math.sqrt(self.fan_in)
+        torch.nn.init.uniform_(self.weights, -bound, bound)
+        if bias:
+            self.bias = torch.nn.parameter.Parameter(torch.empty(out_features, **factory_kwargs))
+            torch.nn.init.zeros_(self.bias)
+        else:
+            self.register_parameter("bias", None)
+
+        assert group_size in GROUP_SIZES, \
+            f"Current kernels only support group size from {GROUP_SIZES}. Selected group size={group_size}"
+        self.group_size = group_size
+        self.num_groups = (out_features + self.group_size - 1) // self.group_size
+        group_locations = torch.randint(high=self.in_features, size=(self.num_groups, fan_in),
+                                        dtype=torch.int32)
+        self.register_buffer("group_locations", group_locations, persistent=True)
+        self._pruned_total = None  # device int32 counter of pruned slots (no host sync)
+
+    def forward(self, features):
+        return ops.group_ffi_mul(features, self.weights, self.group_locations, self.bias,
+                                 gsize=self.group_size)
+
+    def extra_repr(self) -> str:
+        return "in_features={}, out_features={}, fan_in={}, bias={}".format(
+            self.in_features, self.out_features, self.fan_in, self.bias is not None)
+
+    @property
+    def pruned_total(self) -> int:
+        """Total number of slots pruned by rewire() so far (syncs the device)."""
+        return 0 if self._pruned_total is None else int(self._pruned_total.item())
+
+    @torch.no_grad()
+    def rewire(self, seed: int = None):
+        """Prune + regrow every group in one kernel launch (reference rewire.py:143-239).
+
+        ``seed`` keys the Philox streams of the regrowth draws; by default it is
+        drawn from torch's default CPU generator."""
+        W = self.weights
+        if self.out_features == 0:
+            return
+        _C.require_device(W, "weights")
+        if W.dtype != torch.bfloat16:
+            raise NotImplementedError(f"rewire: weights must be bfloat16 (got {W.dtype})")
+        if not W.is_contiguous() or not self.group_locations.is_contiguous():
+            raise RuntimeError("rewire: weights and group_locations must be contiguous")
+        F = self.fan_in
+        if self.prune_mode == "threshold":
+            mode, thr, k = _lib.PRUNE_THRESHOLD, float(self.rewire_threshold), 0
+        else:
+            k = int(F * self.rewire_fraction)
+            if k == 0:
+                return
+            mode, thr = _lib.PRUNE_FRACTION, 0.0
+        if seed is None:
+            seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+        if self._pruned_total is None or self._pruned_total.device != W.device:
+            self._pruned_total = torch.zeros(1, dtype=torch.int32, device=W.device)
+        _lib.call("haste_rewire", W.data_ptr(), self.group_locations.data_ptr(), None,
+                  self._pruned_total.data_ptr(), self.out_features, F, self.group_size,
+                  self.in_features, mode, thr, k,
+                  _lib.REGROW_UNUSED if self.regrow_mode == "unused" else _lib.REGROW_RANDOM,
+                  _lib.INIT_RANDOM if self.init_mode == "random" else _lib.INIT_ZERO,
+                  float(1.0 / math.sqrt(F)), int(seed), _C.stream_of(W))

@@ -1,0 +1,60 @@
+"""Stochastic rounding and the fused SGD step (host side).
+
+Same signatures, assertions and semantics as the reference's Triton host
+functions (shared_ffi/sr_triton.py:51-59 and :172-213), implemented on the HIP
+kernels of libhaste_ffi.so.  Random bits are Triton's tl.randint(seed, i)
+(Philox4x32-10, word 0, counter = element index from 0 per tensor), so the
+results are bit-identical under the FMA contract stated in include/haste_ffi.h.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._C import dtype_code, require_device, stream_of
+
+__all__ = ["stochastic_rounding", "sgd_update"]
+
+
+def stochastic_rounding(x: torch.Tensor, output: torch.Tensor, seed: int) -> None:
+    """output[i] = SR_bf16(x[i], tl.randint(seed, i)) (sr_triton.py:51-59)."""
+    assert x.is_contiguous()
+    assert output.is_contiguous()
+    assert x.shape == output.shape
+    assert x.dtype == torch.float32
+    assert output.dtype != torch.float32
+    if output.dtype != torch.bfloat16:
+        raise NotImplementedError(
+            f"stochastic_rounding: only bfloat16 output is implemented (got {output.dtype}); "
+            "the reference's fp8 variant is not on the FFI path")
+    require_device(x, "x")
+    require_device(output, "output")
+    _lib.call("haste_sr_round_bf16", x.data_ptr(), output.data_ptr(), x.numel(), int(seed), 0,
+              stream_of(x))
+
+
+def sgd_update(weights: torch.Tensor, gradient: torch.Tensor, momentum_buf: torch.Tensor,
+               learning_rate: float, weight_decay: float, momentum: float, use_momentum: bool,
+               stochastic_rounding: bool, seed: int) -> None:
+    """Fused SGD + optional momentum + weight decay + SR, in place on ``weights``
+    (sr_triton.py:172-213).  ``momentum_buf`` may be None when momentum is off."""
+    assert weights.is_contiguous(), "weights must be contiguous"
+    assert gradient.is_contiguous(), "gradient must be contiguous"
+    use_mom_flag = 1 if (use_momentum and momentum != 0.0) else 0
+    if momentum_buf is not None:
+        assert momentum_buf.is_contiguous(), "momentum_buf must be contiguous"
+        assert weights.shape == gradient.shape == momentum_buf.shape
+    else:
+        assert weights.shape == gradient.shape
+        assert not use_mom_flag, "momentum_buf is required when momentum is used"
+    if weights.dtype != torch.bfloat16:
+        raise NotImplementedError(f"sgd_update: weights must be bfloat16 (got {weights.dtype})")
+    require_device(weights, "weights")
+    require_device(gradient, "gradient")
+    if use_mom_flag:
+        assert momentum_buf.dtype == torch.float32
+    _lib.call("haste_sgd_sr_step", weights.data_ptr(), gradient.data_ptr(),
+              dtype_code(gradient.dtype),
+              momentum_buf.data_ptr() if use_mom_flag else None, weights.numel(),
+              float(learning_rate), float(weight_decay), float(momentum), use_mom_flag,
+              1 if stochastic_rounding else 0, int(seed), 0, stream_of(weights))

@@ -1,0 +1,93 @@
+"""One training step of a grouped FFI layer on preallocated buffers.
+
+``FFITrainStep`` runs forward -> backward (features, weights, bias) -> fused
+SR-SGD update of weights and bias, calling libhaste_ffi.so directly with
+buffers allocated once, so a step launches only HIP kernels (no allocator
+traffic, no host sync) and can be captured in a HIP graph.  It computes the
+same quantities as GroupFFIMulFunction + SRSgd with two deliberate choices:
+the weight and bias gradients are kept in fp32 (``grad_dtype``, the SGD kernel
+reads them directly), and the grad of the logits ``dY`` is an input.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _C, _lib
+from .bindings import SR_SEED_GRAD_X
+
+
+class FFITrainStep:
+    def __init__(self, weights: torch.Tensor, bias, group_locations: torch.Tensor, batch: int,
+                 in_features: int, group_size: int, lr: float, weight_decay: float,
+                 seed: int = 42, grad_dtype: torch.dtype = torch.float32):
+        _C.require_device(weights, "weights")
+        if weights.dtype != torch.bfloat16:
+            raise NotImplementedError("FFITrainStep: bf16 weights only")
+        self.W = weights
+        self.bias = bias
+        self.idx = group_locations
+        self.B, self.D, self.G = int(batch), int(in_features), int(group_size)
+        self.O, self.F = weights.shape
+        self.lr, self.wd, self.seed = float(lr), float(weight_decay), int(seed)
+        dev = weights.device
+        self.ldx = _C.round8(self.B)
+        self.ldo = _C.round8(self.O)
+        self.xT_buf = torch.zeros(self.D, self.ldx, dtype=torch.bfloat16, device=dev)
+        self.logits_buf = torch.empty(self.B, self.ldo, dtype=torch.bfloat16, device=dev)
+        self.dX = torch.empty(self.B, self.D, dtype=torch.bfloat16, device=dev)
+        self.grad_dtype = grad_dtype
+        self.dW = torch.empty(self.O, self.F, dtype=grad_dtype, device=dev)
+        self.dbias = torch.empty(self.O, dtype=grad_dtype, device=dev) if bias is not None else None
+        self.ws = _C.bwd_features_workspace(self.B, self.D, self.F, self.O, self.G,
+                                            torch.bfloat16, dev)
+        self.code = _lib.DTYPE_BF16
+        self.gcode = _C.dtype_code(grad_dtype)
+
+    @property
+    def logits(self) -> torch.Tensor:
+        return self.logits_buf[:, : self.O]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """x [B, D] bf16 -> logits [B, O] (view of a [B, ceil8(O)] buffer)."""
+        self.xT_buf[:, : self.B].copy_(x.t())
+        _lib.call("haste_ffi_forward", self.idx.data_ptr(), self.xT_buf.data_ptr(), self.ldx,
+                  self.W.data_ptr(), None if self.bias is None else self.bias.data_ptr(),
+                  self.logits_buf.data_ptr(), self.ldo, self.B, self.D, self.F, self.O, self.G,
+                  self.code, _C.stream_of(self.W))
+        return self.logits
+
+    def backward_features(self, dY: torch.Tensor, lddy: int) -> None:
+        """dX [B, D] bf16 = SR(feature gradient, seed 123) (bindings.py:44-48)."""
+        _lib.call("haste_ffi_bwd_features_sr", self.idx.data_ptr(), self.W.data_ptr(),
+                  dY.data_ptr(), lddy, self.dX.data_ptr(), SR_SEED_GRAD_X, self.ws.data_ptr(),
+                  self.ws.numel(), self.B, self.D, self.F, self.O, self.G, self.code,
+                  _C.stream_of(self.W))
+
+    def backward_weights(self, dY: torch.Tensor, lddy: int) -> None:
+        """dW [O, F] and dbias [O] in grad_dtype."""
+        _lib.call("haste_ffi_bwd_weights", self.idx.data_ptr(), self.xT_buf.data_ptr(), self.ldx,
+                  dY.data_ptr(), lddy, self.dW.data_ptr(), self.gcode,
+                  None if self.dbias is None else self.dbias.data_ptr(), self.gcode, self.B,
+                  self.D, self.F, self.O, self.G, self.code, _C.stream_of(self.W))
+
+    def backward(self, dY: torch.Tensor, lddy: int) -> None:
+        """dY: [B, lddy] bf16 buffer (lddy % 8 == 0) holding grad of the logits."""
+        self.backward_features(dY, lddy)
+        self.backward_weights(dY, lddy)
+
+    def sgd(self) -> None:
+        """SR-SGD (momentum 0) on weights and bias with the current seed, then seed += 1
+        (optim_sr.py:59-62: one seed per step, offsets from 0 per tensor)."""
+        st = _C.stream_of(self.W)
+        _lib.call("haste_sgd_sr_step", self.W.data_ptr(), self.dW.data_ptr(), self.gcode, None,
+                  self.W.numel(), self.lr, self.wd, 0.0, 0, 1, self.seed, 0, st)
+        if self.bias is not None:
+            _lib.call("haste_sgd_sr_step", self.bias.data_ptr(), self.dbias.data_ptr(),
+                      self.gcode, None, self.bias.numel(), self.lr, self.wd, 0.0, 0, 1,
+                      self.seed, 0, st)
+        self.seed += 1
+
+    def step(self, x: torch.Tensor, dY: torch.Tensor, lddy: int) -> None:
+        self.forward(x)
+        self.backward(dY, lddy)
+        self.sgd()

@@ -1,0 +1,142 @@
+/*
+ * haste_ffi.h -- C ABI of the MI355X (gfx950) HASTE fixed-fan-in (FFI) layer.
+ *
+ * Drop-in boundary for HASTE's shared_ffi hot path.  Every pointer is a device
+ * pointer unless stated otherwise; `stream` is a hipStream_t passed as void*
+ * (NULL = the null stream).  Calls are asynchronous on `stream` and never
+ * allocate device memory; scratch space is passed in as `workspace`.
+ * Return value: HASTE_OK (0) or a negative HASTE_ERR_* code; the message for
+ * the calling thread is in haste_last_error().
+ *
+ * Layouts (row-major, element strides):
+ *   idx   int32 [Gc, F]   group_locations, Gc = ceil(O / G); label l uses row l / G
+ *   xT    [D, ldx]        features transposed, columns 0..B-1 used, ldx % 8 == 0
+ *   W     [O, F]          weights
+ *   out   [B, ldo]        logits, columns 0..O-1 written, ldo % 8 == 0
+ *   dY    [B, lddy]       grad of logits, lddy % 8 == 0
+ * Element types are HASTE_DTYPE_* codes; 16-bit tensors must be 16-byte aligned.
+ * Supported: dtype bf16 or f16; G in {16, 32, 64, 128}; F % 16 == 0, 16 <= F <= 256.
+ * The reference envelope is G in {16,32,64}, F <= 128 (F <= 256 for G = 16);
+ * this library accepts the wider set.
+ */
+#ifndef HASTE_FFI_H
+#define HASTE_FFI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    HASTE_OK = 0,
+    HASTE_ERR_INVALID_ARG = -1,
+    HASTE_ERR_UNSUPPORTED = -2,
+    HASTE_ERR_WORKSPACE = -3,
+    HASTE_ERR_HIP = -4
+};
+
+enum { HASTE_DTYPE_BF16 = 0, HASTE_DTYPE_F16 = 1, HASTE_DTYPE_F32 = 2 };
+
+enum { HASTE_PRUNE_THRESHOLD = 0, HASTE_PRUNE_FRACTION = 1 };
+enum { HASTE_REGROW_RANDOM = 0, HASTE_REGROW_UNUSED = 1 };
+enum { HASTE_INIT_ZERO = 0, HASTE_INIT_RANDOM = 1 };
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* haste_last_error(void);
+
+/* ABI version of this library (increments on incompatible changes). */
+int haste_abi_version(void);
+
+/*
+ * Grouped FFI forward:
+ *   out[b, l] = RNE( sum_j xT[idx[l/G, j], b] * W[l, j]  (+ bias[l]) ),  fp32 accumulation.
+ * bias may be NULL.  Replaces ffi_forward_cuda (shared_ffi/ffi_forward_kernels.cu:492-719,
+ * bound at shared_ffi/ffi_wrapper.cpp:22-26,32-44), whose output is [B, ceil8(O)].
+ */
+int haste_ffi_forward(const int32_t* idx, const void* xT, int64_t ldx, const void* W,
+                      const void* bias, void* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
+                      int64_t O, int64_t G, int32_t dtype, void* stream);
+
+/*
+ * Workspace bytes needed by haste_ffi_bwd_features / haste_ffi_bwd_features_sr.
+ * Returns a negative HASTE_ERR_* code for unsupported shapes.
+ */
+int64_t haste_ffi_bwd_features_workspace_size(int64_t B, int64_t D, int64_t F, int64_t O,
+                                              int64_t G, int32_t dtype);
+
+/*
+ * Backward to features, deterministic (no float atomics on any global buffer):
+ *   dXT[d, b] = sum_{g,j: idx[g,j] = d} sum_{l in g} W[l, j] * dY[b, l]     (fp32 [D, B])
+ * Replaces ffi_backward_features_cuda (shared_ffi/ffi_backward_features.cu:417-633,
+ * bound at shared_ffi/ffi_wrapper.cpp:7-12,29).
+ */
+int haste_ffi_bwd_features(const int32_t* idx, const void* W, const void* dY, int64_t lddy,
+                           float* dXT, void* workspace, int64_t workspace_bytes, int64_t B,
+                           int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype,
+                           void* stream);
+
+/*
+ * Backward to features fused with the bf16 stochastic rounding of
+ * shared_ffi/bindings.py:44-48: writes dX[b, d] (bf16 bits, [B, D] row-major) =
+ * SR(dXT[d, b], tl.randint(seed, b*D + d)).  The reference uses seed 123.
+ */
+int haste_ffi_bwd_features_sr(const int32_t* idx, const void* W, const void* dY, int64_t lddy,
+                              uint16_t* dX, uint64_t seed, void* workspace,
+                              int64_t workspace_bytes, int64_t B, int64_t D, int64_t F, int64_t O,
+                              int64_t G, int32_t dtype, void* stream);
+
+/*
+ * Backward to weights (+ optional bias gradient):
+ *   dW[l, j] = sum_b dY[b, l] * xT[idx[l/G, j], b]    stored as dW_dtype (RNE for 16-bit)
+ *   dbias[l] = sum_b dY[b, l]                           stored as dbias_dtype (NULL = skip)
+ * Replaces ffi_backward_weights_cuda (shared_ffi/ffi_backward_weights.cu:486-684, bound at
+ * shared_ffi/ffi_wrapper.cpp:14-19,30) and the bias gradient torch.sum(grad_output, 0)
+ * (shared_ffi/bindings.py:40).
+ */
+int haste_ffi_bwd_weights(const int32_t* idx, const void* xT, int64_t ldx, const void* dY,
+                          int64_t lddy, void* dW, int32_t dW_dtype, void* dbias,
+                          int32_t dbias_dtype, int64_t B, int64_t D, int64_t F, int64_t O,
+                          int64_t G, int32_t dtype, void* stream);
+
+/*
+ * Stochastic rounding fp32 -> bf16: out[i] = SR(x[i], tl.randint(seed, offset0 + i)).
+ * Replaces stochastic_rounding (shared_ffi/sr_triton.py:51-59).
+ */
+int haste_sr_round_bf16(const float* x, uint16_t* out, int64_t n, uint64_t seed,
+                        uint64_t offset0, void* stream);
+
+/*
+ * Fused SGD step on bf16 weights, in place (one pass):
+ *   g' = fma(wd, w, g);  [m' = fma(mu, m, g'); m = m';]  w' = fma(-lr, m' or g', w)
+ *   w  = do_sr ? SR(w', tl.randint(seed, offset0 + i)) : RNE(w')
+ * g_dtype: bf16, f16 or f32.  m (fp32) may be NULL when use_mom == 0.
+ * Replaces sgd_update / _sgd_m_wd_sr (shared_ffi/sr_triton.py:109-213).
+ */
+int haste_sgd_sr_step(uint16_t* w, const void* g, int32_t g_dtype, float* m, int64_t n,
+                      float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
+                      uint64_t seed, uint64_t offset0, void* stream);
+
+/*
+ * On-device rewire of a bf16 FFI layer (prune + regrow), in place on W and idx.
+ * Replaces GroupFixedFanIn.rewire (shared_ffi/rewire.py:143-239) with a
+ * deterministic contract:
+ *   score[g, j] = (sequential fp32 sum over the group's rows of |W[l, j]|) / rows
+ *   prune: THRESHOLD -> score < threshold; FRACTION -> the k smallest (score, j)
+ *   regrow index: RANDOM -> floor(philox(seed; g*F+j, 1, 0).w0 * D / 2^32);
+ *                 UNUSED -> attempts t = 0.. with counter (g*F+j, 1, t), first
+ *                 candidate not present in the group (64 attempts, then the last)
+ *   new weights of every row at a pruned slot: ZERO -> 0;
+ *     RANDOM -> RNE(fma(u01, 2*bound, -bound)), u01 = (philox(seed; l*F+j, 2, 0).w0 >> 8) * 2^-24
+ * scores_out [Gc, F] fp32 and n_pruned (one int32, incremented) may be NULL.
+ */
+int haste_rewire(uint16_t* W, int32_t* idx, float* scores_out, int32_t* n_pruned, int64_t O,
+                 int64_t F, int64_t G, int64_t D, int32_t prune_mode, float threshold, int64_t k,
+                 int32_t regrow_mode, int32_t init_mode, float bound, uint64_t seed,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HASTE_FFI_H */

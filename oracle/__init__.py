@@ -1,0 +1,176 @@
+"""CPU oracle for the HASTE FFI hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker (or as the timed CPU
+baseline).  The product package ``haste_amd`` never imports it; on a machine
+without the HIP library the product raises instead of falling back here.
+
+Two halves:
+
+* ``ffi.py`` -- the reference's layer math restated as a PyTorch-CPU gather + bmm
+  formulation in fp32 (forward, backward-to-features, backward-to-weights,
+  bias gradient).
+* ``haste_oracle.c`` (built to ``libhaste_oracle.so`` by ``oracle/Makefile``) --
+  Philox4x32-10 / ``tl.randint``, stochastic rounding, the fused SGD step and
+  the rewire contract, bound here through ctypes.
+
+Parity pins for every function are listed in each function's docstring; the
+tests that apply them live in ``tests/test_oracle_*.py``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+from .ffi import (  # noqa: F401  (re-exported)
+    ffi_forward,
+    ffi_backward_features,
+    ffi_backward_weights,
+    bias_grad,
+    pad_groups,
+)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libhaste_oracle.so")
+_lib = None
+
+BF16, F16, F32 = 0, 1, 2
+PRUNE_THRESHOLD, PRUNE_FRACTION = 0, 1
+REGROW_RANDOM, REGROW_UNUSED = 0, 1
+INIT_ZERO, INIT_RANDOM = 0, 1
+
+
+def build() -> str:
+    """Compile the oracle C library with oracle/Makefile; returns its path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        i64, u64, f32, c_int = ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_int
+        L.ho_philox4x32.argtypes = [P, P, c_int, P]
+        L.ho_randint.argtypes = [u64, u64]
+        L.ho_randint.restype = ctypes.c_uint32
+        L.ho_randint_array.argtypes = [u64, u64, i64, P]
+        L.ho_sr_bf16.argtypes = [f32, ctypes.c_uint32]
+        L.ho_sr_bf16.restype = ctypes.c_uint16
+        L.ho_f32_to_bf16_rne.argtypes = [f32]
+        L.ho_f32_to_bf16_rne.restype = ctypes.c_uint16
+        L.ho_sr_round_bf16.argtypes = [P, P, i64, u64, u64]
+        L.ho_sgd_sr_step.argtypes = [P, P, c_int, P, i64, f32, f32, f32, c_int, c_int, u64, u64]
+        L.ho_rewire_scores.argtypes = [P, P, i64, i64, i64]
+        L.ho_rewire.argtypes = [P, P, i64, i64, i64, i64, c_int, f32, i64, c_int, c_int, f32, u64, P, P]
+        L.ho_rewire.restype = i64
+        L.ho_num_threads.restype = c_int
+        L.ho_set_num_threads.argtypes = [c_int]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def philox4x32(ctr, key, rounds: int = 10) -> np.ndarray:
+    """Philox4x32-R block function.  Pinned by Random123 KATs."""
+    c = np.ascontiguousarray(np.asarray(ctr, dtype=np.uint32))
+    k = np.ascontiguousarray(np.asarray(key, dtype=np.uint32))
+    out = np.zeros(4, dtype=np.uint32)
+    lib().ho_philox4x32(_ptr(c), _ptr(k), rounds, _ptr(out))
+    return out
+
+
+def randint(seed: int, offset0: int, n: int) -> np.ndarray:
+    """tl.randint(seed, offset0 + arange(n)) (Triton random.py randint4x word 0).
+    Pinned by tests/golden/randint_vectors.json."""
+    out = np.empty(n, dtype=np.uint32)
+    lib().ho_randint_array(seed, offset0, n, _ptr(out))
+    return out
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 round-to-nearest-even, as uint16 bit patterns."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def sr_round_bf16(x: np.ndarray, seed: int, offset0: int = 0) -> np.ndarray:
+    """stochastic_rounding(x, out, seed) (shared_ffi/sr_triton.py:51-59); returns
+    bf16 bit patterns (uint16)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().ho_sr_round_bf16(_ptr(x), _ptr(out), x.size, seed, offset0)
+    return out
+
+
+def sgd_sr_step(w_bits: np.ndarray, g: np.ndarray, m: np.ndarray | None, lr: float, wd: float,
+                mu: float, use_mom: bool, do_sr: bool, seed: int, offset0: int = 0):
+    """_sgd_m_wd_sr (shared_ffi/sr_triton.py:109-168) on bf16 weights given as
+    uint16 bit patterns.  ``g`` is float32, or uint16 bf16 bit patterns.
+    Returns (new weight bits, new momentum or None); inputs are not modified."""
+    w = np.array(w_bits, dtype=np.uint16, copy=True, order="C")
+    if g.dtype == np.uint16:
+        g_dtype = BF16
+    elif g.dtype == np.float16:
+        g_dtype = F16
+    else:
+        g_dtype = F32
+        g = g.astype(np.float32)
+    g = np.ascontiguousarray(g)
+    mm = None if m is None else np.array(m, dtype=np.float32, copy=True, order="C")
+    lib().ho_sgd_sr_step(_ptr(w), _ptr(g), g_dtype, None if mm is None else _ptr(mm), w.size,
+                         np.float32(lr), np.float32(wd), np.float32(mu), int(bool(use_mom)),
+                         int(bool(do_sr)), seed, offset0)
+    return w, mm
+
+
+def rewire_scores(w_bits: np.ndarray, G: int) -> np.ndarray:
+    O, F = w_bits.shape
+    Gc = (O + G - 1) // G
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    s = np.empty((Gc, F), dtype=np.float32)
+    lib().ho_rewire_scores(_ptr(w_bits), _ptr(s), O, F, G)
+    return s
+
+
+def rewire(w_bits: np.ndarray, idx: np.ndarray, G: int, D: int, *, prune_mode: int,
+           threshold: float = 0.0, k: int = 0, regrow_mode: int = REGROW_RANDOM,
+           init_mode: int = INIT_ZERO, bound: float = 0.0, seed: int = 0):
+    """Rewire contract of haste_oracle.c (restating shared_ffi/rewire.py:143-239).
+    Returns (new weight bits, new idx, n_pruned, scores, mask)."""
+    w = np.array(w_bits, dtype=np.uint16, copy=True, order="C")
+    ix = np.array(idx, dtype=np.int32, copy=True, order="C")
+    O, F = w.shape
+    Gc = ix.shape[0]
+    scores = np.empty((Gc, F), dtype=np.float32)
+    mask = np.empty((Gc, F), dtype=np.uint8)
+    n = lib().ho_rewire(_ptr(w), _ptr(ix), O, F, G, D, prune_mode, np.float32(threshold), k,
+                        regrow_mode, init_mode, np.float32(bound), seed, _ptr(scores), _ptr(mask))
+    return w, ix, int(n), scores, mask.astype(bool)
+
+
+def set_num_threads(n: int) -> None:
+    lib().ho_set_num_threads(int(n))
+
+
+def num_threads() -> int:
+    return int(lib().ho_num_threads())

@@ -1,0 +1,290 @@
+/*
+ * haste_oracle.c -- CPU restatement of the integer/bit-level parts of HASTE's
+ * FFI hot path.  TEST INFRASTRUCTURE ONLY: only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg load this library, and only as the checker
+ * (or the timed CPU baseline).  The product path (haste_amd/) never links it.
+ *
+ * What it restates (reference paths relative to the xmc-aalto/haste tree):
+ *   - Philox4x32-10 exactly as Triton's tl.randint(seed, offset) evaluates it
+ *     (Triton 3.x triton/language/random.py philox_impl/randint4x; called from
+ *     shared_ffi/sr_triton.py:11).  Pinned by Random123 KATs and by tl.randint
+ *     vectors produced with the installed Triton 3.6.0 interpreter
+ *     (tests/golden/randint_vectors.json).
+ *   - stochastic_rounding_to_bf16, shared_ffi/sr_triton.py:9-16.
+ *   - _seeded_stochastic_rounding / stochastic_rounding, sr_triton.py:27-59.
+ *   - _sgd_m_wd_sr / sgd_update, sr_triton.py:109-213, with the FMA contract
+ *     g' = fma(wd, w, g); m' = fma(mu, m, g'); w' = fma(-lr, m' or g', w)
+ *     (Triton compiles with fp fusion on, so these products are contracted).
+ *   - GroupFixedFanIn.rewire, shared_ffi/rewire.py:143-239, with the random
+ *     draws replaced by documented Philox streams (torch.randint/uniform_ device
+ *     streams cannot be reproduced) and topk ties broken by (score, slot).
+ *
+ * Parity status of each function is stated in the function's comment.
+ * Built with -ffp-contract=off: every fused multiply-add here is an explicit
+ * fmaf(), nothing else is contracted.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define PHILOX_M0 0xD2511F53u
+#define PHILOX_M1 0xCD9E8D57u
+#define PHILOX_W0 0x9E3779B9u
+#define PHILOX_W1 0xBB67AE85u
+
+/* Philox4x32 with R rounds (Salmon et al., SC'11, "Parallel random numbers:
+ * as easy as 1, 2, 3"; round function as in Triton's philox_impl).
+ * Pinned: Random123 known-answer vectors + tl.randint vectors. */
+void ho_philox4x32(const uint32_t ctr[4], const uint32_t key[2], int rounds, uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < rounds; ++r) {
+        uint64_t p0 = (uint64_t)PHILOX_M0 * c0;
+        uint64_t p1 = (uint64_t)PHILOX_M1 * c2;
+        uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+        k0 += PHILOX_W0;
+        k1 += PHILOX_W1;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* tl.randint(seed, offset): word 0 of Philox4x32-10 with key = (seed lo, seed hi)
+ * and counter = (offset lo, offset hi, 0, 0).  Pinned as above. */
+uint32_t ho_randint(uint64_t seed, uint64_t offset) {
+    uint32_t ctr[4] = {(uint32_t)offset, (uint32_t)(offset >> 32), 0u, 0u};
+    uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t out[4];
+    ho_philox4x32(ctr, key, 10, out);
+    return out[0];
+}
+
+void ho_randint_array(uint64_t seed, uint64_t offset0, int64_t n, uint32_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ho_randint(seed, offset0 + (uint64_t)i);
+}
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float ho_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+float ho_f16_to_f32(uint16_t h);
+
+/* fp32 -> bf16 round-to-nearest-even; NaN -> quiet NaN with the input sign. */
+uint16_t ho_f32_to_bf16_rne(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7FFFu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+/* stochastic_rounding_to_bf16 (sr_triton.py:9-16): add the low 16 random bits to
+ * the fp32 bit pattern (32-bit wrap-around add) and keep the upper half.
+ * NaN inputs give a quiet NaN (the bit trick would otherwise make the payload
+ * depend on the random bits; the reference's NaN result is not pinned).
+ * Pinned: closed form checks (exact values unchanged, round-up probability,
+ * brute-force interval check) in tests/test_oracle_sr.py. */
+uint16_t ho_sr_bf16(float x, uint32_t r) {
+    uint32_t u = f2u(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u = u + (r & 0xFFFFu);
+    return (uint16_t)(u >> 16);
+}
+
+/* stochastic_rounding(x, output, seed) (sr_triton.py:51-59): element i uses
+ * offset offset0 + i under `seed`. */
+void ho_sr_round_bf16(const float* x, uint16_t* out, int64_t n, uint64_t seed, uint64_t offset0) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) out[i] = ho_sr_bf16(x[i], ho_randint(seed, offset0 + (uint64_t)i));
+}
+
+/* IEEE binary16 -> fp32 (exact). */
+float ho_f16_to_f32(uint16_t h) {
+    uint32_t s = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    if (e == 0) {
+        if (m == 0) return u2f(s);
+        float v = ldexpf((float)m, -24);
+        return s ? -v : v;
+    }
+    if (e == 31) return u2f(s | 0x7F800000u | (m << 13));
+    return u2f(s | ((e + 112u) << 23) | (m << 13));
+}
+
+enum { HO_BF16 = 0, HO_F16 = 1, HO_F32 = 2 };
+
+static inline float load_any(const void* p, int dtype, int64_t i) {
+    switch (dtype) {
+    case HO_BF16: return ho_bf16_to_f32(((const uint16_t*)p)[i]);
+    case HO_F16: return ho_f16_to_f32(((const uint16_t*)p)[i]);
+    default: return ((const float*)p)[i];
+    }
+}
+
+/* Fused SGD step (_sgd_m_wd_sr, sr_triton.py:109-168) on bf16 weights, in place.
+ *   g  = float(grad[i]);  w = float(W[i])
+ *   g' = fma(wd, w, g)
+ *   use_mom: m' = fma(mu, m[i], g'); m[i] = m'; w' = fma(-lr, m', w)
+ *   else:    w' = fma(-lr, g', w)
+ *   W[i] = do_sr ? SR(w', randint(seed, offset0 + i)) : RNE(w')
+ * lr, wd, mu are fp32 (Triton passes Python floats as fp32 scalars).
+ * Pinned: exact-rational brute force of the FMA chain on small arrays,
+ * closed-form special cases (lr = 0, wd = 0), tests/test_oracle_sgd.py. */
+void ho_sgd_sr_step(uint16_t* w, const void* g, int g_dtype, float* m, int64_t n,
+                    float lr, float wd, float mu, int use_mom, int do_sr,
+                    uint64_t seed, uint64_t offset0) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float wf = ho_bf16_to_f32(w[i]);
+        float gf = load_any(g, g_dtype, i);
+        gf = fmaf(wd, wf, gf);
+        float upd = gf;
+        if (use_mom) {
+            float mv = fmaf(mu, m[i], gf);
+            m[i] = mv;
+            upd = mv;
+        }
+        float nw = fmaf(-lr, upd, wf);
+        w[i] = do_sr ? ho_sr_bf16(nw, ho_randint(seed, offset0 + (uint64_t)i))
+                     : ho_f32_to_bf16_rne(nw);
+    }
+}
+
+int ho_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+void ho_set_num_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
+/* ---------------------------------------------------------------------------
+ * Rewire (GroupFixedFanIn.rewire, shared_ffi/rewire.py:143-239).
+ *
+ * Contract (deterministic; the reference's random draws come from torch
+ * generators, so this build fixes its own Philox streams):
+ *  1. score[g][j] = (sum over rows l of group g, in ascending l, of fp32 |W[l][j]|)
+ *                   / (float)rows_in_group            (rewire.py:169-185)
+ *  2. prune mask:  threshold mode: score < thr        (rewire.py:188-189)
+ *                  fraction mode:  the k slots with the smallest (score, slot)
+ *                  pairs, k = int(F * fraction)      (rewire.py:190-204)
+ *  3. regrow index for pruned slot (g, j):
+ *       RANDOM (with replacement, as rewire.py:211):
+ *         u = philox(key = seed, ctr = (g*F + j, 1, 0, 0)).w0;  d = (u * D) >> 32
+ *       UNUSED (never an index already present in the group): slots are visited
+ *         in ascending j; attempt t uses ctr = (g*F + j, 1, t, 0); a candidate
+ *         is accepted if it is not among the group's current indices (kept
+ *         slots plus indices regrown earlier in this call); after
+ *         HO_UNUSED_MAX_TRIES failed attempts the last candidate is taken.
+ *  4. weights of every row of the group at a pruned slot:
+ *       ZERO: 0.   RANDOM: u = philox(key = seed, ctr = (l*F + j, 2, 0, 0)).w0,
+ *       v = fma((float)(u >> 8) * 2^-24, 2*bound, -bound), bound = 1/sqrt(F)
+ *       (fp32, passed in), stored RNE to bf16.           (rewire.py:219-239)
+ * Returns the number of pruned slots.  Scores and mask are optional outputs.
+ * Pinned: invariants and brute-force selection in tests/test_oracle_rewire.py.
+ * --------------------------------------------------------------------------- */
+#define HO_UNUSED_MAX_TRIES 64
+
+enum { HO_PRUNE_THRESHOLD = 0, HO_PRUNE_FRACTION = 1 };
+enum { HO_REGROW_RANDOM = 0, HO_REGROW_UNUSED = 1 };
+enum { HO_INIT_ZERO = 0, HO_INIT_RANDOM = 1 };
+
+static uint32_t philox_w0(uint64_t seed, uint32_t c0, uint32_t c1, uint32_t c2) {
+    uint32_t ctr[4] = {c0, c1, c2, 0u};
+    uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t out[4];
+    ho_philox4x32(ctr, key, 10, out);
+    return out[0];
+}
+
+void ho_rewire_scores(const uint16_t* W, float* scores, int64_t O, int64_t F, int64_t G) {
+    int64_t Gc = (O + G - 1) / G;
+    for (int64_t g = 0; g < Gc; ++g) {
+        int64_t l0 = g * G, l1 = l0 + G < O ? l0 + G : O;
+        float cnt = (float)(l1 - l0);
+        for (int64_t j = 0; j < F; ++j) {
+            float s = 0.0f;
+            for (int64_t l = l0; l < l1; ++l) s += fabsf(ho_bf16_to_f32(W[l * F + j]));
+            scores[g * F + j] = s / cnt;
+        }
+    }
+}
+
+int64_t ho_rewire(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G, int64_t D,
+                  int prune_mode, float thr, int64_t k, int regrow_mode, int init_mode,
+                  float bound, uint64_t seed, float* scores_out, uint8_t* mask_out) {
+    int64_t Gc = (O + G - 1) / G;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(Gc * F));
+    uint8_t* mask = (uint8_t*)calloc((size_t)(Gc * F), 1);
+    ho_rewire_scores(W, scores, O, F, G);
+    int64_t total = 0;
+    for (int64_t g = 0; g < Gc; ++g) {
+        float* s = scores + g * F;
+        uint8_t* mk = mask + g * F;
+        if (prune_mode == HO_PRUNE_THRESHOLD) {
+            for (int64_t j = 0; j < F; ++j) mk[j] = s[j] < thr;
+        } else {
+            /* rank of slot j = #slots with (score, slot) lexicographically smaller */
+            for (int64_t j = 0; j < F; ++j) {
+                int64_t rank = 0;
+                for (int64_t q = 0; q < F; ++q)
+                    if (s[q] < s[j] || (s[q] == s[j] && q < j)) ++rank;
+                mk[j] = rank < k;
+            }
+        }
+        int32_t* gi = idx + g * F;
+        for (int64_t j = 0; j < F; ++j) {
+            if (!mk[j]) continue;
+            ++total;
+            uint32_t slot = (uint32_t)(g * F + j);
+            uint32_t cand = (uint32_t)(((uint64_t)philox_w0(seed, slot, 1u, 0u) * (uint64_t)D) >> 32);
+            if (regrow_mode == HO_REGROW_UNUSED) {
+                for (uint32_t t = 0; t < HO_UNUSED_MAX_TRIES; ++t) {
+                    cand = (uint32_t)(((uint64_t)philox_w0(seed, slot, 1u, t) * (uint64_t)D) >> 32);
+                    int used = 0;
+                    for (int64_t q = 0; q < F; ++q) {
+                        /* current index set: kept slots, and pruned slots already regrown (q < j) */
+                        if ((!mk[q] || q < j) && gi[q] == (int32_t)cand) { used = 1; break; }
+                    }
+                    if (!used) break;
+                }
+            }
+            gi[j] = (int32_t)cand;
+        }
+        int64_t l0 = g * G, l1 = l0 + G < O ? l0 + G : O;
+        for (int64_t l = l0; l < l1; ++l) {
+            for (int64_t j = 0; j < F; ++j) {
+                if (!mk[j]) continue;
+                if (init_mode == HO_INIT_ZERO) {
+                    W[l * F + j] = 0;
+                } else {
+                    uint32_t u = philox_w0(seed, (uint32_t)(l * F + j), 2u, 0u);
+                    float u01 = (float)(u >> 8) * 0x1p-24f;
+                    W[l * F + j] = ho_f32_to_bf16_rne(fmaf(u01, 2.0f * bound, -bound));
+                }
+            }
+        }
+    }
+    if (scores_out) memcpy(scores_out, scores, sizeof(float) * (size_t)(Gc * F));
+    if (mask_out) memcpy(mask_out, mask, (size_t)(Gc * F));
+    free(scores);
+    free(mask);
+    return total;
+}

@@ -1,0 +1,109 @@
+"""C-ABI library: loads, exports every declared symbol, and rejects bad
+arguments on the host (these calls return before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from haste_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "haste_ffi.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(haste_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert set(_declared_symbols()) == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared_symbols():
+        assert hasattr(L, name), name
+
+
+def test_version_and_error_string():
+    assert _lib.lib().haste_abi_version() == 1
+    assert isinstance(_lib.last_error(), str)
+
+
+def _fwd(**kw):
+    args = dict(idx=8, xT=16, ldx=64, W=32, bias=None, out=48, ldo=4096, B=64, D=768, F=32,
+                O=4096, G=32, dtype=_lib.DTYPE_BF16, stream=None)
+    args.update(kw)
+    return _lib.lib().haste_ffi_forward(*args.values())
+
+
+def test_forward_rejects_bad_group_size():
+    assert _fwd(G=48) == _lib.HASTE_ERR_UNSUPPORTED
+    assert "group size" in _lib.last_error()
+
+
+def test_forward_rejects_bad_fanin():
+    assert _fwd(F=24) == _lib.HASTE_ERR_INVALID_ARG
+    assert "FANIN size should be multiple of 16" in _lib.last_error()
+    assert _fwd(F=512) == _lib.HASTE_ERR_UNSUPPORTED
+
+
+def test_forward_rejects_bad_strides_and_dtype():
+    assert _fwd(ldx=60) == _lib.HASTE_ERR_INVALID_ARG
+    assert _fwd(ldo=4095) == _lib.HASTE_ERR_INVALID_ARG
+    assert _fwd(dtype=_lib.DTYPE_F32) == _lib.HASTE_ERR_UNSUPPORTED
+    assert _fwd(B=0) == _lib.HASTE_ERR_INVALID_ARG
+    assert _fwd(xT=18) == _lib.HASTE_ERR_INVALID_ARG  # misaligned
+
+
+def test_bwd_features_workspace_size():
+    L = _lib.lib()
+    n = L.haste_ffi_bwd_features_workspace_size(512, 768, 128, 131073, 64, _lib.DTYPE_BF16)
+    assert n > 0 and n % 4 == 0
+    assert L.haste_ffi_bwd_features_workspace_size(512, 768, 128, 131073, 48, 0) < 0
+
+
+def test_bwd_features_rejects_small_workspace():
+    L = _lib.lib()
+    rc = L.haste_ffi_bwd_features(16, 32, 48, 4096, 64, 256, 16, 64, 768, 32, 4096, 32,
+                                  _lib.DTYPE_BF16, None)
+    assert rc == _lib.HASTE_ERR_WORKSPACE
+    assert "workspace too small" in _lib.last_error()
+
+
+def test_sgd_rejects_bad_dtype_and_missing_momentum():
+    L = _lib.lib()
+    assert L.haste_sgd_sr_step(16, 32, 7, None, 100, 0.1, 0.0, 0.0, 0, 1, 1, 0, None) == \
+        _lib.HASTE_ERR_UNSUPPORTED
+    assert L.haste_sgd_sr_step(16, 32, 0, None, 100, 0.1, 0.0, 0.9, 1, 1, 1, 0, None) == \
+        _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_sgd_sr_step(16, 32, 0, None, 0, 0.1, 0.0, 0.0, 0, 1, 1, 0, None) == _lib.HASTE_OK
+
+
+def test_rewire_rejects_bad_modes():
+    L = _lib.lib()
+    assert L.haste_rewire(16, 32, None, None, 100, 8, 16, 50, 5, 0.0, 0, 0, 0, 0.1, 1, None) == \
+        _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_rewire(16, 32, None, None, 100, 8, 16, 50, 1, 0.0, 9, 0, 0, 0.1, 1, None) == \
+        _lib.HASTE_ERR_INVALID_ARG
+
+
+def test_check_raises_haste_error():
+    assert _fwd(G=48) != 0
+    with pytest.raises(_lib.HasteError, match="group size"):
+        _lib.check(_fwd(G=48))
+
+
+def test_python_api_rejects_cpu_tensors():
+    """The product path has no CPU implementation: CPU tensors raise."""
+    from haste_amd import ops, sr
+    x = torch.randn(4, 16).to(torch.bfloat16)
+    W = torch.randn(32, 16).to(torch.bfloat16)
+    idx = torch.zeros(1, 16, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        ops.group_ffi_mul(x, W, idx, None, gsize=32)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        sr.stochastic_rounding(torch.randn(8), torch.empty(8, dtype=torch.bfloat16), 1)

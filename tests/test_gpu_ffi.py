@@ -1,0 +1,164 @@
+"""GPU parity of the FFI kernels (forward, backward to features, backward to
+weights + bias) against the CPU oracle, through the C ABI.
+
+Tolerance: bf16/f16 outputs match the fp32-accumulate
+oracle within rtol 1e-2 / atol 1e-3.  fp32 outputs (dX^T, dW in fp32 mode) are
+checked at rtol 1e-4 / atol 1e-5 (summation order differs only).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from haste_amd import _C, _lib
+
+pytestmark = pytest.mark.gpu
+
+TOL16 = dict(rtol=1e-2, atol=1e-3)
+TOL32 = dict(rtol=1e-4, atol=1e-5)
+
+
+def make_case(B, D, O, G, F, seed=0, dtype=torch.bfloat16, idx_mode="perm"):
+    g = torch.Generator().manual_seed(seed)
+    Gc = (O + G - 1) // G
+    x = torch.randn(B, D, generator=g).to(dtype)
+    bound = 1.0 / F ** 0.5
+    W = ((torch.rand(O, F, generator=g) * 2 - 1) * bound).to(dtype)
+    bias = (torch.randn(O, generator=g) * 0.1).to(dtype)
+    if idx_mode == "perm" and F <= D:
+        idx = torch.stack([torch.randperm(D, generator=g)[:F] for _ in range(Gc)]).to(torch.int32)
+    else:
+        idx = torch.randint(0, D, (Gc, F), generator=g, dtype=torch.int32)
+    if idx_mode == "dups":
+        idx[0, :] = 5                                  # one index for the whole group
+        if Gc > 1:
+            idx[1, : F // 2] = idx[1, F // 2: 2 * (F // 2)]  # every index twice
+        if Gc > 2:
+            idx[2, 3:12] = 7                            # a run of 9 equal indices
+    dY = (torch.randn(B, O, generator=g) * 0.1).to(dtype)
+    return x, W, bias, idx, dY
+
+
+def gpu_forward(x, W, bias, idx, G, dev):
+    B, D = x.shape
+    O, F = W.shape
+    xT = x.t().contiguous().to(dev)
+    return _C.ffi_forward_cuda(idx.to(dev), xT, W.to(dev), None if bias is None else bias.to(dev),
+                               B, D, F, O, G)
+
+
+CASES = [
+    # B, D, O, G, F, idx_mode
+    (64, 768, 4096, 32, 32, "perm"),
+    (64, 768, 4133, 32, 32, "perm"),      # partial last group, O % 8 != 0
+    (100, 300, 1000, 16, 16, "random"),   # B % 8 != 0, G = 16
+    (7, 50, 130, 16, 48, "random"),       # F % 32 != 0, tiny batch
+    (128, 768, 8193, 64, 128, "perm"),    # config 1 shape at reduced O, 1-label last group
+    (96, 512, 2000, 64, 64, "dups"),      # duplicate indices, runs of equal indices
+    (64, 4096, 3000, 32, 256, "random"),  # wide input, F = 256 (config 3 family)
+    (40, 768, 2100, 128, 128, "random"),  # G = 128 (config 4 family)
+    (33, 200, 700, 128, 256, "dups"),
+    (1, 64, 64, 64, 64, "random"),
+]
+
+
+@pytest.mark.parametrize("B,D,O,G,F,mode", CASES)
+def test_forward(dev, B, D, O, G, F, mode):
+    x, W, bias, idx, _ = make_case(B, D, O, G, F, idx_mode=mode)
+    out = gpu_forward(x, W, bias, idx, G, dev)
+    assert out.shape == (B, O)
+    ref = oracle.ffi_forward(idx, x.t().contiguous(), W, bias, G)
+    torch.testing.assert_close(out.float().cpu(), ref, **TOL16)
+    out_nb = gpu_forward(x, W, None, idx, G, dev)
+    torch.testing.assert_close(out_nb.float().cpu(), oracle.ffi_forward(idx, x.t().contiguous(), W, None, G), **TOL16)
+
+
+def test_forward_f16(dev):
+    x, W, bias, idx, _ = make_case(64, 768, 4133, 32, 64, dtype=torch.float16)
+    out = gpu_forward(x, W, bias, idx, 32, dev)
+    torch.testing.assert_close(out.float().cpu(), oracle.ffi_forward(idx, x.t().contiguous(), W, bias, 32), **TOL16)
+
+
+@pytest.mark.parametrize("B,D,O,G,F,mode", CASES)
+def test_backward_features(dev, B, D, O, G, F, mode):
+    x, W, bias, idx, dY = make_case(B, D, O, G, F, idx_mode=mode, seed=1)
+    xT = x.t().contiguous().to(dev)
+    dXT = _C.ffi_backward_features_cuda(xT, W.to(dev), idx.to(dev), dY.to(dev), B, D, F, O, G)
+    ref = oracle.ffi_backward_features(idx, W, dY, G, D)
+    torch.testing.assert_close(dXT.cpu(), ref, **TOL32)
+
+
+@pytest.mark.parametrize("B,D,O,G,F,mode", CASES[:6])
+def test_backward_features_sr_fused(dev, oracle_mod, B, D, O, G, F, mode):
+    """Fused SR output == oracle SR (seed 123, offset b*D+d) of the GPU's own fp32
+    dX, bit for bit; and within tolerance of the fp32 oracle."""
+    x, W, bias, idx, dY = make_case(B, D, O, G, F, idx_mode=mode, seed=2)
+    Wd, idxd = W.to(dev), idx.to(dev)
+    dYd, lddy = _C.rows_aligned(dY.to(dev))
+    dXT = _C.ffi_backward_features_cuda(x.t().contiguous().to(dev), Wd, idxd, dYd, B, D, F, O, G)
+    ws = _C.bwd_features_workspace(B, D, F, O, G, torch.bfloat16, dev)
+    dX = torch.empty(B, D, dtype=torch.bfloat16, device=dev)
+    _lib.call("haste_ffi_bwd_features_sr", idxd.data_ptr(), Wd.data_ptr(), dYd.data_ptr(),
+              lddy, dX.data_ptr(), 123, ws.data_ptr(), ws.numel(), B, D, F, O, G,
+              _lib.DTYPE_BF16, _C.stream_of(Wd))
+    torch.cuda.synchronize()
+    exp = oracle_mod.sr_round_bf16(dXT.t().contiguous().cpu().numpy(), seed=123)
+    got = dX.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, exp)
+    ref = oracle.ffi_backward_features(idx, W, dY, G, D).t()
+    torch.testing.assert_close(dX.float().cpu(), ref, **TOL16)
+
+
+@pytest.mark.parametrize("B,D,O,G,F,mode", CASES)
+def test_backward_weights_and_bias(dev, B, D, O, G, F, mode):
+    x, W, bias, idx, dY = make_case(B, D, O, G, F, idx_mode=mode, seed=3)
+    xT, ldx = _C.padded_transpose(x.to(dev))
+    dYd, lddy = _C.rows_aligned(dY.to(dev))
+    idxd = idx.to(dev)
+    ref_w = oracle.ffi_backward_weights(idx, x.t().contiguous(), dY, G)
+    ref_b = oracle.bias_grad(dY)
+    for wcode, tol in ((_lib.DTYPE_F32, TOL32), (_lib.DTYPE_BF16, TOL16)):
+        dW = torch.empty(O, F, dtype=torch.float32 if wcode == _lib.DTYPE_F32 else torch.bfloat16, device=dev)
+        db = torch.empty(O, dtype=dW.dtype, device=dev)
+        _lib.call("haste_ffi_bwd_weights", idxd.data_ptr(), xT.data_ptr(), ldx, dYd.data_ptr(),
+                  lddy, dW.data_ptr(), wcode, db.data_ptr(), wcode, B, D, F, O, G,
+                  _lib.DTYPE_BF16, _C.stream_of(dYd))
+        torch.testing.assert_close(dW.float().cpu(), ref_w, **tol)
+        torch.testing.assert_close(db.float().cpu(), ref_b, **(TOL32 if wcode == _lib.DTYPE_F32 else dict(rtol=1e-2, atol=1e-2)))
+
+
+def test_backward_weights_reference_api(dev):
+    x, W, bias, idx, dY = make_case(64, 768, 4133, 32, 32, seed=4)
+    dW = _C.ffi_backward_weights_cuda(x.t().contiguous().to(dev), W.to(dev), idx.to(dev),
+                                      dY.to(dev), 64, 768, 32, 4133, 32)
+    assert dW.dtype == torch.bfloat16 and dW.shape == (4133, 32)
+    torch.testing.assert_close(dW.float().cpu(), oracle.ffi_backward_weights(idx, x.t().contiguous(), dY, 32), **TOL16)
+
+
+def test_backward_f16(dev):
+    x, W, bias, idx, dY = make_case(64, 768, 2048, 64, 64, dtype=torch.float16, seed=5)
+    dXT = _C.ffi_backward_features_cuda(x.t().contiguous().to(dev), W.to(dev), idx.to(dev),
+                                        dY.to(dev), 64, 768, 64, 2048, 64)
+    torch.testing.assert_close(dXT.cpu(), oracle.ffi_backward_features(idx, W, dY, 64, 768), **TOL32)
+    dW = _C.ffi_backward_weights_cuda(x.t().contiguous().to(dev), W.to(dev), idx.to(dev),
+                                      dY.to(dev), 64, 768, 64, 2048, 64)
+    torch.testing.assert_close(dW.float().cpu(), oracle.ffi_backward_weights(idx, x.t().contiguous(), dY, 64), **TOL16)
+
+
+def test_backward_features_deterministic(dev):
+    """Same inputs -> bitwise identical fp32 output (no float atomics on global memory)."""
+    x, W, bias, idx, dY = make_case(256, 768, 20000, 64, 128, seed=6, idx_mode="dups")
+    args = (x.t().contiguous().to(dev), W.to(dev), idx.to(dev), dY.to(dev), 256, 768, 128, 20000, 64)
+    a = _C.ffi_backward_features_cuda(*args)
+    b = _C.ffi_backward_features_cuda(*args)
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_out_of_range_indices_are_clamped(dev):
+    x, W, bias, idx, dY = make_case(16, 64, 128, 32, 32, seed=7, idx_mode="random")
+    bad = idx.clone()
+    bad[0, 0] = 10**6
+    bad[1, 1] = -5
+    clamped = bad.clamp(0, 63)
+    out = gpu_forward(x, W, bias, bad, 32, dev)
+    torch.testing.assert_close(out.float().cpu(), oracle.ffi_forward(clamped, x.t().contiguous(), W, bias, 32), **TOL16)

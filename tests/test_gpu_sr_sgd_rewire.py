@@ -1,0 +1,134 @@
+"""GPU bit-exactness of stochastic rounding, the fused SR-SGD step and rewire
+against the CPU oracle (identical Philox seed/offset contract)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from haste_amd import _C, _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("n,offset0,seed", [(1, 0, 123), (1000, 0, 42), (393216, 0, 123),
+                                            (4099, 5, 2**32 + 7), (77, 2**32 - 3, 1)])
+def test_sr_round(dev, n, offset0, seed):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    x[: min(n, 4)] = [0.0, -0.0, np.inf, 1e-40][: min(n, 4)]
+    xd = torch.from_numpy(x).to(dev)
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    _lib.call("haste_sr_round_bf16", xd.data_ptr(), out.data_ptr(), n, seed, offset0, _C.stream_of(xd))
+    assert np.array_equal(bits(out), oracle.sr_round_bf16(x, seed, offset0))
+
+
+def test_sr_round_unaligned_view(dev):
+    x = np.random.default_rng(9).standard_normal(1001).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev)[1:]
+    out = torch.empty(1001, dtype=torch.bfloat16, device=dev)[1:]
+    _lib.call("haste_sr_round_bf16", xd.data_ptr(), out.data_ptr(), 1000, 42, 0, _C.stream_of(xd))
+    assert np.array_equal(bits(out), oracle.sr_round_bf16(x[1:], 42, 0))
+
+
+def test_stochastic_rounding_api(dev):
+    from haste_amd.sr_triton import stochastic_rounding
+    x = torch.randn(512, 768, device=dev)
+    out = torch.empty_like(x, dtype=torch.bfloat16)
+    stochastic_rounding(x, out, 123)
+    assert np.array_equal(bits(out), oracle.sr_round_bf16(x.cpu().numpy(), 123, 0))
+
+
+GRAD_DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+@pytest.mark.parametrize("gdt", GRAD_DTYPES)
+@pytest.mark.parametrize("use_mom,do_sr", [(False, True), (True, True), (False, False), (True, False)])
+@pytest.mark.parametrize("n", [8 * 1000 + 5, 16])
+def test_sgd_step(dev, gdt, use_mom, do_sr, n):
+    g = torch.Generator().manual_seed(n)
+    w = (torch.rand(n, generator=g) - 0.5).to(torch.bfloat16)
+    grad = (torch.randn(n, generator=g) * 0.05).to(gdt)
+    m = torch.randn(n, generator=g) * 0.01
+    wd_, gd_, md_ = w.to(dev), grad.to(dev), m.to(dev)
+    _lib.call("haste_sgd_sr_step", wd_.data_ptr(), gd_.data_ptr(), _C.dtype_code(gdt),
+              md_.data_ptr() if use_mom else None, n, 0.05, 1e-4, 0.9, int(use_mom), int(do_sr),
+              2**33 + 42, 0, _C.stream_of(wd_))
+    if gdt == torch.float32:
+        g_np = grad.numpy()
+    elif gdt == torch.bfloat16:
+        g_np = bits(grad)
+    else:
+        g_np = grad.numpy()
+    ref_w, ref_m = oracle.sgd_sr_step(bits(w), g_np, m.numpy() if use_mom else None, 0.05, 1e-4,
+                                      0.9, use_mom, do_sr, 2**33 + 42)
+    assert np.array_equal(bits(wd_), ref_w)
+    if use_mom:
+        assert np.array_equal(md_.cpu().numpy().view(np.uint32), ref_m.view(np.uint32))
+
+
+def test_sgd_step_config1_size(dev):
+    """Full BASELINE config-1 weight tensor (131073 x 128), fp32 grad, seed 42."""
+    n = 131073 * 128
+    g = torch.Generator().manual_seed(0)
+    w = ((torch.rand(n, generator=g) * 2 - 1) / math.sqrt(128)).to(torch.bfloat16)
+    grad = torch.randn(n, generator=g) * 1e-2
+    wd_, gd_ = w.to(dev), grad.to(dev)
+    _lib.call("haste_sgd_sr_step", wd_.data_ptr(), gd_.data_ptr(), _lib.DTYPE_F32, None, n, 0.05,
+              1e-4, 0.0, 0, 1, 42, 0, _C.stream_of(wd_))
+    ref_w, _ = oracle.sgd_sr_step(bits(w), grad.numpy(), None, 0.05, 1e-4, 0.0, False, True, 42)
+    assert np.array_equal(bits(wd_), ref_w)
+
+
+def test_sgd_update_api(dev):
+    from haste_amd.sr_triton import sgd_update
+    w = (torch.rand(4096) - 0.5).to(torch.bfloat16)
+    grad = torch.randn(4096) * 0.01
+    buf = torch.zeros(4096)
+    wd_ = w.to(dev)
+    sgd_update(wd_, grad.to(dev), buf.to(dev), 0.05, 1e-4, 0.0, True, True, 7)
+    ref_w, _ = oracle.sgd_sr_step(bits(w), grad.numpy(), None, 0.05, 1e-4, 0.0, False, True, 7)
+    assert np.array_equal(bits(wd_), ref_w)
+
+
+REWIRE_CASES = [
+    # O, F, G, D, prune, k/thr, regrow, init
+    (4096, 32, 32, 768, "fraction", 4, "random", "zero"),
+    (131073 // 16, 128, 64, 768, "fraction", 19, "random", "zero"),
+    (10000, 64, 64, 768, "fraction", 9, "unused", "zero"),
+    (3000, 64, 16, 100, "threshold", 0.05, "random", "random"),
+    (2000, 256, 128, 4096, "fraction", 38, "unused", "random"),
+    (777, 16, 32, 40, "fraction", 8, "unused", "random"),
+]
+
+
+@pytest.mark.parametrize("O,F,G,D,prune,kt,regrow,init", REWIRE_CASES)
+def test_rewire(dev, O, F, G, D, prune, kt, regrow, init):
+    rng = np.random.default_rng(O)
+    bound = 1.0 / math.sqrt(F)
+    w = oracle.f32_to_bf16_bits(rng.uniform(-bound, bound, (O, F)).astype(np.float32))
+    Gc = (O + G - 1) // G
+    idx = rng.integers(0, D, (Gc, F)).astype(np.int32)
+    pm = oracle.PRUNE_FRACTION if prune == "fraction" else oracle.PRUNE_THRESHOLD
+    k = kt if prune == "fraction" else 0
+    thr = float(kt) if prune == "threshold" else 0.0
+    rm = oracle.REGROW_UNUSED if regrow == "unused" else oracle.REGROW_RANDOM
+    im = oracle.INIT_RANDOM if init == "random" else oracle.INIT_ZERO
+    seed = 0x1234ABCD5678 + O
+    ref_w, ref_idx, ref_n, ref_s, _ = oracle.rewire(w, idx, G, D, prune_mode=pm, threshold=thr, k=k,
+                                                    regrow_mode=rm, init_mode=im, bound=bound, seed=seed)
+    Wd = torch.from_numpy(w.view(np.int16)).to(dev).view(torch.bfloat16)
+    idxd = torch.from_numpy(idx).to(dev)
+    scores = torch.empty(Gc, F, device=dev)
+    cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("haste_rewire", Wd.data_ptr(), idxd.data_ptr(), scores.data_ptr(), cnt.data_ptr(), O, F,
+              G, D, pm, thr, k, rm, im, bound, seed, _C.stream_of(Wd))
+    assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+    assert np.array_equal(idxd.cpu().numpy(), ref_idx)
+    assert np.array_equal(bits(Wd), ref_w)
+    assert int(cnt.item()) == ref_n
