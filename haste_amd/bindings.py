@@ -7,6 +7,9 @@ Numerics contract (drop-in mode, as the reference):
             fp16 inputs are rounded to nearest instead (bindings.py:49-50)
   dW      = RNE of the fp32 weight gradient, weights dtype
   dbias   = column sum of grad_output (fp32 accumulation), bias dtype
+When a parameter's ``grad_dtype`` is torch.float32 (torch >= 2.10), its
+gradient is returned in fp32 straight from the kernel's accumulator (no
+rounding); SRSgd / sgd_update read fp32 gradients directly.
 
 Differences in mechanics (not in values): the feature gradient is computed
 deterministically and written straight into [B, D] (no fp32 [D, B]
@@ -26,6 +29,12 @@ from . import _C, _lib
 SR_SEED_GRAD_X = 123  # bindings.py:48
 
 
+def _grad_dtype(p: torch.Tensor) -> torch.dtype:
+    """dtype autograd will store for p.grad: p.grad_dtype if set (torch >= 2.10), else p.dtype."""
+    gd = getattr(p, "grad_dtype", None)
+    return gd if gd is not None else p.dtype
+
+
 class GroupFFIMulFunction(torch.autograd.Function):
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
@@ -42,7 +51,8 @@ class GroupFFIMulFunction(torch.autograd.Function):
         ctx.save_for_backward(xT, weights, group_locations)
         ctx.gsize = int(gsize)
         ctx.use_bias = bias is not None
-        ctx.bias_dtype = bias.dtype if bias is not None else None
+        ctx.w_grad_dtype = _grad_dtype(weights)
+        ctx.bias_dtype = _grad_dtype(bias) if bias is not None else None
         return out
 
     @staticmethod
@@ -83,10 +93,10 @@ class GroupFFIMulFunction(torch.autograd.Function):
         grad_w = grad_b = None
         if need_w or need_b:
             ldx = xT.stride(0)
-            grad_w = torch.empty(O, F, dtype=dtype, device=dev) if need_w else None
+            grad_w = torch.empty(O, F, dtype=ctx.w_grad_dtype, device=dev) if need_w else None
             grad_b = torch.empty(O, dtype=ctx.bias_dtype, device=dev) if need_b else None
             if need_w:
-                dw_ptr, dw_code = grad_w.data_ptr(), code
+                dw_ptr, dw_code = grad_w.data_ptr(), _C.dtype_code(ctx.w_grad_dtype)
             else:  # bias only: the kernel still needs a dW target
                 scratch = torch.empty(O, F, dtype=dtype, device=dev)
                 dw_ptr, dw_code = scratch.data_ptr(), code

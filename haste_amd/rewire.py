@@ -9,7 +9,9 @@ contract is deterministic (see include/haste_ffi.h): the reference's
 torch.randint / uniform_ draws and topk tie order are replaced by Philox
 streams keyed by a seed drawn from torch's default CPU generator, and ties in
 fraction mode go to the lower slot.  ``regrow_mode="unused"`` (new) draws only
-indices not already present in the group.
+indices not already present in the group.  ``fp32_grads=True`` (new) keeps
+the weight and bias gradients in fp32 (``grad_dtype``), which the SR-SGD
+kernel consumes directly.
 """
 from __future__ import annotations
 
@@ -40,7 +42,7 @@ class GroupFixedFanIn(torch.nn.Module):
     def __init__(self, in_features: int, out_features: int, fan_in: int, bias: bool = True,
                  device=None, dtype=None, *, group_size=32, prune_mode="threshold",
                  rewire_threshold=None, rewire_fraction=None, growth_mode="random",
-                 init_mode="random", regrow_mode="random", **kwargs):
+                 init_mode="random", regrow_mode="random", fp32_grads=False, **kwargs):
         super().__init__(**kwargs)
         factory_kwargs = {"device": device, "dtype": dtype}
         self.in_features = in_features
@@ -77,6 +79,11 @@ class GroupFixedFanIn(torch.nn.Module):
 
         assert group_size in GROUP_SIZES, \
             f"Current kernels only support group size from {GROUP_SIZES}. Selected group size={group_size}"
+        if fp32_grads:
+            # keep fp32 gradients for low-precision parameters (torch >= 2.10)
+            self.weights.grad_dtype = torch.float32
+            if self.bias is not None:
+                self.bias.grad_dtype = torch.float32
         self.group_size = group_size
         self.num_groups = (out_features + self.group_size - 1) // self.group_size
         group_locations = torch.randint(high=self.in_features, size=(self.num_groups, fan_in),

@@ -97,6 +97,7 @@ def test_srsgd_momentum_and_fp32_params(dev):
     W = torch.nn.Parameter(((torch.rand(256, 32) - 0.5) * 0.2).to(torch.bfloat16).to(dev))
     P = torch.nn.Parameter(torch.randn(100, device=dev))
     opt = SRSgd([W, P], lr=0.1, weight_decay=1e-3, momentum=0.9, seed=5)
+    W.grad_dtype = torch.float32  # fp32 gradient for a bf16 parameter
     W.grad = torch.randn(256, 32, device=dev) * 0.01
     P.grad = torch.randn(100, device=dev)
     w0, g0 = bits(W), W.grad.cpu().numpy()
@@ -108,6 +109,28 @@ def test_srsgd_momentum_and_fp32_params(dev):
                           ref_m.view(np.uint32))
     exp_p = p0 - 0.1 * (P.grad + 1e-3 * p0)
     torch.testing.assert_close(P.detach(), exp_p, rtol=1e-6, atol=1e-6)
+
+
+def test_fp32_grads_mode(dev):
+    """fp32_grads=True: weight/bias gradients come out of the kernel in fp32."""
+    torch.manual_seed(7)
+    B, D, O, G, F = 64, 768, 4096, 32, 32
+    layer = GroupFixedFanIn(D, O, F, group_size=G, rewire_threshold=0.0, dtype=torch.bfloat16,
+                            fp32_grads=True)
+    W, idx = layer.weights.detach().clone(), layer.group_locations.clone()
+    layer = layer.to(dev)
+    x = torch.randn(B, D).to(torch.bfloat16)
+    dY = (torch.randn(B, O) * 0.1).to(torch.bfloat16)
+    layer(x.to(dev)).backward(dY.to(dev))
+    assert layer.weights.grad.dtype == torch.float32 and layer.bias.grad.dtype == torch.float32
+    torch.testing.assert_close(layer.weights.grad.cpu(),
+                               oracle.ffi_backward_weights(idx, x.t().contiguous(), dY, G),
+                               rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(layer.bias.grad.cpu(), oracle.bias_grad(dY), rtol=1e-4, atol=1e-5)
+    w0, g0 = bits(layer.weights), layer.weights.grad.cpu().numpy()
+    SRSgd(layer.parameters(), lr=0.05, weight_decay=1e-4, seed=42).step()
+    ref_w, _ = oracle.sgd_sr_step(w0, g0, None, 0.05, 1e-4, 0.0, False, True, 42)
+    assert np.array_equal(bits(layer.weights), ref_w.reshape(O, F))
 
 
 def test_module_rewire_matches_oracle(dev):
