@@ -4,22 +4,22 @@
 //
 // The reference scatters with fp32 atomicAdd into global memory
 // (shared_ffi/ffi_backward_features.cu:202-212), so its sums depend on timing.
-// Here no float atomic ever touches global memory and every sum has a fixed
-// order:
+// Here no float atomic touches any memory and every sum has a fixed order:
 //
-//  1. prep: per group, the F slots are stably sorted by index, so equal
-//     indices become adjacent runs; the sorted positions of each feature range
-//     are split into 4 quarters at run starts.
-//  2. main: workgroup (group slice s, feature range dr, batch tile bt) keeps a
-//     partial dXT[d in dr, b in bt] in LDS (fp32).  For each group of its slice,
-//     in order, it stages W_g transposed in LDS; each of 8 waves (4 position
-//     quarters x 2 halves of the 32 batch columns) computes P = W_g^T dY_g^T for
-//     its positions with MFMA (M = sorted positions, N = batch, K = labels) and
-//     adds the rows into the LDS partial with plain reads and writes (LDS float
-//     atomics execute one lane at a time).  No two waves own the same word and
-//     no two lanes of one access instruction target the same word (see the
-//     scatter note at bwdf_main_kernel), so every word is updated by one wave
-//     in program order.
+//  1. prep (one workgroup per group): the F slots are stably sorted by index,
+//     so equal indices become adjacent runs; the sorted table, the bounds of
+//     eight value parts of every feature range, and W_g transposed in sorted
+//     slot order (WT[g][p][l] = W[g*G + l][slot(p)]) are written to the
+//     workspace.
+//  2. main: a workgroup (group slice s, feature range dr, 32-column batch tile
+//     bt) keeps the partial dXT[d in dr, b in bt] in LDS (fp32).  Its 8 waves
+//     own fixed value parts of dr, so they never touch the same LDS word and
+//     run through the slice's groups independently (no barriers).  Per group a
+//     wave multiplies the WT rows of its positions with dY_g (MFMA, M = sorted
+//     positions, N = batch, K = labels) and adds the result rows into the LDS
+//     partial with plain reads and writes (LDS float atomics execute one lane
+//     at a time).  Operands come straight from global memory into registers,
+//     two groups ahead.
 //  3. reduce: dXT = sum over slices s = 0..S-1 in ascending order (fp32 out), or
 //     fused with the bf16 stochastic rounding of shared_ffi/bindings.py:44-48.
 #include <algorithm>
@@ -32,25 +32,18 @@ int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, 
 
 namespace {
 
-constexpr int kMainThreads = 512;  // 8 waves
-constexpr int kBT = 32;             // batch columns per workgroup
+constexpr int kWaves = 4;                 // waves per workgroup, one value part each
+constexpr int kMainThreads = 64 * kWaves;
+constexpr int kMetaStride = 16;           // ints of meta per (group, feature range)
+constexpr int kBT = 32;            // batch columns per workgroup
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kTargetCTAs = 256;
-
-// LDS row pitch of the staged W_g^T (elements) and the largest feature range a
-// workgroup can hold in its LDS partial for a given (G, FP).
-constexpr int ws_pitch(int G) { return G + 8; }
-constexpr int max_dc(int G, int FP) {
-    return (kLdsBytes - FP * ws_pitch(G) * 2 - FP * 8 - 256) / 4 / kBT;
-}
-int max_dc_rt(int64_t G, int64_t F) {
-    const int FP = F <= 32 ? 32 : F <= 64 ? 64 : F <= 128 ? 128 : 256;
-    return max_dc((int)G, FP);
-}
+constexpr int kMaxDc = (kLdsBytes - 2 * kMainThreads * 4) / 4 / kBT;  // features in the LDS partial
+static_assert(kMaxDc * kBT * 4 + 2 * kMainThreads * 4 <= kLdsBytes, "LDS budget");
 
 struct BwdFPlan {
     int64_t Gc, nbt, Bp, ndr, Dc, S, gps;  // gps = groups per slice
-    int64_t prep_bytes, ws_bytes;
+    int64_t sorted_off, meta_off, wt_off, prep_bytes, ws_bytes;
 };
 
 BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
@@ -58,68 +51,109 @@ BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
     p.Gc = ceil_div(O, G);
     p.nbt = ceil_div(B, kBT);
     p.Bp = p.nbt * kBT;
-    p.ndr = ceil_div(D, max_dc_rt(G, F));
+    p.ndr = ceil_div(D, kMaxDc);
     p.Dc = ceil_div(D, p.ndr);
     int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
     S = std::min<int64_t>(S, std::max<int64_t>(1, ceil_div(p.Gc, 8)));
     p.gps = ceil_div(p.Gc, S);
     p.S = ceil_div(p.Gc, p.gps);
-    p.prep_bytes = ((p.Gc * F * 8 + p.Gc * p.ndr * 32) + 255) / 256 * 256;
+    auto r256 = [](int64_t x) { return (x + 255) / 256 * 256; };
+    p.sorted_off = 0;
+    p.meta_off = r256(p.Gc * F * 4);
+    p.wt_off = p.meta_off + r256(p.Gc * p.ndr * kMetaStride * 4);
+    p.prep_bytes = p.wt_off + r256(p.Gc * F * G * 2);
     p.ws_bytes = p.S * D * p.Bp * 4;
     return p;
 }
 
 // --------------------------------------------------------------- prep ------
-// sorted[g*F + p] = {index, slot | run << 16} for sorted position p, where run
-// is the number of earlier positions holding the same index.
-// meta[(g*ndr + dr)*8 + w], w = 0..4: position quarter w of feature range dr is
-// [meta[w], meta[w+1]); splits are moved to the start of a run of equal
-// indices, so no feature is shared by two quarters.  meta[5] bounds the colour
-// count of the scatter (see bwdf_main_kernel): ceil((longest run - 1) / 4).
+// sorted[g*F + p] = (index << 8) | (colour + 1) for sorted position p (an
+// arithmetic >> 8 recovers the index; -1 marks an empty entry).  Value part w (of
+// kWaves) of feature range dr owns sorted positions [m[w], m[w+1]), m = meta +
+// (g*ndr + dr)*kMetaStride (its values lie in [d_lo + (Dc'*w)/kWaves,
+// d_lo + (Dc'*(w+1))/kWaves)); m[kWaves + 1] bounds the colour count of the
+// scatter: ceil((longest run - 1) / 4).
+// colour: with rel = p - (first position of p's part), a position is a
+// "head" if rel % 4 == 0 or it starts a run of equal indices; heads get
+// colour rel/4 - (rel - run)/4 (run = rank inside the run), others -1.
+// wt[(g*F + p)*G + l] = W[g*G + l][slot(p)] (0 for labels >= O).
+template <int G>
 __global__ __launch_bounds__(256) void bwdf_prep_kernel(const int32_t* __restrict__ idx,
-                                                        int2* __restrict__ sorted,
-                                                        int* __restrict__ meta, int F, int D,
-                                                        int ndr, int Dc) {
+                                                        const uint16_t* __restrict__ W,
+                                                        int32_t* __restrict__ sorted,
+                                                        int* __restrict__ meta,
+                                                        uint16_t* __restrict__ wt, int F, int D,
+                                                        int64_t O, int ndr, int Dc) {
+    constexpr int LDW = G + 8;
     __shared__ int32_t s[256];
     __shared__ int32_t sv[256];
+    __shared__ int32_t srun[256];
+    __shared__ int32_t sslot[256];
     __shared__ int run_max;
+    __shared__ __attribute__((aligned(16))) uint16_t Wt[256 * LDW];  // Wt[slot][label]
     const int64_t g = blockIdx.x;
-    const int j = threadIdx.x;
-    if (j == 0) run_max = 0;
-    if (j < F) s[j] = min(max(idx[g * F + j], 0), D - 1);
+    const int64_t l0 = g * G;
+    const int tid = threadIdx.x;
+    if (tid == 0) run_max = 0;
+    if (tid < F) s[tid] = min(max(idx[g * F + tid], 0), D - 1);
+    // W_g rows -> LDS transposed: item = (label, 8 slots)
+    for (int it = tid; it < G * (F / 8); it += 256) {
+        const int l = it / (F / 8);
+        const int j0 = (it % (F / 8)) * 8;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (l0 + l < O) v = *reinterpret_cast<const u32x4*>(W + (l0 + l) * F + j0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            Wt[(j0 + e) * LDW + l] = (uint16_t)((e & 1) ? (v[e >> 1] >> 16) : (v[e >> 1] & 0xFFFFu));
+    }
     __syncthreads();
-    if (j < F) {
-        const int v = s[j];
+    if (tid < F) {
+        const int v = s[tid];
         int rank = 0, run = 0;
         for (int q = 0; q < F; ++q) {
             const int u = s[q];
-            rank += (u < v) || (u == v && q < j);
-            run += (u == v && q < j);
+            rank += (u < v) || (u == v && q < tid);
+            run += (u == v && q < tid);
         }
-        sorted[g * F + rank] = make_int2(v, j | (run << 16));
         sv[rank] = v;
+        srun[rank] = run;
+        sslot[rank] = tid;
         atomicMax(&run_max, run);
     }
     __syncthreads();
-    for (int dr = j; dr < ndr; dr += 256) {
-        const int d_lo = dr * Dc, d_hi = min(D, d_lo + Dc);
+    auto lower_bound = [&](int bound) {
         int lo = 0, hi = F;
-        while (lo < hi) { const int m = (lo + hi) >> 1; if (sv[m] < d_lo) lo = m + 1; else hi = m; }
-        const int P0 = lo;
-        hi = F;
-        while (lo < hi) { const int m = (lo + hi) >> 1; if (sv[m] < d_hi) lo = m + 1; else hi = m; }
-        const int P1 = lo;
-        int* m = meta + (g * ndr + dr) * 8;
-        m[0] = P0;
-        for (int w = 1; w < 4; ++w) {
-            int t = P0 + ((P1 - P0) * w) / 4;
-            while (t > P0 && t < P1 && sv[t] == sv[t - 1]) ++t;
-            m[w] = t;
+        while (lo < hi) {
+            const int mm = (lo + hi) >> 1;
+            if (sv[mm] < bound) lo = mm + 1; else hi = mm;
         }
-        m[4] = P1;
-        m[5] = (run_max + 3) / 4;
-        m[6] = 0;
-        m[7] = 0;
+        return lo;
+    };
+    for (int dr = tid; dr < ndr; dr += 256) {
+        const int d_lo = dr * Dc, d_hi = min(D, d_lo + Dc);
+        int* m = meta + (g * ndr + dr) * kMetaStride;
+        for (int w = 0; w <= kWaves; ++w) m[w] = lower_bound(d_lo + ((d_hi - d_lo) * w) / kWaves);
+        m[kWaves + 1] = (run_max + 3) / 4;
+    }
+    if (tid < F) {
+        const int p = tid;
+        const int x = sv[p];
+        const int dr = x / Dc;
+        const int d_lo = dr * Dc, d_hi = min(D, d_lo + Dc);
+        int w = kWaves - 1;
+        while (w > 0 && x < d_lo + ((d_hi - d_lo) * w) / kWaves) --w;
+        const int pb = lower_bound(d_lo + ((d_hi - d_lo) * w) / kWaves);
+        const int rel = p - pb;
+        const int run = srun[p];
+        const bool head = (rel % 4 == 0) || run == 0;
+        sorted[g * F + p] = (x << 8) | (head ? rel / 4 - (rel - run) / 4 + 1 : 0);
+    }
+    // sorted rows of W_g^T: item = (position, 8 labels)
+    for (int it = tid; it < F * (G / 8); it += 256) {
+        const int p = it / (G / 8);
+        const int lc = (it % (G / 8)) * 8;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&Wt[sslot[p] * LDW + lc]);
+        *reinterpret_cast<u32x4*>(wt + ((g * F + p) * G + lc)) = v;
     }
 }
 
@@ -127,34 +161,39 @@ __global__ __launch_bounds__(256) void bwdf_prep_kernel(const int32_t* __restric
 template <typename T, int G, int FP>
 struct BwdFCfg {
     static constexpr int KS = G >= 32 ? G / 32 : 1;  // MFMA k-steps over labels
-    static constexpr int LDW = ws_pitch(G);          // Ws row pitch (elements)
-    static constexpr int ACC = max_dc(G, FP) * kBT;  // LDS partial size (floats)
-    static constexpr int ITEMS = (G / 4) * (FP / 8); // W staging items: 4 labels x 8 slots
-    static constexpr int IPT = (ITEMS + kMainThreads - 1) / kMainThreads;
+    static constexpr int NT = kBT / 16;              // batch n-tiles per wave
+    static constexpr int MAXT = FP >= 256 ? 5 : FP >= 128 ? 3 : 2;  // tiles kept in registers
 };
 
-// 8 waves: wave = 2 * quarter + half.  `half` selects the 16 batch columns of
-// the 32-column tile, `quarter` the sorted-position quarter (its features).
-// The next group's W tile, slot table, quarter bounds and dY fragments are
-// loaded into registers while the current group is computed.
-//
-// Scatter of one MFMA tile (rows = 16 sorted positions, lane holds positions
+typedef int32_t i32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
+template <int KS, int MAXT, int NT>
+struct BwdFRegs {
+    u32x4 a[MAXT][KS];  // WT rows of the wave's positions (A operand)
+    int e[MAXT][4];     // packed slot-table entries of this lane's scatter positions
+    u32x4 b[NT][KS];    // dY fragments (B operand)
+    int pb, pe, maxc;
+};
+
+// Scatter of one MFMA tile (rows = 16 sorted positions; lane holds positions
 // 4*lq + i, i = 0..3, of one batch column): equal indices are adjacent, so a
 // lane first folds each run inside its own 4 positions into the run's first
-// position there (the "head").  Heads of one run that sit in different lanes
-// get successive colours; pass c reads, adds and writes all heads of colour c
-// at once.  Within a pass every lane targets a distinct word, and every word
-// is only ever touched by one wave, in program order.
+// position there (the "head").  Heads of one run that sit in different
+// lanes/tiles get successive colours (their quad index relative to the run
+// start); pass c reads, adds and writes all heads of colour c at once.  Within
+// a pass every lane targets a distinct word, and every word is only ever
+// touched by one wave, in program order (the compiler keeps these plain LDS
+// accesses in order: as far as it knows they may alias).
 template <typename T, int G, int FP>
 __global__ __launch_bounds__(kMainThreads) void bwdf_main_kernel(
-    const int2* __restrict__ sorted, const int* __restrict__ meta, const uint16_t* __restrict__ W,
-    const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
-    int F, int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S) {
+    const int32_t* __restrict__ sorted, const int* __restrict__ meta,
+    const uint16_t* __restrict__ wt, const uint16_t* __restrict__ dY, int64_t lddy,
+    float* __restrict__ ws, int B, int Bp, int D, int F, int64_t O, int64_t Gc, int nbt, int ndr,
+    int Dc, int gps, int S) {
     using C = BwdFCfg<T, G, FP>;
-    __shared__ float acc[C::ACC];
-    __shared__ __attribute__((aligned(16))) uint16_t Ws[FP * C::LDW];
-    __shared__ int2 ss[FP];
-    __shared__ int mb[8];
+    constexpr int KS = C::KS, NT = C::NT, MAXT = C::MAXT;
+    using R = BwdFRegs<KS, MAXT, NT>;
+    __shared__ float acc[kMaxDc * kBT + 2 * kMainThreads];  // + two dummy words per lane
 
     const int64_t work = xcd_remap(blockIdx.x, (int64_t)S * ndr * nbt);
     if (work < 0) return;
@@ -169,132 +208,196 @@ __global__ __launch_bounds__(kMainThreads) void bwdf_main_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int half = wave & 1;
-    const int quarter = wave >> 1;
+    const int part = tid >> 6;  // value part of this wave
     const int lrow = lane & 15;
     const int lq = lane >> 4;
-    const int col = half * 16 + lrow;  // batch column of this lane inside the tile
-
-    u32x4 wreg[C::IPT][4];
-    int2 ssreg = make_int2(0, 0);
-    int mreg = 0;
-    u32x4 bnext[C::KS];
-
-    auto load = [&](int64_t g) {
-        const int64_t l0 = g * G;
-#pragma unroll
-        for (int i = 0; i < C::IPT; ++i) {
-            const int it = tid + i * kMainThreads;
-            const int lc = (it % (G / 4)) * 4;
-            const int j0 = (it / (G / 4)) * 8;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (it < C::ITEMS && l0 + lc + q < O && j0 < F)
-                    wreg[i][q] = *reinterpret_cast<const u32x4*>(W + (l0 + lc + q) * F + j0);
-                else
-                    wreg[i][q] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-        if (tid < F) ssreg = sorted[g * F + tid];
-        if (tid < 8) mreg = meta[(g * ndr + dr) * 8 + tid];
-        const int b = b_base + col;
-#pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
-            const int k = ks * 32 + lq * 8;
-            if (b < B && k < G && l0 + k < O) {
-                bnext[ks] = *reinterpret_cast<const u32x4*>(dY + (int64_t)b * lddy + l0 + k);
-                if (l0 + k + 8 > O) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (l0 + k + e >= O) bnext[ks][e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                }
-            } else {
-                bnext[ks] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
-
-    auto stage = [&]() {
-#pragma unroll
-        for (int i = 0; i < C::IPT; ++i) {
-            const int it = tid + i * kMainThreads;
-            if (it >= C::ITEMS) continue;
-            const int lc = (it % (G / 4)) * 4;
-            const int j0 = (it / (G / 4)) * 8;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int sh = (e & 1) * 16;
-                const uint32_t a0 = (wreg[i][0][e >> 1] >> sh) & 0xFFFFu;
-                const uint32_t a1 = (wreg[i][1][e >> 1] >> sh) & 0xFFFFu;
-                const uint32_t a2 = (wreg[i][2][e >> 1] >> sh) & 0xFFFFu;
-                const uint32_t a3 = (wreg[i][3][e >> 1] >> sh) & 0xFFFFu;
-                *reinterpret_cast<u32x2*>(&Ws[(j0 + e) * C::LDW + lc]) =
-                    u32x2{a0 | (a1 << 16), a2 | (a3 << 16)};
-            }
-        }
-        if (tid < F) ss[tid] = ssreg;
-        if (tid < 8) mb[tid] = mreg;
-    };
 
     for (int i = tid; i < (d_hi - d_lo) * kBT; i += kMainThreads) acc[i] = 0.0f;
-    if (g_begin < g_end) load(g_begin);
+    __syncthreads();
 
-    for (int64_t g = g_begin; g < g_end; ++g) {
-        stage();
-        u32x4 bcur[C::KS];
+    // Branch-free loads: addresses are clamped into the group's blocks and
+    // out-of-range values replaced by selects (divergent branches around
+    // memory operations cost far more than the operations themselves).  The
+    // dY masking only runs for the ragged last group / batch tile.
+    const bool full_b = b_base + kBT <= B;
+    auto load = [&](int64_t g, R& r) {
+        const int* m = meta + (g * ndr + dr) * kMetaStride;
+        r.pb = m[part];
+        r.pe = m[part + 1];
+        r.maxc = m[kWaves + 1];
+        const int64_t l0 = g * G;
+        const uint16_t* wg = wt + g * F * G;
+        const int32_t* sg = sorted + g * F;
+        const bool clamp_p = r.pb + 16 * MAXT + 4 > F;
 #pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) bcur[ks] = bnext[ks];
-        __syncthreads();
-        if (g + 1 < g_end) load(g + 1);
-
-        const int pb = mb[quarter];
-        const int pe = mb[quarter + 1];
-        const int maxc = mb[5];
-        for (int m0 = pb; m0 < pe; m0 += 16) {
-            // A fragments: rows = sorted positions, 8 consecutive labels from Ws.
-            const int pa = m0 + lrow;
-            const int slot = pa < pe ? (ss[pa].y & 0xFFFF) : 0;
-            // scatter metadata of this lane's 4 positions (and the one before)
-            int2 e[4];
-            const int p0 = m0 + lq * 4;  // lane-aligned quad: p0 - pb is a multiple of 4
+        for (int t = 0; t < MAXT; ++t) {
+            if (r.pb + t * 16 >= r.pe) break;  // wave-uniform: no positions left
+            int pa = r.pb + t * 16 + lrow;
+            if (clamp_p) pa = min(pa, F - 1);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) e[i] = (p0 + i < pe) ? ss[p0 + i] : make_int2(-1, 0);
-            f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int ks = 0; ks < KS; ++ks) {
+                const int k = G >= 32 ? ks * 32 + lq * 8 : (lq & 1) * 8;
+                r.a[t][ks] = *reinterpret_cast<const u32x4*>(wg + pa * G + k);
+            }
+            // the lane's 4 consecutive entries with one (4-byte aligned) 16-byte load
+            const int p0 = r.pb + t * 16 + lq * 4;
+            i32x4a v;
+            if (clamp_p && p0 + 4 > F) {
 #pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
+                for (int i = 0; i < 4; ++i) v[i] = sg[min(p0 + i, F - 1)];
+            } else {
+                v = *reinterpret_cast<const i32x4a*>(sg + p0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r.e[t][i] = p0 + i < r.pe ? v[i] : -1;
+        }
+        const bool full = full_b && l0 + G <= O;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int b = b_base + nt * 16 + lrow;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
                 const int k = ks * 32 + lq * 8;
-                u32x4 af = u32x4{0u, 0u, 0u, 0u};
-                if (pa < pe && k < G) af = *reinterpret_cast<const u32x4*>(&Ws[slot * C::LDW + k]);
-                c = mfma16x16x32<T>(af, bcur[ks], c);
-            }
-            // fold runs inside the lane's 4 positions into their heads
-            int addr[4], colour[4];
-            bool head[4];
+                if (full && k < G) {
+                    r.b[nt][ks] = *reinterpret_cast<const u32x4*>(dY + (int64_t)b * lddy + l0 + k);
+                } else {
+                    const int64_t col = min(l0 + min(k, G - 8), lddy - 8);
+                    u32x4 v = *reinterpret_cast<const u32x4*>(dY + (int64_t)min(b, B - 1) * lddy + col);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int p = p0 + i;
-                const int rel = p - pb;
-                const bool valid = e[i].x >= 0;
-                head[i] = valid && (i == 0 || e[i].x != e[i - 1].x);
-                const int run = e[i].y >> 16;
-                colour[i] = rel / 4 - max(rel - run, 0) / 4;
-                addr[i] = (e[i].x - d_lo) * kBT + col;
-            }
-#pragma unroll
-            for (int i = 3; i >= 1; --i)
-                if (e[i].x >= 0 && !head[i]) c[i - 1] += c[i];
-            for (int cc = 0; cc <= maxc; ++cc) {
-                float o[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) o[i] = (head[i] && colour[i] == cc) ? acc[addr[i]] : 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (head[i] && colour[i] == cc) acc[addr[i]] = o[i] + c[i];
+                    for (int q = 0; q < 8; ++q) {
+                        const bool ok = b < B && k + q < G && l0 + k + q < O;
+                        v[q >> 1] &= ok ? 0xFFFFFFFFu : ((q & 1) ? 0x0000FFFFu : 0xFFFF0000u);
+                    }
+                    r.b[nt][ks] = v;
+                }
             }
         }
-        __syncthreads();
+    };
+
+    // Multiply + scatter `ntiles` (<= MAXT) tiles of 16 positions.  Lanes
+    // without work in a pass read and write a private dummy word (two words,
+    // 16 apart, one per batch half), so the LDS accesses need no divergent
+    // branches; tile loops use wave-uniform branches only.
+    const int dummy = kMaxDc * kBT + part * 128 + lane;
+    const int colbase = lrow - d_lo * kBT;
+    auto compute = [&](const u32x4 (&a)[MAXT][KS], const int (&e)[MAXT][4],
+                       const u32x4 (&b)[NT][KS], int ntiles, int maxc) {
+        int addr[MAXT][4], col1[MAXT][4];
+        float o[MAXT][NT][4];
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t >= ntiles) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                addr[t][i] = (e[t][i] >> 8) * kBT + colbase;
+                col1[t][i] = e[t][i] & 0xFF;  // colour + 1; 0 = not a head
+                const int eff = col1[t][i] == 1 ? addr[t][i] : dummy;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) o[t][nt][i] = acc[eff + nt * 16];
+            }
+        }
+        f32x4 c[MAXT][NT];
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t >= ntiles) continue;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                c[t][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) c[t][nt] = mfma16x16x32<T>(a[t][ks], b[nt][ks], c[t][nt]);
+                // fold runs inside the lane's 4 positions into their heads
+#pragma unroll
+                for (int i = 3; i >= 1; --i)
+                    if (maxc > 0) c[t][nt][i - 1] += (col1[t][i] == 0 && e[t][i] >= 0) ? c[t][nt][i] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t >= ntiles) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int eff = col1[t][i] == 1 ? addr[t][i] : dummy;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[eff + nt * 16] = o[t][nt][i] + c[t][nt][i];
+            }
+        }
+        for (int cc = 1; cc <= maxc; ++cc) {
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                if (t >= ntiles) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int eff = col1[t][i] == cc + 1 ? addr[t][i] : dummy;
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) o[t][nt][i] = acc[eff + nt * 16];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                if (t >= ntiles) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int eff = col1[t][i] == cc + 1 ? addr[t][i] : dummy;
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) acc[eff + nt * 16] = o[t][nt][i] + c[t][nt][i];
+                }
+            }
+        }
+    };
+
+    // Tiles beyond MAXT (only for heavily duplicated index sets): loaded and
+    // processed MAXT at a time, without prefetch.
+    auto overflow = [&](int64_t g, const R& r) {
+        const int total = (r.pe - r.pb + 15) / 16;
+        const uint16_t* wg = wt + g * F * G;
+        const int32_t* sg = sorted + g * F;
+        for (int t0 = MAXT; t0 < total; t0 += MAXT) {
+            u32x4 a[MAXT][KS];
+            int e[MAXT][4];
+#pragma unroll
+            for (int t = 0; t < MAXT; ++t) {
+                const int pa = min(r.pb + (t0 + t) * 16 + lrow, F - 1);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int k = G >= 32 ? ks * 32 + lq * 8 : (lq & 1) * 8;
+                    a[t][ks] = *reinterpret_cast<const u32x4*>(wg + pa * G + k);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int p = r.pb + (t0 + t) * 16 + lq * 4 + i;
+                    const int v = sg[min(p, F - 1)];
+                    e[t][i] = p < r.pe ? v : -1;
+                }
+            }
+            compute(a, e, r.b, min(MAXT, total - t0), r.maxc);
+        }
+    };
+
+    auto process = [&](int64_t g, const R& r) {
+        const int total = (r.pe - r.pb + 15) / 16;
+        compute(r.a, r.e, r.b, min(MAXT, total), r.maxc);
+        if (total > MAXT) overflow(g, r);
+    };
+
+    // Three register sets: group g is computed while g+1 and g+2 are in flight.
+    if (g_begin < g_end) {
+        R r0, r1, r2;
+        load(g_begin, r0);
+        if (g_begin + 1 < g_end) load(g_begin + 1, r1);
+        int64_t g = g_begin;
+        while (true) {
+            if (g + 2 < g_end) load(g + 2, r2);
+            process(g, r0);
+            if (++g >= g_end) break;
+            if (g + 2 < g_end) load(g + 2, r0);
+            process(g, r1);
+            if (++g >= g_end) break;
+            if (g + 2 < g_end) load(g + 2, r1);
+            process(g, r2);
+            if (++g >= g_end) break;
+        }
     }
+    __syncthreads();
 
     // ---- write the partial: ws[s][d][bt*32 + b] ----
     for (int i = tid; i < (d_hi - d_lo) * kBT; i += kMainThreads) {
@@ -345,37 +448,35 @@ __global__ __launch_bounds__(256) void bwdf_reduce_sr_kernel(const float* __rest
 }
 
 template <typename T, int G, int FP>
-int launch_main(const int2* sorted, const int* meta, const uint16_t* W, const uint16_t* dY, int64_t lddy,
-                float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F, int64_t O,
-                hipStream_t st) {
+int launch_main(const int32_t* sorted, const int* meta, const uint16_t* wt, const uint16_t* dY,
+                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
+                int64_t O, hipStream_t st) {
     const int64_t nlog = p.S * p.ndr * p.nbt;
     const int64_t grid = 8 * ceil_div(nlog, 8);
     bwdf_main_kernel<T, G, FP><<<dim3((unsigned)grid), dim3(kMainThreads), 0, st>>>(
-        sorted, meta, W, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, (int)F, O, p.Gc, (int)p.nbt,
+        sorted, meta, wt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, (int)F, O, p.Gc, (int)p.nbt,
         (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
     return HASTE_OK;
 }
 
 template <typename T, int G>
-int dispatch_fp(const int2* sorted, const int* meta, const uint16_t* W, const uint16_t* dY, int64_t lddy, float* ws,
-                const BwdFPlan& p, int64_t B, int64_t D, int64_t F, int64_t O, hipStream_t st) {
-    if (F <= 32) return launch_main<T, G, 32>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
-    if (F <= 64) return launch_main<T, G, 64>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
-    if (F <= 128) return launch_main<T, G, 128>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
-    return launch_main<T, G, 256>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
+int dispatch_fp(const int32_t* sorted, const int* meta, const uint16_t* wt, const uint16_t* dY,
+                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
+                int64_t O, hipStream_t st) {
+#define HASTE_BWDF_ARGS sorted, meta, wt, dY, lddy, ws, p, B, D, F, O, st
+    if (F <= 32) return launch_main<T, G, 32>(HASTE_BWDF_ARGS);
+    if (F <= 64) return launch_main<T, G, 64>(HASTE_BWDF_ARGS);
+    if (F <= 128) return launch_main<T, G, 128>(HASTE_BWDF_ARGS);
+    return launch_main<T, G, 256>(HASTE_BWDF_ARGS);
+#undef HASTE_BWDF_ARGS
 }
 
-template <typename T>
-int dispatch_g(const int2* sorted, const int* meta, const uint16_t* W, const uint16_t* dY, int64_t lddy, float* ws,
-               const BwdFPlan& p, int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
-               hipStream_t st) {
-    switch (G) {
-    case 16: return dispatch_fp<T, 16>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
-    case 32: return dispatch_fp<T, 32>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
-    case 64: return dispatch_fp<T, 64>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
-    default: return dispatch_fp<T, 128>(sorted, meta, W, dY, lddy, ws, p, B, D, F, O, st);
-    }
+template <int G>
+void launch_prep(const int32_t* idx, const uint16_t* W, int32_t* sorted, int* meta, uint16_t* wt,
+                 const BwdFPlan& p, int64_t D, int64_t F, int64_t O, hipStream_t st) {
+    bwdf_prep_kernel<G><<<dim3((unsigned)p.Gc), dim3(256), 0, st>>>(
+        idx, W, sorted, meta, wt, (int)F, (int)D, O, (int)p.ndr, (int)p.Dc);
 }
 
 // Runs prep + main; leaves the per-slice partials in the workspace.
@@ -396,16 +497,31 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
                   (long long)workspace_bytes, (long long)(p.prep_bytes + p.ws_bytes));
         return HASTE_ERR_WORKSPACE;
     }
-    int2* sorted = static_cast<int2*>(workspace);
-    int* meta = reinterpret_cast<int*>(sorted + p.Gc * F);
-    float* ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.prep_bytes);
-    bwdf_prep_kernel<<<dim3((unsigned)p.Gc), dim3(256), 0, st>>>(idx, sorted, meta, (int)F,
-                                                                     (int)D, (int)p.ndr, (int)p.Dc);
-    HASTE_CHECK_LAUNCH(fn);
+    char* base = static_cast<char*>(workspace);
+    int32_t* sorted = reinterpret_cast<int32_t*>(base + p.sorted_off);
+    int* meta = reinterpret_cast<int*>(base + p.meta_off);
+    uint16_t* wt = reinterpret_cast<uint16_t*>(base + p.wt_off);
+    float* ws = reinterpret_cast<float*>(base + p.prep_bytes);
     auto* w = static_cast<const uint16_t*>(W);
     auto* y = static_cast<const uint16_t*>(dY);
-    rc = dtype == HASTE_DTYPE_BF16 ? dispatch_g<BF16>(sorted, meta, w, y, lddy, ws, p, B, D, F, O, G, st)
-                                   : dispatch_g<F16>(sorted, meta, w, y, lddy, ws, p, B, D, F, O, G, st);
+    switch (G) {
+#define HASTE_BWDF_G(GG)                                                                      \
+    case GG:                                                                                  \
+        launch_prep<GG>(idx, w, sorted, meta, wt, p, D, F, O, st);                            \
+        HASTE_CHECK_LAUNCH(fn);                                                               \
+        rc = dtype == HASTE_DTYPE_BF16                                                        \
+                 ? dispatch_fp<BF16, GG>(sorted, meta, wt, y, lddy, ws, p, B, D, F, O, st)    \
+                 : dispatch_fp<F16, GG>(sorted, meta, wt, y, lddy, ws, p, B, D, F, O, st);    \
+        break;
+        HASTE_BWDF_G(16)
+        HASTE_BWDF_G(32)
+        HASTE_BWDF_G(64)
+        HASTE_BWDF_G(128)
+#undef HASTE_BWDF_G
+    default:
+        set_error("%s: unsupported group size %lld", fn, (long long)G);
+        return HASTE_ERR_UNSUPPORTED;
+    }
     *plan_out = p;
     return rc;
 }
