@@ -49,6 +49,24 @@ def phase_bytes(B, D, O, G, F):
     }
 
 
+TRAFFIC_FILE = "profiles/traffic_config%d.txt"
+COPY_BYTES = 256 * 1024 * 1024
+
+
+def measured_traffic(config, phase):
+    """HBM bytes per launch of ``phase`` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (lines ``TRAFFIC <phase> <bytes>``), or None if absent."""
+    path = os.path.join(ROOT, TRAFFIC_FILE % config)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "TRAFFIC" and parts[1] == phase:
+                return float(parts[2])
+    return None
+
+
 def make_inputs(cfg, dev):
     import numpy as np
     import torch
@@ -133,6 +151,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phases", action="store_true",
                     help="also print per-phase event timings to stderr")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed steps, copy a 256 MiB fp32 buffer 3 times (a kernel "
+                         "of known traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the FFI path shards by label "
@@ -222,6 +243,17 @@ def main():
         "phases_hbm_frac": {n: round(phase_gbs[n] / HBM_PEAK_GBS, 4) for n in names},
         "wall_s": wall,
     }
+    tr = measured_traffic(args.config, dom)
+    if tr is not None:
+        result["roofline"]["traffic"] = tr
+        result["roofline"]["traffic_source"] = TRAFFIC_FILE % args.config
+    if args.copy_calibration:
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg)
     print(json.dumps(result), flush=True)
