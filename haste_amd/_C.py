@@ -27,6 +27,11 @@ def round8(n: int) -> int:
     return (int(n) + 7) // 8 * 8
 
 
+def round64(n: int) -> int:
+    """Row length in 2-byte elements rounded to 128 bytes (one cache line)."""
+    return (int(n) + 63) // 64 * 64
+
+
 def dtype_code(dtype: torch.dtype) -> int:
     try:
         return _DTYPE_CODE[dtype]
@@ -62,13 +67,16 @@ def rows_aligned(t: torch.Tensor) -> Tuple[torch.Tensor, int]:
 
 
 def padded_transpose(features: torch.Tensor) -> Tuple[torch.Tensor, int]:
-    """features [B, D] -> (xT [D, B] view of a [D, round8(B)] buffer, ld)."""
+    """features [B, D] -> (xT [D, B] view of a [D, round8(B)] buffer, ld), by the
+    HIP transpose kernel (padding columns are zero)."""
     B, D = features.shape
     ld = round8(B)
     buf = torch.empty(D, ld, dtype=features.dtype, device=features.device)
-    xT = buf[:, :B]
-    xT.copy_(features.t())
-    return xT, ld
+    x, ldx = (features, features.stride(0)) if features.stride(1) == 1 else (
+        features.contiguous(), D)
+    _lib.call("haste_transpose_features", x.data_ptr(), ldx, buf.data_ptr(), ld, B, D,
+              stream_of(features))
+    return buf[:, :B], ld
 
 
 def _check_locations(locations: torch.Tensor, L: int, FANIN: int, gsize: int) -> torch.Tensor:

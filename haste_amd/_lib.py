@@ -25,6 +25,14 @@ PRUNE_THRESHOLD, PRUNE_FRACTION = 0, 1
 REGROW_RANDOM, REGROW_UNUSED = 0, 1
 INIT_ZERO, INIT_RANDOM = 0, 1
 
+
+
+class SgdTensor(ctypes.Structure):
+    """haste_sgd_tensor of include/haste_ffi.h."""
+    _fields_ = [("w", ctypes.c_void_p), ("g", ctypes.c_void_p), ("m", ctypes.c_void_p),
+                ("n", ctypes.c_int64), ("offset0", ctypes.c_uint64)]
+
+
 # Every symbol declared in include/haste_ffi.h: name -> (restype, argtypes).
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -46,6 +54,9 @@ SIGNATURES = {
     "haste_sr_round_bf16": (ctypes.c_int, [_P, _P, _I64, _U64, _U64, _P]),
     "haste_sgd_sr_step": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _F32, _F32, _F32, _I32, _I32,
                                          _U64, _U64, _P]),
+    "haste_sgd_sr_step_multi": (ctypes.c_int, [ctypes.POINTER(SgdTensor), _I32, _I32, _F32, _F32,
+                                               _F32, _I32, _I32, _U64, _P]),
+    "haste_transpose_features": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I64, _P]),
     "haste_rewire": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _F32, _I64,
                                     _I32, _I32, _F32, _U64, _P]),
 }

@@ -59,26 +59,54 @@ __device__ __forceinline__ uint32_t sgd_one(float w, float g, float* m, bool use
     return f32_to_bf16_rne(nw);
 }
 
-// Vector path: requires 16-byte aligned w, g (and m) and n_vec = n / 8 items.
+// One launch updates up to kMaxSegs tensors ("segments"), each with its own
+// offset base; every thread handles kVec consecutive elements of one segment
+// (16-byte vector loads when the segment is aligned, element loads for the
+// segment's tail or an unaligned segment), so a tensor needs no second launch
+// for its tail and several small tensors (weights + bias) share one launch.
+constexpr int kMaxSegs = 8;
+constexpr int kSgdThreads = 256;
+constexpr int64_t kSegBlockElems = (int64_t)kSgdThreads * kVec;
+
+struct SgdSeg {
+    uint16_t* w;
+    const void* g;
+    float* m;
+    int64_t n;
+    uint64_t off0;
+    int64_t blk0;  // first block of this segment
+    int32_t vec;   // 16-byte aligned w, g (and m)
+};
+struct SgdBatch {
+    SgdSeg s[kMaxSegs];
+    int32_t count;
+};
+
 template <int GD, bool USE_MOM, bool DO_SR>
-__global__ __launch_bounds__(256) void sgd_sr_vec_kernel(uint16_t* __restrict__ w,
-                                                         const void* __restrict__ g,
-                                                         float* __restrict__ m, int64_t n_vec,
-                                                         float lr, float wd, float mu,
-                                                         uint64_t seed, uint64_t offset0) {
+__global__ __launch_bounds__(kSgdThreads) void sgd_sr_kernel(const SgdBatch b, float lr, float wd,
+                                                             float mu, uint64_t seed) {
     const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < n_vec; v += stride) {
-        const int64_t i = v * kVec;
+    int t = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxSegs; ++k)
+        if (k < b.count && (int64_t)blockIdx.x >= b.s[k].blk0) t = k;
+    uint16_t* __restrict__ w = b.s[t].w;
+    const void* __restrict__ g = b.s[t].g;
+    float* __restrict__ m = b.s[t].m;
+    const int64_t n = b.s[t].n;
+    const uint64_t offset0 = b.s[t].off0;
+    const int64_t i = ((int64_t)blockIdx.x - b.s[t].blk0) * kSegBlockElems +
+                      (int64_t)threadIdx.x * kVec;
+    if (b.s[t].vec && i + kVec <= n) {
         u32x4 wv = *reinterpret_cast<const u32x4*>(w + i);
         float gf[kVec];
         load_grad8<GD>(g, i, gf);
         float mv[kVec];
         if constexpr (USE_MOM) {
-            float4 a = reinterpret_cast<const float4*>(m + i)[0];
-            float4 b = reinterpret_cast<const float4*>(m + i)[1];
-            mv[0] = a.x; mv[1] = a.y; mv[2] = a.z; mv[3] = a.w;
-            mv[4] = b.x; mv[5] = b.y; mv[6] = b.z; mv[7] = b.w;
+            f32x4 a = reinterpret_cast<const f32x4*>(m + i)[0];
+            f32x4 c = reinterpret_cast<const f32x4*>(m + i)[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { mv[e] = a[e]; mv[4 + e] = c[e]; }
         }
         uint32_t outb[kVec];
 #pragma unroll
@@ -92,40 +120,57 @@ __global__ __launch_bounds__(256) void sgd_sr_vec_kernel(uint16_t* __restrict__ 
         for (int q = 0; q < 4; ++q) ov[q] = outb[2 * q] | (outb[2 * q + 1] << 16);
         *reinterpret_cast<u32x4*>(w + i) = ov;
         if constexpr (USE_MOM) {
-            reinterpret_cast<float4*>(m + i)[0] = make_float4(mv[0], mv[1], mv[2], mv[3]);
-            reinterpret_cast<float4*>(m + i)[1] = make_float4(mv[4], mv[5], mv[6], mv[7]);
+            f32x4 a, c;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { a[e] = mv[e]; c[e] = mv[4 + e]; }
+            reinterpret_cast<f32x4*>(m + i)[0] = a;
+            reinterpret_cast<f32x4*>(m + i)[1] = c;
+        }
+    } else {
+        for (int e = 0; e < kVec; ++e) {
+            const int64_t j = i + e;
+            if (j >= n) break;
+            float mv = USE_MOM ? m[j] : 0.f;
+            w[j] = (uint16_t)sgd_one(bf16_bits_to_f32(w[j]), load_grad1<GD>(g, j), &mv, USE_MOM,
+                                     lr, wd, mu, DO_SR, offset0 + (uint64_t)j, k0, k1);
+            if (USE_MOM) m[j] = mv;
         }
     }
 }
 
-// Scalar path for the tail (or unaligned tensors): elements [i0, n).
-template <int GD>
-__global__ __launch_bounds__(256) void sgd_sr_scalar_kernel(uint16_t* __restrict__ w,
-                                                            const void* __restrict__ g,
-                                                            float* __restrict__ m, int64_t i0,
-                                                            int64_t n, float lr, float wd,
-                                                            float mu, int use_mom, int do_sr,
-                                                            uint64_t seed, uint64_t offset0) {
-    const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = i0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        float dummy = 0.f;
-        float* mp = use_mom ? (m + i) : &dummy;
-        w[i] = (uint16_t)sgd_one(bf16_bits_to_f32(w[i]), load_grad1<GD>(g, i), mp, use_mom != 0,
-                                 lr, wd, mu, do_sr != 0, offset0 + (uint64_t)i, k0, k1);
-    }
-}
+struct SgdTensor {
+    uint16_t* w;
+    const void* g;
+    float* m;
+    int64_t n;
+    uint64_t offset0;
+};
 
 template <int GD>
-int launch_sgd(uint16_t* w, const void* g, float* m, int64_t n, float lr, float wd, float mu,
-               int use_mom, int do_sr, uint64_t seed, uint64_t offset0, hipStream_t st) {
-    const bool vec_ok = aligned16(w) && aligned16(g) && (!use_mom || aligned16(m));
-    int64_t n_vec = vec_ok ? n / kVec : 0;
-    if (n_vec > 0) {
-        const int64_t blocks = std::min<int64_t>(ceil_div(n_vec, 256), 1 << 20);
+int launch_sgd(const SgdTensor* ts, int count, float lr, float wd, float mu, int use_mom,
+               int do_sr, uint64_t seed, hipStream_t st) {
+    for (int base = 0; base < count; base += kMaxSegs) {
+        SgdBatch b{};
+        int64_t blocks = 0;
+        int c = 0;
+        for (int k = base; k < count && c < kMaxSegs; ++k) {
+            if (ts[k].n == 0) continue;
+            SgdSeg& s = b.s[c++];
+            s.w = ts[k].w;
+            s.g = ts[k].g;
+            s.m = ts[k].m;
+            s.n = ts[k].n;
+            s.off0 = ts[k].offset0;
+            s.blk0 = blocks;
+            s.vec = aligned16(s.w) && aligned16(s.g) && (!use_mom || aligned16(s.m));
+            blocks += ceil_div(s.n, kSegBlockElems);
+        }
+        b.count = c;
+        if (c == 0) continue;
+        HASTE_CHECK_ARG(blocks < (int64_t)1 << 31, "haste_sgd_sr_step: tensors too large");
 #define HASTE_SGD_LAUNCH(UM, SR)                                                               \
-    sgd_sr_vec_kernel<GD, UM, SR><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(              \
-        w, g, m, n_vec, lr, wd, mu, seed, offset0)
+    sgd_sr_kernel<GD, UM, SR><<<dim3((unsigned)blocks), dim3(kSgdThreads), 0, st>>>(b, lr, wd, \
+                                                                                   mu, seed)
         if (use_mom && do_sr) HASTE_SGD_LAUNCH(true, true);
         else if (use_mom) HASTE_SGD_LAUNCH(true, false);
         else if (do_sr) HASTE_SGD_LAUNCH(false, true);
@@ -133,23 +178,16 @@ int launch_sgd(uint16_t* w, const void* g, float* m, int64_t n, float lr, float 
 #undef HASTE_SGD_LAUNCH
         HASTE_CHECK_LAUNCH("haste_sgd_sr_step");
     }
-    const int64_t i0 = n_vec * kVec;
-    if (i0 < n) {
-        const int64_t blocks = std::min<int64_t>(ceil_div(n - i0, 256), 1 << 20);
-        sgd_sr_scalar_kernel<GD><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-            w, g, m, i0, n, lr, wd, mu, use_mom, do_sr, seed, offset0);
-        HASTE_CHECK_LAUNCH("haste_sgd_sr_step");
-    }
     return HASTE_OK;
 }
 
-__global__ __launch_bounds__(256) void sr_round_vec_kernel(const float* __restrict__ x,
-                                                           uint16_t* __restrict__ out,
-                                                           int64_t n_vec, uint32_t k0,
-                                                           uint32_t k1, uint64_t offset0) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < n_vec; v += stride) {
-        const int64_t i = v * kVec;
+// SR fp32 -> bf16 over one tensor; vector loads when aligned, element loads for the tail.
+__global__ __launch_bounds__(256) void sr_round_kernel(const float* __restrict__ x,
+                                                       uint16_t* __restrict__ out, int64_t n,
+                                                       int32_t vec, uint32_t k0, uint32_t k1,
+                                                       uint64_t offset0) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kVec;
+    if (vec && i + kVec <= n) {
         f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + i));
         f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + i) + 1);
         float xf[kVec] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
@@ -163,17 +201,14 @@ __global__ __launch_bounds__(256) void sr_round_vec_kernel(const float* __restri
 #pragma unroll
         for (int q = 0; q < 4; ++q) ov[q] = ob[2 * q] | (ob[2 * q + 1] << 16);
         *reinterpret_cast<u32x4*>(out + i) = ov;
-    }
-}
-
-__global__ __launch_bounds__(256) void sr_round_scalar_kernel(const float* __restrict__ x,
-                                                              uint16_t* __restrict__ out,
-                                                              int64_t i0, int64_t n, uint32_t k0,
-                                                              uint32_t k1, uint64_t offset0) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = i0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        uint64_t off = offset0 + (uint64_t)i;
-        out[i] = (uint16_t)sr_bf16(x[i], philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, k0, k1));
+    } else {
+        for (int e = 0; e < kVec; ++e) {
+            const int64_t j = i + e;
+            if (j >= n) break;
+            uint64_t off = offset0 + (uint64_t)j;
+            out[j] = (uint16_t)sr_bf16(x[j], philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u,
+                                                       k0, k1));
+        }
     }
 }
 
@@ -182,21 +217,11 @@ __global__ __launch_bounds__(256) void sr_round_scalar_kernel(const float* __res
 int sr_round_bf16(const float* x, uint16_t* out, int64_t n, uint64_t seed, uint64_t offset0,
                   hipStream_t st) {
     const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
-    const bool vec_ok = aligned16(x) && aligned16(out);
-    int64_t n_vec = vec_ok ? n / kVec : 0;
-    if (n_vec > 0) {
-        const int64_t blocks = std::min<int64_t>(ceil_div(n_vec, 256), 1 << 20);
-        sr_round_vec_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(x, out, n_vec, k0, k1,
-                                                                        offset0);
-        HASTE_CHECK_LAUNCH("haste_sr_round_bf16");
-    }
-    const int64_t i0 = n_vec * kVec;
-    if (i0 < n) {
-        const int64_t blocks = std::min<int64_t>(ceil_div(n - i0, 256), 1 << 20);
-        sr_round_scalar_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(x, out, i0, n, k0,
-                                                                           k1, offset0);
-        HASTE_CHECK_LAUNCH("haste_sr_round_bf16");
-    }
+    const int64_t blocks = ceil_div(n, (int64_t)256 * kVec);
+    HASTE_CHECK_ARG(blocks < (int64_t)1 << 31, "haste_sr_round_bf16: tensor too large");
+    sr_round_kernel<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+        x, out, n, aligned16(x) && aligned16(out), k0, k1, offset0);
+    HASTE_CHECK_LAUNCH("haste_sr_round_bf16");
     return HASTE_OK;
 }
 
@@ -210,6 +235,24 @@ extern "C" int haste_sr_round_bf16(const float* x, uint16_t* out, int64_t n, uin
     return haste::sr_round_bf16(x, out, n, seed, offset0, static_cast<hipStream_t>(stream));
 }
 
+namespace {
+int sgd_dispatch(const haste::SgdTensor* ts, int count, int32_t g_dtype, float lr, float wd,
+                 float mu, int32_t use_mom, int32_t do_sr, uint64_t seed, hipStream_t st,
+                 const char* fn) {
+    switch (g_dtype) {
+    case HASTE_DTYPE_BF16:
+        return haste::launch_sgd<HASTE_DTYPE_BF16>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
+    case HASTE_DTYPE_F16:
+        return haste::launch_sgd<HASTE_DTYPE_F16>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
+    case HASTE_DTYPE_F32:
+        return haste::launch_sgd<HASTE_DTYPE_F32>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
+    default:
+        haste::set_error("%s: unsupported gradient dtype code %d", fn, (int)g_dtype);
+        return HASTE_ERR_UNSUPPORTED;
+    }
+}
+}  // namespace
+
 extern "C" int haste_sgd_sr_step(uint16_t* w, const void* g, int32_t g_dtype, float* m, int64_t n,
                                  float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
                                  uint64_t seed, uint64_t offset0, void* stream) {
@@ -217,19 +260,36 @@ extern "C" int haste_sgd_sr_step(uint16_t* w, const void* g, int32_t g_dtype, fl
     if (n == 0) return HASTE_OK;
     HASTE_CHECK_ARG(w != nullptr && g != nullptr, "haste_sgd_sr_step: null pointer");
     HASTE_CHECK_ARG(!use_mom || m != nullptr, "haste_sgd_sr_step: momentum buffer is NULL");
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    switch (g_dtype) {
-    case HASTE_DTYPE_BF16:
-        return haste::launch_sgd<HASTE_DTYPE_BF16>(w, g, m, n, lr, wd, mu, use_mom, do_sr, seed,
-                                                   offset0, st);
-    case HASTE_DTYPE_F16:
-        return haste::launch_sgd<HASTE_DTYPE_F16>(w, g, m, n, lr, wd, mu, use_mom, do_sr, seed,
-                                                  offset0, st);
-    case HASTE_DTYPE_F32:
-        return haste::launch_sgd<HASTE_DTYPE_F32>(w, g, m, n, lr, wd, mu, use_mom, do_sr, seed,
-                                                  offset0, st);
-    default:
-        haste::set_error("haste_sgd_sr_step: unsupported gradient dtype code %d", (int)g_dtype);
-        return HASTE_ERR_UNSUPPORTED;
+    const haste::SgdTensor t{w, g, m, n, offset0};
+    return sgd_dispatch(&t, 1, g_dtype, lr, wd, mu, use_mom, do_sr, seed,
+                        static_cast<hipStream_t>(stream), "haste_sgd_sr_step");
+}
+
+extern "C" int haste_sgd_sr_step_multi(const haste_sgd_tensor* tensors, int32_t count,
+                                       int32_t g_dtype, float lr, float wd, float mu,
+                                       int32_t use_mom, int32_t do_sr, uint64_t seed,
+                                       void* stream) {
+    HASTE_CHECK_ARG(count >= 0, "haste_sgd_sr_step_multi: count must be >= 0 (got %d)",
+                    (int)count);
+    if (count == 0) return HASTE_OK;
+    HASTE_CHECK_ARG(tensors != nullptr, "haste_sgd_sr_step_multi: null tensor list");
+    haste::SgdTensor ts[64];
+    for (int base = 0; base < count; base += 64) {
+        const int c = std::min<int>(64, count - base);
+        for (int k = 0; k < c; ++k) {
+            const haste_sgd_tensor& t = tensors[base + k];
+            HASTE_CHECK_ARG(t.n >= 0, "haste_sgd_sr_step_multi: tensor %d: n must be >= 0",
+                            base + k);
+            HASTE_CHECK_ARG(t.n == 0 || (t.w != nullptr && t.g != nullptr),
+                            "haste_sgd_sr_step_multi: tensor %d: null pointer", base + k);
+            HASTE_CHECK_ARG(t.n == 0 || !use_mom || t.m != nullptr,
+                            "haste_sgd_sr_step_multi: tensor %d: momentum buffer is NULL",
+                            base + k);
+            ts[k] = haste::SgdTensor{t.w, t.g, t.m, t.n, t.offset0};
+        }
+        int rc = sgd_dispatch(ts, c, g_dtype, lr, wd, mu, use_mom, do_sr, seed,
+                              static_cast<hipStream_t>(stream), "haste_sgd_sr_step_multi");
+        if (rc != HASTE_OK) return rc;
     }
+    return HASTE_OK;
 }

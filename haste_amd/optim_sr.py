@@ -6,7 +6,8 @@ Semantics kept from the reference:
     step (optim_sr.py:59-62); every tensor of the group uses that seed with
     offsets restarting at 0 (so weights and bias share random streams);
   * fp32 params take the plain torch path (optim_sr.py:73-84);
-  * low-precision params are updated in place by one fused kernel
+  * low-precision params are updated in place by one fused kernel (one
+    launch per gradient dtype covers all of the group's tensors)
     (g' = fma(wd, w, g); m' = fma(mu, m, g'); w' = fma(-lr, m' or g', w);
     SR to bf16 with tl.randint(seed, i), or RNE when SR is off);
   * non-contiguous params are updated through a contiguous copy.
@@ -20,7 +21,7 @@ from __future__ import annotations
 import torch
 from torch.optim import Optimizer
 
-from .sr import sgd_update
+from .sr import sgd_update_multi
 
 __all__ = ["SRSgd", "SGD_SR"]
 
@@ -63,6 +64,8 @@ class SRSgd(Optimizer):
             group["seed"] += 1
             mom_on = self._uses_momentum(group)
 
+            # bf16 tensors are updated by one fused launch per gradient dtype
+            batches = {}
             for p in group["params"]:
                 if p.grad is None:
                     continue
@@ -83,11 +86,18 @@ class SRSgd(Optimizer):
                 w = p.data
                 w_contig = w if w.is_contiguous() else w.contiguous()
                 g_contig = grad if grad.is_contiguous() else grad.contiguous()
-                sgd_update(w_contig, g_contig, self._momentum_buf(p) if mom_on else None,
-                           learning_rate=lr, weight_decay=wd, momentum=mu,
-                           use_momentum=use_mom, stochastic_rounding=sr, seed=seed)
-                if w_contig.data_ptr() != w.data_ptr():
-                    p.data.copy_(w_contig)
+                b = batches.setdefault(grad.dtype, ([], [], [], []))
+                b[0].append(w_contig)
+                b[1].append(g_contig)
+                b[2].append(self._momentum_buf(p) if mom_on else None)
+                b[3].append(p)
+            for ws, gs, ms, ps in batches.values():
+                sgd_update_multi(ws, gs, ms if mom_on else None, learning_rate=lr,
+                                 weight_decay=wd, momentum=mu, use_momentum=use_mom,
+                                 stochastic_rounding=sr, seed=seed)
+                for w_contig, p in zip(ws, ps):
+                    if w_contig.data_ptr() != p.data.data_ptr():
+                        p.data.copy_(w_contig)
         return loss
 
 

@@ -13,7 +13,7 @@ import torch
 from . import _lib
 from ._C import dtype_code, require_device, stream_of
 
-__all__ = ["stochastic_rounding", "sgd_update"]
+__all__ = ["stochastic_rounding", "sgd_update", "sgd_update_multi"]
 
 
 def stochastic_rounding(x: torch.Tensor, output: torch.Tensor, seed: int) -> None:
@@ -58,3 +58,34 @@ def sgd_update(weights: torch.Tensor, gradient: torch.Tensor, momentum_buf: torc
               momentum_buf.data_ptr() if use_mom_flag else None, weights.numel(),
               float(learning_rate), float(weight_decay), float(momentum), use_mom_flag,
               1 if stochastic_rounding else 0, int(seed), 0, stream_of(weights))
+
+
+def sgd_update_multi(weights, gradients, momentum_bufs, learning_rate: float, weight_decay: float,
+                     momentum: float, use_momentum: bool, stochastic_rounding: bool,
+                     seed: int) -> None:
+    """``sgd_update`` over several tensors in one launch per 8 tensors; every
+    tensor uses ``seed`` with offsets from 0 (as a loop of sgd_update calls,
+    optim_sr.py:64-112).  Gradients must share one dtype."""
+    n = len(weights)
+    assert len(gradients) == n and (momentum_bufs is None or len(momentum_bufs) == n)
+    if n == 0:
+        return
+    use_mom_flag = 1 if (use_momentum and momentum != 0.0) else 0
+    gdt = gradients[0].dtype
+    arr = (_lib.SgdTensor * n)()
+    for i, (w, g) in enumerate(zip(weights, gradients)):
+        m = None if momentum_bufs is None else momentum_bufs[i]
+        assert w.is_contiguous() and g.is_contiguous() and w.shape == g.shape
+        assert g.dtype == gdt, "sgd_update_multi: gradients must share one dtype"
+        if w.dtype != torch.bfloat16:
+            raise NotImplementedError(f"sgd_update: weights must be bfloat16 (got {w.dtype})")
+        require_device(w, "weights")
+        require_device(g, "gradient")
+        if use_mom_flag:
+            assert m is not None and m.is_contiguous() and m.shape == w.shape
+            assert m.dtype == torch.float32
+        arr[i] = _lib.SgdTensor(w.data_ptr(), g.data_ptr(), m.data_ptr() if use_mom_flag else None,
+                                w.numel(), 0)
+    _lib.call("haste_sgd_sr_step_multi", arr, n, dtype_code(gdt), float(learning_rate),
+              float(weight_decay), float(momentum), use_mom_flag, 1 if stochastic_rounding else 0,
+              int(seed), stream_of(weights[0]))

@@ -118,6 +118,33 @@ int haste_sgd_sr_step(uint16_t* w, const void* g, int32_t g_dtype, float* m, int
                       uint64_t seed, uint64_t offset0, void* stream);
 
 /*
+ * The same step over several tensors in one launch (one kernel per 8
+ * tensors): tensor i uses offsets offset0_i + j.  SRSgd.step calls
+ * sgd_update once per parameter (shared_ffi/optim_sr.py:64-112, all
+ * parameters of a group share the seed and start at offset 0); this entry
+ * point replaces that loop.  n == 0 entries are skipped.
+ */
+typedef struct haste_sgd_tensor {
+    uint16_t* w;
+    const void* g;
+    float* m;
+    int64_t n;
+    uint64_t offset0;
+} haste_sgd_tensor;
+
+int haste_sgd_sr_step_multi(const haste_sgd_tensor* tensors, int32_t count, int32_t g_dtype,
+                            float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
+                            uint64_t seed, void* stream);
+
+/*
+ * xT[d, b] = x[b, d] for a bf16/f16 matrix x [B, D] with row stride ldx;
+ * xT has row stride ldt >= B, and columns B..ldt-1 of xT are set to zero.
+ * Replaces features.transpose(0, 1).contiguous() (shared_ffi/bindings.py:19).
+ */
+int haste_transpose_features(const uint16_t* x, int64_t ldx, uint16_t* xT, int64_t ldt, int64_t B,
+                             int64_t D, void* stream);
+
+/*
  * On-device rewire of a bf16 FFI layer (prune + regrow), in place on W and idx.
  * Replaces GroupFixedFanIn.rewire (shared_ffi/rewire.py:143-239) with a
  * deterministic contract:

@@ -96,6 +96,47 @@ def test_sgd_update_api(dev):
     assert np.array_equal(bits(wd_), ref_w)
 
 
+@pytest.mark.parametrize("use_mom", [False, True])
+def test_sgd_multi_matches_per_tensor_oracle(dev, use_mom):
+    """One launch over tensors of mixed sizes (tails, an unaligned view, an empty one)
+    with their own offset bases equals one oracle call per tensor."""
+    sizes = [131073 * 8 + 3, 131073, 5, 0, 4096, 17]
+    offs = [0, 0, 7, 0, 2**32 - 2, 123]
+    g = torch.Generator().manual_seed(11)
+    ws, gs, ms, views = [], [], [], []
+    for i, n in enumerate(sizes):
+        w = (torch.rand(n + 1, generator=g) - 0.5).to(torch.bfloat16)
+        gr = torch.randn(n + 1, generator=g) * 0.05
+        m = torch.randn(n + 1, generator=g) * 0.01
+        ws.append(w), gs.append(gr), ms.append(m)
+        sl = slice(1, n + 1) if i == 1 else slice(0, n)  # tensor 1 is a 2-byte-offset view
+        views.append((w.to(dev)[sl], gr.to(dev)[sl], m.to(dev)[sl], sl))
+    arr = (_lib.SgdTensor * len(sizes))(*[
+        _lib.SgdTensor(w.data_ptr(), gr.data_ptr(), m.data_ptr() if use_mom else None, n, off)
+        for (w, gr, m, _), n, off in zip(views, sizes, offs)])
+    _lib.call("haste_sgd_sr_step_multi", arr, len(sizes), _lib.DTYPE_F32, 0.05, 1e-4, 0.9,
+              int(use_mom), 1, 2**32 + 5, _C.stream_of(views[0][0]))
+    for (w, gr, m, sl), n, off, w0, g0, m0 in zip(views, sizes, offs, ws, gs, ms):
+        ref_w, ref_m = oracle.sgd_sr_step(bits(w0[sl]), g0[sl].numpy(),
+                                          m0[sl].numpy() if use_mom else None, 0.05, 1e-4, 0.9,
+                                          use_mom, True, 2**32 + 5, off)
+        assert np.array_equal(bits(w), ref_w), n
+        if use_mom:
+            assert np.array_equal(m.cpu().numpy().view(np.uint32), ref_m.view(np.uint32)), n
+
+
+@pytest.mark.parametrize("B,D,ldt", [(512, 768, 512), (50, 300, 64), (1, 7, 8), (130, 64, 192)])
+def test_transpose_features(dev, B, D, ldt):
+    x = torch.randn(B, D + 3).to(torch.bfloat16)
+    xd = x.to(dev)[:, :D] if D % 8 else x.to(dev)[:, :D].contiguous()
+    out = torch.full((D, ldt), 7.0, dtype=torch.bfloat16, device=dev)
+    _lib.call("haste_transpose_features", xd.data_ptr(), xd.stride(0), out.data_ptr(), ldt, B, D,
+              _C.stream_of(xd))
+    o = out.cpu()
+    assert torch.equal(o[:, :B], x[:, :D].t())
+    assert torch.count_nonzero(o[:, B:].float()) == 0
+
+
 REWIRE_CASES = [
     # O, F, G, D, prune, k/thr, regrow, init
     (4096, 32, 32, 768, "fraction", 4, "random", "zero"),
