@@ -6,20 +6,25 @@
 // (shared_ffi/ffi_backward_features.cu:202-212), so its sums depend on timing.
 // Here no float atomic touches any memory and every sum has a fixed order:
 //
-//  1. prep (one workgroup per group): the F slots are stably sorted by index,
-//     so equal indices become adjacent runs; the sorted table, the bounds of
-//     eight value parts of every feature range, and W_g transposed in sorted
-//     slot order (WT[g][p][l] = W[g*G + l][slot(p)]) are written to the
-//     workspace.
-//  2. main: a workgroup (group slice s, feature range dr, 32-column batch tile
-//     bt) keeps the partial dXT[d in dr, b in bt] in LDS (fp32).  Its 8 waves
-//     own fixed value parts of dr, so they never touch the same LDS word and
-//     run through the slice's groups independently (no barriers).  Per group a
-//     wave multiplies the WT rows of its positions with dY_g (MFMA, M = sorted
-//     positions, N = batch, K = labels) and adds the result rows into the LDS
-//     partial with plain reads and writes (LDS float atomics execute one lane
-//     at a time).  Operands come straight from global memory into registers,
-//     two groups ahead.
+//  1. prep (one workgroup per group g): the distinct indices of the group are
+//     split by feature range (Dc features each) and laid out in tiles of 16
+//     positions.  A tile row holds the group's weights for that feature,
+//     transposed (WT[pos][label]).  An index that occurs k > 1 times in the
+//     group gets sum_j W[l, j] (fp32, ascending j) split into a 16-bit "hi"
+//     row (layer 0) and the 16-bit rounding of the remainder as a "lo" row
+//     (layer 1), so inside a layer every feature occurs once.
+//  2. main: a workgroup owns (group slice s, feature range r, batch tile of
+//     BT columns) and keeps dXT[range, tile] as an fp32 partial in LDS.  Wave
+//     w owns batch rows [w*RPW, (w+1)*RPW) of the tile, so no two waves touch
+//     the same LDS word and the waves never synchronise.  Per group a wave
+//     multiplies its dY rows with the range's tiles (MFMA, M = batch rows,
+//     N = 16 positions, K = labels); a lane then holds four consecutive
+//     batch values of one feature and adds them into LDS with one 16-byte
+//     read and one 16-byte write.  Reads of all tiles of a layer are issued
+//     before their writes (a layer's features are distinct); a wave's LDS
+//     accesses execute in program order, so layer 1 and later groups see
+//     the earlier writes.  Operands come from global memory into registers,
+//     NS groups ahead.
 //  3. reduce: dXT = sum over slices s = 0..S-1 in ascending order (fp32 out), or
 //     fused with the bf16 stochastic rounding of shared_ffi/bindings.py:44-48.
 #include <algorithm>
@@ -32,377 +37,366 @@ int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, 
 
 namespace {
 
-constexpr int kWaves = 4;                 // waves per workgroup, one value part each
-constexpr int kMainThreads = 64 * kWaves;
-constexpr int kMetaStride = 16;           // ints of meta per (group, feature range)
-constexpr int kBT = 32;            // batch columns per workgroup
-constexpr int kLdsBytes = 160 * 1024;
+constexpr int kMainThreads = 256;  // 4 waves
+constexpr int kAccPad = 4;         // fp32 words of padding per LDS row (bank spread)
+constexpr int kDummyFloats = 4 * kMainThreads;  // one 16-byte dummy slot per lane
+constexpr int kAccBytes = 140 * 1024;           // LDS for the partial (incl. dummies)
 constexpr int kTargetCTAs = 256;
-constexpr int kMaxDc = (kLdsBytes - 2 * kMainThreads * 4) / 4 / kBT;  // features in the LDS partial
-static_assert(kMaxDc * kBT * 4 + 2 * kMainThreads * 4 <= kLdsBytes, "LDS budget");
+constexpr int kMaxRanges = 128;  // feature ranges per group handled by prep
+constexpr int kMetaStride = 4;   // ints per (group, range): tile begin, layer-1 begin, end
+
+__host__ __device__ constexpr int acc_stride(int bt) { return bt + kAccPad; }
+__host__ __device__ constexpr int max_dc(int bt) {
+    return (kAccBytes / 4 - kDummyFloats) / acc_stride(bt);
+}
 
 struct BwdFPlan {
-    int64_t Gc, nbt, Bp, ndr, Dc, S, gps;  // gps = groups per slice
-    int64_t sorted_off, meta_off, wt_off, prep_bytes, ws_bytes;
+    int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;
+    int64_t tfeat_off, meta_off, twt_off, prep_bytes, ws_bytes;
 };
 
 BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
     BwdFPlan p;
     p.Gc = ceil_div(O, G);
-    p.nbt = ceil_div(B, kBT);
-    p.Bp = p.nbt * kBT;
-    p.ndr = ceil_div(D, kMaxDc);
+    p.BT = B <= 64 ? 64 : 128;
+    p.nbt = ceil_div(B, p.BT);
+    p.Bp = p.nbt * p.BT;
+    p.ndr = ceil_div(D, max_dc((int)p.BT));
     p.Dc = ceil_div(D, p.ndr);
     int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
     S = std::min<int64_t>(S, std::max<int64_t>(1, ceil_div(p.Gc, 8)));
     p.gps = ceil_div(p.Gc, S);
     p.S = ceil_div(p.Gc, p.gps);
+    // tiles per group: layer 0 holds <= F distinct features, layer 1 <= F/2, and
+    // each non-empty range pads its layer to a multiple of 16
+    const int64_t r0 = std::min<int64_t>(p.ndr, F), r1 = std::min<int64_t>(p.ndr, F / 2);
+    p.Tcap = ceil_div(F + 15 * r0, 16) + ceil_div(F / 2 + 15 * r1, 16);
     auto r256 = [](int64_t x) { return (x + 255) / 256 * 256; };
-    p.sorted_off = 0;
-    p.meta_off = r256(p.Gc * F * 4);
-    p.wt_off = p.meta_off + r256(p.Gc * p.ndr * kMetaStride * 4);
-    p.prep_bytes = p.wt_off + r256(p.Gc * F * G * 2);
+    p.tfeat_off = 0;
+    p.meta_off = r256(p.Gc * p.Tcap * 16 * 4);
+    p.twt_off = p.meta_off + r256(p.Gc * p.ndr * kMetaStride * 4);
+    p.prep_bytes = p.twt_off + r256(p.Gc * p.Tcap * 16 * G * 2);
     p.ws_bytes = p.S * D * p.Bp * 4;
     return p;
 }
 
 // --------------------------------------------------------------- prep ------
-// sorted[g*F + p] = (index << 8) | (colour + 1) for sorted position p (an
-// arithmetic >> 8 recovers the index; -1 marks an empty entry).  Value part w (of
-// kWaves) of feature range dr owns sorted positions [m[w], m[w+1]), m = meta +
-// (g*ndr + dr)*kMetaStride (its values lie in [d_lo + (Dc'*w)/kWaves,
-// d_lo + (Dc'*(w+1))/kWaves)); m[kWaves + 1] bounds the colour count of the
-// scatter: ceil((longest run - 1) / 4).
-// colour: with rel = p - (first position of p's part), a position is a
-// "head" if rel % 4 == 0 or it starts a run of equal indices; heads get
-// colour rel/4 - (rel - run)/4 (run = rank inside the run), others -1.
-// wt[(g*F + p)*G + l] = W[g*G + l][slot(p)] (0 for labels >= O).
-template <int G>
+// Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*4 + 0..2]
+// = (tb, tm, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative to
+// g*Tcap).  tfeat[t*16 + p] = feature - r*Dc of position p of tile t, or -1 for
+// padding; twt[(t*16 + p)*G + l] = weight of label l (0 for padding and for
+// labels >= O).  Features within a range's layer are in ascending order.
+template <typename T, int G>
 __global__ __launch_bounds__(256) void bwdf_prep_kernel(const int32_t* __restrict__ idx,
                                                         const uint16_t* __restrict__ W,
-                                                        int32_t* __restrict__ sorted,
+                                                        int* __restrict__ tfeat,
                                                         int* __restrict__ meta,
-                                                        uint16_t* __restrict__ wt, int F, int D,
-                                                        int64_t O, int ndr, int Dc) {
-    constexpr int LDW = G + 8;
-    __shared__ int32_t s[256];
-    __shared__ int32_t sv[256];
-    __shared__ int32_t srun[256];
-    __shared__ int32_t sslot[256];
-    __shared__ int run_max;
-    __shared__ __attribute__((aligned(16))) uint16_t Wt[256 * LDW];  // Wt[slot][label]
+                                                        uint16_t* __restrict__ twt, int F, int D,
+                                                        int64_t O, int ndr, int Dc, int Tcap) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_w[G * 256];  // W_g [label][slot]
+    __shared__ int s_idx[256];
+    __shared__ int s_flag[256];  // bit 0: first occurrence, bit 1: occurs more than once
+    __shared__ int s_perm[256];  // slots in (index, slot) order
+    __shared__ int s_cnt[2][kMaxRanges];
+    __shared__ int s_tile[kMaxRanges][3];
+    __shared__ int s_ntiles;
     const int64_t g = blockIdx.x;
     const int64_t l0 = g * G;
     const int tid = threadIdx.x;
-    if (tid == 0) run_max = 0;
-    if (tid < F) s[tid] = min(max(idx[g * F + tid], 0), D - 1);
-    // W_g rows -> LDS transposed: item = (label, 8 slots)
+    for (int i = tid; i < 2 * kMaxRanges; i += 256) (&s_cnt[0][0])[i] = 0;
+    if (tid < F) s_idx[tid] = min(max(idx[g * F + tid], 0), D - 1);
     for (int it = tid; it < G * (F / 8); it += 256) {
-        const int l = it / (F / 8);
-        const int j0 = (it % (F / 8)) * 8;
+        const int l = it / (F / 8), j0 = (it % (F / 8)) * 8;
         u32x4 v = u32x4{0u, 0u, 0u, 0u};
         if (l0 + l < O) v = *reinterpret_cast<const u32x4*>(W + (l0 + l) * F + j0);
+        *reinterpret_cast<u32x4*>(&s_w[l * F + j0]) = v;
+    }
+    __syncthreads();
+    int f = 0, rank = 0, cnt = 0;
+    bool first = false;
+    if (tid < F) {
+        f = s_idx[tid];
+        int before = 0;
+        for (int k = 0; k < F; ++k) {
+            const int v = s_idx[k];
+            rank += v < f;
+            before += (v == f) & (k < tid);
+            cnt += v == f;
+        }
+        rank += before;
+        first = before == 0;
+        s_perm[rank] = tid;
+        s_flag[tid] = (first ? 1 : 0) | (cnt > 1 ? 2 : 0);
+    }
+    __syncthreads();
+    const int r = f / Dc;
+    const int r_lo = r * Dc;
+    int pu = 0, pd = 0;  // rank among the range's distinct / duplicated features
+    if (tid < F && first) {
+        for (int k = 0; k < F; ++k) {
+            const int v = s_idx[k], fl = s_flag[k];
+            const bool in = (fl & 1) && v >= r_lo && v < f;
+            pu += in;
+            pd += in && (fl & 2);
+        }
+        atomicAdd(&s_cnt[0][r], 1);
+        if (cnt > 1) atomicAdd(&s_cnt[1][r], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int t = 0;
+        for (int rr = 0; rr < ndr; ++rr) {
+            s_tile[rr][0] = t;
+            t += (s_cnt[0][rr] + 15) / 16;
+            s_tile[rr][1] = t;
+            t += (s_cnt[1][rr] + 15) / 16;
+            s_tile[rr][2] = t;
+        }
+        s_ntiles = t;
+    }
+    __syncthreads();
+    for (int rr = tid; rr < ndr; rr += 256) {
+        int* m = meta + (g * ndr + rr) * kMetaStride;
+        m[0] = s_tile[rr][0];
+        m[1] = s_tile[rr][1];
+        m[2] = s_tile[rr][2];
+        m[3] = 0;
+    }
+    const int64_t tbase = g * Tcap;
+    if (tid < F && first) {
+        const int t0 = s_tile[r][0] + pu / 16, p0 = pu % 16;
+        const int t1 = s_tile[r][1] + pd / 16, p1 = pd % 16;
+        tfeat[(tbase + t0) * 16 + p0] = f - r_lo;
+        if (cnt > 1) tfeat[(tbase + t1) * 16 + p1] = f - r_lo;
+        uint16_t* hi_row = twt + ((tbase + t0) * 16 + p0) * G;
+        uint16_t* lo_row = twt + ((tbase + t1) * 16 + p1) * G;
+#pragma unroll 1
+        for (int lc = 0; lc < G; lc += 8) {
+            u32x4 hv, lv;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            Wt[(j0 + e) * LDW + l] = (uint16_t)((e & 1) ? (v[e >> 1] >> 16) : (v[e >> 1] & 0xFFFFu));
-    }
-    __syncthreads();
-    if (tid < F) {
-        const int v = s[tid];
-        int rank = 0, run = 0;
-        for (int q = 0; q < F; ++q) {
-            const int u = s[q];
-            rank += (u < v) || (u == v && q < tid);
-            run += (u == v && q < tid);
+            for (int e = 0; e < 8; ++e) {
+                const int l = lc + e;
+                uint32_t hb, lb = 0;
+                if (cnt == 1) {
+                    hb = s_w[l * F + tid];
+                } else {
+                    float sum = 0.0f;
+                    for (int q = 0; q < cnt; ++q) sum += bits_to_f32<T>(s_w[l * F + s_perm[rank + q]]);
+                    hb = f32_to_bits<T>(sum);
+                    lb = f32_to_bits<T>(sum - bits_to_f32<T>(hb));
+                }
+                if (e & 1) {
+                    hv[e >> 1] |= hb << 16;
+                    lv[e >> 1] |= lb << 16;
+                } else {
+                    hv[e >> 1] = hb;
+                    lv[e >> 1] = lb;
+                }
+            }
+            *reinterpret_cast<u32x4*>(hi_row + lc) = hv;
+            if (cnt > 1) *reinterpret_cast<u32x4*>(lo_row + lc) = lv;
         }
-        sv[rank] = v;
-        srun[rank] = run;
-        sslot[rank] = tid;
-        atomicMax(&run_max, run);
     }
-    __syncthreads();
-    auto lower_bound = [&](int bound) {
-        int lo = 0, hi = F;
-        while (lo < hi) {
-            const int mm = (lo + hi) >> 1;
-            if (sv[mm] < bound) lo = mm + 1; else hi = mm;
-        }
-        return lo;
-    };
-    for (int dr = tid; dr < ndr; dr += 256) {
-        const int d_lo = dr * Dc, d_hi = min(D, d_lo + Dc);
-        int* m = meta + (g * ndr + dr) * kMetaStride;
-        for (int w = 0; w <= kWaves; ++w) m[w] = lower_bound(d_lo + ((d_hi - d_lo) * w) / kWaves);
-        m[kWaves + 1] = (run_max + 3) / 4;
-    }
-    if (tid < F) {
-        const int p = tid;
-        const int x = sv[p];
-        const int dr = x / Dc;
-        const int d_lo = dr * Dc, d_hi = min(D, d_lo + Dc);
-        int w = kWaves - 1;
-        while (w > 0 && x < d_lo + ((d_hi - d_lo) * w) / kWaves) --w;
-        const int pb = lower_bound(d_lo + ((d_hi - d_lo) * w) / kWaves);
-        const int rel = p - pb;
-        const int run = srun[p];
-        const bool head = (rel % 4 == 0) || run == 0;
-        sorted[g * F + p] = (x << 8) | (head ? rel / 4 - (rel - run) / 4 + 1 : 0);
-    }
-    // sorted rows of W_g^T: item = (position, 8 labels)
-    for (int it = tid; it < F * (G / 8); it += 256) {
-        const int p = it / (G / 8);
-        const int lc = (it % (G / 8)) * 8;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(&Wt[sslot[p] * LDW + lc]);
-        *reinterpret_cast<u32x4*>(wt + ((g * F + p) * G + lc)) = v;
+    // padding slots of every range's layers
+    const int nslots = s_ntiles * 16;
+    for (int i = tid; i < nslots; i += 256) {
+        const int t = i / 16, p = i % 16;
+        int rr = 0;
+        while (t >= s_tile[rr][2]) ++rr;  // empty ranges have tb == te and are skipped
+        const bool lay1 = t >= s_tile[rr][1];
+        const int used = lay1 ? s_cnt[1][rr] : s_cnt[0][rr];
+        const int slot = (t - s_tile[rr][lay1 ? 1 : 0]) * 16 + p;
+        if (slot < used) continue;
+        tfeat[(tbase + t) * 16 + p] = -1;
+        uint16_t* row = twt + ((tbase + t) * 16 + p) * G;
+        for (int lc = 0; lc < G; lc += 8)
+            *reinterpret_cast<u32x4*>(row + lc) = u32x4{0u, 0u, 0u, 0u};
     }
 }
 
 // --------------------------------------------------------------- main ------
-template <typename T, int G, int FP>
+template <int G, int RPW, int FP>
 struct BwdFCfg {
     static constexpr int KS = G >= 32 ? G / 32 : 1;  // MFMA k-steps over labels
-    static constexpr int NT = kBT / 16;              // batch n-tiles per wave
-    static constexpr int MAXT = FP >= 256 ? 5 : FP >= 128 ? 3 : 2;  // tiles kept in registers
+    static constexpr int MT = RPW / 16;              // 16-row batch tiles per wave
+    static constexpr int BT = 4 * RPW;               // batch columns per workgroup
+    static constexpr int AS = acc_stride(BT);
+    static constexpr int NS = G >= 128 ? 2 : 3;      // groups in flight per wave
+    // tiles per group kept in registers (a range's usual share of F, padded)
+    static constexpr int MAXT = FP >= 256 ? 6 : FP >= 128 ? 4 : 3;
 };
 
-typedef int32_t i32x4a __attribute__((ext_vector_type(4), aligned(4)));
-
-template <int KS, int MAXT, int NT>
+template <int KS, int MT, int MAXT>
 struct BwdFRegs {
-    u32x4 a[MAXT][KS];  // WT rows of the wave's positions (A operand)
-    int e[MAXT][4];     // packed slot-table entries of this lane's scatter positions
-    u32x4 b[NT][KS];    // dY fragments (B operand)
-    int pb, pe, maxc;
+    u32x4 a[MT][KS];    // dY rows of the wave (A operand)
+    u32x4 b[MAXT][KS];  // tile rows (B operand)
+    int f[MAXT];        // feature (relative to the range) of this lane's tile column
+    int tb, tm, te;     // tiles of the group's range (relative to the group base)
 };
 
-// Scatter of one MFMA tile (rows = 16 sorted positions; lane holds positions
-// 4*lq + i, i = 0..3, of one batch column): equal indices are adjacent, so a
-// lane first folds each run inside its own 4 positions into the run's first
-// position there (the "head").  Heads of one run that sit in different
-// lanes/tiles get successive colours (their quad index relative to the run
-// start); pass c reads, adds and writes all heads of colour c at once.  Within
-// a pass every lane targets a distinct word, and every word is only ever
-// touched by one wave, in program order (the compiler keeps these plain LDS
-// accesses in order: as far as it knows they may alias).
-template <typename T, int G, int FP>
+template <typename T, int G, int RPW, int FP>
 __global__ __launch_bounds__(kMainThreads) void bwdf_main_kernel(
-    const int32_t* __restrict__ sorted, const int* __restrict__ meta,
-    const uint16_t* __restrict__ wt, const uint16_t* __restrict__ dY, int64_t lddy,
-    float* __restrict__ ws, int B, int Bp, int D, int F, int64_t O, int64_t Gc, int nbt, int ndr,
-    int Dc, int gps, int S) {
-    using C = BwdFCfg<T, G, FP>;
-    constexpr int KS = C::KS, NT = C::NT, MAXT = C::MAXT;
-    using R = BwdFRegs<KS, MAXT, NT>;
-    __shared__ float acc[kMaxDc * kBT + 2 * kMainThreads];  // + two dummy words per lane
+    const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
+    const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
+    int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
+    using C = BwdFCfg<G, RPW, FP>;
+    constexpr int KS = C::KS, MT = C::MT, BT = C::BT, AS = C::AS, NS = C::NS, MAXT = C::MAXT;
+    using R = BwdFRegs<KS, MT, MAXT>;
+    __shared__ __attribute__((aligned(16))) float acc[max_dc(BT) * AS + kDummyFloats];
 
     const int64_t work = xcd_remap(blockIdx.x, (int64_t)S * ndr * nbt);
     if (work < 0) return;
     const int bt = (int)(work % nbt);
-    const int dr = (int)((work / nbt) % ndr);
+    const int r = (int)((work / nbt) % ndr);
     const int s = (int)(work / ((int64_t)nbt * ndr));
-    const int d_lo = dr * Dc;
-    const int d_hi = min(D, d_lo + Dc);
-    const int b_base = bt * kBT;
-    const int64_t g_begin = (int64_t)s * gps;
-    const int64_t g_end = min(Gc, g_begin + gps);
+    const int d_lo = r * Dc;
+    const int dn = min(Dc, D - d_lo);
+    const int64_t g_lo = (int64_t)s * gps;
+    const int64_t g_hi = min<int64_t>(Gc, g_lo + gps);
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int part = tid >> 6;  // value part of this wave
-    const int lrow = lane & 15;
-    const int lq = lane >> 4;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15;  // A row within an M tile / B column (tile position)
+    const int kq = lane >> 4;   // which 8 of the 32 K elements
+    const bool kq_ok = G >= 32 || kq < 2;
 
-    for (int i = tid; i < (d_hi - d_lo) * kBT; i += kMainThreads) acc[i] = 0.0f;
+    for (int i = tid * 4; i < dn * AS; i += kMainThreads * 4)
+        *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
     __syncthreads();
 
-    // Branch-free loads: addresses are clamped into the group's blocks and
-    // out-of-range values replaced by selects (divergent branches around
-    // memory operations cost far more than the operations themselves).  The
-    // dY masking only runs for the ragged last group / batch tile.
-    const bool full_b = b_base + kBT <= B;
-    auto load = [&](int64_t g, R& r) {
-        const int* m = meta + (g * ndr + dr) * kMetaStride;
-        r.pb = m[part];
-        r.pe = m[part + 1];
-        r.maxc = m[kWaves + 1];
-        const int64_t l0 = g * G;
-        const uint16_t* wg = wt + g * F * G;
-        const int32_t* sg = sorted + g * F;
-        const bool clamp_p = r.pb + 16 * MAXT + 4 > F;
+    // this lane's dY rows (clamped: rows >= B only feed partial columns never read)
+    const uint16_t* yrow[MT];
 #pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (r.pb + t * 16 >= r.pe) break;  // wave-uniform: no positions left
-            int pa = r.pb + t * 16 + lrow;
-            if (clamp_p) pa = min(pa, F - 1);
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const int k = G >= 32 ? ks * 32 + lq * 8 : (lq & 1) * 8;
-                r.a[t][ks] = *reinterpret_cast<const u32x4*>(wg + pa * G + k);
-            }
-            // the lane's 4 consecutive entries with one (4-byte aligned) 16-byte load
-            const int p0 = r.pb + t * 16 + lq * 4;
-            i32x4a v;
-            if (clamp_p && p0 + 4 > F) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = sg[min(p0 + i, F - 1)];
-            } else {
-                v = *reinterpret_cast<const i32x4a*>(sg + p0);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) r.e[t][i] = p0 + i < r.pe ? v[i] : -1;
-        }
-        const bool full = full_b && l0 + G <= O;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int b = b_base + nt * 16 + lrow;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const int k = ks * 32 + lq * 8;
-                if (full && k < G) {
-                    r.b[nt][ks] = *reinterpret_cast<const u32x4*>(dY + (int64_t)b * lddy + l0 + k);
-                } else {
-                    const int64_t col = min(l0 + min(k, G - 8), lddy - 8);
-                    u32x4 v = *reinterpret_cast<const u32x4*>(dY + (int64_t)min(b, B - 1) * lddy + col);
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        const bool ok = b < B && k + q < G && l0 + k + q < O;
-                        v[q >> 1] &= ok ? 0xFFFFFFFFu : ((q & 1) ? 0x0000FFFFu : 0xFFFF0000u);
-                    }
-                    r.b[nt][ks] = v;
-                }
-            }
-        }
-    };
+    for (int mt = 0; mt < MT; ++mt) {
+        const int b = min(bt * BT + wave * RPW + mt * 16 + col, B - 1);
+        yrow[mt] = dY + (int64_t)b * lddy;
+    }
+    const int kofs = kq_ok ? kq * 8 : 0;
+    const int dummy = max_dc(BT) * AS + tid * 4;
+    const int bofs = wave * RPW + kq * 4;  // batch column of this lane's first D row
 
-    // Multiply + scatter `ntiles` (<= MAXT) tiles of 16 positions.  Lanes
-    // without work in a pass read and write a private dummy word (two words,
-    // 16 apart, one per batch half), so the LDS accesses need no divergent
-    // branches; tile loops use wave-uniform branches only.
-    const int dummy = kMaxDc * kBT + part * 128 + lane;
-    const int colbase = lrow - d_lo * kBT;
-    auto compute = [&](const u32x4 (&a)[MAXT][KS], const int (&e)[MAXT][4],
-                       const u32x4 (&b)[NT][KS], int ntiles, int maxc) {
-        int addr[MAXT][4], col1[MAXT][4];
-        float o[MAXT][NT][4];
+    auto load = [&](R& x, int64_t g) {
+        const int* m = meta + (g * ndr + r) * kMetaStride;
+        x.tb = m[0];
+        x.tm = m[1];
+        x.te = m[2];
+        const int64_t c0 = g * G;
+        if (c0 + G <= O) {
 #pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t >= ntiles) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                addr[t][i] = (e[t][i] >> 8) * kBT + colbase;
-                col1[t][i] = e[t][i] & 0xFF;  // colour + 1; 0 = not a head
-                const int eff = col1[t][i] == 1 ? addr[t][i] : dummy;
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) o[t][nt][i] = acc[eff + nt * 16];
-            }
-        }
-        f32x4 c[MAXT][NT];
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t >= ntiles) continue;
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                c[t][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) c[t][nt] = mfma16x16x32<T>(a[t][ks], b[nt][ks], c[t][nt]);
-                // fold runs inside the lane's 4 positions into their heads
-#pragma unroll
-                for (int i = 3; i >= 1; --i)
-                    if (maxc > 0) c[t][nt][i - 1] += (col1[t][i] == 0 && e[t][i] >= 0) ? c[t][nt][i] : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t >= ntiles) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int eff = col1[t][i] == 1 ? addr[t][i] : dummy;
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) acc[eff + nt * 16] = o[t][nt][i] + c[t][nt][i];
-            }
-        }
-        for (int cc = 1; cc <= maxc; ++cc) {
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                if (t >= ntiles) continue;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int eff = col1[t][i] == cc + 1 ? addr[t][i] : dummy;
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) o[t][nt][i] = acc[eff + nt * 16];
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                if (t >= ntiles) continue;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int eff = col1[t][i] == cc + 1 ? addr[t][i] : dummy;
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) acc[eff + nt * 16] = o[t][nt][i] + c[t][nt][i];
-                }
-            }
-        }
-    };
-
-    // Tiles beyond MAXT (only for heavily duplicated index sets): loaded and
-    // processed MAXT at a time, without prefetch.
-    auto overflow = [&](int64_t g, const R& r) {
-        const int total = (r.pe - r.pb + 15) / 16;
-        const uint16_t* wg = wt + g * F * G;
-        const int32_t* sg = sorted + g * F;
-        for (int t0 = MAXT; t0 < total; t0 += MAXT) {
-            u32x4 a[MAXT][KS];
-            int e[MAXT][4];
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                const int pa = min(r.pb + (t0 + t) * 16 + lrow, F - 1);
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    const int k = G >= 32 ? ks * 32 + lq * 8 : (lq & 1) * 8;
-                    a[t][ks] = *reinterpret_cast<const u32x4*>(wg + pa * G + k);
+                    u32x4 v = *reinterpret_cast<const u32x4*>(yrow[mt] + c0 + ks * 32 + kofs);
+                    x.a[mt][ks] = kq_ok ? v : u32x4{0u, 0u, 0u, 0u};
                 }
+        } else {  // last group: labels >= O read as zero
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int p = r.pb + (t0 + t) * 16 + lq * 4 + i;
-                    const int v = sg[min(p, F - 1)];
-                    e[t][i] = p < r.pe ? v : -1;
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int64_t c = c0 + ks * 32 + kofs;
+                    uint32_t h[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) h[e] = (kq_ok && c + e < O) ? yrow[mt][c + e] : 0u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) x.a[mt][ks][q] = h[2 * q] | (h[2 * q + 1] << 16);
                 }
+        }
+        const int64_t tbase = g * Tcap + x.tb;
+        const int nt = x.te - x.tb;
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t >= nt) break;
+            const int64_t row = (tbase + t) * 16 + col;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 v = *reinterpret_cast<const u32x4*>(twt + row * G + ks * 32 + kofs);
+                x.b[t][ks] = kq_ok ? v : u32x4{0u, 0u, 0u, 0u};
             }
-            compute(a, e, r.b, min(MAXT, total - t0), r.maxc);
+            x.f[t] = tfeat[row];
         }
     };
 
-    auto process = [&](int64_t g, const R& r) {
-        const int total = (r.pe - r.pb + 15) / 16;
-        compute(r.a, r.e, r.b, min(MAXT, total), r.maxc);
-        if (total > MAXT) overflow(g, r);
+    auto addr = [&](int f, int mt) { return f >= 0 ? f * AS + bofs + mt * 16 : dummy; };
+
+    // read-add-write of tiles [t0, t1) of one layer (features distinct)
+    auto rmw = [&](const R& x, const f32x4 (&c)[MAXT][MT], int t0, int t1) {
+        f32x4 old[MAXT][MT];
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t < t0 || t >= t1) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                old[t][mt] = *reinterpret_cast<const f32x4*>(&acc[addr(x.f[t], mt)]);
+        }
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t < t0 || t >= t1) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                *reinterpret_cast<f32x4*>(&acc[addr(x.f[t], mt)]) = old[t][mt] + c[t][mt];
+        }
     };
 
-    // Three register sets: group g is computed while g+1 and g+2 are in flight.
-    if (g_begin < g_end) {
-        R r0, r1, r2;
-        load(g_begin, r0);
-        if (g_begin + 1 < g_end) load(g_begin + 1, r1);
-        int64_t g = g_begin;
-        while (true) {
-            if (g + 2 < g_end) load(g + 2, r2);
-            process(g, r0);
-            if (++g >= g_end) break;
-            if (g + 2 < g_end) load(g + 2, r0);
-            process(g, r1);
-            if (++g >= g_end) break;
-            if (g + 2 < g_end) load(g + 2, r1);
-            process(g, r2);
-            if (++g >= g_end) break;
+    auto compute = [&](const R& x, int64_t g) {
+        const int nt = x.te - x.tb;
+        const int nreg = min(nt, MAXT);
+        const int n0 = min(x.tm - x.tb, nreg);
+        f32x4 c[MAXT][MT];
+#pragma unroll
+        for (int t = 0; t < MAXT; ++t) {
+            if (t >= nreg) break;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(x.a[mt][ks], x.b[t][ks], v);
+                c[t][mt] = v;
+            }
+        }
+        rmw(x, c, 0, n0);
+        if (n0 < nreg) rmw(x, c, n0, nreg);
+        // tiles beyond the register set (ranges holding an unusual share of F)
+        for (int t = MAXT; t < nt; ++t) {
+            const int64_t row = (g * Tcap + x.tb + t) * 16 + col;
+            u32x4 bb[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 v = *reinterpret_cast<const u32x4*>(twt + row * G + ks * 32 + kofs);
+                bb[ks] = kq_ok ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+            const int f = tfeat[row];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(x.a[mt][ks], bb[ks], v);
+                f32x4* p = reinterpret_cast<f32x4*>(&acc[addr(f, mt)]);
+                *p = *p + v;
+            }
+        }
+    };
+
+    R rg[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+        if (g_lo + k < g_hi) load(rg[k], g_lo + k);
+    for (int64_t g = g_lo; g < g_hi; g += NS) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            if (g + k >= g_hi) break;
+            compute(rg[k], g + k);
+            if (g + k + NS < g_hi) load(rg[k], g + k + NS);
         }
     }
     __syncthreads();
 
-    // ---- write the partial: ws[s][d][bt*32 + b] ----
-    for (int i = tid; i < (d_hi - d_lo) * kBT; i += kMainThreads) {
-        const int d = i / kBT, b = i % kBT;
-        ws[((int64_t)s * D + d_lo + d) * Bp + b_base + b] = acc[i];
+    // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----
+    float* out = ws + ((int64_t)s * D + d_lo) * Bp + (int64_t)bt * BT;
+    for (int i = tid; i < dn * (BT / 4); i += kMainThreads) {
+        const int d = i / (BT / 4), b4 = (i % (BT / 4)) * 4;
+        *reinterpret_cast<f32x4*>(out + (int64_t)d * Bp + b4) =
+            *reinterpret_cast<const f32x4*>(&acc[d * AS + b4]);
     }
 }
 
@@ -447,36 +441,36 @@ __global__ __launch_bounds__(256) void bwdf_reduce_sr_kernel(const float* __rest
     }
 }
 
-template <typename T, int G, int FP>
-int launch_main(const int32_t* sorted, const int* meta, const uint16_t* wt, const uint16_t* dY,
-                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
-                int64_t O, hipStream_t st) {
+template <typename T, int G, int RPW, int FP>
+int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
+                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
+                hipStream_t st) {
     const int64_t nlog = p.S * p.ndr * p.nbt;
     const int64_t grid = 8 * ceil_div(nlog, 8);
-    bwdf_main_kernel<T, G, FP><<<dim3((unsigned)grid), dim3(kMainThreads), 0, st>>>(
-        sorted, meta, wt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, (int)F, O, p.Gc, (int)p.nbt,
-        (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S);
+    bwdf_main_kernel<T, G, RPW, FP><<<dim3((unsigned)grid), dim3(kMainThreads), 0, st>>>(
+        tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
+        (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
     return HASTE_OK;
 }
 
-template <typename T, int G>
-int dispatch_fp(const int32_t* sorted, const int* meta, const uint16_t* wt, const uint16_t* dY,
+template <typename T, int G, int RPW>
+int dispatch_fp(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                 int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
                 int64_t O, hipStream_t st) {
-#define HASTE_BWDF_ARGS sorted, meta, wt, dY, lddy, ws, p, B, D, F, O, st
-    if (F <= 32) return launch_main<T, G, 32>(HASTE_BWDF_ARGS);
-    if (F <= 64) return launch_main<T, G, 64>(HASTE_BWDF_ARGS);
-    if (F <= 128) return launch_main<T, G, 128>(HASTE_BWDF_ARGS);
-    return launch_main<T, G, 256>(HASTE_BWDF_ARGS);
+#define HASTE_BWDF_ARGS tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st
+    if (F <= 64) return launch_main<T, G, RPW, 64>(HASTE_BWDF_ARGS);
+    if (F <= 128) return launch_main<T, G, RPW, 128>(HASTE_BWDF_ARGS);
+    return launch_main<T, G, RPW, 256>(HASTE_BWDF_ARGS);
 #undef HASTE_BWDF_ARGS
 }
 
-template <int G>
-void launch_prep(const int32_t* idx, const uint16_t* W, int32_t* sorted, int* meta, uint16_t* wt,
-                 const BwdFPlan& p, int64_t D, int64_t F, int64_t O, hipStream_t st) {
-    bwdf_prep_kernel<G><<<dim3((unsigned)p.Gc), dim3(256), 0, st>>>(
-        idx, W, sorted, meta, wt, (int)F, (int)D, O, (int)p.ndr, (int)p.Dc);
+template <typename T, int G>
+int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
+             int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
+             int64_t O, hipStream_t st) {
+    if (p.BT == 64) return dispatch_fp<T, G, 16>(tfeat, meta, twt, dY, lddy, ws, p, B, D, F, O, st);
+    return dispatch_fp<T, G, 32>(tfeat, meta, twt, dY, lddy, ws, p, B, D, F, O, st);
 }
 
 // Runs prep + main; leaves the per-slice partials in the workspace.
@@ -492,26 +486,38 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     HASTE_CHECK_ARG(aligned16(W) && aligned16(dY) && aligned16(workspace),
                     "%s: W, dY and workspace must be 16-byte aligned", fn);
     const BwdFPlan p = make_plan(B, D, F, O, G);
+    if (p.ndr > kMaxRanges) {
+        set_error("%s: D = %lld is too large (at most %lld features)", fn, (long long)D,
+                  (long long)kMaxRanges * max_dc((int)p.BT));
+        return HASTE_ERR_UNSUPPORTED;
+    }
     if (workspace == nullptr || workspace_bytes < p.prep_bytes + p.ws_bytes) {
         set_error("%s: workspace too small (%lld bytes, need %lld)", fn,
                   (long long)workspace_bytes, (long long)(p.prep_bytes + p.ws_bytes));
         return HASTE_ERR_WORKSPACE;
     }
     char* base = static_cast<char*>(workspace);
-    int32_t* sorted = reinterpret_cast<int32_t*>(base + p.sorted_off);
+    int* tfeat = reinterpret_cast<int*>(base + p.tfeat_off);
     int* meta = reinterpret_cast<int*>(base + p.meta_off);
-    uint16_t* wt = reinterpret_cast<uint16_t*>(base + p.wt_off);
+    uint16_t* twt = reinterpret_cast<uint16_t*>(base + p.twt_off);
     float* ws = reinterpret_cast<float*>(base + p.prep_bytes);
     auto* w = static_cast<const uint16_t*>(W);
     auto* y = static_cast<const uint16_t*>(dY);
+    const dim3 pgrid((unsigned)p.Gc);
     switch (G) {
-#define HASTE_BWDF_G(GG)                                                                      \
-    case GG:                                                                                  \
-        launch_prep<GG>(idx, w, sorted, meta, wt, p, D, F, O, st);                            \
-        HASTE_CHECK_LAUNCH(fn);                                                               \
-        rc = dtype == HASTE_DTYPE_BF16                                                        \
-                 ? dispatch_fp<BF16, GG>(sorted, meta, wt, y, lddy, ws, p, B, D, F, O, st)    \
-                 : dispatch_fp<F16, GG>(sorted, meta, wt, y, lddy, ws, p, B, D, F, O, st);    \
+#define HASTE_BWDF_G(GG)                                                                        \
+    case GG:                                                                                    \
+        if (dtype == HASTE_DTYPE_BF16) {                                                        \
+            bwdf_prep_kernel<BF16, GG><<<pgrid, dim3(256), 0, st>>>(                            \
+                idx, w, tfeat, meta, twt, (int)F, (int)D, O, (int)p.ndr, (int)p.Dc, (int)p.Tcap); \
+            HASTE_CHECK_LAUNCH(fn);                                                             \
+            rc = run_main<BF16, GG>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);          \
+        } else {                                                                                \
+            bwdf_prep_kernel<F16, GG><<<pgrid, dim3(256), 0, st>>>(                             \
+                idx, w, tfeat, meta, twt, (int)F, (int)D, O, (int)p.ndr, (int)p.Dc, (int)p.Tcap); \
+            HASTE_CHECK_LAUNCH(fn);                                                             \
+            rc = run_main<F16, GG>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);           \
+        }                                                                                       \
         break;
         HASTE_BWDF_G(16)
         HASTE_BWDF_G(32)
