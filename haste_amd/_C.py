@@ -157,7 +157,7 @@ def ffi_backward_features_cuda(features: torch.Tensor, weights: torch.Tensor,
     out = torch.empty(H, B, dtype=torch.float32, device=weights.device)
     _lib.call("haste_ffi_bwd_features", locations.data_ptr(), W.data_ptr(), dY.data_ptr(), lddy,
               out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, FANIN, L, gsize,
-              dtype_code(weights.dtype), stream_of(weights))
+              dtype_code(weights.dtype), 0, stream_of(weights))
     return out
 
 

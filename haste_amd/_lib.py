@@ -45,10 +45,12 @@ SIGNATURES = {
     "haste_ffi_forward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                          _I64, _I32, _P]),
     "haste_ffi_bwd_features_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I32]),
+    "haste_ffi_bwd_features_plan": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                                   _I32, _P]),
     "haste_ffi_bwd_features": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64,
-                                              _I64, _I64, _I32, _P]),
+                                              _I64, _I64, _I32, _I32, _P]),
     "haste_ffi_bwd_features_sr": (ctypes.c_int, [_P, _P, _P, _I64, _P, _U64, _P, _I64, _I64, _I64,
-                                                 _I64, _I64, _I64, _I32, _P]),
+                                                 _I64, _I64, _I64, _I32, _I32, _P]),
     "haste_ffi_bwd_weights": (ctypes.c_int, [_P, _P, _I64, _P, _I64, _P, _I32, _P, _I32, _I64,
                                              _I64, _I64, _I64, _I64, _I32, _P]),
     "haste_sr_round_bf16": (ctypes.c_int, [_P, _P, _I64, _U64, _U64, _P]),

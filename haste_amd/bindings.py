@@ -82,12 +82,12 @@ class GroupFFIMulFunction(torch.autograd.Function):
                 grad_x = torch.empty(B, D, dtype=dtype, device=dev)
                 _lib.call("haste_ffi_bwd_features_sr", locs.data_ptr(), W.data_ptr(),
                           dY.data_ptr(), lddy, grad_x.data_ptr(), SR_SEED_GRAD_X, ws.data_ptr(),
-                          ws.numel(), B, D, F, O, gsize, code, stream)
+                          ws.numel(), B, D, F, O, gsize, code, 0, stream)
             else:
                 dxt = torch.empty(D, B, dtype=torch.float32, device=dev)
                 _lib.call("haste_ffi_bwd_features", locs.data_ptr(), W.data_ptr(), dY.data_ptr(),
                           lddy, dxt.data_ptr(), ws.data_ptr(), ws.numel(), B, D, F, O, gsize,
-                          code, stream)
+                          code, 0, stream)
                 grad_x = dxt.t().to(dtype).contiguous()
 
         grad_w = grad_b = None

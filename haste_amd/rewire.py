@@ -136,3 +136,7 @@ class GroupFixedFanIn(torch.nn.Module):
                   _lib.REGROW_UNUSED if self.regrow_mode == "unused" else _lib.REGROW_RANDOM,
                   _lib.INIT_RANDOM if self.init_mode == "random" else _lib.INIT_ZERO,
                   float(1.0 / math.sqrt(F)), int(seed), _C.stream_of(W))
+        # the kernel wrote through raw pointers: tell torch (and index-plan caches
+        # keyed on the version counter) that both tensors changed
+        torch.autograd.graph.increment_version(self.weights)
+        torch.autograd.graph.increment_version(self.group_locations)

@@ -42,6 +42,7 @@ class FFITrainStep:
         self.dbias = torch.empty(self.O, dtype=grad_dtype, device=dev) if bias is not None else None
         self.ws = _C.bwd_features_workspace(self.B, self.D, self.F, self.O, self.G,
                                             torch.bfloat16, dev)
+        self._plan_version = None  # idx._version the workspace plan was made for
         self.code = _lib.DTYPE_BF16
         self.gcode = _C.dtype_code(grad_dtype)
         ts = [(self.W, self.dW)] + ([(bias, self.dbias)] if bias is not None else [])
@@ -81,10 +82,13 @@ class FFITrainStep:
     def backward_features(self, dY: torch.Tensor, lddy: int) -> None:
         """dX [B, D] bf16 = SR(feature gradient, seed 123) (bindings.py:44-48)."""
         self._check_dY(dY, lddy)
+        # the index plan depends on idx only: rebuilt when idx changes (rewire)
+        ready = int(self._plan_version == self.idx._version)
         _lib.call("haste_ffi_bwd_features_sr", self.idx.data_ptr(), self.W.data_ptr(),
                   dY.data_ptr(), lddy, self.dX.data_ptr(), SR_SEED_GRAD_X, self.ws.data_ptr(),
-                  self.ws.numel(), self.B, self.D, self.F, self.O, self.G, self.code,
+                  self.ws.numel(), self.B, self.D, self.F, self.O, self.G, self.code, ready,
                   _C.stream_of(self.W))
+        self._plan_version = self.idx._version
 
     def backward_weights(self, dY: torch.Tensor, lddy: int) -> None:
         """dW [O, F] and dbias [O] in grad_dtype."""

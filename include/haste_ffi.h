@@ -66,15 +66,29 @@ int64_t haste_ffi_bwd_features_workspace_size(int64_t B, int64_t D, int64_t F, i
                                               int64_t G, int32_t dtype);
 
 /*
+ * Writes the index-dependent part of the bwd-features workspace (the "plan":
+ * per group, the distinct indices laid out in tiles per feature range).  It
+ * depends on idx and the sizes only, so a caller may compute it once and pass
+ * plan_ready = 1 to later haste_ffi_bwd_features[_sr] calls on the same
+ * workspace for as long as idx is unchanged (e.g. between two rewires).
+ * No counterpart in the reference (which has no index preprocessing).
+ */
+int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace, int64_t workspace_bytes,
+                                int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+                                int32_t dtype, void* stream);
+
+/*
  * Backward to features, deterministic (no float atomics on any global buffer):
  *   dXT[d, b] = sum_{g,j: idx[g,j] = d} sum_{l in g} W[l, j] * dY[b, l]     (fp32 [D, B])
+ * plan_ready = 0 computes the plan in this call; 1 reuses the plan already in
+ * the workspace (see haste_ffi_bwd_features_plan).
  * Replaces ffi_backward_features_cuda (shared_ffi/ffi_backward_features.cu:417-633,
  * bound at shared_ffi/ffi_wrapper.cpp:7-12,29).
  */
 int haste_ffi_bwd_features(const int32_t* idx, const void* W, const void* dY, int64_t lddy,
                            float* dXT, void* workspace, int64_t workspace_bytes, int64_t B,
                            int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype,
-                           void* stream);
+                           int32_t plan_ready, void* stream);
 
 /*
  * Backward to features fused with the bf16 stochastic rounding of
@@ -84,7 +98,7 @@ int haste_ffi_bwd_features(const int32_t* idx, const void* W, const void* dY, in
 int haste_ffi_bwd_features_sr(const int32_t* idx, const void* W, const void* dY, int64_t lddy,
                               uint16_t* dX, uint64_t seed, void* workspace,
                               int64_t workspace_bytes, int64_t B, int64_t D, int64_t F, int64_t O,
-                              int64_t G, int32_t dtype, void* stream);
+                              int64_t G, int32_t dtype, int32_t plan_ready, void* stream);
 
 /*
  * Backward to weights (+ optional bias gradient):

@@ -69,7 +69,7 @@ def test_bwd_features_workspace_size():
 def test_bwd_features_rejects_small_workspace():
     L = _lib.lib()
     rc = L.haste_ffi_bwd_features(16, 32, 48, 4096, 64, 256, 16, 64, 768, 32, 4096, 32,
-                                  _lib.DTYPE_BF16, None)
+                                  _lib.DTYPE_BF16, 0, None)
     assert rc == _lib.HASTE_ERR_WORKSPACE
     assert "workspace too small" in _lib.last_error()
 

@@ -175,3 +175,32 @@ def test_train_step_matches_api(dev):
     ref_w, _ = oracle.sgd_sr_step(w0, dw_np, None, 0.05, 1e-4, 0.0, False, True, 42)
     assert np.array_equal(bits(layer.weights), ref_w.reshape(O, F))
     assert st.seed == 43
+
+
+def test_train_step_replans_after_rewire(dev):
+    """FFITrainStep reuses its index plan across steps and rebuilds it when
+    rewire() changes group_locations."""
+    torch.manual_seed(8)
+    B, D, O, G, F = 96, 768, 5000, 64, 64
+    layer = GroupFixedFanIn(D, O, F, group_size=G, prune_mode="fraction", rewire_fraction=0.25,
+                            dtype=torch.bfloat16).to(dev)
+    x = torch.randn(B, D, device=dev).to(torch.bfloat16)
+    st = FFITrainStep(layer.weights.data, layer.bias.data, layer.group_locations, B, D, G, 0.05,
+                      1e-4, seed=1)
+    dY = torch.zeros(B, st.ldo, dtype=torch.bfloat16, device=dev)
+    dY[:, :O] = (torch.randn(B, O, device=dev) * 0.1).to(torch.bfloat16)
+
+    def check():
+        st.backward_features(dY, st.ldo)
+        torch.cuda.synchronize()
+        ref = oracle.ffi_backward_features(layer.group_locations.cpu(), layer.weights.detach().cpu(),
+                                           dY[:, :O].cpu(), G, D)
+        # bf16 SR of the fp32 gradient: within one bf16 ulp of the oracle's values
+        torch.testing.assert_close(st.dX.float().cpu(), ref.t(), rtol=2e-2, atol=2e-3)
+
+    check()
+    check()  # plan reused
+    v0 = layer.group_locations._version
+    layer.rewire(seed=3)
+    assert layer.group_locations._version != v0
+    check()  # plan rebuilt for the new indices

@@ -100,7 +100,7 @@ def test_backward_features_sr_fused(dev, oracle_mod, B, D, O, G, F, mode):
     dX = torch.empty(B, D, dtype=torch.bfloat16, device=dev)
     _lib.call("haste_ffi_bwd_features_sr", idxd.data_ptr(), Wd.data_ptr(), dYd.data_ptr(),
               lddy, dX.data_ptr(), 123, ws.data_ptr(), ws.numel(), B, D, F, O, G,
-              _lib.DTYPE_BF16, _C.stream_of(Wd))
+              _lib.DTYPE_BF16, 0, _C.stream_of(Wd))
     torch.cuda.synchronize()
     exp = oracle_mod.sr_round_bf16(dXT.t().contiguous().cpu().numpy(), seed=123)
     got = dX.cpu().view(torch.int16).numpy().view(np.uint16)
