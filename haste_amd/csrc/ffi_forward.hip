@@ -2,12 +2,15 @@
 //
 //   out[b, l] = RNE( sum_j xT[idx[g, j], b] * W[l, j] + bias[l] ),  g = l / G
 //
-// One workgroup = one label group g x a chunk of the batch.  Per batch tile of
-// 64 columns, the gathered rows xT[idx[g, :], b0:b0+64] are loaded with 16-byte
-// loads (xT is tiny and L2 resident), transposed in registers and stored to LDS
-// as Xs[b][j] so each MFMA B-fragment is one 16-byte LDS read.  W fragments
-// (MFMA A operand: label rows x 8 contiguous fan-in slots) are loaded straight
-// from HBM into VGPRs once per workgroup and reused over the whole batch chunk.
+// One workgroup = one label group g x a chunk of the batch, in tiles of 64
+// batch columns.  MFMA orientation: M = labels, N = batch, K = fan-in slots.
+//  - A: W fragments (label rows x 8 contiguous slots) loaded once per
+//    workgroup from HBM into VGPRs and reused over the whole batch chunk.
+//  - B: the gathered rows xT[idx[g, j], b0:b0+64] are copied row-major into LDS
+//    (16-byte copies, Xg[slot][batch]; xT is small and L2 resident) and read
+//    back with ds_read_b64_tr_b16, which hands each lane 4 consecutive slots of
+//    one batch column.  The next tile's rows are fetched into registers while
+//    the current tile's MFMAs run (two LDS buffers).
 // bf16/f16 MFMA 16x16x32 with fp32 accumulation; bias is added in fp32 and the
 // result rounded to nearest even (as dump_and_store_tile,
 // shared_ffi/ffi_forward_kernels.cu:85-101).
@@ -18,32 +21,41 @@
 namespace haste {
 namespace {
 
-constexpr int kBT = 64;       // batch columns per tile
-constexpr int kThreads = 256; // 4 waves
+constexpr int kBT = 64;        // batch columns per tile
+constexpr int kThreads = 256;  // 4 waves
 
 template <typename T, int G, int FP>
 struct FwdCfg {
-    static constexpr int KS = FP / 32;            // MFMA k-steps
-    static constexpr int MTILES = G / 16;         // label tiles in the group
+    static constexpr int KS = FP / 32;                  // MFMA k-steps
+    static constexpr int MTILES = G / 16;               // label tiles in the group
     static constexpr int WM = MTILES < 4 ? MTILES : 4;  // waves along labels
-    static constexpr int WN = 4 / WM;             // waves along batch
-    static constexpr int MT = MTILES / WM;        // label tiles per wave
-    static constexpr int NT = (kBT / 16) / WN;    // batch tiles per wave
-    static constexpr int LDX = FP + 8;            // LDS row pitch (elements), +16 B vs bank conflicts
-    static constexpr int ITEMS = (FP / 4) * (kBT / 8);  // gather items per batch tile
+    static constexpr int WN = 4 / WM;                   // waves along batch
+    static constexpr int MT = MTILES / WM;              // label tiles per wave
+    static constexpr int NT = (kBT / 16) / WN;          // batch tiles per wave
+    static constexpr int RB = kBT * 2 + 16;             // LDS bytes per gathered row
+    static constexpr int PIECES = FP * (kBT / 8);       // 16-byte pieces per tile
+    static constexpr int PPT = PIECES / kThreads;       // >= 1 (FP >= 32)
 };
 
-__device__ __forceinline__ uint32_t half_of(const u32x4& v, int e) {
-    return (e & 1) ? (v[e >> 1] >> 16) : (v[e >> 1] & 0xFFFFu);
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of
+// the 8-byte rows addressed by lanes 4k + i/4 (k = 0..3) as its element k.
+__device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
+    typedef fp16x4_t __attribute__((address_space(3))) * lds_p;
+    const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (lds_p)(__attribute__((address_space(3))) char*)(p));
+    return __builtin_bit_cast(u32x2, v);
 }
 
 template <typename T, int G, int FP>
-__global__ __launch_bounds__(kThreads) void ffi_fwd_kernel(
+__global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
     int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk) {
     using C = FwdCfg<T, G, FP>;
-    __shared__ __attribute__((aligned(16))) uint16_t Xs[kBT * C::LDX];
+    constexpr int KS = C::KS, MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT;
+    __shared__ __attribute__((aligned(16))) char Xg[2][FP * RB];
     __shared__ int32_t sidx[FP];
 
     const int64_t work = xcd_remap(blockIdx.x, Gc * nchunks);
@@ -52,94 +64,108 @@ __global__ __launch_bounds__(kThreads) void ffi_fwd_kernel(
     const int chunk = (int)(work % nchunks);
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave % C::WM;
-    const int wn = wave / C::WM;
-    const int lrow = lane & 15;  // row of A / column of B / column of D
-    const int lq = lane >> 4;    // quad: K-chunk of A/B, row-quad of D
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % C::WM, wn = wave / C::WM;
+    const int col = lane & 15;  // row of A / column of B / column of D
+    const int kq = lane >> 4;   // K-chunk of A/B, row-quad of D
 
-    // Indices outside [0, D) are clamped (the reference leaves them undefined).
+    // Indices outside [0, D) are clamped (the reference leaves them undefined);
+    // slots >= F gather row 0 (their W columns are zero).
     for (int j = tid; j < FP; j += kThreads)
         sidx[j] = j < F ? min(max(idx[g * F + j], 0), D - 1) : 0;
 
     // W fragments (A operand) and bias for this wave's label tiles.
-    u32x4 wf[C::MT][C::KS];
-    float bv[C::MT][4];
+    u32x4 wf[MT][KS];
+    float bv[MT][4];
 #pragma unroll
-    for (int mt = 0; mt < C::MT; ++mt) {
-        const int64_t l = g * G + (int64_t)(wm * C::MT + mt) * 16 + lrow;
+    for (int mt = 0; mt < MT; ++mt) {
+        const int64_t l = g * G + (int64_t)(wm * MT + mt) * 16 + col;
 #pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
-            const int k = ks * 32 + lq * 8;
+        for (int ks = 0; ks < KS; ++ks) {
+            const int k = ks * 32 + kq * 8;
             if (l < O && k < F)
                 wf[mt][ks] = *reinterpret_cast<const u32x4*>(W + l * F + k);
             else
                 wf[mt][ks] = u32x4{0u, 0u, 0u, 0u};
         }
-        const int64_t lb = g * G + (int64_t)(wm * C::MT + mt) * 16 + lq * 4;
+        const int64_t lb = g * G + (int64_t)(wm * MT + mt) * 16 + kq * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             bv[mt][i] = (bias != nullptr && lb + i < O) ? bits_to_f32<T>(bias[lb + i]) : 0.0f;
     }
     __syncthreads();
 
-    const int b_chunk0 = chunk * tiles_per_chunk * kBT;
-    for (int t = 0; t < tiles_per_chunk; ++t) {
-        const int b_base = b_chunk0 + t * kBT;
-        if (b_base >= B) break;
-
-        // ---- gather xT[idx[j], b_base + 0..63] into Xs[b][j] ----
-        for (int it = tid; it < C::ITEMS; it += kThreads) {
-            const int jq = it % (FP / 4);
-            const int bo = it / (FP / 4);
-            const int j0 = jq * 4;
-            const int b0 = b_base + bo * 8;
-            u32x4 v[4];
+    // piece p of a tile: slot p / 8, batch columns 8 * (p % 8) .. +7
+    // (columns >= B read as zero)
+    auto fetch = [&](int b_base, u32x4 (&v)[PPT]) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (j0 + q < F && b0 < B)
-                    v[q] = *reinterpret_cast<const u32x4*>(xT + (int64_t)sidx[j0 + q] * ldx + b0);
-                else
-                    v[q] = u32x4{0u, 0u, 0u, 0u};
-            }
+        for (int q = 0; q < PPT; ++q) {
+            const int p = tid + q * kThreads;
+            const int j = p / (kBT / 8), b0 = b_base + (p % (kBT / 8)) * 8;
+            v[q] = u32x4{0u, 0u, 0u, 0u};
+            if (b0 < B) {
+                v[q] = *reinterpret_cast<const u32x4*>(xT + (int64_t)sidx[j] * ldx + b0);
+                if (b0 + 8 > B) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                uint32_t lo = half_of(v[0], e) | (half_of(v[1], e) << 16);
-                uint32_t hi = half_of(v[2], e) | (half_of(v[3], e) << 16);
-                if (b0 + e >= B) { lo = 0u; hi = 0u; }
-                *reinterpret_cast<u32x2*>(&Xs[(bo * 8 + e) * C::LDX + j0]) = u32x2{lo, hi};
+                    for (int e = 0; e < 8; ++e)
+                        if (b0 + e >= B) v[q][e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                }
             }
         }
-        __syncthreads();
+    };
+    auto stash = [&](int buf, const u32x4 (&v)[PPT]) {
+#pragma unroll
+        for (int q = 0; q < PPT; ++q) {
+            const int p = tid + q * kThreads;
+            *reinterpret_cast<u32x4*>(&Xg[buf][(p / (kBT / 8)) * RB + (p % (kBT / 8)) * 16]) = v[q];
+        }
+    };
 
-        // ---- MFMA: D[label][batch] = W_tile x Xg^T ----
-        f32x4 acc[C::MT][C::NT];
+    const int b_chunk0 = chunk * tiles_per_chunk * kBT;
+    const int ntiles = min(tiles_per_chunk, (B - b_chunk0 + kBT - 1) / kBT);
+    u32x4 xv[PPT];
+    fetch(b_chunk0, xv);
+    stash(0, xv);
+    if (ntiles > 1) fetch(b_chunk0 + kBT, xv);
+    __syncthreads();
+
+    // lane's tr-read address: slot 8*kq + col/4 (+4 for the second half), batch
+    // columns n0 + 4*(col%4)
+    const int tr_off = (kq * 8 + col / 4) * RB + (col % 4) * 8;
+    for (int t = 0; t < ntiles; ++t) {
+        const int b_base = b_chunk0 + t * kBT;
+        const char* xs = Xg[t & 1];
+        f32x4 acc[MT][NT];
 #pragma unroll
-        for (int mt = 0; mt < C::MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int nt = 0; nt < C::NT; ++nt) {
-            const int n0 = (wn * C::NT + nt) * 16;
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n0 = (wn * NT + nt) * 16;
 #pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
-                const u32x4 bfrag =
-                    *reinterpret_cast<const u32x4*>(&Xs[(n0 + lrow) * C::LDX + ks * 32 + lq * 8]);
+            for (int ks = 0; ks < KS; ++ks) {
+                const char* p = xs + tr_off + ks * 32 * RB + n0 * 2;
+                const u32x2 lo = lds_read_tr16(p);
+                const u32x2 hi = lds_read_tr16(p + 4 * RB);
+                const u32x4 bf = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt)
-                    acc[mt][nt] = mfma16x16x32<T>(wf[mt][ks], bfrag, acc[mt][nt]);
+                for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16x16x32<T>(wf[mt][ks], bf, acc[mt][nt]);
             }
+        }
+        if (t + 1 < ntiles) {
+            stash((t + 1) & 1, xv);
+            if (t + 2 < ntiles) fetch(b_base + 2 * kBT, xv);
         }
 
         // ---- epilogue: + bias (fp32), RNE, store 4 consecutive labels per lane ----
 #pragma unroll
-        for (int nt = 0; nt < C::NT; ++nt) {
-            const int b = b_base + (wn * C::NT + nt) * 16 + lrow;
+        for (int nt = 0; nt < NT; ++nt) {
+            const int b = b_base + (wn * NT + nt) * 16 + col;
             if (b >= B) continue;
 #pragma unroll
-            for (int mt = 0; mt < C::MT; ++mt) {
-                const int64_t l = g * G + (int64_t)(wm * C::MT + mt) * 16 + lq * 4;
+            for (int mt = 0; mt < MT; ++mt) {
+                const int64_t l = g * G + (int64_t)(wm * MT + mt) * 16 + kq * 4;
                 uint32_t h[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) h[i] = f32_to_bits<T>(acc[mt][nt][i] + bv[mt][i]);
