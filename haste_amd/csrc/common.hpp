@@ -87,12 +87,27 @@ __device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
+// Two floats -> two packed 16-bit values (low half = a), round to nearest even
+// by the hardware conversion (v_cvt_pk_bf16_f32 / v_cvt_f16_f32); NaN stays NaN.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ uint32_t pack2_rne(float a, float b);
+
 template <typename T>
 __device__ __forceinline__ uint32_t f32_to_bits(float f);
 template <>
 __device__ __forceinline__ uint32_t f32_to_bits<BF16>(float f) { return f32_to_bf16_rne(f); }
 template <>
 __device__ __forceinline__ uint32_t f32_to_bits<F16>(float f) { return f32_to_f16_rne(f); }
+template <>
+__device__ __forceinline__ uint32_t pack2_rne<BF16>(float a, float b) {
+    return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});
+}
+template <>
+__device__ __forceinline__ uint32_t pack2_rne<F16>(float a, float b) {
+    return __builtin_bit_cast(uint32_t, f16x2_t{(_Float16)a, (_Float16)b});
+}
 
 // ---------------------------------------------------------------- MFMA ------
 // D(16x16 f32) += A(16x32) * B(32x16); lane L supplies A row L%16 and B column
@@ -140,6 +155,55 @@ __device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t r) {
     uint32_t u = __float_as_uint(x);
     if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
     return (u + (r & 0xFFFFu)) >> 16;
+}
+
+// ------------------------------------------------------- buffer access ------
+// Raw buffer resources (stride 0): the hardware range-checks every access
+// against num_records, returning 0 for loads and dropping stores that fall
+// outside.  Kernels use this instead of branches around memory operations, so
+// every path issues the same number of vector-memory instructions and the
+// compiler can wait for exactly the loads it needs (a branch around a store
+// makes it wait for all outstanding stores instead).  An offset of kOOB is
+// outside every resource built here (num_records is kept below 2^31).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int64_t kMaxRsrcBytes = 0x7FFFFF00;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    const int64_t n = bytes < 0 ? 0 : (bytes > kMaxRsrcBytes ? kMaxRsrcBytes : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n,
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x2 buf_load8(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store16(u32x4 v, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store8(u32x2 v, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store4(uint32_t v, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store2(uint16_t v, rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of
+// the 8-byte rows addressed by lanes 4k + i/4 (k = 0..3) as its element k.
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+__device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
+    typedef fp16x4_t __attribute__((address_space(3))) * lds_p;
+    const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+        (lds_p)(__attribute__((address_space(3))) char*)(p));
+    return __builtin_bit_cast(u32x2, v);
 }
 
 // Workgroup-id remap so that consecutive logical ids land on the same XCD

@@ -2,15 +2,25 @@
 //
 //   out[b, l] = RNE( sum_j xT[idx[g, j], b] * W[l, j] + bias[l] ),  g = l / G
 //
-// One workgroup = one label group g x a chunk of the batch, in tiles of 64
-// batch columns.  MFMA orientation: M = labels, N = batch, K = fan-in slots.
+// One workgroup = one label group g x a chunk of the batch (the whole batch
+// up to 512 columns), walked in tiles of 64 batch columns.  MFMA orientation:
+// M = labels, N = batch, K = fan-in slots.
 //  - A: W fragments (label rows x 8 contiguous slots) loaded once per
-//    workgroup from HBM into VGPRs and reused over the whole batch chunk.
+//    workgroup into VGPRs and reused over the whole batch chunk.  A wave holds
+//    the fragments of MT label tiles (all G labels when they fit in 64
+//    registers), so the waves split the batch columns of a tile.
 //  - B: the gathered rows xT[idx[g, j], b0:b0+64] are copied row-major into LDS
 //    (16-byte copies, Xg[slot][batch]; xT is small and L2 resident) and read
 //    back with ds_read_b64_tr_b16, which hands each lane 4 consecutive slots of
-//    one batch column.  The next tile's rows are fetched into registers while
-//    the current tile's MFMAs run (two LDS buffers).
+//    one batch column.  Tile t+2's rows are fetched into registers while tile
+//    t's MFMAs run (two LDS buffers).
+//  - Epilogue: results are staged per wave in LDS and stored as whole 128-byte
+//    row segments (a lane's MFMA output covers only 8 bytes of a row; 8-byte
+//    stores spread over 16 rows cost four times the L2 write requests).
+//  - Every load and store of the tile loop is a raw buffer access: rows past B,
+//    labels past O and slots past F are range-checked by the hardware instead
+//    of branched around, so the loop issues a fixed number of memory
+//    instructions and each wait covers only the loads it needs.
 // bf16/f16 MFMA 16x16x32 with fp32 accumulation; bias is added in fp32 and the
 // result rounded to nearest even (as dump_and_store_tile,
 // shared_ffi/ffi_forward_kernels.cu:85-101).
@@ -23,109 +33,108 @@ namespace {
 
 constexpr int kBT = 64;        // batch columns per tile
 constexpr int kThreads = 256;  // 4 waves
+constexpr int kMaxTilesPerWG = 8;
 
-template <typename T, int G, int FP>
+template <int G, int FP>
 struct FwdCfg {
-    static constexpr int KS = FP / 32;                  // MFMA k-steps
-    static constexpr int MTILES = G / 16;               // label tiles in the group
-    static constexpr int WM = MTILES < 4 ? MTILES : 4;  // waves along labels
-    static constexpr int WN = 4 / WM;                   // waves along batch
-    static constexpr int MT = MTILES / WM;              // label tiles per wave
-    static constexpr int NT = (kBT / 16) / WN;          // batch tiles per wave
-    static constexpr int RB = kBT * 2 + 16;             // LDS bytes per gathered row
-    static constexpr int PIECES = FP * (kBT / 8);       // 16-byte pieces per tile
-    static constexpr int PPT = PIECES / kThreads;       // >= 1 (FP >= 32)
+    static constexpr int KS = FP / 32;     // MFMA k-steps
+    static constexpr int MTILES = G / 16;  // label tiles in the group
+    // waves along labels: a wave keeps MT*KS W fragments (<= 16, 64 VGPRs)
+    static constexpr int WM = MTILES * KS <= 16 ? 1 : (MTILES * KS <= 32 ? 2 : 4);
+    static constexpr int WN = 4 / WM;             // waves along the batch
+    static constexpr int MT = MTILES / WM;        // label tiles per wave
+    static constexpr int NT = (kBT / 16) / WN;    // 16-column batch tiles per wave
+    static constexpr int RB = kBT * 2 + 16;       // LDS bytes per gathered row
+    static constexpr int PIECES = FP * (kBT / 8); // 16-byte pieces per tile
+    static constexpr int PPT = PIECES / kThreads; // >= 1 (FP >= 32)
+    static constexpr int SRB = MT * 32 + 16;      // LDS bytes per staged output row
+    static constexpr int STG = NT * 16 * SRB;     // staged output bytes per wave
+    static_assert(MTILES % WM == 0 && PPT >= 1, "tile shape");
 };
 
-typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of
-// the 8-byte rows addressed by lanes 4k + i/4 (k = 0..3) as its element k.
-__device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
-    typedef fp16x4_t __attribute__((address_space(3))) * lds_p;
-    const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-        (lds_p)(__attribute__((address_space(3))) char*)(p));
-    return __builtin_bit_cast(u32x2, v);
-}
-
-template <typename T, int G, int FP>
-__global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
-    const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
-    const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
-    int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk) {
-    using C = FwdCfg<T, G, FP>;
-    constexpr int KS = C::KS, MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT;
-    __shared__ __attribute__((aligned(16))) char Xg[2][FP * RB];
-    __shared__ int32_t sidx[FP];
-
-    const int64_t work = xcd_remap(blockIdx.x, Gc * nchunks);
-    if (work < 0) return;
-    const int64_t g = work / nchunks;
-    const int chunk = (int)(work % nchunks);
-
+// LAST: the workgroup's group is the last one and holds fewer than G labels;
+// its stores are per element so that no column >= O is written.
+template <typename T, int G, int FP, bool LAST>
+__device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
+                                          const uint16_t* __restrict__ xT, int64_t ldx,
+                                          const uint16_t* __restrict__ W,
+                                          const uint16_t* __restrict__ bias,
+                                          uint16_t* __restrict__ out, int64_t ldo, int B, int D,
+                                          int F, int64_t O, int64_t g, int b_chunk0, int ntiles,
+                                          char (*Xg)[FP * FwdCfg<G, FP>::RB], int32_t* sidx,
+                                          char (*stg)[FwdCfg<G, FP>::STG]) {
+    using C = FwdCfg<G, FP>;
+    constexpr int KS = C::KS, MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SRB = C::SRB;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave % C::WM, wn = wave / C::WM;
     const int col = lane & 15;  // row of A / column of B / column of D
     const int kq = lane >> 4;   // K-chunk of A/B, row-quad of D
+    const int64_t l0 = g * G;
+    const int nl = (int)std::min<int64_t>(G, O - l0);  // labels of this group
 
     // Indices outside [0, D) are clamped (the reference leaves them undefined);
-    // slots >= F gather row 0 (their W columns are zero).
+    // slots >= F gather row 0 (their W columns read as zero).
     for (int j = tid; j < FP; j += kThreads)
         sidx[j] = j < F ? min(max(idx[g * F + j], 0), D - 1) : 0;
 
-    // W fragments (A operand) and bias for this wave's label tiles.
+    // W fragments (A operand) and bias of this wave's label tiles; rows >= O and
+    // slots >= F are outside the resources and read as zero.
+    const rsrc_t wr = make_rsrc(W + l0 * F, (int64_t)nl * F * 2);
+    const rsrc_t br = bias != nullptr ? make_rsrc(bias + l0, (int64_t)nl * 2) : make_rsrc(W, 0);
     u32x4 wf[MT][KS];
     float bv[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const int64_t l = g * G + (int64_t)(wm * MT + mt) * 16 + col;
+        const int lr = (wm * MT + mt) * 16 + col;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const int k = ks * 32 + kq * 8;
-            if (l < O && k < F)
-                wf[mt][ks] = *reinterpret_cast<const u32x4*>(W + l * F + k);
-            else
-                wf[mt][ks] = u32x4{0u, 0u, 0u, 0u};
+            wf[mt][ks] = buf_load16(wr, k < F ? (uint32_t)(lr * F + k) * 2 : kOOB);
         }
-        const int64_t lb = g * G + (int64_t)(wm * MT + mt) * 16 + kq * 4;
+        const int lb = (wm * MT + mt) * 16 + kq * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            bv[mt][i] = (bias != nullptr && lb + i < O) ? bits_to_f32<T>(bias[lb + i]) : 0.0f;
+            bv[mt][i] = bits_to_f32<T>(__builtin_amdgcn_raw_buffer_load_b16(br, (lb + i) * 2, 0, 0));
     }
     __syncthreads();
 
-    // piece p of a tile: slot p / 8, batch columns 8 * (p % 8) .. +7
-    // (columns >= B read as zero)
+    // piece p of a tile: slot p / 8, batch columns 8 * (p % 8) .. +7; chunks
+    // starting at or past B read as zero, columns >= B of a partial chunk are
+    // masked when stashed
+    const rsrc_t xr = make_rsrc(xT, (int64_t)D * ldx * 2);
+    int pj[PPT], pc[PPT];
+#pragma unroll
+    for (int q = 0; q < PPT; ++q) {
+        const int p = tid + q * kThreads;
+        pj[q] = p / (kBT / 8);
+        pc[q] = (p % (kBT / 8)) * 8;
+    }
+    int64_t prow[PPT];
+#pragma unroll
+    for (int q = 0; q < PPT; ++q) prow[q] = (int64_t)sidx[pj[q]] * ldx;
     auto fetch = [&](int b_base, u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
-            const int p = tid + q * kThreads;
-            const int j = p / (kBT / 8), b0 = b_base + (p % (kBT / 8)) * 8;
-            v[q] = u32x4{0u, 0u, 0u, 0u};
-            if (b0 < B) {
-                v[q] = *reinterpret_cast<const u32x4*>(xT + (int64_t)sidx[j] * ldx + b0);
-                if (b0 + 8 > B) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (b0 + e >= B) v[q][e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                }
-            }
+            const int b0 = b_base + pc[q];
+            v[q] = buf_load16(xr, b0 < B ? (uint32_t)(prow[q] + b0) * 2 : kOOB);
         }
     };
-    auto stash = [&](int buf, const u32x4 (&v)[PPT]) {
+    auto stash = [&](int buf, int b_base, const u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
-            const int p = tid + q * kThreads;
-            *reinterpret_cast<u32x4*>(&Xg[buf][(p / (kBT / 8)) * RB + (p % (kBT / 8)) * 16]) = v[q];
+            const int nv = B - (b_base + pc[q]);  // valid columns in this chunk
+            u32x4 m = v[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                m[e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
+            *reinterpret_cast<u32x4*>(&Xg[buf][pj[q] * RB + pc[q] * 2]) = m;
         }
     };
 
-    const int b_chunk0 = chunk * tiles_per_chunk * kBT;
-    const int ntiles = min(tiles_per_chunk, (B - b_chunk0 + kBT - 1) / kBT);
     u32x4 xv[PPT];
     fetch(b_chunk0, xv);
-    stash(0, xv);
+    stash(0, b_chunk0, xv);
     if (ntiles > 1) fetch(b_chunk0 + kBT, xv);
     __syncthreads();
 
@@ -137,12 +146,10 @@ __global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
         const char* xs = Xg[t & 1];
         f32x4 acc[MT][NT];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int n0 = (wn * NT + nt) * 16;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const char* p = xs + tr_off + ks * 32 * RB + n0 * 2;
@@ -154,33 +161,76 @@ __global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
             }
         }
         if (t + 1 < ntiles) {
-            stash((t + 1) & 1, xv);
+            stash((t + 1) & 1, b_base + kBT, xv);
             if (t + 2 < ntiles) fetch(b_base + 2 * kBT, xv);
         }
 
-        // ---- epilogue: + bias (fp32), RNE, store 4 consecutive labels per lane ----
+        // ---- epilogue: + bias (fp32), RNE.  A lane holds 4 consecutive labels of
+        // one batch row; they are staged in LDS and written as row segments.
+        // Rows >= B fall outside the tile's resource.  The last (partial) group
+        // stores per element instead, so no column >= O is written. ----
+        const rsrc_t orr = make_rsrc(out + (int64_t)b_base * ldo + l0,
+                                     (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            const int b = b_base + (wn * NT + nt) * 16 + col;
-            if (b >= B) continue;
+            const int rb = (wn * NT + nt) * 16 + col;  // row within the tile
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const int64_t l = g * G + (int64_t)(wm * MT + mt) * 16 + kq * 4;
-                uint32_t h[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) h[i] = f32_to_bits<T>(acc[mt][nt][i] + bv[mt][i]);
-                uint16_t* dst = out + (int64_t)b * ldo + l;
-                if (l + 3 < O) {
-                    *reinterpret_cast<u32x2*>(dst) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+                const int ll = (wm * MT + mt) * 16 + kq * 4;  // label within the group
+                const f32x4 v = acc[mt][nt];
+                const u32x2 h = u32x2{pack2_rne<T>(v[0] + bv[mt][0], v[1] + bv[mt][1]),
+                                      pack2_rne<T>(v[2] + bv[mt][2], v[3] + bv[mt][3])};
+                const uint32_t off = (uint32_t)((int64_t)rb * ldo + ll) * 2;
+                if constexpr (!LAST) {
+                    *reinterpret_cast<u32x2*>(&stg[wave][(nt * 16 + col) * SRB + (mt * 16 + kq * 4) * 2]) = h;
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        if (l + i < O) dst[i] = (uint16_t)h[i];
+                        buf_store2((uint16_t)(h[i >> 1] >> ((i & 1) * 16)), orr,
+                                   ll + i < nl ? off + 2 * i : kOOB);
                 }
+            }
+        }
+        // staged rows go out as 16-byte stores, whole row segments per
+        // instruction (full 128-byte lines at MT = 4); the wave reads back only
+        // what it wrote, and a wave's LDS accesses complete in order
+        if constexpr (!LAST) {
+            constexpr int LPR = MT * 2;     // lanes per staged row (MT*32 bytes)
+            constexpr int RPI = 64 / LPR;   // rows per instruction
+#pragma unroll
+            for (int r0 = 0; r0 < NT * 16; r0 += RPI) {
+                const int rr = r0 + lane / LPR, cb = (lane % LPR) * 16;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(&stg[wave][rr * SRB + cb]);
+                const int rb = wn * NT * 16 + rr;
+                buf_store16(v, orr, (uint32_t)((int64_t)rb * ldo * 2 + (wm * MT * 16) * 2 + cb));
             }
         }
         __syncthreads();
     }
+}
+
+template <typename T, int G, int FP>
+__global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
+    const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
+    int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk) {
+    using C = FwdCfg<G, FP>;
+    __shared__ __attribute__((aligned(16))) char Xg[2][FP * C::RB];
+    __shared__ int32_t sidx[FP];
+    __shared__ __attribute__((aligned(16))) char stg[4][C::STG];
+
+    const int64_t work = xcd_remap(blockIdx.x, Gc * nchunks);
+    if (work < 0) return;
+    const int64_t g = work / nchunks;
+    const int chunk = (int)(work % nchunks);
+    const int b_chunk0 = chunk * tiles_per_chunk * kBT;
+    const int ntiles = min(tiles_per_chunk, (B - b_chunk0 + kBT - 1) / kBT);
+    if ((g + 1) * G > O)
+        fwd_group<T, G, FP, true>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
+                                  ntiles, Xg, sidx, stg);
+    else
+        fwd_group<T, G, FP, false>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
+                                   ntiles, Xg, sidx, stg);
 }
 
 template <typename T, int G, int FP>
@@ -189,12 +239,18 @@ int launch_fwd(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16
                int64_t O, hipStream_t st) {
     const int64_t Gc = ceil_div(O, G);
     const int64_t ntiles = ceil_div(B, kBT);
-    int64_t tpc = std::max<int64_t>(1, std::min<int64_t>(ntiles, (Gc * ntiles) / 8192));
-    const int64_t nchunks = ceil_div(ntiles, tpc);
+    // whole batch per workgroup (up to kMaxTilesPerWG tiles); split further only
+    // when there are too few groups to fill the GPU
+    int64_t nchunks = ceil_div(ntiles, kMaxTilesPerWG);
+    while (Gc * nchunks < 2048 && nchunks < ntiles) ++nchunks;
+    const int64_t tpc = ceil_div(ntiles, nchunks);
+    nchunks = ceil_div(ntiles, tpc);
     const int64_t nlogical = Gc * nchunks;
     const int64_t grid = 8 * ceil_div(nlogical, 8);
-    if (grid > 0x7FFFFFFF) {
-        set_error("haste_ffi_forward: problem too large (grid %lld)", (long long)grid);
+    if (grid > 0x7FFFFFFF || (int64_t)kBT * ldo * 2 > kMaxRsrcBytes ||
+        D * ldx * 2 > kMaxRsrcBytes) {
+        set_error("haste_ffi_forward: problem too large (grid %lld, ldo %lld, D*ldx %lld)",
+                  (long long)grid, (long long)ldo, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
     ffi_fwd_kernel<T, G, FP><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(

@@ -162,3 +162,24 @@ def test_out_of_range_indices_are_clamped(dev):
     clamped = bad.clamp(0, 63)
     out = gpu_forward(x, W, bias, bad, 32, dev)
     torch.testing.assert_close(out.float().cpu(), oracle.ffi_forward(clamped, x.t().contiguous(), W, bias, 32), **TOL16)
+
+
+@pytest.mark.parametrize("B,O,G,F", [(70, 1001, 64, 128), (64, 4133, 32, 32), (65, 700, 128, 64)])
+def test_forward_leaves_columns_past_O_untouched(dev, B, O, G, F):
+    """The logits may sit inside a wider row (e.g. a head/tail concat at a column
+    offset): columns >= O of an ld-padded output, and rows past B, keep their
+    contents."""
+    D = 256
+    x, W, bias, idx, _ = make_case(B, D, O, G, F, idx_mode="random")
+    ldo = (O + 63) // 64 * 64 + 64
+    out = torch.full((B + 3, ldo), 7.0, dtype=torch.bfloat16, device=dev)
+    xT, ldx = _C.padded_transpose(x.to(dev))
+    idx_d, W_d, b_d = idx.to(dev), W.to(dev), bias.to(dev)  # alive until the kernel ran
+    _lib.call("haste_ffi_forward", idx_d.data_ptr(), xT.data_ptr(), ldx, W_d.data_ptr(),
+              b_d.data_ptr(), out.data_ptr(), ldo, B, D, F, O, G, _lib.DTYPE_BF16,
+              _C.stream_of(out))
+    torch.cuda.synchronize()
+    ref = oracle.ffi_forward(idx, x.t().contiguous(), W, bias, G)
+    torch.testing.assert_close(out[:B, :O].float().cpu(), ref, **TOL16)
+    assert bool((out[:B, O:] == 7.0).all()), "columns >= O were written"
+    assert bool((out[B:] == 7.0).all()), "rows >= B were written"
