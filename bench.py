@@ -1,9 +1,10 @@
 """FFI fwd + bwd + SR-SGD step throughput on one MI355X (BASELINE.json metric).
 
 One step = forward logits (incl. the X -> X^T copy), backward to features
-(deterministic, fused SR to bf16 with seed 123), backward to weights (fp32) +
-bias gradient (fp32), and the fused SR-SGD update of weights and bias
-(lr 0.05, wd 1e-4, momentum 0, seed 42 + step).  Inputs are synthetic and
+(deterministic, fused SR to bf16 with seed 123), and backward to weights and
+bias (fp32, kept on chip) fused with the SR-SGD update of weights and bias
+(lr 0.05, wd 1e-4, momentum 0, seed 42 + step; bit-identical to separate
+gradient and SGD kernels, whose step time is reported as "unfused").  Inputs are synthetic and
 resident in HBM before timing; the grad of the logits dY = bf16(sigmoid(z) - Y)
 is computed once from the initial logits (Y binary,
 ~5 positives per row, Zipf(1.1) over labels).
@@ -38,12 +39,15 @@ CONFIGS = {
 
 
 def phase_bytes(B, D, O, G, F):
-    """Algorithmic HBM bytes per phase (bf16 tensors, fp32 weight/bias grads,
-    momentum 0): every tensor read or written once."""
+    """Algorithmic HBM bytes per phase (bf16 tensors, momentum 0): every tensor
+    read or written once.  bwd_weights_sgd keeps the fp32 gradients on chip:
+    dY, X, idx read, W and bias read and written.  The unfused phases
+    (bwd_weights writing fp32 dW/dbias, sgd reading them) are listed too."""
     Gc = (O + G - 1) // G
     return {
         "fwd": 2 * B * O + 2 * O * F + 4 * Gc * F + 2 * B * D + 2 * O,
         "bwd_features": 2 * B * O + 2 * O * F + 4 * Gc * F + 2 * B * D,
+        "bwd_weights_sgd": 2 * B * O + 2 * B * D + 4 * Gc * F + (2 + 2) * O * F + (2 + 2) * O,
         "bwd_weights": 2 * B * O + 2 * B * D + 4 * Gc * F + 4 * O * F + 4 * O,
         "sgd": (2 + 4 + 2) * O * F + (2 + 4 + 2) * O,
     }
@@ -178,45 +182,45 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
-    names = ["fwd", "bwd_features", "bwd_weights", "sgd"]
+    names = ["fwd", "bwd_features", "bwd_weights_sgd"]
+    fns = [lambda: st.forward(x), lambda: st.backward_features(dY_buf, ldy),
+           lambda: st.backward_weights_sgd(dY_buf, ldy)]
 
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record(stream)
-        st.forward(x)
-        if ev is not None:
-            ev[1].record(stream)
-        st.backward(dY_buf, ldy) if ev is None else _timed_backward(st, dY_buf, ldy, ev, stream)
-        if ev is not None:
-            ev[3].record(stream)
-        st.sgd()
-        if ev is not None:
-            ev[4].record(stream)
+    def timed(fn_list, steps, warmup):
+        for _ in range(warmup):
+            for fn in fn_list:
+                fn()
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fn_list) + 1)]
+               for _ in range(steps)]
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        w0 = time.perf_counter()
+        for k in range(steps):
+            evs[k][0].record(stream)
+            for i, fn in enumerate(fn_list):
+                fn()
+                evs[k][i + 1].record(stream)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - w0
+        per = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / steps for i in range(len(fn_list))]
+        return t0.elapsed_time(t1) / steps, per, wall_s
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    wall0 = time.perf_counter()
-    for k in range(args.steps):
-        step(evs[k])
-    t1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    total_ms = t0.elapsed_time(t1)
-    ms_per_step = total_ms / args.steps
-    phase_ms = {n: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / args.steps
-                for i, n in enumerate(names)}
+    ms_per_step, per, wall = timed(fns, args.steps, args.warmup)
+    phase_ms = dict(zip(names, per))
+    # the same step with separate gradient and SGD kernels (identical results)
+    un_names = ["fwd", "bwd_features", "bwd_weights", "sgd"]
+    un_ms, un_per, _ = timed([lambda: st.forward(x), lambda: st.backward_features(dY_buf, ldy),
+                              lambda: st.backward_weights(dY_buf, ldy), st.sgd],
+                             max(5, args.steps // 2), 2)
 
     pb = phase_bytes(B, D, O, G, F)
     phase_gbs = {n: pb[n] / (phase_ms[n] * 1e-3) / 1e9 for n in names}
     dom = max(names, key=lambda n: phase_ms[n])
-    step_bytes = sum(pb.values())
+    step_bytes = sum(pb[n] for n in names)
     flops = 3 * 2 * B * O * F
     result = {
         "metric": METRIC,
@@ -241,6 +245,8 @@ def main():
                           "mfma_frac": flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS},
         "phases_us": {n: round(phase_ms[n] * 1e3, 2) for n in names},
         "phases_hbm_frac": {n: round(phase_gbs[n] / HBM_PEAK_GBS, 4) for n in names},
+        "unfused": {"ms_per_step": un_ms, "samples_per_s": B / (un_ms * 1e-3),
+                    "phases_us": {n: round(v * 1e3, 2) for n, v in zip(un_names, un_per)}},
         "wall_s": wall,
     }
     tr = measured_traffic(args.config, dom)
@@ -257,12 +263,6 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg)
     print(json.dumps(result), flush=True)
-
-
-def _timed_backward(st, dY, ldy, ev, stream):
-    st.backward_features(dY, ldy)
-    ev[2].record(stream)
-    st.backward_weights(dY, ldy)
 
 
 if __name__ == "__main__":

@@ -149,12 +149,44 @@ __device__ __forceinline__ uint32_t philox_w0(uint32_t c0, uint32_t c1, uint32_t
     return c0;
 }
 
+// The same for offsets below 2^32 (counter words 1..3 zero): with the zeros
+// folded the first round needs one vector multiply and the second round's
+// other product is wave-uniform.
+__device__ __forceinline__ uint32_t philox_w0_32(uint32_t c0, uint32_t k0, uint32_t k1) {
+    return philox_w0(c0, 0u, 0u, k0, k1);
+}
+
 // Stochastic rounding fp32 -> bf16 bits (random low 16 bits added to the fp32
 // pattern, upper half kept); NaN -> quiet NaN.
 __device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t r) {
     uint32_t u = __float_as_uint(x);
     if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
     return (u + (r & 0xFFFFu)) >> 16;
+}
+
+// One element of the fused SGD step (shared_ffi/sr_triton.py:109-168) under the
+// FMA contract g' = fma(wd, w, g); m' = fma(mu, m, g'); w' = fma(-lr, m' or g', w),
+// then SR with the random word r (only its low 16 bits are used) or RNE.
+// Returns the new bf16 bits; *m is updated when use_mom.
+__device__ __forceinline__ uint32_t sgd_one_r(float w, float g, float* m, bool use_mom, float lr,
+                                              float wd, float mu, bool do_sr, uint32_t r) {
+    g = __builtin_fmaf(wd, w, g);
+    float upd = g;
+    if (use_mom) {
+        float mv = __builtin_fmaf(mu, *m, g);
+        *m = mv;
+        upd = mv;
+    }
+    float nw = __builtin_fmaf(-lr, upd, w);
+    return do_sr ? sr_bf16(nw, r) : f32_to_bf16_rne(nw);
+}
+
+// The same with r = tl.randint(seed, off).
+__device__ __forceinline__ uint32_t sgd_one(float w, float g, float* m, bool use_mom, float lr,
+                                            float wd, float mu, bool do_sr, uint64_t off,
+                                            uint32_t k0, uint32_t k1) {
+    const uint32_t r = do_sr ? philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, k0, k1) : 0u;
+    return sgd_one_r(w, g, m, use_mom, lr, wd, mu, do_sr, r);
 }
 
 // ------------------------------------------------------- buffer access ------
@@ -164,7 +196,8 @@ __device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t r) {
 // every path issues the same number of vector-memory instructions and the
 // compiler can wait for exactly the loads it needs (a branch around a store
 // makes it wait for all outstanding stores instead).  An offset of kOOB is
-// outside every resource built here (num_records is kept below 2^31).
+// outside every resource built here (num_records is kept below 2^31).  An
+// access that crosses num_records is out of range as a whole.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr uint32_t kOOB = 0x80000000u;
 constexpr int64_t kMaxRsrcBytes = 0x7FFFFF00;

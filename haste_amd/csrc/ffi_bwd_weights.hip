@@ -1,4 +1,5 @@
-// Grouped fixed-fan-in backward to weights (+ bias gradient), gfx950.
+// Grouped fixed-fan-in backward to weights (+ bias gradient), gfx950, optionally
+// fused with the SR-SGD update of the weights and bias.
 //
 //   dW[l, j] = sum_b dY[b, l] * xT[idx[g, j], b]        g = l / G
 //   dbias[l] = sum_b dY[b, l]
@@ -8,16 +9,22 @@
 //  - A (slots x batch) comes straight from L2: for slot j a fragment is 8
 //    consecutive batch entries of row xT[idx[g, j]] (one 16-byte load).
 //  - B (batch x labels) is dY[b, g*G:(g+1)*G], copied row-major into LDS in
-//    chunks of 64 batch rows (double-buffered, the next chunk's loads in flight
-//    during the current chunk's MFMAs) and read back with ds_read_b64_tr_b16,
-//    which hands each lane 4 consecutive batch values of one label: dY needs no
-//    transposition pass.
-//  - D holds 4 consecutive slots of one label per lane: dW rows are written 16
-//    bytes (fp32) per lane.
-// The bias gradient is one extra MFMA per label tile with A = ones, so dY is
-// read once for both outputs (the reference reads it a second time for
-// torch.sum, shared_ffi/bindings.py:40).
+//    chunks of 64 batch rows (double-buffered, the chunk after next in flight
+//    in registers) and read back with ds_read_b64_tr_b16, which hands each lane
+//    4 consecutive batch values of one label: dY needs no transposition pass.
+//  - Every load of the batch loop is a raw buffer access (rows past B, labels
+//    past O and slots past F read as zero by the hardware's range check), so
+//    the loop has no branches around memory operations.
+//  - The bias gradient is one extra MFMA per label tile with A = ones, so dY is
+//    read once for both outputs (the reference reads it a second time for
+//    torch.sum, shared_ffi/bindings.py:40).
+//  - Epilogue: the fp32 gradient tile is staged in LDS and processed as whole
+//    rows, 8 consecutive slots per thread: it is stored (fp32 or RNE 16-bit)
+//    and/or, in the fused mode, applied to W in place by the SGD step of
+//    haste_sgd_sr_step (same FMA chain, same Philox offsets l*F + j for W and l
+//    for the bias), so the fp32 gradient need not make a round trip to HBM.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -28,7 +35,8 @@ int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, 
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kKC = 64;  // batch rows per LDS stage
+constexpr int kKC = 64;               // batch rows per LDS stage
+constexpr int kStgBytes = 34 * 1024;  // LDS for one pass of the staged gradient tile
 
 template <int G, int FP>
 struct BwdWCfg {
@@ -42,6 +50,15 @@ struct BwdWCfg {
     static constexpr int RB = 2 * G + 16;                     // LDS bytes per staged dY row
     static constexpr int PIECES = kKC * G / 8;                // 16-byte pieces per chunk
     static constexpr int PPT = (PIECES + kThreads - 1) / kThreads;
+    static constexpr int SP = FP + 4;                         // staged gradient row (floats)
+    static constexpr int PR0 = kStgBytes / (SP * 4) / 16 * 16;
+    static constexpr int PR = PR0 < G ? PR0 : G;              // labels per epilogue pass
+    static constexpr int YS_BYTES = 2 * kKC * RB;
+    static constexpr int STG_BYTES = PR * SP * 4;
+    static constexpr int LDS_BYTES = YS_BYTES > STG_BYTES ? YS_BYTES : STG_BYTES;
+    static constexpr int CPR = FP / 8;                        // 8-slot chunks per staged row
+    static constexpr int WPT = (PR * CPR + kThreads - 1) / kThreads;  // chunks per thread, pass 0
+    static_assert(PR >= 16 && G % PR == 0, "epilogue pass shape");
 };
 
 template <typename T>
@@ -51,30 +68,39 @@ __device__ __forceinline__ uint32_t one_pair<BF16>() { return 0x3F803F80u; }
 template <>
 __device__ __forceinline__ uint32_t one_pair<F16>() { return 0x3C003C00u; }
 
-typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of
-// the 8-byte rows addressed by lanes 4k + i/4 (k = 0..3) as its element k.
-__device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
-    typedef fp16x4_t __attribute__((address_space(3))) * lds_p;
-    const fp16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-        (lds_p)(__attribute__((address_space(3))) char*)(p));
-    return __builtin_bit_cast(u32x2, v);
+// Keep the first nv 16-bit elements of an 8-element fragment (nv >= 8: all).
+__device__ __forceinline__ u32x4 keep_first(u32x4 v, int nv) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
+    return v;
 }
+
+// Parameters of the fused SGD epilogue (unused when SGD == false).
+struct SgdArgs {
+    uint16_t* W;
+    uint16_t* bias;
+    float* mW;
+    float* mb;
+    float lr, wd, mu;
+    int use_mom, do_sr;
+    uint32_t k0, k1;
+};
 
 // Two waves per SIMD (at most 256 registers each) hide the chunk pipeline's load
 // latency; the largest tile set (G = 128, 256 slots) needs more registers.
 template <int G, int FP>
 constexpr int bwdw_waves_per_simd() { return G * FP >= 128 * 256 ? 1 : 2; }
 
-template <typename T, int G, int FP>
+template <typename T, int G, int FP, bool SGD>
 __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_bwd_w_kernel(
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
     const uint16_t* __restrict__ dY, int64_t lddy, void* __restrict__ dW, int dW_dtype,
-    void* __restrict__ dbias, int dbias_dtype, int B, int D, int F, int64_t O) {
+    void* __restrict__ dbias, int dbias_dtype, int B, int D, int F, int64_t O, SgdArgs sg) {
     using C = BwdWCfg<G, FP>;
-    constexpr int MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT;
-    __shared__ __attribute__((aligned(16))) char Ys[2][kKC * RB];
+    constexpr int MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SP = C::SP, PR = C::PR;
+    __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
+    char (*Ys)[kKC * RB] = reinterpret_cast<char (*)[kKC * RB]>(lds);
+    float* stg = reinterpret_cast<float*>(lds);
 
     const int64_t g = blockIdx.x;
     const int tid = threadIdx.x;
@@ -83,68 +109,60 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     const bool active = wn < C::WN;
     const int col = lane & 15, kq = lane >> 4;
     const int64_t l0 = g * G;
+    const int nl = (int)std::min<int64_t>(G, O - l0);  // labels of this group
     const int nchunks = (B + kKC - 1) / kKC;
 
-    // A rows: this lane's slots
-    const uint16_t* xrow[MT];
+    // A rows: this lane's slots (slots >= F, and inactive waves, read as zero)
+    const rsrc_t xr = make_rsrc(xT, (int64_t)D * ldx * 2);
+    int64_t xoff[MT];
     bool jvalid[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         const int j = (wm * MT + mt) * 16 + col;
         jvalid[mt] = active && j < F;
         const int d = jvalid[mt] ? min(max(idx[g * F + j], 0), D - 1) : 0;
-        xrow[mt] = xT + (int64_t)d * ldx;
+        xoff[mt] = (int64_t)d * ldx;
     }
 
-    // dY chunk c (rows c*64 ..) -> registers; rows >= B and labels >= O are zero
+    // dY chunk c (rows c*64 ..) -> registers; rows >= B and labels >= O read as
+    // zero (labels of a partial 8-label piece are masked when stashed).  An
+    // access that crosses the end of a resource reads as zero as a whole, so the
+    // resource covers the last row up to the 8-label piece boundary (inside the
+    // row: lddy is a multiple of 8 and >= O).
+    int pr[PPT], pcc[PPT];
+#pragma unroll
+    for (int q = 0; q < PPT; ++q) {
+        const int p = tid + q * kThreads;
+        pr[q] = p / (G / 8);
+        pcc[q] = (p % (G / 8)) * 8;
+    }
     auto fetch = [&](int c, u32x4 (&v)[PPT]) {
+        const int b0 = c * kKC;
+        const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy + l0,
+                                    ((int64_t)(std::min(kKC, B - b0) - 1) * lddy + (nl + 7) / 8 * 8) * 2);
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
-            const int p = tid + q * kThreads;
-            const int r = p / (G / 8), cc = p % (G / 8);
-            const int64_t b = (int64_t)c * kKC + r;
-            const int64_t l = l0 + cc * 8;
-            v[q] = u32x4{0u, 0u, 0u, 0u};
-            if (p < C::PIECES && b < B) {
-                if (l + 8 <= O) {
-                    v[q] = *reinterpret_cast<const u32x4*>(dY + b * lddy + l);
-                } else if (l < O) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (l + e < O) v[q][e >> 1] |= (uint32_t)dY[b * lddy + l + e] << ((e & 1) * 16);
-                }
-            }
+            const bool ok = tid + q * kThreads < C::PIECES && pcc[q] < nl;
+            v[q] = buf_load16(yr, ok ? (uint32_t)((int64_t)pr[q] * lddy + pcc[q]) * 2 : kOOB);
         }
     };
     auto stash = [&](int buf, const u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
-            const int p = tid + q * kThreads;
-            if (p < C::PIECES) {
-                const int r = p / (G / 8), cc = p % (G / 8);
-                *reinterpret_cast<u32x4*>(&Ys[buf][r * RB + cc * 16]) = v[q];
-            }
+            if (tid + q * kThreads < C::PIECES)
+                *reinterpret_cast<u32x4*>(&Ys[buf][pr[q] * RB + pcc[q] * 2]) =
+                    keep_first(v[q], nl - pcc[q]);
         }
     };
     // A fragments of chunk c: 8 consecutive batch entries of each slot row
-    // (entries >= B read as zero)
+    // (entries >= B read as zero; a partial 8-entry piece is masked at use)
     auto fetch_a = [&](int c, u32x4 (&a)[2][MT]) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int bk = c * kKC + ks * 32 + kq * 8;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                u32x4 v = u32x4{0u, 0u, 0u, 0u};
-                if (jvalid[mt] && bk < B) {
-                    v = *reinterpret_cast<const u32x4*>(xrow[mt] + bk);
-                    if (bk + 8 > B) {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            if (bk + e >= B) v[e >> 1] &= (e & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                    }
-                }
-                a[ks][mt] = v;
-            }
+            for (int mt = 0; mt < MT; ++mt)
+                a[ks][mt] = buf_load16(xr, jvalid[mt] && bk < B ? (uint32_t)(xoff[mt] + bk) * 2 : kOOB);
         }
     };
 
@@ -158,26 +176,37 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     }
     const uint32_t op = one_pair<T>();
     const u32x4 ones = u32x4{op, op, op, op};
-    const bool do_bias = dbias != nullptr && wm == 0 && active;
+    const bool do_bias = (dbias != nullptr || (SGD && sg.bias != nullptr)) && wm == 0 && active;
 
-    u32x4 yv[PPT];
-    fetch(0, yv);
-    stash(0, yv);
-    if (nchunks > 1) fetch(1, yv);
-    u32x4 a[2][MT];
-    fetch_a(0, a);
+    const rsrc_t wr = make_rsrc(SGD ? sg.W + l0 * F : nullptr, SGD ? (int64_t)nl * F * 2 : 0);
+    constexpr int CPR = C::CPR, WPT = C::WPT;
+
+    // Ping-pong register sets by chunk parity (the loop body is unrolled twice),
+    // so no register copy waits on a load: dY pieces are fetched two chunks
+    // ahead, A fragments one chunk ahead.  Chunks past the end load nothing
+    // (every offset is out of range), so each body issues the same loads.
+    u32x4 yr[2][PPT];
+    u32x4 ar[2][2][MT];
+    fetch(0, yr[0]);
+    fetch(1, yr[1]);
+    fetch_a(0, ar[0]);
+    stash(0, yr[0]);
+    fetch(2, yr[0]);
     __syncthreads();
 
     // lane's tr-read address inside a staged chunk: row 8*kq + 4*half + col/4,
     // labels n0 + 4*(col%4)
     const int tr_off = (kq * 8 + col / 4) * RB + (col % 4) * 8;
-    for (int c = 0; c < nchunks; ++c) {
-        const char* ys = Ys[c & 1];
-        u32x4 an[2][MT];
-        if (c + 1 < nchunks) fetch_a(c + 1, an);
-        if (active) {
+    auto body = [&](int c, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        fetch_a(c + 1, ar[1 - P]);
+        if (active && c < nchunks) {
+            const char* ys = Ys[P];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
+                const int nv = B - (c * kKC + ks * 32 + kq * 8);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) ar[P][ks][mt] = keep_first(ar[P][ks][mt], nv);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     const char* p = ys + tr_off + ks * 32 * RB + (wn * NT + nt) * 32;
@@ -186,98 +215,190 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                     const u32x4 bf = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
-                        acc[mt][nt] = mfma16x16x32<T>(a[ks][mt], bf, acc[mt][nt]);
+                        acc[mt][nt] = mfma16x16x32<T>(ar[P][ks][mt], bf, acc[mt][nt]);
                     if (do_bias) accb[nt] = mfma16x16x32<T>(ones, bf, accb[nt]);
                 }
             }
         }
-        if (c + 1 < nchunks) {
-            stash((c + 1) & 1, yv);
-            if (c + 2 < nchunks) fetch(c + 2, yv);
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) a[ks][mt] = an[ks][mt];
-        }
+        stash(1 - P, yr[1 - P]);  // chunk c + 1 (zeros past the end)
+        fetch(c + 3, yr[1 - P]);
         __syncthreads();
+    };
+    for (int c = 0; c < nchunks; c += 2) {
+        body(c, std::integral_constant<int, 0>{});
+        body(c + 1, std::integral_constant<int, 1>{});
     }
 
-    if (!active) return;
-    // ---- epilogue: lane holds slots 4*kq..+3 of label col in each tile ----
+    // ---- bias: lane (col, kq = 0) of a wave with wm == 0 holds the column sum of
+    // label (wn*NT + nt)*16 + col in accb[nt][0] ----
+    if (do_bias && kq == 0) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const int64_t l = l0 + (wn * NT + nt) * 16 + col;
-        if (l >= O) continue;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const int j = (wm * MT + mt) * 16 + kq * 4;
-            if (j >= F) continue;
-            const f32x4 v = acc[mt][nt];
-            if (dW_dtype == HASTE_DTYPE_F32) {
-                *reinterpret_cast<f32x4*>(static_cast<float*>(dW) + l * F + j) = v;
-            } else {
-                u32x2 h;
-                if (dW_dtype == HASTE_DTYPE_BF16) {
-                    h[0] = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
-                    h[1] = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
-                } else {
-                    h[0] = f32_to_f16_rne(v[0]) | (f32_to_f16_rne(v[1]) << 16);
-                    h[1] = f32_to_f16_rne(v[2]) | (f32_to_f16_rne(v[3]) << 16);
+        for (int nt = 0; nt < NT; ++nt) {
+            const int ll = (wn * NT + nt) * 16 + col;
+            if (ll >= nl) continue;
+            const int64_t l = l0 + ll;
+            const float v = accb[nt][0];
+            if (dbias != nullptr) {
+                if (dbias_dtype == HASTE_DTYPE_F32)
+                    static_cast<float*>(dbias)[l] = v;
+                else if (dbias_dtype == HASTE_DTYPE_BF16)
+                    static_cast<uint16_t*>(dbias)[l] = (uint16_t)f32_to_bf16_rne(v);
+                else
+                    static_cast<uint16_t*>(dbias)[l] = (uint16_t)f32_to_f16_rne(v);
+            }
+            if constexpr (SGD) {
+                if (sg.bias != nullptr) {
+                    float mv = sg.use_mom ? sg.mb[l] : 0.f;
+                    sg.bias[l] = (uint16_t)sgd_one(bf16_bits_to_f32(sg.bias[l]), v, &mv,
+                                                   sg.use_mom, sg.lr, sg.wd, sg.mu, sg.do_sr,
+                                                   (uint64_t)l, sg.k0, sg.k1);
+                    if (sg.use_mom) sg.mb[l] = mv;
                 }
-                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(dW) + l * F + j) = h;
             }
         }
-        if (do_bias && kq == 0) {
-            const float v = accb[nt][0];
-            if (dbias_dtype == HASTE_DTYPE_F32)
-                static_cast<float*>(dbias)[l] = v;
-            else if (dbias_dtype == HASTE_DTYPE_BF16)
-                static_cast<uint16_t*>(dbias)[l] = (uint16_t)f32_to_bf16_rne(v);
-            else
-                static_cast<uint16_t*>(dbias)[l] = (uint16_t)f32_to_f16_rne(v);
+    }
+
+    // ---- gradient tile: staged in LDS (labels [p0, p0+PR) per pass), then
+    // processed as rows of 8 consecutive slots per thread ----
+    const int esz = dW_dtype == HASTE_DTYPE_F32 ? 4 : 2;
+    const rsrc_t gr = make_rsrc(dW != nullptr ? static_cast<char*>(dW) + l0 * F * esz : nullptr,
+                                dW != nullptr ? (int64_t)nl * F * esz : 0);
+    const rsrc_t mr = make_rsrc(SGD && sg.use_mom ? sg.mW + l0 * F : nullptr,
+                                SGD && sg.use_mom ? (int64_t)nl * F * 4 : 0);
+#pragma unroll 1
+    for (int p0 = 0; p0 < G; p0 += PR) {
+        if (active) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int ll = (wn * NT + nt) * 16;
+                if (ll < p0 || ll >= p0 + PR) continue;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    *reinterpret_cast<f32x4*>(&stg[(ll - p0 + col) * SP + (wm * MT + mt) * 16 + kq * 4]) =
+                        acc[mt][nt];
+            }
         }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < WPT; ++q) {
+            const int it = tid + q * kThreads;
+            if (it >= PR * CPR) break;
+            const int lr = p0 + it / CPR, j0 = (it % CPR) * 8;
+            const f32x4 g0 = *reinterpret_cast<const f32x4*>(&stg[(lr - p0) * SP + j0]);
+            const f32x4 g1 = *reinterpret_cast<const f32x4*>(&stg[(lr - p0) * SP + j0 + 4]);
+            const bool in = j0 < F;  // rows >= nl fall outside every resource
+            const uint32_t e = (uint32_t)(lr * F + j0);
+            if (dW != nullptr) {
+                if (dW_dtype == HASTE_DTYPE_F32) {
+                    buf_store16(__builtin_bit_cast(u32x4, g0), gr, in ? e * 4 : kOOB);
+                    buf_store16(__builtin_bit_cast(u32x4, g1), gr, in ? e * 4 + 16 : kOOB);
+                } else {
+                    const u32x4 h = dW_dtype == HASTE_DTYPE_BF16
+                        ? u32x4{pack2_rne<BF16>(g0[0], g0[1]), pack2_rne<BF16>(g0[2], g0[3]),
+                                pack2_rne<BF16>(g1[0], g1[1]), pack2_rne<BF16>(g1[2], g1[3])}
+                        : u32x4{pack2_rne<F16>(g0[0], g0[1]), pack2_rne<F16>(g0[2], g0[3]),
+                                pack2_rne<F16>(g1[0], g1[1]), pack2_rne<F16>(g1[2], g1[3])};
+                    buf_store16(h, gr, in ? e * 2 : kOOB);
+                }
+            }
+            if constexpr (SGD) {
+                const u32x4 wv = buf_load16(wr, in ? e * 2 : kOOB);
+                float gv[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+                float mv[8];
+                if (sg.use_mom) {
+                    const f32x4 m0 = __builtin_bit_cast(f32x4, buf_load16(mr, in ? e * 4 : kOOB));
+                    const f32x4 m1 = __builtin_bit_cast(f32x4, buf_load16(mr, in ? e * 4 + 16 : kOOB));
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) { mv[k] = m0[k]; mv[4 + k] = m1[k]; }
+                }
+                const uint32_t off = (uint32_t)((l0 + lr) * F + j0);
+                uint32_t ob[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t wb = (k & 1) ? (wv[k >> 1] >> 16) : (wv[k >> 1] & 0xFFFFu);
+                    const uint32_t r = sg.do_sr ? philox_w0_32(off + k, sg.k0, sg.k1) : 0u;
+                    ob[k] = sgd_one_r(bf16_bits_to_f32(wb), gv[k], &mv[k], sg.use_mom, sg.lr,
+                                      sg.wd, sg.mu, sg.do_sr, r);
+                }
+                buf_store16(u32x4{ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16),
+                                  ob[4] | (ob[5] << 16), ob[6] | (ob[7] << 16)},
+                            wr, in ? e * 2 : kOOB);
+                if (sg.use_mom) {
+                    buf_store16(__builtin_bit_cast(u32x4, f32x4{mv[0], mv[1], mv[2], mv[3]}), mr,
+                                in ? e * 4 : kOOB);
+                    buf_store16(__builtin_bit_cast(u32x4, f32x4{mv[4], mv[5], mv[6], mv[7]}), mr,
+                                in ? e * 4 + 16 : kOOB);
+                }
+            }
+        }
+        if (p0 + PR < G) __syncthreads();
     }
 }
 
-template <typename T, int G, int FP>
+template <typename T, int G, int FP, bool SGD>
 int launch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY, int64_t lddy,
            void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B, int64_t D, int64_t F,
-           int64_t O, hipStream_t st) {
+           int64_t O, const SgdArgs& sg, hipStream_t st) {
     const int64_t Gc = ceil_div(O, G);
-    if (Gc > 0x7FFFFFFF) {
-        set_error("haste_ffi_bwd_weights: too many groups");
+    if (Gc > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes || (int64_t)kKC * lddy * 2 > kMaxRsrcBytes ||
+        (int64_t)G * F * 4 > kMaxRsrcBytes) {
+        set_error("haste_ffi_bwd_weights: problem too large (Gc %lld, lddy %lld, D*ldx %lld)",
+                  (long long)Gc, (long long)lddy, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
-    ffi_bwd_w_kernel<T, G, FP><<<dim3((unsigned)Gc), dim3(kThreads), 0, st>>>(
-        idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, (int)B, (int)D, (int)F, O);
+    ffi_bwd_w_kernel<T, G, FP, SGD><<<dim3((unsigned)Gc), dim3(kThreads), 0, st>>>(
+        idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, (int)B, (int)D, (int)F, O, sg);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_weights");
     return HASTE_OK;
 }
 
-template <typename T, int G>
-int dispatch_fp(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY,
-                int64_t lddy, void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B,
-                int64_t D, int64_t F, int64_t O, hipStream_t st) {
-#define HASTE_BWDW_ARGS idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, B, D, F, O, st
-    if (F <= 32) return launch<T, G, 32>(HASTE_BWDW_ARGS);
-    if (F <= 64) return launch<T, G, 64>(HASTE_BWDW_ARGS);
-    if (F <= 128) return launch<T, G, 128>(HASTE_BWDW_ARGS);
-    return launch<T, G, 256>(HASTE_BWDW_ARGS);
-#undef HASTE_BWDW_ARGS
+template <typename T, bool SGD>
+int dispatch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY,
+             int64_t lddy, void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B,
+             int64_t D, int64_t F, int64_t O, int64_t G, const SgdArgs& sg, hipStream_t st) {
+#define HASTE_BWDW_FP(GG)                                                                        \
+    do {                                                                                         \
+        if (F <= 32) return launch<T, GG, 32, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,  \
+                                                   dbias_dtype, B, D, F, O, sg, st);             \
+        if (F <= 64) return launch<T, GG, 64, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,  \
+                                                   dbias_dtype, B, D, F, O, sg, st);             \
+        if (F <= 128) return launch<T, GG, 128, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype,       \
+                                                     dbias, dbias_dtype, B, D, F, O, sg, st);    \
+        return launch<T, GG, 256, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, \
+                                       B, D, F, O, sg, st);                                      \
+    } while (0)
+    switch (G) {
+    case 16: HASTE_BWDW_FP(16);
+    case 32: HASTE_BWDW_FP(32);
+    case 64: HASTE_BWDW_FP(64);
+    case 128: HASTE_BWDW_FP(128);
+    default: break;
+    }
+#undef HASTE_BWDW_FP
+    set_error("haste_ffi_bwd_weights: unsupported group size %lld", (long long)G);
+    return HASTE_ERR_UNSUPPORTED;
 }
 
-template <typename T>
-int dispatch_g(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY,
-               int64_t lddy, void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B,
-               int64_t D, int64_t F, int64_t O, int64_t G, hipStream_t st) {
-#define HASTE_BWDW_ARGS idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, B, D, F, O, st
-    switch (G) {
-    case 16: return dispatch_fp<T, 16>(HASTE_BWDW_ARGS);
-    case 32: return dispatch_fp<T, 32>(HASTE_BWDW_ARGS);
-    case 64: return dispatch_fp<T, 64>(HASTE_BWDW_ARGS);
-    default: return dispatch_fp<T, 128>(HASTE_BWDW_ARGS);
-    }
-#undef HASTE_BWDW_ARGS
+int check_bwdw(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, const void* dY,
+               int64_t lddy, int32_t dW_dtype, void* dbias, int32_t dbias_dtype, int64_t B,
+               int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype) {
+    int rc = check_ffi_shape(fn, B, D, F, O, G, dtype);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(idx && xT && dY, "%s: null pointer", fn);
+    HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
+                    "%s: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)", fn,
+                    (long long)ldx, (long long)B);
+    HASTE_CHECK_ARG(lddy >= O && lddy % 8 == 0,
+                    "%s: lddy must be >= O and a multiple of 8 (lddy=%lld O=%lld)", fn,
+                    (long long)lddy, (long long)O);
+    HASTE_CHECK_ARG(aligned16(xT) && aligned16(dY), "%s: xT and dY must be 16-byte aligned", fn);
+    HASTE_CHECK_ARG(dW_dtype == HASTE_DTYPE_F32 || dW_dtype == HASTE_DTYPE_BF16 ||
+                        dW_dtype == HASTE_DTYPE_F16,
+                    "%s: bad dW dtype %d", fn, (int)dW_dtype);
+    HASTE_CHECK_ARG(dbias == nullptr || dbias_dtype == HASTE_DTYPE_F32 ||
+                        dbias_dtype == HASTE_DTYPE_BF16 || dbias_dtype == HASTE_DTYPE_F16,
+                    "%s: bad dbias dtype %d", fn, (int)dbias_dtype);
+    return HASTE_OK;
 }
 
 }  // namespace
@@ -288,29 +409,50 @@ extern "C" int haste_ffi_bwd_weights(const int32_t* idx, const void* xT, int64_t
                                      void* dbias, int32_t dbias_dtype, int64_t B, int64_t D,
                                      int64_t F, int64_t O, int64_t G, int32_t dtype,
                                      void* stream) {
-    int rc = haste::check_ffi_shape("haste_ffi_bwd_weights", B, D, F, O, G, dtype);
+    const char* fn = "haste_ffi_bwd_weights";
+    int rc = haste::check_bwdw(fn, idx, xT, ldx, dY, lddy, dW_dtype, dbias, dbias_dtype, B, D, F,
+                               O, G, dtype);
     if (rc != HASTE_OK) return rc;
-    HASTE_CHECK_ARG(idx && xT && dY && dW, "haste_ffi_bwd_weights: null pointer");
-    HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
-                    "haste_ffi_bwd_weights: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)",
-                    (long long)ldx, (long long)B);
-    HASTE_CHECK_ARG(lddy >= O && lddy % 8 == 0,
-                    "haste_ffi_bwd_weights: lddy must be >= O and a multiple of 8 (lddy=%lld O=%lld)",
-                    (long long)lddy, (long long)O);
-    HASTE_CHECK_ARG(haste::aligned16(xT) && haste::aligned16(dY),
-                    "haste_ffi_bwd_weights: xT and dY must be 16-byte aligned");
-    HASTE_CHECK_ARG(dW_dtype == HASTE_DTYPE_F32 || dW_dtype == HASTE_DTYPE_BF16 ||
-                        dW_dtype == HASTE_DTYPE_F16,
-                    "haste_ffi_bwd_weights: bad dW dtype %d", (int)dW_dtype);
-    HASTE_CHECK_ARG(dbias == nullptr || dbias_dtype == HASTE_DTYPE_F32 ||
-                        dbias_dtype == HASTE_DTYPE_BF16 || dbias_dtype == HASTE_DTYPE_F16,
-                    "haste_ffi_bwd_weights: bad dbias dtype %d", (int)dbias_dtype);
+    HASTE_CHECK_ARG(dW != nullptr, "%s: null pointer", fn);
+    HASTE_CHECK_ARG(haste::aligned16(dW), "%s: dW must be 16-byte aligned", fn);
     auto* x = static_cast<const uint16_t*>(xT);
     auto* y = static_cast<const uint16_t*>(dY);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const haste::SgdArgs none{};
     if (dtype == HASTE_DTYPE_BF16)
-        return haste::dispatch_g<haste::BF16>(idx, x, ldx, y, lddy, dW, dW_dtype, dbias,
-                                              dbias_dtype, B, D, F, O, G, st);
-    return haste::dispatch_g<haste::F16>(idx, x, ldx, y, lddy, dW, dW_dtype, dbias, dbias_dtype,
-                                         B, D, F, O, G, st);
+        return haste::dispatch<haste::BF16, false>(idx, x, ldx, y, lddy, dW, dW_dtype, dbias,
+                                                  dbias_dtype, B, D, F, O, G, none, st);
+    return haste::dispatch<haste::F16, false>(idx, x, ldx, y, lddy, dW, dW_dtype, dbias,
+                                             dbias_dtype, B, D, F, O, G, none, st);
+}
+
+extern "C" int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx,
+                                         const void* dY, int64_t lddy, uint16_t* W,
+                                         uint16_t* bias, float* m_W, float* m_bias, void* dW,
+                                         int32_t dW_dtype, void* dbias, int32_t dbias_dtype,
+                                         float lr, float wd, float mu, int32_t use_mom,
+                                         int32_t do_sr, uint64_t seed, int64_t B, int64_t D,
+                                         int64_t F, int64_t O, int64_t G, int32_t dtype,
+                                         void* stream) {
+    const char* fn = "haste_ffi_bwd_weights_sgd";
+    int rc = haste::check_bwdw(fn, idx, xT, ldx, dY, lddy, dW_dtype, dbias, dbias_dtype, B, D, F,
+                               O, G, dtype);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(dtype == HASTE_DTYPE_BF16, "%s: the SGD step updates bf16 weights only", fn);
+    if (O * F > 0xFFFFFFFFll) {
+        haste::set_error("%s: O*F = %lld exceeds 2^32 - 1 elements", fn, (long long)(O * F));
+        return HASTE_ERR_UNSUPPORTED;
+    }
+    HASTE_CHECK_ARG(W != nullptr && haste::aligned16(W), "%s: W must be a 16-byte aligned pointer",
+                    fn);
+    HASTE_CHECK_ARG(dW == nullptr || haste::aligned16(dW), "%s: dW must be 16-byte aligned", fn);
+    HASTE_CHECK_ARG(!use_mom || (m_W != nullptr && haste::aligned16(m_W) &&
+                                 (bias == nullptr || m_bias != nullptr)),
+                    "%s: momentum buffers missing or misaligned", fn);
+    const haste::SgdArgs sg{W, bias, m_W, m_bias, lr, wd, mu, use_mom ? 1 : 0, do_sr ? 1 : 0,
+                            (uint32_t)seed, (uint32_t)(seed >> 32)};
+    return haste::dispatch<haste::BF16, true>(idx, static_cast<const uint16_t*>(xT), ldx,
+                                              static_cast<const uint16_t*>(dY), lddy, dW, dW_dtype,
+                                              dbias, dbias_dtype, B, D, F, O, G, sg,
+                                              static_cast<hipStream_t>(stream));
 }

@@ -44,21 +44,6 @@ __device__ __forceinline__ float load_grad1(const void* g, int64_t i) {
     }
 }
 
-__device__ __forceinline__ uint32_t sgd_one(float w, float g, float* m, bool use_mom, float lr,
-                                            float wd, float mu, bool do_sr, uint64_t off,
-                                            uint32_t k0, uint32_t k1) {
-    g = __builtin_fmaf(wd, w, g);
-    float upd = g;
-    if (use_mom) {
-        float mv = __builtin_fmaf(mu, *m, g);
-        *m = mv;
-        upd = mv;
-    }
-    float nw = __builtin_fmaf(-lr, upd, w);
-    if (do_sr) return sr_bf16(nw, philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, k0, k1));
-    return f32_to_bf16_rne(nw);
-}
-
 // One launch updates up to kMaxSegs tensors ("segments"), each with its own
 // offset base; every thread handles kVec consecutive elements of one segment
 // (16-byte vector loads when the segment is aligned, element loads for the

@@ -1,12 +1,15 @@
 """One training step of a grouped FFI layer on preallocated buffers.
 
-``FFITrainStep`` runs forward -> backward (features, weights, bias) -> fused
-SR-SGD update of weights and bias, calling libhaste_ffi.so directly with
-buffers allocated once, so a step launches only HIP kernels (no allocator
-traffic, no host sync) and can be captured in a HIP graph.  It computes the
-same quantities as GroupFFIMulFunction + SRSgd with two deliberate choices:
-the weight and bias gradients are kept in fp32 (``grad_dtype``, the SGD kernel
-reads them directly), and the grad of the logits ``dY`` is an input.
+``FFITrainStep`` runs forward -> backward to features -> backward to weights
+and bias fused with the SR-SGD update of weights and bias, calling
+libhaste_ffi.so directly with buffers allocated once, so a step launches only
+HIP kernels (no allocator traffic, no host sync) and can be captured in a HIP
+graph.  It computes the same quantities as GroupFFIMulFunction + SRSgd with
+two deliberate choices: the weight and bias gradients are fp32 (``grad_dtype``)
+and, in ``step``, never leave the chip (the SGD update is applied in the
+epilogue of the weight-gradient kernel; the result is bit-identical to
+``backward_weights`` followed by ``sgd``), and the grad of the logits ``dY`` is
+an input.
 """
 from __future__ import annotations
 
@@ -38,14 +41,34 @@ class FFITrainStep:
         self.logits_buf = torch.empty(self.B, self.ldo, dtype=torch.bfloat16, device=dev)
         self.dX = torch.empty(self.B, self.D, dtype=torch.bfloat16, device=dev)
         self.grad_dtype = grad_dtype
-        self.dW = torch.empty(self.O, self.F, dtype=grad_dtype, device=dev)
-        self.dbias = torch.empty(self.O, dtype=grad_dtype, device=dev) if bias is not None else None
+        self._dW = None      # allocated by the first unfused backward_weights call
+        self._dbias = None
         self.ws = _C.bwd_features_workspace(self.B, self.D, self.F, self.O, self.G,
                                             torch.bfloat16, dev)
         self._plan_version = None  # idx._version the workspace plan was made for
         self.code = _lib.DTYPE_BF16
         self.gcode = _C.dtype_code(grad_dtype)
-        ts = [(self.W, self.dW)] + ([(bias, self.dbias)] if bias is not None else [])
+        self._sgd_args = None
+
+    @property
+    def dW(self) -> torch.Tensor:
+        """[O, F] weight gradient of the last ``backward_weights`` call."""
+        self._grad_buffers()
+        return self._dW
+
+    @property
+    def dbias(self):
+        self._grad_buffers()
+        return self._dbias
+
+    def _grad_buffers(self) -> None:
+        if self._dW is not None:
+            return
+        dev = self.W.device
+        self._dW = torch.empty(self.O, self.F, dtype=self.grad_dtype, device=dev)
+        if self.bias is not None:
+            self._dbias = torch.empty(self.O, dtype=self.grad_dtype, device=dev)
+        ts = [(self.W, self._dW)] + ([(self.bias, self._dbias)] if self.bias is not None else [])
         self._sgd_tensors = (_lib.SgdTensor * len(ts))(
             *[_lib.SgdTensor(w.data_ptr(), g.data_ptr(), None, w.numel(), 0) for w, g in ts])
         self._sgd_args = [self._sgd_tensors, len(ts), self.gcode, self.lr, self.wd, 0.0, 0, 1,
@@ -93,6 +116,7 @@ class FFITrainStep:
     def backward_weights(self, dY: torch.Tensor, lddy: int) -> None:
         """dW [O, F] and dbias [O] in grad_dtype."""
         self._check_dY(dY, lddy)
+        self._grad_buffers()
         _lib.call("haste_ffi_bwd_weights", self.idx.data_ptr(), self.xT_buf.data_ptr(), self.ldx,
                   dY.data_ptr(), lddy, self.dW.data_ptr(), self.gcode,
                   None if self.dbias is None else self.dbias.data_ptr(), self.gcode, self.B,
@@ -105,13 +129,31 @@ class FFITrainStep:
 
     def sgd(self) -> None:
         """SR-SGD (momentum 0) on weights and bias with the current seed, then seed += 1
-        (optim_sr.py:59-62: one seed per step, offsets from 0 per tensor); one launch."""
+        (optim_sr.py:59-62: one seed per step, offsets from 0 per tensor); one launch.
+        Applies the gradients of the last ``backward_weights`` call."""
+        self._grad_buffers()
         self._sgd_args[-2] = self.seed
         self._sgd_args[-1] = _C.stream_of(self.W)
         _lib.call("haste_sgd_sr_step_multi", *self._sgd_args)
         self.seed += 1
 
+    def backward_weights_sgd(self, dY: torch.Tensor, lddy: int) -> None:
+        """Weight and bias gradients (fp32, kept on chip) applied at once by SR-SGD
+        (momentum 0) with the current seed, then seed += 1: bit-identical to
+        ``backward_weights`` + ``sgd`` with fp32 gradients, in one kernel."""
+        self._check_dY(dY, lddy)
+        if self.grad_dtype != torch.float32:
+            raise ValueError("FFITrainStep.backward_weights_sgd: the fused update uses fp32 "
+                             "gradients (grad_dtype=torch.float32)")
+        _lib.call("haste_ffi_bwd_weights_sgd", self.idx.data_ptr(), self.xT_buf.data_ptr(),
+                  self.ldx, dY.data_ptr(), lddy, self.W.data_ptr(),
+                  None if self.bias is None else self.bias.data_ptr(), None, None, None,
+                  _lib.DTYPE_F32, None, _lib.DTYPE_F32, self.lr, self.wd, 0.0, 0, 1, self.seed,
+                  self.B, self.D, self.F, self.O, self.G, self.code, _C.stream_of(self.W))
+        self.seed += 1
+
     def step(self, x: torch.Tensor, dY: torch.Tensor, lddy: int) -> None:
+        """forward -> backward to features (dX) -> fused weight/bias gradient + SR-SGD."""
         self.forward(x)
-        self.backward(dY, lddy)
-        self.sgd()
+        self.backward_features(dY, lddy)
+        self.backward_weights_sgd(dY, lddy)

@@ -114,6 +114,27 @@ int haste_ffi_bwd_weights(const int32_t* idx, const void* xT, int64_t ldx, const
                           int64_t G, int32_t dtype, void* stream);
 
 /*
+ * Backward to weights fused with the SR-SGD step on the bf16 weights and bias:
+ * computes the fp32 gradients of haste_ffi_bwd_weights and applies to W [O, F]
+ * and bias [O] (in place) the update of haste_sgd_sr_step with g = those fp32
+ * gradients -- element offsets l*F + j for W and l for the bias, both from 0,
+ * one seed -- so the result is bit-identical to haste_ffi_bwd_weights (fp32
+ * dW, dbias) followed by haste_sgd_sr_step_multi over {W, bias}.  The gradients
+ * are also stored when dW / dbias are non-NULL.  bias may be NULL (no bias);
+ * m_W [O, F] and m_bias [O] are fp32 momentum buffers read when use_mom.
+ * dtype must be bf16.  Replaces, for one FFI layer, ffi_backward_weights_cuda
+ * (shared_ffi/ffi_backward_weights.cu:486-684) + torch.sum(grad_output, 0)
+ * (shared_ffi/bindings.py:40) + SRSgd.step's sgd_update calls on the layer's
+ * weights and bias (shared_ffi/optim_sr.py:64-112, shared_ffi/sr_triton.py:172-213).
+ */
+int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx, const void* dY,
+                              int64_t lddy, uint16_t* W, uint16_t* bias, float* m_W,
+                              float* m_bias, void* dW, int32_t dW_dtype, void* dbias,
+                              int32_t dbias_dtype, float lr, float wd, float mu, int32_t use_mom,
+                              int32_t do_sr, uint64_t seed, int64_t B, int64_t D, int64_t F,
+                              int64_t O, int64_t G, int32_t dtype, void* stream);
+
+/*
  * Stochastic rounding fp32 -> bf16: out[i] = SR(x[i], tl.randint(seed, offset0 + i)).
  * Replaces stochastic_rounding (shared_ffi/sr_triton.py:51-59).
  */

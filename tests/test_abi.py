@@ -107,3 +107,21 @@ def test_python_api_rejects_cpu_tensors():
         ops.group_ffi_mul(x, W, idx, None, gsize=32)
     with pytest.raises(RuntimeError, match="HIP device"):
         sr.stochastic_rounding(torch.randn(8), torch.empty(8, dtype=torch.bfloat16), 1)
+
+
+def _bwdw_sgd(**kw):
+    args = dict(idx=16, xT=16, ldx=64, dY=32, lddy=4096, W=48, bias=None, mW=None, mb=None,
+                dW=None, dW_dtype=_lib.DTYPE_F32, dbias=None, dbias_dtype=_lib.DTYPE_F32,
+                lr=0.05, wd=1e-4, mu=0.0, use_mom=0, do_sr=1, seed=42, B=64, D=768, F=32, O=4096,
+                G=32, dtype=_lib.DTYPE_BF16, stream=None)
+    args.update(kw)
+    return _lib.lib().haste_ffi_bwd_weights_sgd(*args.values())
+
+
+def test_bwd_weights_sgd_rejects_bad_arguments():
+    assert _bwdw_sgd(dtype=_lib.DTYPE_F16) == _lib.HASTE_ERR_INVALID_ARG
+    assert "bf16 weights only" in _lib.last_error()
+    assert _bwdw_sgd(use_mom=1) == _lib.HASTE_ERR_INVALID_ARG  # no momentum buffers
+    assert _bwdw_sgd(W=None) == _lib.HASTE_ERR_INVALID_ARG
+    assert _bwdw_sgd(G=48) == _lib.HASTE_ERR_UNSUPPORTED
+    assert _bwdw_sgd(lddy=4092) == _lib.HASTE_ERR_INVALID_ARG

@@ -1,0 +1,128 @@
+"""GPU parity of the fused weight-gradient + SR-SGD kernel
+(haste_ffi_bwd_weights_sgd) through the C ABI.
+
+Bar: bit-exact.  The fused kernel must give exactly the bits of
+haste_ffi_bwd_weights (fp32 dW, dbias) followed by haste_sgd_sr_step_multi on
+{W, bias} (same seed, offsets from 0 per tensor), and that SGD result must be
+bit-exact against the CPU oracle's SGD applied to the same fp32 gradients.
+The fp32 gradients themselves match the oracle's fp32 contraction within
+rtol 1e-4 / atol 1e-5 (summation order only).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from haste_amd import _C, _lib
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # B, D, O, G, F, bias, momentum, do_sr
+    (64, 768, 4096, 32, 32, True, False, True),
+    (128, 768, 8193, 64, 128, True, False, True),    # config 1 shape, 1-label last group
+    (100, 300, 1000, 16, 48, True, True, True),      # B % 8 != 0, F % 32 != 0, momentum
+    (96, 512, 2050, 64, 64, False, False, True),     # no bias, partial last group
+    (40, 768, 2100, 128, 128, True, True, False),    # G = 128, RNE instead of SR
+    (33, 200, 700, 128, 256, True, False, True),     # G = 128, F = 256 (several epilogue passes)
+    (64, 4096, 3000, 32, 256, True, True, True),     # wide input, F = 256
+]
+
+
+def bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def setup(B, D, O, G, F, seed):
+    g = torch.Generator().manual_seed(seed)
+    Gc = (O + G - 1) // G
+    x = torch.randn(B, D, generator=g).to(torch.bfloat16)
+    W = ((torch.rand(O, F, generator=g) * 2 - 1) / F ** 0.5).to(torch.bfloat16)
+    bias = (torch.randn(O, generator=g) * 0.1).to(torch.bfloat16)
+    idx = torch.randint(0, D, (Gc, F), generator=g, dtype=torch.int32)
+    lddy = (O + 7) // 8 * 8
+    dY = torch.zeros(B, lddy, dtype=torch.bfloat16)
+    dY[:, :O] = (torch.randn(B, O, generator=g) * 0.1).to(torch.bfloat16)
+    mW = torch.randn(O, F, generator=g) * 0.01
+    mb = torch.randn(O, generator=g) * 0.01
+    return x, W, bias, idx, dY, lddy, mW, mb
+
+
+@pytest.mark.parametrize("B,D,O,G,F,has_bias,use_mom,do_sr", CASES)
+def test_fused_matches_separate_and_oracle(dev, B, D, O, G, F, has_bias, use_mom, do_sr):
+    x, W, bias, idx, dY, lddy, mW, mb = setup(B, D, O, G, F, seed=O + F)
+    lr, wd, mu, seed = 0.05, 1e-4, 0.9, 42 + G
+    xT, ldx = _C.padded_transpose(x.to(dev))
+    idx_d, dY_d = idx.to(dev), dY.to(dev)
+    st = _C.stream_of(dY_d)
+
+    # separate path: fp32 gradients, then the multi-tensor SGD kernel
+    dW = torch.empty(O, F, dtype=torch.float32, device=dev)
+    db = torch.empty(O, dtype=torch.float32, device=dev)
+    _lib.call("haste_ffi_bwd_weights", idx_d.data_ptr(), xT.data_ptr(), ldx, dY_d.data_ptr(),
+              lddy, dW.data_ptr(), _lib.DTYPE_F32, db.data_ptr(), _lib.DTYPE_F32, B, D, F, O, G,
+              _lib.DTYPE_BF16, st)
+    W1, b1, mW1, mb1 = W.to(dev), bias.to(dev), mW.to(dev), mb.to(dev)
+    ts = [(W1, dW, mW1)] + ([(b1, db, mb1)] if has_bias else [])
+    arr = (_lib.SgdTensor * len(ts))(*[_lib.SgdTensor(w.data_ptr(), g_.data_ptr(),
+                                                      m.data_ptr() if use_mom else None,
+                                                      w.numel(), 0) for w, g_, m in ts])
+    _lib.call("haste_sgd_sr_step_multi", arr, len(ts), _lib.DTYPE_F32, lr, wd, mu, int(use_mom),
+              int(do_sr), seed, st)
+
+    # fused path (also storing the gradients)
+    W2, b2, mW2, mb2 = W.to(dev), bias.to(dev), mW.to(dev), mb.to(dev)
+    dW2 = torch.full((O, F), 7.0, dtype=torch.float32, device=dev)
+    db2 = torch.full((O,), 7.0, dtype=torch.float32, device=dev)
+    _lib.call("haste_ffi_bwd_weights_sgd", idx_d.data_ptr(), xT.data_ptr(), ldx, dY_d.data_ptr(),
+              lddy, W2.data_ptr(), b2.data_ptr() if has_bias else None,
+              mW2.data_ptr() if use_mom else None, mb2.data_ptr() if use_mom else None,
+              dW2.data_ptr(), _lib.DTYPE_F32, db2.data_ptr(), _lib.DTYPE_F32, lr, wd, mu,
+              int(use_mom), int(do_sr), seed, B, D, F, O, G, _lib.DTYPE_BF16, st)
+    torch.cuda.synchronize()
+
+    assert torch.equal(dW2, dW), "fused kernel's fp32 dW differs from haste_ffi_bwd_weights"
+    assert torch.equal(db2, db)
+    assert np.array_equal(bits(W2), bits(W1)), "fused SGD differs from the separate path"
+    if has_bias:
+        assert np.array_equal(bits(b2), bits(b1))
+    else:
+        assert np.array_equal(bits(b2), bits(bias))
+    if use_mom:
+        assert torch.equal(mW2, mW1)
+        if has_bias:
+            assert torch.equal(mb2, mb1)
+
+    # oracle: fp32 gradients within summation-order tolerance, SGD bit-exact on them
+    ref_dw = oracle.ffi_backward_weights(idx, x.t().contiguous(), dY[:, :O], G)
+    torch.testing.assert_close(dW.cpu(), ref_dw, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(db.cpu(), oracle.bias_grad(dY[:, :O]), rtol=1e-4, atol=1e-5)
+    w_ref, m_ref = oracle.sgd_sr_step(bits(W).reshape(-1), dW.cpu().numpy().reshape(-1),
+                                      mW.numpy().reshape(-1).copy() if use_mom else None, lr, wd,
+                                      mu, use_mom, do_sr, seed)
+    assert np.array_equal(bits(W2).reshape(-1), w_ref)
+    if use_mom:
+        assert np.array_equal(mW2.cpu().numpy().reshape(-1), m_ref)
+
+
+def test_train_step_fused_equals_unfused(dev):
+    """FFITrainStep.step (fused weight-gradient + SGD) leaves W and bias bit-identical
+    to backward_weights + sgd, over two steps (the seed advances by one per step)."""
+    from haste_amd.step import FFITrainStep
+
+    B, D, O, G, F = 128, 768, 8193, 64, 128
+    x, W, bias, idx, dY, lddy, _, _ = setup(B, D, O, G, F, seed=5)
+    x_d, dY_d, idx_d = x.to(dev), dY.to(dev), idx.to(dev)
+    Wa, ba, Wb, bb = W.to(dev), bias.to(dev), W.to(dev), bias.to(dev)
+    sa = FFITrainStep(Wa, ba, idx_d, B, D, G, 0.05, 1e-4, seed=9)
+    sb = FFITrainStep(Wb, bb, idx_d, B, D, G, 0.05, 1e-4, seed=9)
+    for _ in range(2):
+        sa.step(x_d, dY_d, lddy)
+        sb.forward(x_d)
+        sb.backward(dY_d, lddy)
+        sb.sgd()
+    torch.cuda.synchronize()
+    assert sa.seed == sb.seed == 11
+    assert np.array_equal(bits(Wa), bits(Wb))
+    assert np.array_equal(bits(ba), bits(bb))
+    assert torch.equal(sa.dX, sb.dX)
