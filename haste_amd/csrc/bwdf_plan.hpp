@@ -1,0 +1,94 @@
+// Layout of the backward-to-features workspace ("plan" + transposed weights),
+// shared by the bwd-features kernels and the fused weight-gradient + SGD kernel,
+// which can refresh the transposed weights of the updated W for the next step.
+//
+// Per group g (Gc = ceil(O/G) groups), the distinct indices of idx[g, :] are
+// split by feature range (ndr ranges of Dc features) and laid out in tiles of
+// 16 positions; an index occurring k > 1 times gets a "hi" row in layer 0 and
+// a "lo" row in layer 1.  Workspace regions (byte offsets in BwdFPlan):
+//   tfeat  int32 [Gc, Tcap*16]  LDS byte offset of the position's feature row
+//   tsrc   int32 [Gc, Tcap*16]  (start << 10) | (count << 1) | lo: the position
+//                               sums W over slots perm[g*F + start .. +count)
+//   perm   int32 [Gc, F]        slots of the group sorted by index
+//   meta   int32 [Gc, ndr, 4]   tiles [tb, tm) layer 0, [tm, te) layer 1 per range
+//   twt    16-bit [Gc, Tcap*16, G]  W^T: row p = sum of W columns of position p
+//   partials fp32 [S, D, Bp]    per-slice partial sums of dX^T
+#pragma once
+
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace haste {
+
+constexpr int kAccPad = 4;         // fp32 words of padding per LDS row (bank spread)
+constexpr int kTrashRows = 16;     // LDS rows written by padding tile columns (one per column)
+constexpr int kAccBytes = 144 * 1024;  // LDS for the partial (incl. trash rows)
+constexpr int kTargetCTAs = 256;
+constexpr int kMaxRanges = 128;  // feature ranges per group handled by prep
+constexpr int kMetaStride = 4;   // ints per (group, range): tile begin, layer-1 begin, end
+
+__host__ __device__ constexpr int acc_stride(int bt) { return bt + kAccPad; }
+__host__ __device__ constexpr int max_dc(int bt) {
+    return kAccBytes / 4 / acc_stride(bt) - kTrashRows;
+}
+
+struct BwdFPlan {
+    int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;
+    int64_t tfeat_off, tsrc_off, perm_off, meta_off, twt_off, prep_bytes, ws_bytes;
+};
+
+inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
+    BwdFPlan p;
+    p.Gc = ceil_div(O, G);
+    p.BT = B <= 64 ? 64 : 128;
+    p.nbt = ceil_div(B, p.BT);
+    p.Bp = p.nbt * p.BT;
+    p.ndr = ceil_div(D, max_dc((int)p.BT));
+    p.Dc = ceil_div(D, p.ndr);
+    int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
+    S = std::min<int64_t>(S, std::max<int64_t>(1, ceil_div(p.Gc, 8)));
+    p.gps = ceil_div(p.Gc, S);
+    p.S = ceil_div(p.Gc, p.gps);
+    // tiles per group: layer 0 holds <= F distinct features, layer 1 <= F/2, and
+    // each non-empty range pads its layer to a multiple of 16
+    const int64_t r0 = std::min<int64_t>(p.ndr, F), r1 = std::min<int64_t>(p.ndr, F / 2);
+    p.Tcap = ceil_div(F + 15 * r0, 16) + ceil_div(F / 2 + 15 * r1, 16);
+    auto r256 = [](int64_t x) { return (x + 255) / 256 * 256; };
+    p.tfeat_off = 0;
+    p.tsrc_off = r256(p.Gc * p.Tcap * 16 * 4);
+    p.perm_off = p.tsrc_off + r256(p.Gc * p.Tcap * 16 * 4);
+    p.meta_off = p.perm_off + r256(p.Gc * F * 4);
+    p.twt_off = p.meta_off + r256(p.Gc * p.ndr * kMetaStride * 4);
+    p.prep_bytes = p.twt_off + r256(p.Gc * p.Tcap * 16 * G * 2);
+    p.ws_bytes = p.S * D * p.Bp * 4;
+    return p;
+}
+
+// One 16-byte chunk (labels lc .. lc+7 of the group) of the W^T row described by
+// src (a tsrc entry): a single W column, or for a duplicated index the 16-bit
+// rounding of the fp32 sum of its columns (ascending slot order) -- the "hi"
+// row -- or the rounding of the remainder -- the "lo" row; padding rows are 0.
+// wv(l, slot) returns the 16-bit pattern of W[l0 + l, slot].
+template <typename T, typename WV>
+__device__ __forceinline__ u32x4 wt_chunk(int src, const int* perm_g, WV wv, int lc) {
+    const int start = src >> 10, cnt = (src >> 1) & 511, lo = src & 1;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (cnt == 1) {
+        const int slot = perm_g[start];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) v[e >> 1] = wv(lc + e, slot) | (wv(lc + e + 1, slot) << 16);
+    } else if (cnt > 1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float sum = 0.0f;
+            for (int q = 0; q < cnt; ++q) sum += bits_to_f32<T>(wv(lc + e, perm_g[start + q]));
+            const uint32_t hb = f32_to_bits<T>(sum);
+            const uint32_t b = lo ? f32_to_bits<T>(sum - bits_to_f32<T>(hb)) : hb;
+            v[e >> 1] |= (e & 1) ? (b << 16) : b;
+        }
+    }
+    return v;
+}
+
+}  // namespace haste

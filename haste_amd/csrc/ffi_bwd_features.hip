@@ -34,7 +34,7 @@
 //     fused with the bf16 stochastic rounding of shared_ffi/bindings.py:44-48.
 #include <algorithm>
 
-#include "common.hpp"
+#include "bwdf_plan.hpp"
 
 #ifndef HASTE_BWDF_STATIC_TILES
 #define HASTE_BWDF_STATIC_TILES 0  // 1: always MAXT tile loads per ring slot (measured slower)
@@ -47,50 +47,6 @@ int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, 
 namespace {
 
 constexpr int kMainThreads = 256;  // 4 waves
-constexpr int kAccPad = 4;         // fp32 words of padding per LDS row (bank spread)
-constexpr int kTrashRows = 16;     // LDS rows written by padding tile columns (one per column)
-constexpr int kAccBytes = 144 * 1024;  // LDS for the partial (incl. trash rows)
-constexpr int kTargetCTAs = 256;
-constexpr int kMaxRanges = 128;  // feature ranges per group handled by prep
-constexpr int kMetaStride = 4;   // ints per (group, range): tile begin, layer-1 begin, end
-
-__host__ __device__ constexpr int acc_stride(int bt) { return bt + kAccPad; }
-__host__ __device__ constexpr int max_dc(int bt) {
-    return kAccBytes / 4 / acc_stride(bt) - kTrashRows;
-}
-
-struct BwdFPlan {
-    int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;
-    int64_t tfeat_off, tsrc_off, perm_off, meta_off, twt_off, prep_bytes, ws_bytes;
-};
-
-BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
-    BwdFPlan p;
-    p.Gc = ceil_div(O, G);
-    p.BT = B <= 64 ? 64 : 128;
-    p.nbt = ceil_div(B, p.BT);
-    p.Bp = p.nbt * p.BT;
-    p.ndr = ceil_div(D, max_dc((int)p.BT));
-    p.Dc = ceil_div(D, p.ndr);
-    int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
-    S = std::min<int64_t>(S, std::max<int64_t>(1, ceil_div(p.Gc, 8)));
-    p.gps = ceil_div(p.Gc, S);
-    p.S = ceil_div(p.Gc, p.gps);
-    // tiles per group: layer 0 holds <= F distinct features, layer 1 <= F/2, and
-    // each non-empty range pads its layer to a multiple of 16
-    const int64_t r0 = std::min<int64_t>(p.ndr, F), r1 = std::min<int64_t>(p.ndr, F / 2);
-    p.Tcap = ceil_div(F + 15 * r0, 16) + ceil_div(F / 2 + 15 * r1, 16);
-    auto r256 = [](int64_t x) { return (x + 255) / 256 * 256; };
-    p.tfeat_off = 0;
-    p.tsrc_off = r256(p.Gc * p.Tcap * 16 * 4);
-    p.perm_off = p.tsrc_off + r256(p.Gc * p.Tcap * 16 * 4);
-    p.meta_off = p.perm_off + r256(p.Gc * F * 4);
-    p.twt_off = p.meta_off + r256(p.Gc * p.ndr * kMetaStride * 4);
-    p.prep_bytes = p.twt_off + r256(p.Gc * p.Tcap * 16 * G * 2);
-    p.ws_bytes = p.S * D * p.Bp * 4;
-    return p;
-}
-
 // --------------------------------------------------------------- plan ------
 // Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*4 + 0..2]
 // = (tb, tm, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative to
@@ -231,23 +187,7 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
     constexpr int CH = G / 8;  // 16-byte chunks per row
     for (int it = tid; it < nrows * CH; it += 256) {
         const int row = it / CH, lc = (it % CH) * 8;
-        const int src = tsrc[(g * Tcap) * 16 + row];
-        const int start = src >> 10, cnt = (src >> 1) & 511, lo = src & 1;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (cnt == 1) {
-            const int slot = s_perm[start];
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) v[e >> 1] = wv(lc + e, slot) | (wv(lc + e + 1, slot) << 16);
-        } else if (cnt > 1) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float sum = 0.0f;
-                for (int q = 0; q < cnt; ++q) sum += bits_to_f32<T>(wv(lc + e, s_perm[start + q]));
-                const uint32_t hb = f32_to_bits<T>(sum);
-                const uint32_t b = lo ? f32_to_bits<T>(sum - bits_to_f32<T>(hb)) : hb;
-                v[e >> 1] |= (e & 1) ? (b << 16) : b;
-            }
-        }
+        const u32x4 v = wt_chunk<T>(tsrc[(g * Tcap) * 16 + row], s_perm, wv, lc);
         *reinterpret_cast<u32x4*>(twt + ((g * Tcap) * 16 + row) * G + lc) = v;
     }
 }
@@ -690,7 +630,7 @@ int check_bwdf(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, int64
     return HASTE_OK;
 }
 
-// Runs [plan +] gather + main; leaves the per-slice partials in the workspace.
+// Runs [plan +] [gather +] main; leaves the per-slice partials in the workspace.
 int run_partials(const char* fn, const int32_t* idx, const void* W, const void* dY, int64_t lddy,
                  void* workspace, int64_t workspace_bytes, int64_t B, int64_t D, int64_t F,
                  int64_t O, int64_t G, int32_t dtype, int32_t plan_ready, hipStream_t st,
@@ -703,6 +643,8 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
                     "%s: lddy must be >= O and a multiple of 8 (lddy=%lld O=%lld)", fn,
                     (long long)lddy, (long long)O);
     HASTE_CHECK_ARG(aligned16(W) && aligned16(dY), "%s: W and dY must be 16-byte aligned", fn);
+    HASTE_CHECK_ARG(plan_ready >= 0 && plan_ready <= 2, "%s: plan_ready must be 0, 1 or 2 (got %d)",
+                    fn, (int)plan_ready);
     char* base = static_cast<char*>(workspace);
     int* tfeat = reinterpret_cast<int*>(base + p.tfeat_off);
     int* tsrc = reinterpret_cast<int*>(base + p.tsrc_off);
@@ -719,18 +661,23 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
             acc_stride((int)p.BT) * 4, max_dc((int)p.BT));
         HASTE_CHECK_LAUNCH(fn);
     }
+    const bool gather = plan_ready != 2;
     switch (G) {
 #define HASTE_BWDF_G(GG)                                                                        \
     case GG:                                                                                    \
         if (dtype == HASTE_DTYPE_BF16) {                                                        \
-            bwdf_gather_kernel<BF16, GG><<<pgrid, dim3(256), 0, st>>>(                          \
-                w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);                  \
-            HASTE_CHECK_LAUNCH(fn);                                                             \
+            if (gather) {                                                                       \
+                bwdf_gather_kernel<BF16, GG><<<pgrid, dim3(256), 0, st>>>(                      \
+                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);              \
+                HASTE_CHECK_LAUNCH(fn);                                                         \
+            }                                                                                   \
             rc = run_main<BF16, GG>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);          \
         } else {                                                                                \
-            bwdf_gather_kernel<F16, GG><<<pgrid, dim3(256), 0, st>>>(                           \
-                w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);                  \
-            HASTE_CHECK_LAUNCH(fn);                                                             \
+            if (gather) {                                                                       \
+                bwdf_gather_kernel<F16, GG><<<pgrid, dim3(256), 0, st>>>(                       \
+                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);              \
+                HASTE_CHECK_LAUNCH(fn);                                                         \
+            }                                                                                   \
             rc = run_main<F16, GG>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);           \
         }                                                                                       \
         break;

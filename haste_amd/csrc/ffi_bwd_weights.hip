@@ -26,7 +26,7 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "common.hpp"
+#include "bwdf_plan.hpp"
 
 namespace haste {
 int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
@@ -75,7 +75,9 @@ __device__ __forceinline__ u32x4 keep_first(u32x4 v, int nv) {
     return v;
 }
 
-// Parameters of the fused SGD epilogue (unused when SGD == false).
+// Parameters of the fused SGD epilogue (unused when SGD == false).  twt != NULL:
+// also write W^T of the updated weights into the bwd-features workspace
+// (tsrc / perm / meta of its plan, Tcap tile rows per group).
 struct SgdArgs {
     uint16_t* W;
     uint16_t* bias;
@@ -84,6 +86,11 @@ struct SgdArgs {
     float lr, wd, mu;
     int use_mom, do_sr;
     uint32_t k0, k1;
+    uint16_t* twt;
+    const int* tsrc;
+    const int* perm;
+    const int* meta;
+    int ndr, Tcap;
 };
 
 // Two waves per SIMD (at most 256 registers each) hide the chunk pipeline's load
@@ -99,6 +106,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     using C = BwdWCfg<G, FP>;
     constexpr int MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SP = C::SP, PR = C::PR;
     __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
+    __shared__ int s_perm[SGD ? FP : 1];
     char (*Ys)[kKC * RB] = reinterpret_cast<char (*)[kKC * RB]>(lds);
     float* stg = reinterpret_cast<float*>(lds);
 
@@ -265,6 +273,11 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                                 dW != nullptr ? (int64_t)nl * F * esz : 0);
     const rsrc_t mr = make_rsrc(SGD && sg.use_mom ? sg.mW + l0 * F : nullptr,
                                 SGD && sg.use_mom ? (int64_t)nl * F * 4 : 0);
+    const bool do_wt = SGD && sg.twt != nullptr;
+    if constexpr (SGD) {
+        if (do_wt)
+            for (int j = tid; j < F; j += kThreads) s_perm[j] = sg.perm[g * F + j];
+    }
 #pragma unroll 1
     for (int p0 = 0; p0 < G; p0 += PR) {
         if (active) {
@@ -320,14 +333,35 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                     ob[k] = sgd_one_r(bf16_bits_to_f32(wb), gv[k], &mv[k], sg.use_mom, sg.lr,
                                       sg.wd, sg.mu, sg.do_sr, r);
                 }
-                buf_store16(u32x4{ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16),
-                                  ob[4] | (ob[5] << 16), ob[6] | (ob[7] << 16)},
-                            wr, in ? e * 2 : kOOB);
+                const u32x4 wn = u32x4{ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16),
+                                       ob[4] | (ob[5] << 16), ob[6] | (ob[7] << 16)};
+                buf_store16(wn, wr, in ? e * 2 : kOOB);
+                // the updated weights replace this thread's own staged gradients
+                // (the first 16 of its 32 bytes), for the W^T pass below
+                if (do_wt) *reinterpret_cast<u32x4*>(&stg[(lr - p0) * SP + j0]) = wn;
                 if (sg.use_mom) {
                     buf_store16(__builtin_bit_cast(u32x4, f32x4{mv[0], mv[1], mv[2], mv[3]}), mr,
                                 in ? e * 4 : kOOB);
                     buf_store16(__builtin_bit_cast(u32x4, f32x4{mv[4], mv[5], mv[6], mv[7]}), mr,
                                 in ? e * 4 + 16 : kOOB);
+                }
+            }
+        }
+        if constexpr (SGD) {
+            if (do_wt) {
+                // W^T tile rows of this group, labels [p0, p0 + PR): 16-byte chunks
+                // of 8 labels, as the bwd-features gather kernel builds them
+                __syncthreads();
+                auto wv = [&](int l, int slot) -> uint32_t {
+                    return reinterpret_cast<const uint16_t*>(
+                        &stg[(l - p0) * SP + (slot >> 3) * 8])[slot & 7];
+                };
+                const int nrows = sg.meta[(g * sg.ndr + sg.ndr - 1) * kMetaStride + 2] * 16;
+                const int64_t rbase = g * sg.Tcap * 16;
+                for (int it = tid; it < nrows * (PR / 8); it += kThreads) {
+                    const int row = it / (PR / 8), lc = p0 + (it % (PR / 8)) * 8;
+                    const u32x4 v = wt_chunk<BF16>(sg.tsrc[rbase + row], s_perm, wv, lc);
+                    *reinterpret_cast<u32x4*>(sg.twt + (rbase + row) * G + lc) = v;
                 }
             }
         }
@@ -431,7 +465,8 @@ extern "C" int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int
                                          uint16_t* bias, float* m_W, float* m_bias, void* dW,
                                          int32_t dW_dtype, void* dbias, int32_t dbias_dtype,
                                          float lr, float wd, float mu, int32_t use_mom,
-                                         int32_t do_sr, uint64_t seed, int64_t B, int64_t D,
+                                         int32_t do_sr, uint64_t seed, void* bwdf_workspace,
+                                         int64_t bwdf_workspace_bytes, int64_t B, int64_t D,
                                          int64_t F, int64_t O, int64_t G, int32_t dtype,
                                          void* stream) {
     const char* fn = "haste_ffi_bwd_weights_sgd";
@@ -449,8 +484,23 @@ extern "C" int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int
     HASTE_CHECK_ARG(!use_mom || (m_W != nullptr && haste::aligned16(m_W) &&
                                  (bias == nullptr || m_bias != nullptr)),
                     "%s: momentum buffers missing or misaligned", fn);
-    const haste::SgdArgs sg{W, bias, m_W, m_bias, lr, wd, mu, use_mom ? 1 : 0, do_sr ? 1 : 0,
-                            (uint32_t)seed, (uint32_t)(seed >> 32)};
+    haste::SgdArgs sg{W, bias, m_W, m_bias, lr, wd, mu, use_mom ? 1 : 0, do_sr ? 1 : 0,
+                      (uint32_t)seed, (uint32_t)(seed >> 32), nullptr, nullptr, nullptr, nullptr,
+                      0, 0};
+    if (bwdf_workspace != nullptr) {
+        const haste::BwdFPlan p = haste::make_plan(B, D, F, O, G);
+        HASTE_CHECK_ARG(haste::aligned16(bwdf_workspace) &&
+                            bwdf_workspace_bytes >= p.prep_bytes + p.ws_bytes,
+                        "%s: bwd-features workspace too small or misaligned (%lld bytes, need %lld)",
+                        fn, (long long)bwdf_workspace_bytes, (long long)(p.prep_bytes + p.ws_bytes));
+        char* base = static_cast<char*>(bwdf_workspace);
+        sg.twt = reinterpret_cast<uint16_t*>(base + p.twt_off);
+        sg.tsrc = reinterpret_cast<const int*>(base + p.tsrc_off);
+        sg.perm = reinterpret_cast<const int*>(base + p.perm_off);
+        sg.meta = reinterpret_cast<const int*>(base + p.meta_off);
+        sg.ndr = (int)p.ndr;
+        sg.Tcap = (int)p.Tcap;
+    }
     return haste::dispatch<haste::BF16, true>(idx, static_cast<const uint16_t*>(xT), ldx,
                                               static_cast<const uint16_t*>(dY), lddy, dW, dW_dtype,
                                               dbias, dbias_dtype, B, D, F, O, G, sg,

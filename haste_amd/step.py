@@ -46,6 +46,10 @@ class FFITrainStep:
         self.ws = _C.bwd_features_workspace(self.B, self.D, self.F, self.O, self.G,
                                             torch.bfloat16, dev)
         self._plan_version = None  # idx._version the workspace plan was made for
+        # W._version for which the workspace holds W^T of the current weights
+        # (written by backward_features, or by backward_weights_sgd for the weights
+        # it updates); None when stale
+        self._wt_version = None
         self.code = _lib.DTYPE_BF16
         self.gcode = _C.dtype_code(grad_dtype)
         self._sgd_args = None
@@ -105,13 +109,17 @@ class FFITrainStep:
     def backward_features(self, dY: torch.Tensor, lddy: int) -> None:
         """dX [B, D] bf16 = SR(feature gradient, seed 123) (bindings.py:44-48)."""
         self._check_dY(dY, lddy)
-        # the index plan depends on idx only: rebuilt when idx changes (rewire)
-        ready = int(self._plan_version == self.idx._version)
+        # the index plan depends on idx only: rebuilt when idx changes (rewire);
+        # W^T is reused when the last fused weight update wrote it for these weights
+        ready = 0
+        if self._plan_version == self.idx._version:
+            ready = 2 if self._wt_version == self.W._version else 1
         _lib.call("haste_ffi_bwd_features_sr", self.idx.data_ptr(), self.W.data_ptr(),
                   dY.data_ptr(), lddy, self.dX.data_ptr(), SR_SEED_GRAD_X, self.ws.data_ptr(),
                   self.ws.numel(), self.B, self.D, self.F, self.O, self.G, self.code, ready,
                   _C.stream_of(self.W))
         self._plan_version = self.idx._version
+        self._wt_version = self.W._version
 
     def backward_weights(self, dY: torch.Tensor, lddy: int) -> None:
         """dW [O, F] and dbias [O] in grad_dtype."""
@@ -135,6 +143,7 @@ class FFITrainStep:
         self._sgd_args[-2] = self.seed
         self._sgd_args[-1] = _C.stream_of(self.W)
         _lib.call("haste_sgd_sr_step_multi", *self._sgd_args)
+        self._wt_version = None  # W changed, W^T not refreshed
         self.seed += 1
 
     def backward_weights_sgd(self, dY: torch.Tensor, lddy: int) -> None:
@@ -145,11 +154,16 @@ class FFITrainStep:
         if self.grad_dtype != torch.float32:
             raise ValueError("FFITrainStep.backward_weights_sgd: the fused update uses fp32 "
                              "gradients (grad_dtype=torch.float32)")
+        # refresh W^T in the bwd-features workspace when its plan matches idx
+        plan_ok = self._plan_version == self.idx._version
         _lib.call("haste_ffi_bwd_weights_sgd", self.idx.data_ptr(), self.xT_buf.data_ptr(),
                   self.ldx, dY.data_ptr(), lddy, self.W.data_ptr(),
                   None if self.bias is None else self.bias.data_ptr(), None, None, None,
                   _lib.DTYPE_F32, None, _lib.DTYPE_F32, self.lr, self.wd, 0.0, 0, 1, self.seed,
+                  self.ws.data_ptr() if plan_ok else None, self.ws.numel() if plan_ok else 0,
                   self.B, self.D, self.F, self.O, self.G, self.code, _C.stream_of(self.W))
+        # the kernel writes W in place (torch's version counter does not move)
+        self._wt_version = self.W._version if plan_ok else None
         self.seed += 1
 
     def step(self, x: torch.Tensor, dY: torch.Tensor, lddy: int) -> None:

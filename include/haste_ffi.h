@@ -81,7 +81,10 @@ int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace, int64_t wor
  * Backward to features, deterministic (no float atomics on any global buffer):
  *   dXT[d, b] = sum_{g,j: idx[g,j] = d} sum_{l in g} W[l, j] * dY[b, l]     (fp32 [D, B])
  * plan_ready = 0 computes the plan in this call; 1 reuses the plan already in
- * the workspace (see haste_ffi_bwd_features_plan).
+ * the workspace (see haste_ffi_bwd_features_plan); 2 also reuses the
+ * transposed weights in the workspace, valid when W has not changed since the
+ * call that wrote them (a bwd-features call, or haste_ffi_bwd_weights_sgd with
+ * this workspace, which writes those of the weights it updates).
  * Replaces ffi_backward_features_cuda (shared_ffi/ffi_backward_features.cu:417-633,
  * bound at shared_ffi/ffi_wrapper.cpp:7-12,29).
  */
@@ -122,7 +125,10 @@ int haste_ffi_bwd_weights(const int32_t* idx, const void* xT, int64_t ldx, const
  * dW, dbias) followed by haste_sgd_sr_step_multi over {W, bias}.  The gradients
  * are also stored when dW / dbias are non-NULL.  bias may be NULL (no bias);
  * m_W [O, F] and m_bias [O] are fp32 momentum buffers read when use_mom.
- * dtype must be bf16.  Replaces, for one FFI layer, ffi_backward_weights_cuda
+ * bwdf_workspace (may be NULL): a haste_ffi_bwd_features workspace holding the
+ * plan for the current idx; the kernel then also writes into it the transposed
+ * weights of the UPDATED W, so the next haste_ffi_bwd_features[_sr] call may
+ * pass plan_ready = 2.  dtype must be bf16; O*F < 2^32.  Replaces, for one FFI layer, ffi_backward_weights_cuda
  * (shared_ffi/ffi_backward_weights.cu:486-684) + torch.sum(grad_output, 0)
  * (shared_ffi/bindings.py:40) + SRSgd.step's sgd_update calls on the layer's
  * weights and bias (shared_ffi/optim_sr.py:64-112, shared_ffi/sr_triton.py:172-213).
@@ -131,7 +137,8 @@ int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx, c
                               int64_t lddy, uint16_t* W, uint16_t* bias, float* m_W,
                               float* m_bias, void* dW, int32_t dW_dtype, void* dbias,
                               int32_t dbias_dtype, float lr, float wd, float mu, int32_t use_mom,
-                              int32_t do_sr, uint64_t seed, int64_t B, int64_t D, int64_t F,
+                              int32_t do_sr, uint64_t seed, void* bwdf_workspace,
+                              int64_t bwdf_workspace_bytes, int64_t B, int64_t D, int64_t F,
                               int64_t O, int64_t G, int32_t dtype, void* stream);
 
 /*

@@ -112,7 +112,7 @@ def test_python_api_rejects_cpu_tensors():
 def _bwdw_sgd(**kw):
     args = dict(idx=16, xT=16, ldx=64, dY=32, lddy=4096, W=48, bias=None, mW=None, mb=None,
                 dW=None, dW_dtype=_lib.DTYPE_F32, dbias=None, dbias_dtype=_lib.DTYPE_F32,
-                lr=0.05, wd=1e-4, mu=0.0, use_mom=0, do_sr=1, seed=42, B=64, D=768, F=32, O=4096,
+                lr=0.05, wd=1e-4, mu=0.0, use_mom=0, do_sr=1, seed=42, ws=None, ws_bytes=0, B=64, D=768, F=32, O=4096,
                 G=32, dtype=_lib.DTYPE_BF16, stream=None)
     args.update(kw)
     return _lib.lib().haste_ffi_bwd_weights_sgd(*args.values())
@@ -125,3 +125,4 @@ def test_bwd_weights_sgd_rejects_bad_arguments():
     assert _bwdw_sgd(W=None) == _lib.HASTE_ERR_INVALID_ARG
     assert _bwdw_sgd(G=48) == _lib.HASTE_ERR_UNSUPPORTED
     assert _bwdw_sgd(lddy=4092) == _lib.HASTE_ERR_INVALID_ARG
+    assert _bwdw_sgd(ws=64, ws_bytes=16) == _lib.HASTE_ERR_INVALID_ARG  # workspace too small

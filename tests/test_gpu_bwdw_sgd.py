@@ -78,7 +78,7 @@ def test_fused_matches_separate_and_oracle(dev, B, D, O, G, F, has_bias, use_mom
               lddy, W2.data_ptr(), b2.data_ptr() if has_bias else None,
               mW2.data_ptr() if use_mom else None, mb2.data_ptr() if use_mom else None,
               dW2.data_ptr(), _lib.DTYPE_F32, db2.data_ptr(), _lib.DTYPE_F32, lr, wd, mu,
-              int(use_mom), int(do_sr), seed, B, D, F, O, G, _lib.DTYPE_BF16, st)
+              int(use_mom), int(do_sr), seed, None, 0, B, D, F, O, G, _lib.DTYPE_BF16, st)
     torch.cuda.synchronize()
 
     assert torch.equal(dW2, dW), "fused kernel's fp32 dW differs from haste_ffi_bwd_weights"
@@ -105,24 +105,27 @@ def test_fused_matches_separate_and_oracle(dev, B, D, O, G, F, has_bias, use_mom
         assert np.array_equal(mW2.cpu().numpy().reshape(-1), m_ref)
 
 
-def test_train_step_fused_equals_unfused(dev):
-    """FFITrainStep.step (fused weight-gradient + SGD) leaves W and bias bit-identical
-    to backward_weights + sgd, over two steps (the seed advances by one per step)."""
+@pytest.mark.parametrize("B,D,O,G,F", [(128, 768, 8193, 64, 128), (72, 500, 3001, 32, 64)])
+def test_train_step_fused_equals_unfused(dev, B, D, O, G, F):
+    """FFITrainStep.step (fused weight-gradient + SGD, which also hands the next
+    step's bwd-features the transposed updated weights) gives dX, W and bias
+    bit-identical to backward + sgd (which rebuild W^T every step), step by
+    step; idx is drawn with replacement, so duplicated indices (hi/lo W^T rows)
+    occur."""
     from haste_amd.step import FFITrainStep
 
-    B, D, O, G, F = 128, 768, 8193, 64, 128
     x, W, bias, idx, dY, lddy, _, _ = setup(B, D, O, G, F, seed=5)
     x_d, dY_d, idx_d = x.to(dev), dY.to(dev), idx.to(dev)
     Wa, ba, Wb, bb = W.to(dev), bias.to(dev), W.to(dev), bias.to(dev)
     sa = FFITrainStep(Wa, ba, idx_d, B, D, G, 0.05, 1e-4, seed=9)
     sb = FFITrainStep(Wb, bb, idx_d, B, D, G, 0.05, 1e-4, seed=9)
-    for _ in range(2):
+    for step in range(3):
         sa.step(x_d, dY_d, lddy)
         sb.forward(x_d)
         sb.backward(dY_d, lddy)
         sb.sgd()
-    torch.cuda.synchronize()
-    assert sa.seed == sb.seed == 11
-    assert np.array_equal(bits(Wa), bits(Wb))
-    assert np.array_equal(bits(ba), bits(bb))
-    assert torch.equal(sa.dX, sb.dX)
+        torch.cuda.synchronize()
+        assert torch.equal(sa.dX, sb.dX), f"dX differs at step {step}"
+        assert np.array_equal(bits(Wa), bits(Wb)), f"W differs at step {step}"
+        assert np.array_equal(bits(ba), bits(bb))
+    assert sa.seed == sb.seed == 12
