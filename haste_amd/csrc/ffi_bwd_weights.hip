@@ -278,6 +278,20 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
         if (do_wt)
             for (int j = tid; j < F; j += kThreads) s_perm[j] = sg.perm[g * F + j];
     }
+    // W^T chunk it = tid + k*256 (k < kWtPre) is tile row it / (PR/8) of the group:
+    // its tsrc entry is loaded here, long before the W^T pass needs it
+    constexpr int kWtPre = 8;
+    int wsrc[SGD ? kWtPre : 1];
+    int wt_rows = 0;
+    if constexpr (SGD) {
+        if (do_wt) {
+            wt_rows = sg.meta[(g * sg.ndr + sg.ndr - 1) * kMetaStride + 2] * 16;
+            const rsrc_t tr = make_rsrc(sg.tsrc + g * sg.Tcap * 16, (int64_t)sg.Tcap * 16 * 4);
+#pragma unroll
+            for (int k = 0; k < kWtPre; ++k)
+                wsrc[k] = (int)buf_load4(tr, (uint32_t)((tid + k * kThreads) / (PR / 8)) * 4);
+        }
+    }
 #pragma unroll 1
     for (int p0 = 0; p0 < G; p0 += PR) {
         if (active) {
@@ -356,9 +370,18 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                     return reinterpret_cast<const uint16_t*>(
                         &stg[(l - p0) * SP + (slot >> 3) * 8])[slot & 7];
                 };
-                const int nrows = sg.meta[(g * sg.ndr + sg.ndr - 1) * kMetaStride + 2] * 16;
                 const int64_t rbase = g * sg.Tcap * 16;
-                for (int it = tid; it < nrows * (PR / 8); it += kThreads) {
+                const int nch = wt_rows * (PR / 8);
+#pragma unroll
+                for (int k = 0; k < kWtPre; ++k) {
+                    const int it = tid + k * kThreads;
+                    if (it < nch) {
+                        const int row = it / (PR / 8), lc = p0 + (it % (PR / 8)) * 8;
+                        const u32x4 v = wt_chunk<BF16>(wsrc[k], s_perm, wv, lc);
+                        *reinterpret_cast<u32x4*>(sg.twt + (rbase + row) * G + lc) = v;
+                    }
+                }
+                for (int it = tid + kWtPre * kThreads; it < nch; it += kThreads) {
                     const int row = it / (PR / 8), lc = p0 + (it % (PR / 8)) * 8;
                     const u32x4 v = wt_chunk<BF16>(sg.tsrc[rbase + row], s_perm, wv, lc);
                     *reinterpret_cast<u32x4*>(sg.twt + (rbase + row) * G + lc) = v;
