@@ -21,16 +21,27 @@
 
 namespace haste {
 
-constexpr int kAccPad = 4;         // fp32 words of padding per LDS row (bank spread)
-constexpr int kTrashRows = 16;     // LDS rows written by padding tile columns (one per column)
-constexpr int kAccBytes = 144 * 1024;  // LDS for the partial (incl. trash rows)
+constexpr int kAccPad = 4;        // fp32 words of padding per LDS partial row (bank spread)
+constexpr int kTrashRows = 4;     // LDS partial rows that padding tile columns add into
 constexpr int kTargetCTAs = 256;
-constexpr int kMaxRanges = 128;  // feature ranges per group handled by prep
-constexpr int kMetaStride = 4;   // ints per (group, range): tile begin, layer-1 begin, end
+constexpr int kMaxRanges = 128;   // feature ranges per group handled by the plan kernel
+constexpr int kMetaStride = 4;    // ints per (group, range): tile begin, layer-1 begin, end
+constexpr int kLdsBytes = 160 * 1024;
+constexpr int kLdsMisc = 1024;    // LDS the main kernel keeps for other things
 
+// The main kernel stages each group's W^T tiles (and their partial-row offsets)
+// in a double-buffered LDS ring of ring_tiles(G) tiles of 16 rows; a W^T row is
+// 2G bytes, stored with 32 bytes of padding (conflict-free 16-byte reads of 16
+// rows).  Ranges with more tiles take the rest from global memory.
+__host__ __device__ constexpr int ring_tiles(int G) { return G <= 16 ? 8 : G <= 32 ? 6 : G <= 64 ? 4 : 2; }
+__host__ __device__ constexpr int ring_row_bytes(int G) { return 2 * G + 32; }
+__host__ __device__ constexpr int ring_bytes(int G) {
+    return 2 * ring_tiles(G) * 16 * (ring_row_bytes(G) + 4);
+}
 __host__ __device__ constexpr int acc_stride(int bt) { return bt + kAccPad; }
-__host__ __device__ constexpr int max_dc(int bt) {
-    return kAccBytes / 4 / acc_stride(bt) - kTrashRows;
+// Features per range: the LDS partial holds (Dc + kTrashRows) rows of bt fp32.
+__host__ __device__ constexpr int max_dc(int bt, int G) {
+    return (kLdsBytes - kLdsMisc - ring_bytes(G)) / 4 / acc_stride(bt) - kTrashRows;
 }
 
 struct BwdFPlan {
@@ -44,7 +55,7 @@ inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G)
     p.BT = B <= 64 ? 64 : 128;
     p.nbt = ceil_div(B, p.BT);
     p.Bp = p.nbt * p.BT;
-    p.ndr = ceil_div(D, max_dc((int)p.BT));
+    p.ndr = ceil_div(D, max_dc((int)p.BT, (int)G));
     p.Dc = ceil_div(D, p.ndr);
     int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
     S = std::min<int64_t>(S, std::max<int64_t>(1, ceil_div(p.Gc, 8)));

@@ -34,11 +34,10 @@
 //     fused with the bf16 stochastic rounding of shared_ffi/bindings.py:44-48.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "bwdf_plan.hpp"
 
-#ifndef HASTE_BWDF_STATIC_TILES
-#define HASTE_BWDF_STATIC_TILES 0  // 1: always MAXT tile loads per ring slot (measured slower)
-#endif
 
 namespace haste {
 int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
@@ -46,13 +45,12 @@ int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, 
 
 namespace {
 
-constexpr int kMainThreads = 256;  // 4 waves
 // --------------------------------------------------------------- plan ------
 // Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*4 + 0..2]
 // = (tb, tm, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative to
 // g*Tcap); meta[(g*ndr + ndr-1)*4 + 2] is the group's tile count.  For tile row
 // (t, p): tfeat = byte offset of the feature's row in the main kernel's LDS
-// partial, (feature - r*Dc) * row_bytes, or (trash_row + p) * row_bytes for
+// partial, (feature - r*Dc) * row_bytes, or (trash_row + p % kTrashRows) * row_bytes for
 // padding; tsrc = (start << 10) |
 // (count << 1) | lo: the row sums W over slots perm[g*F + start ..
 // start+count) (count 0 = padding); lo selects the remainder row.
@@ -149,7 +147,7 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         const int tl0 = s_tile[rr][lay1 ? 1 : 0];
         const int nt = (lay1 ? s_tile[rr][2] : s_tile[rr][1]) - tl0;
         if (p * nt + (t - tl0) < used) continue;
-        tfeat[(tbase + t) * 16 + p] = (trash_row + p) * row_bytes;
+        tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
         tsrc[(tbase + t) * 16 + p] = 0;
     }
 }
@@ -193,39 +191,52 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
 }
 
 // --------------------------------------------------------------- main ------
-template <int G, int RPW, int FP>
+// A workgroup owns (group slice s, feature range r, batch tile of BT = 16*WAVES
+// columns) and keeps dXT[range, tile] as an fp32 partial in LDS.  Wave w owns
+// batch rows [16w, 16w+16) of the tile, so no two waves touch the same LDS
+// word of the partial.  Per group:
+//  - the group's W^T tiles for the range (and the partial-row offsets of their
+//    positions) are staged once into a double-buffered LDS ring, shared by all
+//    waves: each thread copies 16-byte chunks loaded two groups ahead;
+//  - each wave multiplies its dY rows (16 x G, loaded one group ahead) with
+//    the tiles (MFMA, M = batch rows, N = 16 positions, K = labels); a lane then
+//    holds four consecutive batch values of one position and adds them into
+//    the partial row of the position's feature with one 16-byte read and one
+//    16-byte write.  Within a layer the tiles' features are distinct, so all
+//    reads of a layer are issued before its writes; a wave's LDS accesses
+//    complete in order, so layer 1 (the second rows of duplicated indices)
+//    and later groups see the earlier writes.  Padding positions add into
+//    trash rows that are never read.
+//  - one barrier per group publishes the next group's ring buffer.
+// Ranges holding more than RT tiles in a group process the rest in further
+// rounds staged synchronously (rare: a range's share of F is usually ~F/ndr).
+template <int G, int WAVES>
 struct BwdFCfg {
     static constexpr int KS = G >= 32 ? G / 32 : 1;  // MFMA k-steps over labels
-    static constexpr int MT = RPW / 16;              // 16-row batch tiles per wave
-    static constexpr int BT = 4 * RPW;               // batch columns per workgroup
+    static constexpr int BT = 16 * WAVES;            // batch columns per workgroup
     static constexpr int AS = acc_stride(BT);
-    static constexpr int NS = G >= 128 ? 2 : 3;      // groups in flight per wave
-    // tiles per group kept in registers (a range's usual share of F, padded)
-    static constexpr int MAXT = FP >= 256 ? 6 : FP >= 128 ? 4 : 3;
+    static constexpr int RT = ring_tiles(G);
+    static constexpr int RB = ring_row_bytes(G);
+    static constexpr int RING = RT * 16 * RB;        // bytes per ring buffer
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int CH = G / 8;                 // 16-byte chunks per W^T row
+    static constexpr int SPT = (RT * 16 * CH + THREADS - 1) / THREADS;  // staged chunks per thread
+    static constexpr int DCMAX = max_dc(BT, G);
+    static_assert(DCMAX > 0, "LDS budget");
 };
 
-template <int KS, int MT, int MAXT>
-struct BwdFRegs {
-    u32x4 a[MT][KS];    // dY rows of the wave (A operand)
-    u32x4 b[MAXT][KS];  // tile rows (B operand)
-    int f[MAXT];        // LDS byte offset of this lane's tile column (feature row)
-    int tb, tm, te;     // tiles of the group's range (relative to the group base)
-};
-
-// Per-wave LDS ring of group tile ranges: kMetaChunk groups per chunk, two chunks.
-constexpr int kMetaChunk = 64;
-constexpr int kMetaInts = kMainThreads / 64 * 2 * kMetaChunk * 2;
-
-template <typename T, int G, int RPW, int FP>
-__global__ __launch_bounds__(kMainThreads) void bwdf_main_kernel(
+template <typename T, int G, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
     const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
     int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
-    using C = BwdFCfg<G, RPW, FP>;
-    constexpr int KS = C::KS, MT = C::MT, BT = C::BT, AS = C::AS, NS = C::NS, MAXT = C::MAXT;
-    using R = BwdFRegs<KS, MT, MAXT>;
-    __shared__ __attribute__((aligned(16))) float acc[(max_dc(BT) + kTrashRows) * AS];
-    __shared__ __attribute__((aligned(16))) int s_meta[kMetaInts];
+    using C = BwdFCfg<G, WAVES>;
+    constexpr int KS = C::KS, BT = C::BT, AS = C::AS, RT = C::RT, RB = C::RB, CH = C::CH;
+    constexpr int SPT = C::SPT, NTH = C::THREADS;
+    __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
+    __shared__ __attribute__((aligned(16))) char ring[2][C::RING];
+    __shared__ int fring[2][RT * 16];
+    __shared__ int rmeta[2][2];
 
     const int64_t work = xcd_remap(blockIdx.x, (int64_t)S * ndr * nbt);
     if (work < 0) return;
@@ -236,288 +247,231 @@ __global__ __launch_bounds__(kMainThreads) void bwdf_main_kernel(
     const int dn = min(Dc, D - d_lo);
     const int64_t g_lo = (int64_t)s * gps;
     const int64_t g_hi = min<int64_t>(Gc, g_lo + gps);
-    const int64_t g_full = min<int64_t>(g_hi, O / G);  // groups before it have G labels
+    const int ng = (int)(g_hi - g_lo);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int col = lane & 15;  // A row within an M tile / B column (tile position)
+    const int col = lane & 15;  // A row within the M tile / B column (tile position)
     const int kq = lane >> 4;   // which 8 of the 32 K elements
     const bool kq_ok = G >= 32 || kq < 2;
-
-    for (int i = tid * 4; i < dn * AS; i += kMainThreads * 4)
-        *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
-    __syncthreads();
-
-    // this lane's dY rows (clamped: rows >= B only feed partial columns never read)
-    const uint16_t* yrow[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int b = min(bt * BT + wave * RPW + mt * 16 + col, B - 1);
-        yrow[mt] = dY + (int64_t)b * lddy;
-    }
     const int kofs = kq_ok ? kq * 8 : 0;
-    char* const acc_b = reinterpret_cast<char*>(acc) + (wave * RPW + kq * 4) * 4;
+    const int trash_f = (C::DCMAX + (col & (kTrashRows - 1))) * AS * 4;
 
-    // Tile ranges (tb, tm, te) of the slice's groups reach the wave through a
-    // per-wave LDS ring (lane L loads group c*64 + L of chunk c), so that reading
-    // them is an in-order LDS access like the partial's reads and writes.
-    // Entries are packed to two ints, (tb | tm << 16, te), both of which are used.
-    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-    int* const my_meta = s_meta + wave * 2 * kMetaChunk * 2;
-    auto meta_chunk = [&](int64_t c) {
-        const int64_t g = g_lo + c * kMetaChunk + lane;
-        return *reinterpret_cast<const i32x4*>(meta + (min<int64_t>(g, g_hi - 1) * ndr + r) *
-                                                           kMetaStride);
-    };
-    auto put_chunk = [&](int64_t c, i32x4 v) {
-        *reinterpret_cast<i32x2*>(my_meta + ((c & 1) * kMetaChunk + lane) * 2) =
-            i32x2{v[0] | (v[1] << 16), v[2]};
-    };
-    auto read_meta = [&](int64_t i) {  // i = g - g_lo
-        return *reinterpret_cast<const i32x2*>(
-            my_meta + (((i / kMetaChunk) & 1) * kMetaChunk + i % kMetaChunk) * 2);
-    };
-    auto unpack_meta = [&](R& x, i32x2 m) {
-        const int m0 = __builtin_amdgcn_readfirstlane(m[0]);
-        x.tb = m0 & 0xFFFF;
-        x.tm = m0 >> 16;
-        x.te = __builtin_amdgcn_readfirstlane(m[1]);
-    };
+    for (int i = tid * 4; i < dn * AS; i += NTH * 4)
+        *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // tile rows of a group (tb/te set); slots past the range's last tile point at
-    // this lane's trash row (their MFMA results are added there and never read)
-    const int trash_f = (max_dc(BT) + col) * AS * 4;
-    auto load_tiles = [&](R& x, int64_t g) {
-        const int64_t tbase = g * Tcap + x.tb;
-        const int nt = x.te - x.tb;
-#if HASTE_BWDF_STATIC_TILES
-        // always MAXT tile loads (slots past the last tile re-read it: L1 hits), so
-        // the compiler knows how many loads follow each ring slot's
+    // dY of this lane's row (rows >= B read as zero; labels >= O are masked at use)
+    const int b0 = bt * BT;
+    const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy,
+                                ((int64_t)(min(BT, B - b0) - 1) * lddy + (O + 7) / 8 * 8) * 2);
+    const int64_t yoff = (int64_t)(wave * 16 + col) * lddy + kofs;
+    auto load_y = [&](int64_t g, u32x4 (&a)[KS]) {
 #pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            const int64_t row = (tbase + max(0, min(t, nt - 1))) * 16 + col;
+        for (int ks = 0; ks < KS; ++ks)
+            a[ks] = buf_load16(yr, kq_ok ? (uint32_t)((yoff + g * G + ks * 32) * 2) : kOOB);
+    };
+    auto mask_y = [&](int64_t g, u32x4 (&a)[KS]) {  // labels >= O (last group) -> 0
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int64_t nv = O - (g * G + ks * 32 + kofs);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                a[ks][e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
+        }
+    };
+
+    // Tile range (tb, tm, te) of group g in range r: tb | tm << 16, te.
+    auto load_meta = [&](int64_t g) -> u32x2 {
+        // a vector load (the same address in every lane), consumed an iteration
+        // later through uniform_meta
+        typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+        const i32x4 m = *reinterpret_cast<const i32x4*>(
+            meta + (min<int64_t>(g, g_hi - 1) * ndr + r) * kMetaStride);
+        return u32x2{(uint32_t)(m[0] | (m[1] << 16)), (uint32_t)m[2]};
+    };
+    // the same in every lane: made wave-uniform (it decides branches with barriers)
+    auto uniform_meta = [](u32x2 m) -> u32x2 {
+        return u32x2{(uint32_t)__builtin_amdgcn_readfirstlane((int)m[0]),
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)m[1])};
+    };
+    // Stage tiles [tb + t0, tb + t0 + RT) of group g into registers: W^T chunks
+    // and the positions' partial-row offsets (past the range's tiles: zero W^T
+    // rows, trash offsets).
+    struct Stage {
+        u32x4 w[SPT];
+        int f;
+    };
+    auto load_stage = [&](int64_t g, u32x2 mv, int t0, Stage& st) {
+        const u32x2 m = uniform_meta(mv);
+        // wave-uniform (SGPR) values, so the buffer descriptors below are scalar
+        const int tb = __builtin_amdgcn_readfirstlane((int)(m[0] & 0xFFFF) + t0);
+        const int nrow = __builtin_amdgcn_readfirstlane(max(0, min(RT, (int)m[1] - tb)) * 16);
+        const int64_t row0 = ((int64_t)__builtin_amdgcn_readfirstlane((int)g) * Tcap + tb) * 16;
+        const rsrc_t wr = make_rsrc(twt + row0 * G, (int64_t)nrow * G * 2);
+#pragma unroll
+        for (int k = 0; k < SPT; ++k) {
+            const int c = tid + k * NTH;
+            st.w[k] = buf_load16(wr, c < RT * 16 * CH ? (uint32_t)c * 16 : kOOB);
+        }
+        const rsrc_t fr = make_rsrc(tfeat + row0, (int64_t)nrow * 4);
+        st.f = (int)buf_load4(fr, tid < RT * 16 ? (uint32_t)tid * 4 : kOOB);
+        st.f = tid < nrow ? st.f : -1;
+    };
+    auto store_stage = [&](int buf, const Stage& st, u32x2 mv, int t0) {
+        const u32x2 m = uniform_meta(mv);
+#pragma unroll
+        for (int k = 0; k < SPT; ++k) {
+            const int c = tid + k * NTH;
+            if (c < RT * 16 * CH)
+                *reinterpret_cast<u32x4*>(&ring[buf][(c / CH) * RB + (c % CH) * 16]) = st.w[k];
+        }
+        if (tid < RT * 16) fring[buf][tid] = st.f >= 0 ? st.f : (C::DCMAX + (tid & (kTrashRows - 1))) * AS * 4;
+        if (tid == 0) {
+            const int tb = (int)(m[0] & 0xFFFF) + t0;
+            rmeta[buf][0] = max(0, (int)(m[0] >> 16) - tb);  // layer-0 tiles of this round
+            rmeta[buf][1] = max(0, min(RT, (int)m[1] - tb));  // tiles of this round
+        }
+    };
+
+    // Batch columns of a partial row are permuted: the 4 columns a lane adds (its
+    // wave's rows 4kq .. 4kq+3) sit at column (kq & 1) * BT/2 + 8*wave + 4*(kq >> 1),
+    // so in one 16-byte RMW instruction the lanes of kq = 0 and 1 are 256 bytes
+    // apart: reads (32 lanes, 512-byte bank window) and writes (16 lanes, 256
+    // bytes) are conflict-free when a tile's features differ mod 16, which the
+    // plan's dealing arranges.
+    auto perm_col = [](int w, int q) { return (q & 1) * (BT / 2) + w * 8 + (q >> 1) * 4; };
+    char* const acc_b = reinterpret_cast<char*>(acc) + perm_col(wave, kq) * 4;
+    // Multiply-accumulate the staged round in ring[buf] with dY fragments a.
+    // The round's tiles are processed by code specialised for their count
+    // (a uniform switch), with no per-tile branches: the reads of a pass are
+    // all issued before its writes.
+    auto compute_n = [&](int buf, const u32x4 (&a)[KS], int n0, auto ntiles) {
+        constexpr int NTL = decltype(ntiles)::value;
+        f32x4 c[NTL];
+        int f[NTL];
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) {
+            f[t] = fring[buf][t * 16 + col];
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                u32x4 v = *reinterpret_cast<const u32x4*>(twt + row * G + ks * 32 + kofs);
-                x.b[t][ks] = kq_ok ? v : u32x4{0u, 0u, 0u, 0u};
+                u32x4 bfr = *reinterpret_cast<const u32x4*>(&ring[buf][(t * 16 + col) * RB + ks * 64 + kq * 16]);
+                if (!kq_ok) bfr = u32x4{0u, 0u, 0u, 0u};
+                v = mfma16x16x32<T>(a[ks], bfr, v);
             }
-            const int f = tfeat[row];
-            x.f[t] = t < nt ? f : trash_f;
+            c[t] = v;
         }
-#else
+        // layer 0 (layer-1 tiles go to the trash rows), then layer 1 if any
+        f32x4 old[NTL];
+        int fa[NTL];
 #pragma unroll
-        for (int t = 0; t < MAXT; ++t) x.f[t] = trash_f;
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t >= nt) break;
-            const int64_t row = (tbase + t) * 16 + col;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                u32x4 v = *reinterpret_cast<const u32x4*>(twt + row * G + ks * 32 + kofs);
-                x.b[t][ks] = kq_ok ? v : u32x4{0u, 0u, 0u, 0u};
-            }
-            x.f[t] = tfeat[row];
+        for (int t = 0; t < NTL; ++t) {
+            fa[t] = t < n0 ? f[t] : trash_f;
+            old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
         }
-#endif
-    };
-
-    auto load = [&](R& x, int64_t g, i32x2 m) {  // g < g_full: all G labels
-        unpack_meta(x, m);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + c[t];
+        if (n0 < NTL) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                u32x4 v = *reinterpret_cast<const u32x4*>(yrow[mt] + g * G + ks * 32 + kofs);
-                x.a[mt][ks] = kq_ok ? v : u32x4{0u, 0u, 0u, 0u};
+            for (int t = 0; t < NTL; ++t) {
+                fa[t] = t >= n0 ? f[t] : trash_f;
+                old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
             }
-        load_tiles(x, g);
-    };
-
-    auto mfma_tiles = [&](const R& x, int nreg, f32x4 (&c)[MAXT][MT]) {
 #pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t >= nreg) continue;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(x.a[mt][ks], x.b[t][ks], v);
-                c[t][mt] = v;
-            }
+            for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + c[t];
         }
     };
-
-    // acc[feature rows of tiles t0..t1-1] += c: all reads of the tiles are issued
-    // before their writes (the tiles' features are distinct)
-    auto rmw = [&](const R& x, const f32x4 (&c)[MAXT][MT], int t0, int t1) {
-        f32x4 old[MAXT][MT];
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t < t0 || t >= t1) continue;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                old[t][mt] = *reinterpret_cast<const f32x4*>(acc_b + x.f[t] + mt * 64);
+    auto compute = [&](int buf, const u32x4 (&a)[KS]) {
+        const int n0 = __builtin_amdgcn_readfirstlane(rmeta[buf][0]);
+        const int nt = __builtin_amdgcn_readfirstlane(rmeta[buf][1]);
+        static_assert(RT <= 8, "ring tiles");
+        switch (nt) {
+        case 0: break;
+        case 1: compute_n(buf, a, n0, std::integral_constant<int, 1>{}); break;
+        case 2: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 2 ? 2 : 1)>{}); break;
+        case 3: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 3 ? 3 : 1)>{}); break;
+        case 4: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 4 ? 4 : 1)>{}); break;
+        case 5: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 5 ? 5 : 1)>{}); break;
+        case 6: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 6 ? 6 : 1)>{}); break;
+        case 7: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 7 ? 7 : 1)>{}); break;
+        default: compute_n(buf, a, n0, std::integral_constant<int, RT>{}); break;
         }
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            if (t < t0 || t >= t1) continue;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                *reinterpret_cast<f32x4*>(acc_b + x.f[t] + mt * 64) = old[t][mt] + c[t][mt];
+    };
+    // Further rounds of a group whose range holds more than RT tiles: staged
+    // synchronously into ring[buf] (not in use by any wave at this point).
+    auto extra_rounds = [&](int64_t g, u32x2 mv, int buf, const u32x4 (&a)[KS]) {
+        const u32x2 m = uniform_meta(mv);
+        const int ntot = (int)m[1] - (int)(m[0] & 0xFFFF);
+        for (int t0 = RT; t0 < ntot; t0 += RT) {
+            Stage st;
+            load_stage(g, m, t0, st);
+            store_stage(buf, st, m, t0);
+            __syncthreads();
+            compute(buf, a);
+            __syncthreads();
         }
     };
 
-    // Writes of the second 16-row block (mt = 1) of the previous group, deferred:
-    // that block's columns are disjoint from the first block's, so the next group's
-    // first-block reads may be issued before them (reads then overlap writes).
-    // Every step issues the same LDS operations (unused tile slots go to the trash
-    // rows), so each wait covers exactly the operations it needs.
-    struct Pend {
-        f32x4 old[MAXT], c[MAXT];
-        int f[MAXT];
-    } pend;
-    auto pend_clear = [&]() {
-#pragma unroll
-        for (int t = 0; t < MAXT; ++t) {
-            pend.old[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            pend.c[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            pend.f[t] = trash_f;
-        }
-    };
-    pend_clear();
-    auto flush = [&]() {
-        if constexpr (MT == 2) {
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t)
-                *reinterpret_cast<f32x4*>(acc_b + pend.f[t] + 64) = pend.old[t] + pend.c[t];
-        }
-    };
-    // the same, re-reading the values (nothing else touches those words before):
-    // keeps the fast path's adds next to their writes instead of at the loop head
-    auto flush_rmw = [&]() {
-        if constexpr (MT == 2) {
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                f32x4* q = reinterpret_cast<f32x4*>(acc_b + pend.f[t] + 64);
-                *q = *q + pend.c[t];
-            }
-        }
-    };
-
-    auto compute = [&](const R& x, int64_t g) {
-        const int nt = x.te - x.tb;
-        const int n0 = x.tm - x.tb;
-        if (MT == 2 && n0 == nt && nt <= MAXT) {
-            // one layer, all tiles in registers: R0(g) W1(g-1) R1(g) W0(g); W1(g) deferred
-            f32x4 c[MAXT][MT];
-            mfma_tiles(x, MAXT, c);
-            f32x4 o0[MAXT];
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t) o0[t] = *reinterpret_cast<const f32x4*>(acc_b + x.f[t]);
-            flush();
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t) {
-                pend.old[t] = *reinterpret_cast<const f32x4*>(acc_b + x.f[t] + 64);
-                pend.c[t] = c[t][MT - 1];
-                pend.f[t] = x.f[t];
-            }
-#pragma unroll
-            for (int t = 0; t < MAXT; ++t)
-                *reinterpret_cast<f32x4*>(acc_b + x.f[t]) = o0[t] + c[t][0];
-            return;
-        }
-        flush_rmw();
-        pend_clear();
-        const int nreg = min(nt, MAXT);
-        const int n0r = min(n0, nreg);
-        f32x4 c[MAXT][MT];
-        mfma_tiles(x, nreg, c);
-        rmw(x, c, 0, n0r);
-        if (n0r < nreg) rmw(x, c, n0r, nreg);
-        // tiles beyond the register set (ranges holding an unusual share of F)
-        for (int t = MAXT; t < nt; ++t) {
-            const int64_t row = (g * Tcap + x.tb + t) * 16 + col;
-            u32x4 bb[KS];
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                u32x4 v = *reinterpret_cast<const u32x4*>(twt + row * G + ks * 32 + kofs);
-                bb[ks] = kq_ok ? v : u32x4{0u, 0u, 0u, 0u};
-            }
-            char* p = acc_b + tfeat[row];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                f32x4 v = *reinterpret_cast<const f32x4*>(p + mt * 64);
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(x.a[mt][ks], bb[ks], v);
-                *reinterpret_cast<f32x4*>(p + mt * 64) = v;
-            }
-        }
-    };
-
-    // Meta chunks 0 and 1 in LDS, chunk 2 in registers.  Iteration i looks up
-    // groups [i + NS, i + 2NS): chunk (i + NS) / 64 and possibly the next one,
-    // so entering a new chunk frees the slot of the one before it.
-    put_chunk(0, meta_chunk(0));
-    put_chunk(1, meta_chunk(1));
-    i32x4 mnext = meta_chunk(2);
-    int64_t c_top = 1;  // newest chunk in LDS
-
-    if (g_lo < g_full) {
-        // ring of NS groups in flight; slots past the last full group re-load it
-        // (never computed)
-        const int64_t nfull = g_full - g_lo;
-        R rg[NS];
-#pragma unroll
-        for (int k = 0; k < NS; ++k) {
-            const int64_t ik = min<int64_t>(k, nfull - 1);
-            load(rg[k], g_lo + ik, read_meta(ik));
-        }
-        for (int64_t i = 0; i < nfull; i += NS) {
-            if ((i + NS) / kMetaChunk + 1 > c_top) {
-                ++c_top;
-                put_chunk(c_top, mnext);
-                mnext = meta_chunk(c_top + 1);
-            }
-#pragma unroll
-            for (int k = 0; k < NS; ++k) {
-                const int64_t in = min<int64_t>(i + k + NS, nfull - 1);
-                const i32x2 m = read_meta(in);  // issued before compute's LDS traffic
-                if (i + k < nfull) compute(rg[k], g_lo + i + k);
-                load(rg[k], g_lo + in, m);
-            }
-        }
-    }
-    flush_rmw();
-    pend_clear();
-    if (g_full < g_hi) {  // the last group, holding O % G labels: columns >= O read as 0
-        R x;
-        const int64_t g = g_full;
-        put_chunk((g - g_lo) / kMetaChunk, meta_chunk((g - g_lo) / kMetaChunk));
-        unpack_meta(x, read_meta(g - g_lo));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const int64_t c = g * G + ks * 32 + kofs;
-                uint32_t h[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = (kq_ok && c + e < O) ? yrow[mt][c + e] : 0u;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) x.a[mt][ks][q] = h[2 * q] | (h[2 * q + 1] << 16);
-            }
-        load_tiles(x, g);
-        compute(x, g);
-        flush_rmw();
+    // ---- pipeline: ring[i % 2] holds group i; the W^T stages of groups i+1
+    // and i+2 and the dY fragments of groups i+1 and i+2 are in registers or
+    // in flight (three register sets, slot i % 3): each load is issued two
+    // iterations before its use, in the same order every iteration (meta, W^T
+    // stage, dY), so a wait never covers a load issued later. ----
+    Stage stg[3];
+    u32x4 ya[3][KS];
+    u32x2 mq[4];  // meta of groups i .. i+3
+    if (ng > 0) {
+        mq[0] = load_meta(g_lo);
+        load_stage(g_lo, mq[0], 0, stg[0]);
+        store_stage(0, stg[0], mq[0], 0);
+        mq[1] = load_meta(g_lo + 1);
+        mq[2] = load_meta(g_lo + 2);
+        mq[3] = load_meta(g_lo + 3);
+        load_stage(g_lo + 1, mq[1], 0, stg[1]);
+        load_y(g_lo, ya[0]);
+        load_stage(g_lo + 2, mq[2], 0, stg[2]);
+        load_y(g_lo + 1, ya[1]);
     }
     __syncthreads();
+    auto body = [&](int i, auto p2, auto p3) {
+        constexpr int P = decltype(p2)::value;   // ring buffer of group i
+        constexpr int Q = decltype(p3)::value;   // register slot of group i
+        const int64_t g = g_lo + i;
+        const u32x2 m4 = load_meta(g + 4);
+        load_stage(g + 3, mq[3], 0, stg[Q]);
+        load_y(g + 2, ya[(Q + 2) % 3]);
+        mask_y(g, ya[Q]);
+        compute(P, ya[Q]);
+        const u32x2 mi = uniform_meta(mq[0]);
+        if ((int)mi[1] - (int)(mi[0] & 0xFFFF) > RT) {  // uniform, rare
+            __syncthreads();
+            extra_rounds(g, mi, P, ya[Q]);
+        }
+        store_stage(1 - P, stg[(Q + 1) % 3], mq[1], 0);
+        mq[0] = mq[1];
+        mq[1] = mq[2];
+        mq[2] = mq[3];
+        mq[3] = m4;
+        __syncthreads();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    for (int i = 0; i < ng; i += 6) {
+        body(i, I0{}, I0{});
+        if (i + 1 < ng) body(i + 1, I1{}, I1{});
+        if (i + 2 < ng) body(i + 2, I0{}, I2{});
+        if (i + 3 < ng) body(i + 3, I1{}, I0{});
+        if (i + 4 < ng) body(i + 4, I0{}, I1{});
+        if (i + 5 < ng) body(i + 5, I1{}, I2{});
+    }
 
     // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----
     float* out = ws + ((int64_t)s * D + d_lo) * Bp + (int64_t)bt * BT;
-    for (int i = tid; i < dn * (BT / 4); i += kMainThreads) {
-        const int d = i / (BT / 4), b4 = (i % (BT / 4)) * 4;
-        *reinterpret_cast<f32x4*>(out + (int64_t)d * Bp + b4) =
-            *reinterpret_cast<const f32x4*>(&acc[d * AS + b4]);
+    for (int i = tid; i < dn * (BT / 4); i += NTH) {
+        const int d = i / (BT / 4), q = i % (BT / 4);  // natural columns 4q .. 4q+3
+        *reinterpret_cast<f32x4*>(out + (int64_t)d * Bp + q * 4) =
+            *reinterpret_cast<const f32x4*>(&acc[d * AS + perm_col(q / 4, q % 4)]);
     }
 }
 
@@ -577,36 +531,30 @@ __global__ __launch_bounds__(256) void bwdf_reduce_sr_kernel(const float* __rest
     }
 }
 
-template <typename T, int G, int RPW, int FP>
+template <typename T, int G, int WAVES>
 int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                 int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
                 hipStream_t st) {
     const int64_t nlog = p.S * p.ndr * p.nbt;
     const int64_t grid = 8 * ceil_div(nlog, 8);
-    bwdf_main_kernel<T, G, RPW, FP><<<dim3((unsigned)grid), dim3(kMainThreads), 0, st>>>(
+    if ((int64_t)p.BT * lddy * 2 > kMaxRsrcBytes) {
+        set_error("haste_ffi_bwd_features: lddy = %lld too large", (long long)lddy);
+        return HASTE_ERR_UNSUPPORTED;
+    }
+    bwdf_main_kernel<T, G, WAVES><<<dim3((unsigned)grid), dim3(64 * WAVES), 0, st>>>(
         tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
         (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
     return HASTE_OK;
 }
 
-template <typename T, int G, int RPW>
-int dispatch_fp(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
-                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
-                int64_t O, hipStream_t st) {
-#define HASTE_BWDF_ARGS tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st
-    if (F <= 64) return launch_main<T, G, RPW, 64>(HASTE_BWDF_ARGS);
-    if (F <= 128) return launch_main<T, G, RPW, 128>(HASTE_BWDF_ARGS);
-    return launch_main<T, G, RPW, 256>(HASTE_BWDF_ARGS);
-#undef HASTE_BWDF_ARGS
-}
-
 template <typename T, int G>
 int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
              int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
              int64_t O, hipStream_t st) {
-    if (p.BT == 64) return dispatch_fp<T, G, 16>(tfeat, meta, twt, dY, lddy, ws, p, B, D, F, O, st);
-    return dispatch_fp<T, G, 32>(tfeat, meta, twt, dY, lddy, ws, p, B, D, F, O, st);
+    (void)F;
+    if (p.BT == 64) return launch_main<T, G, 4>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    return launch_main<T, G, 8>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
 // Checks the arguments and the workspace size; returns the plan.
@@ -617,7 +565,7 @@ int check_bwdf(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, int64
     const BwdFPlan p = make_plan(B, D, F, O, G);
     if (p.ndr > kMaxRanges) {
         set_error("%s: D = %lld is too large (at most %lld features)", fn, (long long)D,
-                  (long long)kMaxRanges * max_dc((int)p.BT));
+                  (long long)kMaxRanges * max_dc((int)p.BT, (int)G));
         return HASTE_ERR_UNSUPPORTED;
     }
     HASTE_CHECK_ARG(aligned16(workspace), "%s: workspace must be 16-byte aligned", fn);
@@ -658,7 +606,7 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     if (!plan_ready) {
         bwdf_plan_kernel<<<pgrid, dim3(256), 0, st>>>(
             idx, tfeat, tsrc, perm, meta, (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap,
-            acc_stride((int)p.BT) * 4, max_dc((int)p.BT));
+            acc_stride((int)p.BT) * 4, max_dc((int)p.BT, (int)G));
         HASTE_CHECK_LAUNCH(fn);
     }
     const bool gather = plan_ready != 2;
@@ -720,7 +668,7 @@ extern "C" int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace,
         idx, reinterpret_cast<int*>(base + p.tfeat_off), reinterpret_cast<int*>(base + p.tsrc_off),
         reinterpret_cast<int*>(base + p.perm_off), reinterpret_cast<int*>(base + p.meta_off),
         (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap, haste::acc_stride((int)p.BT) * 4,
-        haste::max_dc((int)p.BT));
+        haste::max_dc((int)p.BT, (int)G));
     HASTE_CHECK_LAUNCH(fn);
     return HASTE_OK;
 }
