@@ -10,7 +10,8 @@
 //   tsrc   int32 [Gc, Tcap*16]  (start << 10) | (count << 1) | lo: the position
 //                               sums W over slots perm[g*F + start .. +count)
 //   perm   int32 [Gc, F]        slots of the group sorted by index
-//   meta   int32 [Gc, ndr, 4]   tiles [tb, tm) layer 0, [tm, te) layer 1 per range
+//   meta   int32 [Gc, ndr, 2]   tb | tm << 16, te: tiles [tb, tm) layer 0, [tm, te)
+//                               layer 1 of the range
 //   twt    16-bit [Gc, Tcap*16, G]  W^T: row p = sum of W columns of position p
 //   partials fp32 [S, D, Bp]    per-slice partial sums of dX^T
 #pragma once
@@ -25,9 +26,10 @@ constexpr int kAccPad = 4;        // fp32 words of padding per LDS partial row (
 constexpr int kTrashRows = 4;     // LDS partial rows that padding tile columns add into
 constexpr int kTargetCTAs = 256;
 constexpr int kMaxRanges = 128;   // feature ranges per group handled by the plan kernel
-constexpr int kMetaStride = 4;    // ints per (group, range): tile begin, layer-1 begin, end
+constexpr int kMetaStride = 2;    // ints per (group, range): tb | tm << 16, te
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kLdsMisc = 1024;    // LDS the main kernel keeps for other things
+constexpr int kGroupUnroll = 6;   // groups per unrolled iteration of the main kernel's loop
 
 // The main kernel stages each group's W^T tiles (and their partial-row offsets)
 // in a double-buffered LDS ring of ring_tiles(G) tiles of 16 rows; a W^T row is
@@ -59,7 +61,9 @@ inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G)
     p.Dc = ceil_div(D, p.ndr);
     int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
     S = std::min<int64_t>(S, std::max<int64_t>(1, ceil_div(p.Gc, 8)));
-    p.gps = ceil_div(p.Gc, S);
+    // the main kernel's group loop is unrolled kGroupUnroll times without
+    // guards: only the last slice runs (empty) iterations past its groups
+    p.gps = ceil_div(ceil_div(p.Gc, S), kGroupUnroll) * kGroupUnroll;
     p.S = ceil_div(p.Gc, p.gps);
     // tiles per group: layer 0 holds <= F distinct features, layer 1 <= F/2, and
     // each non-empty range pads its layer to a multiple of 16

@@ -201,10 +201,18 @@ __device__ __forceinline__ uint32_t sgd_one(float w, float g, float* m, bool use
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr uint32_t kOOB = 0x80000000u;
 constexpr int64_t kMaxRsrcBytes = 0x7FFFFF00;
+// s_waitcnt operand (gfx9 encoding) that waits for every vector-memory op and
+// for nothing else: vmcnt 0, expcnt 7 and lgkmcnt 15 (no wait)
+constexpr int kWaitVmcnt0 = (7 << 4) | (15 << 8);
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
     const int64_t n = bytes < 0 ? 0 : (bytes > kMaxRsrcBytes ? kMaxRsrcBytes : bytes);
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n,
+                                             0x00020000);
+}
+// The same for a size the caller knows to lie in [0, kMaxRsrcBytes] (no clamp).
+__device__ __forceinline__ rsrc_t make_rsrc_u32(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                              0x00020000);
 }
 __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {

@@ -46,9 +46,9 @@ int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, 
 namespace {
 
 // --------------------------------------------------------------- plan ------
-// Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*4 + 0..2]
-// = (tb, tm, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative to
-// g*Tcap); meta[(g*ndr + ndr-1)*4 + 2] is the group's tile count.  For tile row
+// Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*2 + 0..1]
+// = (tb | tm << 16, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative
+// to g*Tcap); meta[(g*ndr + ndr-1)*2 + 1] is the group's tile count.  For tile row
 // (t, p): tfeat = byte offset of the feature's row in the main kernel's LDS
 // partial, (feature - r*Dc) * row_bytes, or (trash_row + p % kTrashRows) * row_bytes for
 // padding; tsrc = (start << 10) |
@@ -118,10 +118,8 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
     __syncthreads();
     for (int rr = tid; rr < ndr; rr += 256) {
         int* m = meta + (g * ndr + rr) * kMetaStride;
-        m[0] = s_tile[rr][0];
-        m[1] = s_tile[rr][1];
-        m[2] = s_tile[rr][2];
-        m[3] = 0;
+        m[0] = s_tile[rr][0] | (s_tile[rr][1] << 16);
+        m[1] = s_tile[rr][2];
     }
     const int64_t tbase = g * Tcap;
     if (tid < F && first) {
@@ -176,7 +174,7 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
         for (int q = 0; q < 4; ++q) s_w[l * ldw + j0 / 2 + q] = v[q];
     }
     if (tid < F) s_perm[tid] = perm[g * F + tid];
-    const int nrows = meta[(g * ndr + ndr - 1) * kMetaStride + 2] * 16;
+    const int nrows = meta[(g * ndr + ndr - 1) * kMetaStride + 1] * 16;
     __syncthreads();
     auto wv = [&](int l, int slot) -> uint32_t {
         const uint32_t w2 = s_w[l * ldw + (slot >> 1)];
@@ -264,72 +262,81 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     const int b0 = bt * BT;
     const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy,
                                 ((int64_t)(min(BT, B - b0) - 1) * lddy + (O + 7) / 8 * 8) * 2);
-    const int64_t yoff = (int64_t)(wave * 16 + col) * lddy + kofs;
-    auto load_y = [&](int64_t g, u32x4 (&a)[KS]) {
+    // byte offset of the lane's first label in the tile (32 bits: the tile's
+    // resource spans at most kMaxRsrcBytes; g * G * 2 < 2 * lddy for real groups)
+    const uint32_t yoff2 = (uint32_t)(((int64_t)(wave * 16 + col) * lddy + kofs) * 2);
+    auto load_y = [&](int64_t g, u32x4 (&a)[KS]) __attribute__((always_inline)) {
+        const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-            a[ks] = buf_load16(yr, kq_ok ? (uint32_t)((yoff + g * G + ks * 32) * 2) : kOOB);
+            a[ks] = buf_load16(yr, kq_ok ? yoff2 + go + ks * 64 : kOOB);
     };
-    auto mask_y = [&](int64_t g, u32x4 (&a)[KS]) {  // labels >= O (last group) -> 0
+    // labels >= O read as zero: only the last group has any (a uniform branch)
+    auto mask_y = [&](int64_t g, u32x4 (&a)[KS]) __attribute__((always_inline)) {
+        const int64_t rem = O - g * G;  // labels of group g below O
+        if (rem >= G) return;
+        const int nr = (int)max<int64_t>(rem, 0);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const int64_t nv = O - (g * G + ks * 32 + kofs);
+            const int nv = nr - (ks * 32 + kofs);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 a[ks][e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
         }
     };
 
-    // Tile range (tb, tm, te) of group g in range r: tb | tm << 16, te.
-    auto load_meta = [&](int64_t g) -> u32x2 {
-        // a vector load (the same address in every lane), consumed an iteration
-        // later through uniform_meta
-        typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-        const i32x4 m = *reinterpret_cast<const i32x4*>(
-            meta + (min<int64_t>(g, g_hi - 1) * ndr + r) * kMetaStride);
-        return u32x2{(uint32_t)(m[0] | (m[1] << 16)), (uint32_t)m[2]};
+    // Tile range of group g_lo + i in range r: tb | tm << 16, te (layer-0 tiles
+    // [tb, tm), layer-1 tiles [tm, te)).  A buffer load, i.e. a vector-memory op
+    // consumed DEPTH iterations later: a scalar load would hold up every later
+    // LDS wait of the wave until it returns; both words are used, so no register
+    // of the load is free for reuse (which would wait for it).  Groups past the
+    // slice read as zero (no tiles), so iterations past them do nothing.
+    const rsrc_t mr = make_rsrc(meta + (g_lo * ndr + r) * kMetaStride,
+                                ((int64_t)(max(ng, 1) - 1) * ndr + 1) * kMetaStride * 4);
+    auto load_meta = [&](int i) __attribute__((always_inline)) -> u32x2 {
+        return buf_load8(mr, i < ng ? (uint32_t)(i * ndr * kMetaStride * 4) : kOOB);
     };
-    // the same in every lane: made wave-uniform (it decides branches with barriers)
-    auto uniform_meta = [](u32x2 m) -> u32x2 {
+    // wave-uniform (SGPR) form
+    auto uniform_meta = [](const u32x2& m) __attribute__((always_inline)) -> u32x2 {
         return u32x2{(uint32_t)__builtin_amdgcn_readfirstlane((int)m[0]),
                      (uint32_t)__builtin_amdgcn_readfirstlane((int)m[1])};
     };
-    // Stage tiles [tb + t0, tb + t0 + RT) of group g into registers: W^T chunks
-    // and the positions' partial-row offsets (past the range's tiles: zero W^T
-    // rows, trash offsets).
+    // Stage tiles [tb + t0, tb + t0 + RT) of group g_lo + i into registers: W^T
+    // chunks and the positions' partial-row offsets (past the range's tiles:
+    // zero W^T rows, trash offsets).  m is uniform.
     struct Stage {
         u32x4 w[SPT];
         int f;
     };
-    auto load_stage = [&](int64_t g, u32x2 mv, int t0, Stage& st) {
-        const u32x2 m = uniform_meta(mv);
+    auto load_stage = [&](int i, u32x2 m, int t0, Stage& st) __attribute__((always_inline)) {
         // wave-uniform (SGPR) values, so the buffer descriptors below are scalar
         const int tb = __builtin_amdgcn_readfirstlane((int)(m[0] & 0xFFFF) + t0);
         const int nrow = __builtin_amdgcn_readfirstlane(max(0, min(RT, (int)m[1] - tb)) * 16);
-        const int64_t row0 = ((int64_t)__builtin_amdgcn_readfirstlane((int)g) * Tcap + tb) * 16;
-        const rsrc_t wr = make_rsrc(twt + row0 * G, (int64_t)nrow * G * 2);
+        const int64_t row0 = ((g_lo + __builtin_amdgcn_readfirstlane(i)) * Tcap + tb) * 16;
+        const rsrc_t wr = make_rsrc_u32(twt + row0 * G, (uint32_t)nrow * G * 2);
 #pragma unroll
         for (int k = 0; k < SPT; ++k) {
             const int c = tid + k * NTH;
             st.w[k] = buf_load16(wr, c < RT * 16 * CH ? (uint32_t)c * 16 : kOOB);
         }
-        const rsrc_t fr = make_rsrc(tfeat + row0, (int64_t)nrow * 4);
+        const rsrc_t fr = make_rsrc_u32(tfeat + row0, (uint32_t)nrow * 4);
+        // used as loaded (rows past nrow are selected away in store_stage): an
+        // operation on a pending load would wait for it here
         st.f = (int)buf_load4(fr, tid < RT * 16 ? (uint32_t)tid * 4 : kOOB);
-        st.f = tid < nrow ? st.f : -1;
     };
-    auto store_stage = [&](int buf, const Stage& st, u32x2 mv, int t0) {
-        const u32x2 m = uniform_meta(mv);
+    auto store_stage = [&](int buf, const Stage& st, u32x2 m, int t0) __attribute__((always_inline)) {
+        const int tb = (int)(m[0] & 0xFFFF) + t0;
+        const int nt = max(0, min(RT, (int)m[1] - tb));  // tiles of this round
 #pragma unroll
         for (int k = 0; k < SPT; ++k) {
             const int c = tid + k * NTH;
             if (c < RT * 16 * CH)
                 *reinterpret_cast<u32x4*>(&ring[buf][(c / CH) * RB + (c % CH) * 16]) = st.w[k];
         }
-        if (tid < RT * 16) fring[buf][tid] = st.f >= 0 ? st.f : (C::DCMAX + (tid & (kTrashRows - 1))) * AS * 4;
+        if (tid < RT * 16) fring[buf][tid] = tid < nt * 16 ? st.f : (C::DCMAX + (tid & (kTrashRows - 1))) * AS * 4;
         if (tid == 0) {
-            const int tb = (int)(m[0] & 0xFFFF) + t0;
             rmeta[buf][0] = max(0, (int)(m[0] >> 16) - tb);  // layer-0 tiles of this round
-            rmeta[buf][1] = max(0, min(RT, (int)m[1] - tb));  // tiles of this round
+            rmeta[buf][1] = nt;
         }
     };
 
@@ -345,7 +352,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // The round's tiles are processed by code specialised for their count
     // (a uniform switch), with no per-tile branches: the reads of a pass are
     // all issued before its writes.
-    auto compute_n = [&](int buf, const u32x4 (&a)[KS], int n0, auto ntiles) {
+    auto compute_n = [&](int buf, const u32x4 (&a)[KS], int n0, auto ntiles) __attribute__((always_inline)) {
         constexpr int NTL = decltype(ntiles)::value;
         f32x4 c[NTL];
         int f[NTL];
@@ -381,7 +388,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
             for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + c[t];
         }
     };
-    auto compute = [&](int buf, const u32x4 (&a)[KS]) {
+    auto compute = [&](int buf, const u32x4 (&a)[KS]) __attribute__((always_inline)) {
         const int n0 = __builtin_amdgcn_readfirstlane(rmeta[buf][0]);
         const int nt = __builtin_amdgcn_readfirstlane(rmeta[buf][1]);
         static_assert(RT <= 8, "ring tiles");
@@ -399,12 +406,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     };
     // Further rounds of a group whose range holds more than RT tiles: staged
     // synchronously into ring[buf] (not in use by any wave at this point).
-    auto extra_rounds = [&](int64_t g, u32x2 mv, int buf, const u32x4 (&a)[KS]) {
-        const u32x2 m = uniform_meta(mv);
+    auto extra_rounds = [&](int i, u32x2 m, int buf, const u32x4 (&a)[KS]) __attribute__((always_inline)) {
         const int ntot = (int)m[1] - (int)(m[0] & 0xFFFF);
         for (int t0 = RT; t0 < ntot; t0 += RT) {
             Stage st;
-            load_stage(g, m, t0, st);
+            load_stage(i, m, t0, st);
             store_stage(buf, st, m, t0);
             __syncthreads();
             compute(buf, a);
@@ -412,58 +418,69 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         }
     };
 
-    // ---- pipeline: ring[i % 2] holds group i; the W^T stages of groups i+1
-    // and i+2 and the dY fragments of groups i+1 and i+2 are in registers or
-    // in flight (three register sets, slot i % 3): each load is issued two
-    // iterations before its use, in the same order every iteration (meta, W^T
-    // stage, dY), so a wait never covers a load issued later. ----
-    Stage stg[3];
-    u32x4 ya[3][KS];
-    u32x2 mq[4];  // meta of groups i .. i+3
-    if (ng > 0) {
-        mq[0] = load_meta(g_lo);
-        load_stage(g_lo, mq[0], 0, stg[0]);
-        store_stage(0, stg[0], mq[0], 0);
-        mq[1] = load_meta(g_lo + 1);
-        mq[2] = load_meta(g_lo + 2);
-        mq[3] = load_meta(g_lo + 3);
-        load_stage(g_lo + 1, mq[1], 0, stg[1]);
-        load_y(g_lo, ya[0]);
-        load_stage(g_lo + 2, mq[2], 0, stg[2]);
-        load_y(g_lo + 1, ya[1]);
+    // ---- pipeline: ring[i % 2] holds group i.  Every global load is issued
+    // DEPTH iterations before its use, in the same order every iteration (W^T
+    // stage of group i+1+DEPTH, dY of group i+DEPTH, meta of group i+1+2*DEPTH),
+    // so the one wait of an iteration (on the meta it converts) covers exactly
+    // the loads of iteration i-DEPTH.  Register sets rotate over NS slots
+    // (group h in slot h % NS), resolved at compile time by unrolling
+    // kGroupUnroll iterations (a multiple of NS and of the 2 ring buffers);
+    // the loop runs whole unrolled iterations without guards. ----
+    constexpr int DEPTH = 5, NS = DEPTH + 1;
+    static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0, "unroll");
+    Stage stg[NS];
+    u32x4 ya[NS][KS];
+    u32x2 mraw[NS];
+    u32x2 mu[DEPTH + 1];  // uniform meta of groups i .. i+DEPTH
+    {
+        u32x2 m0[DEPTH + 1];
+#pragma unroll
+        for (int k = 0; k <= DEPTH; ++k) m0[k] = load_meta(k);
+#pragma unroll
+        for (int k = 0; k <= DEPTH; ++k) mu[k] = uniform_meta(m0[k]);
+        load_stage(0, mu[0], 0, stg[0]);
+        store_stage(0, stg[0], mu[0], 0);
+        // iterations -DEPTH .. -1 of the steady-state load sequence, kept in
+        // that order (the loop's wait counts assume it)
+#pragma unroll
+        for (int k = 1; k <= DEPTH; ++k) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_stage(k, mu[k], 0, stg[k % NS]);
+            load_y(g_lo + k - 1, ya[(k - 1) % NS]);
+            mraw[(k + DEPTH) % NS] = load_meta(k + DEPTH);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
-    auto body = [&](int i, auto p2, auto p3) {
-        constexpr int P = decltype(p2)::value;   // ring buffer of group i
-        constexpr int Q = decltype(p3)::value;   // register slot of group i
-        const int64_t g = g_lo + i;
-        const u32x2 m4 = load_meta(g + 4);
-        load_stage(g + 3, mq[3], 0, stg[Q]);
-        load_y(g + 2, ya[(Q + 2) % 3]);
-        mask_y(g, ya[Q]);
+    auto body = [&](int i, auto q) __attribute__((always_inline)) {
+        constexpr int Q = decltype(q)::value;  // i % NS
+        constexpr int P = Q % 2;               // ring buffer of group i
+        const u32x2 mn = uniform_meta(mraw[(Q + 1 + DEPTH) % NS]);
+        load_stage(i + 1 + DEPTH, mn, 0, stg[(Q + 1 + DEPTH) % NS]);
+        load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS]);
+        mraw[(Q + 1 + 2 * DEPTH) % NS] = load_meta(i + 1 + 2 * DEPTH);
+        mask_y(g_lo + i, ya[Q]);
         compute(P, ya[Q]);
-        const u32x2 mi = uniform_meta(mq[0]);
-        if ((int)mi[1] - (int)(mi[0] & 0xFFFF) > RT) {  // uniform, rare
+        if ((int)mu[0][1] - (int)(mu[0][0] & 0xFFFF) > RT) {  // uniform, rare
             __syncthreads();
-            extra_rounds(g, mi, P, ya[Q]);
+            extra_rounds(i, mu[0], P, ya[Q]);
+            // the rounds consumed their loads (only some threads use a stage's
+            // position offsets); say so, so later code need not wait for them
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         }
-        store_stage(1 - P, stg[(Q + 1) % 3], mq[1], 0);
-        mq[0] = mq[1];
-        mq[1] = mq[2];
-        mq[2] = mq[3];
-        mq[3] = m4;
+        store_stage(1 - P, stg[(Q + 1) % NS], mu[1], 0);
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) mu[k] = mu[k + 1];
+        mu[DEPTH] = mn;
         __syncthreads();
     };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-    for (int i = 0; i < ng; i += 6) {
-        body(i, I0{}, I0{});
-        if (i + 1 < ng) body(i + 1, I1{}, I1{});
-        if (i + 2 < ng) body(i + 2, I0{}, I2{});
-        if (i + 3 < ng) body(i + 3, I1{}, I0{});
-        if (i + 4 < ng) body(i + 4, I0{}, I1{});
-        if (i + 5 < ng) body(i + 5, I1{}, I2{});
+    for (int i = 0; i < ng; i += kGroupUnroll) {
+        body(i, std::integral_constant<int, 0>{});
+        body(i + 1, std::integral_constant<int, 1>{});
+        body(i + 2, std::integral_constant<int, 2>{});
+        body(i + 3, std::integral_constant<int, 3>{});
+        body(i + 4, std::integral_constant<int, 4>{});
+        body(i + 5, std::integral_constant<int, 5>{});
     }
 
     // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----

@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     int wt_rows = 0;
     if constexpr (SGD) {
         if (do_wt) {
-            wt_rows = sg.meta[(g * sg.ndr + sg.ndr - 1) * kMetaStride + 2] * 16;
+            wt_rows = sg.meta[(g * sg.ndr + sg.ndr - 1) * kMetaStride + 1] * 16;
             const rsrc_t tr = make_rsrc(sg.tsrc + g * sg.Tcap * 16, (int64_t)sg.Tcap * 16 * 4);
 #pragma unroll
             for (int k = 0; k < kWtPre; ++k)
