@@ -204,6 +204,9 @@ constexpr int64_t kMaxRsrcBytes = 0x7FFFFF00;
 // s_waitcnt operand (gfx9 encoding) that waits for every vector-memory op and
 // for nothing else: vmcnt 0, expcnt 7 and lgkmcnt 15 (no wait)
 constexpr int kWaitVmcnt0 = (7 << 4) | (15 << 8);
+// s_waitcnt operand that waits until at most n LDS/scalar-memory ops are
+// outstanding (n <= 15) and for nothing else (vmcnt 63, expcnt 7)
+__host__ __device__ constexpr int wait_lgkmcnt(int n) { return 0xF | (7 << 4) | (n << 8) | (3 << 14); }
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
     const int64_t n = bytes < 0 ? 0 : (bytes > kMaxRsrcBytes ? kMaxRsrcBytes : bytes);

@@ -234,7 +234,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
     __shared__ __attribute__((aligned(16))) char ring[2][C::RING];
     __shared__ int fring[2][RT * 16];
-    __shared__ int rmeta[2][2];
 
     const int64_t work = xcd_remap(blockIdx.x, (int64_t)S * ndr * nbt);
     if (work < 0) return;
@@ -334,10 +333,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
                 *reinterpret_cast<u32x4*>(&ring[buf][(c / CH) * RB + (c % CH) * 16]) = st.w[k];
         }
         if (tid < RT * 16) fring[buf][tid] = tid < nt * 16 ? st.f : (C::DCMAX + (tid & (kTrashRows - 1))) * AS * 4;
-        if (tid == 0) {
-            rmeta[buf][0] = max(0, (int)(m[0] >> 16) - tb);  // layer-0 tiles of this round
-            rmeta[buf][1] = nt;
-        }
     };
 
     // Batch columns of a partial row are permuted: the 4 columns a lane adds (its
@@ -348,64 +343,92 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // plan's dealing arranges.
     auto perm_col = [](int w, int q) { return (q & 1) * (BT / 2) + w * 8 + (q >> 1) * 4; };
     char* const acc_b = reinterpret_cast<char*>(acc) + perm_col(wave, kq) * 4;
-    // Multiply-accumulate the staged round in ring[buf] with dY fragments a.
-    // The round's tiles are processed by code specialised for their count
-    // (a uniform switch), with no per-tile branches: the reads of a pass are
-    // all issued before its writes.
-    auto compute_n = [&](int buf, const u32x4 (&a)[KS], int n0, auto ntiles) __attribute__((always_inline)) {
-        constexpr int NTL = decltype(ntiles)::value;
-        f32x4 c[NTL];
-        int f[NTL];
+    // A round is up to RT staged tiles of one group.  Its MFMAs run on all RT
+    // ring tiles (rows past the round's tiles are zero) and the products stay
+    // in registers; the partial update (read, add, write) of a round runs in
+    // the next iteration, in the same code as the next round's MFMAs, so the
+    // products' latency and the update's LDS traffic overlap the next group.
+    struct Round {
+        f32x4 c[RT];  // dY rows x W^T tile t
+        int f[RT];    // partial-row byte offset of the lane's position in tile t
+        int n0, nt;   // uniform: layer-0 tiles and tiles of the round (nt 0: nothing to add)
+    };
+    auto round_counts = [](u32x2 m, int t0, Round& r) __attribute__((always_inline)) {
+        const int tb = (int)(m[0] & 0xFFFF) + t0;
+        r.n0 = max(0, (int)(m[0] >> 16) - tb);
+        r.nt = max(0, min(RT, (int)m[1] - tb));
+    };
+    // ring and offset reads of the round staged in ring[buf]
+    auto read_round = [&](int buf, u32x4 (&bf)[RT][KS], Round& r) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < NTL; ++t) {
-            f[t] = fring[buf][t * 16 + col];
-            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < RT; ++t) {
+            r.f[t] = fring[buf][t * 16 + col];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                u32x4 bfr = *reinterpret_cast<const u32x4*>(&ring[buf][(t * 16 + col) * RB + ks * 64 + kq * 16]);
-                if (!kq_ok) bfr = u32x4{0u, 0u, 0u, 0u};
-                v = mfma16x16x32<T>(a[ks], bfr, v);
+                bf[t][ks] = *reinterpret_cast<const u32x4*>(&ring[buf][(t * 16 + col) * RB + ks * 64 + kq * 16]);
+                if (!kq_ok) bf[t][ks] = u32x4{0u, 0u, 0u, 0u};
             }
-            c[t] = v;
         }
-        // layer 0 (layer-1 tiles go to the trash rows), then layer 1 if any
-        f32x4 old[NTL];
-        int fa[NTL];
+    };
+    auto mma_round = [&](const u32x4 (&a)[KS], const u32x4 (&bf)[RT][KS], Round& r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(a[ks], bf[t][ks], v);
+            r.c[t] = v;
+        }
+    };
+    // Partial update of the first NTL tiles of round pr: layer 0 (layer-1 tiles
+    // add into trash rows), then layer 1 if any; a pass issues all its reads
+    // before its writes (a layer's features are distinct), and a wave's LDS
+    // accesses complete in order, so later passes and rounds see the writes.
+    // The MFMAs of round cur (if given) are issued between the first pass's
+    // reads and writes.
+    auto update_n = [&](const Round& pr, auto ntiles, auto mma) __attribute__((always_inline)) {
+        constexpr int NTL = decltype(ntiles)::value;
+        f32x4 old[NTL > 0 ? NTL : 1];
+        int fa[NTL > 0 ? NTL : 1];
 #pragma unroll
         for (int t = 0; t < NTL; ++t) {
-            fa[t] = t < n0 ? f[t] : trash_f;
+            fa[t] = t < pr.n0 ? pr.f[t] : trash_f;
             old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
         }
+        mma();
 #pragma unroll
-        for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + c[t];
-        if (n0 < NTL) {
+        for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + pr.c[t];
+        if (pr.n0 < NTL) {
 #pragma unroll
             for (int t = 0; t < NTL; ++t) {
-                fa[t] = t >= n0 ? f[t] : trash_f;
+                fa[t] = t >= pr.n0 ? pr.f[t] : trash_f;
                 old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
             }
 #pragma unroll
-            for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + c[t];
+            for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + pr.c[t];
         }
+        // every LDS op of the wave but the last pass's NTL writes has completed
+        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(NTL));
     };
-    auto compute = [&](int buf, const u32x4 (&a)[KS]) __attribute__((always_inline)) {
-        const int n0 = __builtin_amdgcn_readfirstlane(rmeta[buf][0]);
-        const int nt = __builtin_amdgcn_readfirstlane(rmeta[buf][1]);
+    // update of round pr specialised for its tile count (a uniform switch), with mma()
+    auto update = [&](const Round& pr, auto mma) __attribute__((always_inline)) {
         static_assert(RT <= 8, "ring tiles");
-        switch (nt) {
-        case 0: break;
-        case 1: compute_n(buf, a, n0, std::integral_constant<int, 1>{}); break;
-        case 2: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 2 ? 2 : 1)>{}); break;
-        case 3: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 3 ? 3 : 1)>{}); break;
-        case 4: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 4 ? 4 : 1)>{}); break;
-        case 5: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 5 ? 5 : 1)>{}); break;
-        case 6: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 6 ? 6 : 1)>{}); break;
-        case 7: compute_n(buf, a, n0, std::integral_constant<int, (RT >= 7 ? 7 : 1)>{}); break;
-        default: compute_n(buf, a, n0, std::integral_constant<int, RT>{}); break;
+        using std::integral_constant;
+        switch (pr.nt) {
+        case 0: update_n(pr, integral_constant<int, 0>{}, mma); break;
+        case 1: update_n(pr, integral_constant<int, 1>{}, mma); break;
+        case 2: update_n(pr, integral_constant<int, (RT >= 2 ? 2 : 1)>{}, mma); break;
+        case 3: update_n(pr, integral_constant<int, (RT >= 3 ? 3 : 1)>{}, mma); break;
+        case 4: update_n(pr, integral_constant<int, (RT >= 4 ? 4 : 1)>{}, mma); break;
+        case 5: update_n(pr, integral_constant<int, (RT >= 5 ? 5 : 1)>{}, mma); break;
+        case 6: update_n(pr, integral_constant<int, (RT >= 6 ? 6 : 1)>{}, mma); break;
+        case 7: update_n(pr, integral_constant<int, (RT >= 7 ? 7 : 1)>{}, mma); break;
+        default: update_n(pr, integral_constant<int, RT>{}, mma); break;
         }
     };
-    // Further rounds of a group whose range holds more than RT tiles: staged
-    // synchronously into ring[buf] (not in use by any wave at this point).
+    auto no_mma = []() __attribute__((always_inline)) {};
+    // Further rounds of a group whose range holds more than RT tiles, done
+    // synchronously after the group's first round: staged into ring[buf] (not
+    // in use by any wave at this point), multiplied and added at once.
     auto extra_rounds = [&](int i, u32x2 m, int buf, const u32x4 (&a)[KS]) __attribute__((always_inline)) {
         const int ntot = (int)m[1] - (int)(m[0] & 0xFFFF);
         for (int t0 = RT; t0 < ntot; t0 += RT) {
@@ -413,7 +436,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
             load_stage(i, m, t0, st);
             store_stage(buf, st, m, t0);
             __syncthreads();
-            compute(buf, a);
+            Round r;
+            u32x4 bf[RT][KS];
+            read_round(buf, bf, r);
+            mma_round(a, bf, r);
+            round_counts(m, t0, r);
+            update(r, no_mma);
             __syncthreads();
         }
     };
@@ -425,13 +453,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // the loads of iteration i-DEPTH.  Register sets rotate over NS slots
     // (group h in slot h % NS), resolved at compile time by unrolling
     // kGroupUnroll iterations (a multiple of NS and of the 2 ring buffers);
-    // the loop runs whole unrolled iterations without guards. ----
+    // the loop runs whole unrolled iterations without guards.  Iteration i
+    // stages group i+1 into ring[1 - i % 2] (read by every wave before the
+    // last barrier), reads and multiplies group i's first round and adds
+    // group i-1's products into the partial. ----
     constexpr int DEPTH = 5, NS = DEPTH + 1;
     static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0, "unroll");
     Stage stg[NS];
     u32x4 ya[NS][KS];
     u32x2 mraw[NS];
     u32x2 mu[DEPTH + 1];  // uniform meta of groups i .. i+DEPTH
+    Round rd[2];          // round of group i in rd[i % 2]
+    rd[0].nt = rd[1].nt = 0;
+    rd[0].n0 = rd[1].n0 = 0;
     {
         u32x2 m0[DEPTH + 1];
 #pragma unroll
@@ -459,20 +493,34 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         load_stage(i + 1 + DEPTH, mn, 0, stg[(Q + 1 + DEPTH) % NS]);
         load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS]);
         mraw[(Q + 1 + 2 * DEPTH) % NS] = load_meta(i + 1 + 2 * DEPTH);
+        store_stage(1 - P, stg[(Q + 1) % NS], mu[1], 0);
         mask_y(g_lo + i, ya[Q]);
-        compute(P, ya[Q]);
+        u32x4 bf[RT][KS];
+        read_round(P, bf, rd[P]);
+        asm volatile("" ::: "memory");  // the update's LDS ops stay after the stage and reads
+        update(rd[1 - P], [&]() __attribute__((always_inline)) { mma_round(ya[Q], bf, rd[P]); });
+        round_counts(mu[0], 0, rd[P]);
         if ((int)mu[0][1] - (int)(mu[0][0] & 0xFFFF) > RT) {  // uniform, rare
+            // add this round now, then the group's further rounds in order
+            update(rd[P], no_mma);
+            rd[P].nt = 0;
             __syncthreads();
             extra_rounds(i, mu[0], P, ya[Q]);
             // the rounds consumed their loads (only some threads use a stage's
             // position offsets); say so, so later code need not wait for them
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         }
-        store_stage(1 - P, stg[(Q + 1) % NS], mu[1], 0);
 #pragma unroll
         for (int k = 0; k < DEPTH; ++k) mu[k] = mu[k + 1];
         mu[DEPTH] = mn;
-        __syncthreads();
+        // Barrier without draining the wave's LDS queue: other waves next write
+        // ring[P] and read ring[1 - P], and this wave's reads of ring[P] and
+        // fring[P] and writes of ring[1 - P] have completed (the update's wait);
+        // only its last partial writes may still be in flight, and no other
+        // wave touches those words.
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
     for (int i = 0; i < ng; i += kGroupUnroll) {
         body(i, std::integral_constant<int, 0>{});
@@ -482,6 +530,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         body(i + 4, std::integral_constant<int, 4>{});
         body(i + 5, std::integral_constant<int, 5>{});
     }
+    static_assert(kGroupUnroll % 2 == 0, "the last iteration's round is in rd[1]");
+    update(rd[1], no_mma);
+    __syncthreads();
 
     // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----
     float* out = ws + ((int64_t)s * D + d_lo) * Bp + (int64_t)bt * BT;
