@@ -14,22 +14,21 @@
 //     Inside a layer, features are dealt round-robin over the tiles in order
 //     of (feature mod 16, feature), so the 16 lanes of a tile mostly hit
 //     distinct LDS bank groups in step 2.
-//     gather (every call): tile row p of group g = W_g column of p's slot,
-//     transposed (WT[pos][label]); a duplicated index gets
+//     gather (when W changed since the last call): tile row p of group g = W_g
+//     column of p's slot, transposed (WT[pos][label]); a duplicated index gets
 //     sum_j W[l, j] (fp32, ascending j) split into its 16-bit rounding (hi)
-//     and the 16-bit rounding of the remainder (lo).
-//  2. main: a workgroup owns (group slice s, feature range r, batch tile of
-//     BT columns) and keeps dXT[range, tile] as an fp32 partial in LDS.  Wave
-//     w owns batch rows [w*RPW, (w+1)*RPW) of the tile, so no two waves touch
-//     the same LDS word and the waves never synchronise.  Per group a wave
-//     multiplies its dY rows with the range's tiles (MFMA, M = batch rows,
-//     N = 16 positions, K = labels); a lane then holds four consecutive
-//     batch values of one feature and adds them into LDS with one 16-byte
-//     read and one 16-byte write.  Reads of all tiles of a layer are issued
-//     before their writes (a layer's features are distinct); a wave's LDS
-//     accesses execute in program order, so layer 1 and later groups see
-//     the earlier writes.  Operands come from global memory into registers,
-//     NS groups ahead.
+//     and the 16-bit rounding of the remainder (lo).  The fused weight-gradient
+//     + SGD kernel writes the same rows for the weights it updates.
+//  2. main: a workgroup owns (group slice s, feature range r, batch tile of BT
+//     columns) and keeps dXT[range, tile] as an fp32 partial in LDS; wave w
+//     owns batch rows [16w, 16w+16), so no two waves touch one LDS word.  Per
+//     group the range's WT tiles are staged once into an LDS ring shared by
+//     the waves; each wave multiplies its dY rows with them (MFMA, M = batch
+//     rows, N = 16 positions, K = labels) and, one group later, a lane adds
+//     four consecutive batch values of one position into the partial row of
+//     the position's feature (one 16-byte read and one 16-byte write).  A
+//     wave's LDS accesses complete in program order, so layer 1 and later
+//     groups see the earlier writes.
 //  3. reduce: dXT = sum over slices s = 0..S-1 in ascending order (fp32 out), or
 //     fused with the bf16 stochastic rounding of shared_ffi/bindings.py:44-48.
 #include <algorithm>
