@@ -10,10 +10,11 @@
 //     changes): the distinct indices of every group are split by feature
 //     range (Dc features each) and laid out in tiles of 16 positions.  An
 //     index that occurs k > 1 times in the group gets a "hi" row in layer 0
-//     and a "lo" row in layer 1, so inside a layer every feature occurs once.
-//     Inside a layer, features are dealt round-robin over the tiles in order
-//     of (feature mod 16, feature), so the 16 lanes of a tile mostly hit
-//     distinct LDS bank groups in step 2.
+//     and a "lo" row in layer 1 at the same (tile, position) of its layer, so
+//     inside a layer every feature occurs once and layer-1 tile t pairs with
+//     layer-0 tile t.  Features are dealt over the tiles position by position
+//     in order of (feature mod 16, feature), so the 16 lanes of a tile mostly
+//     hit distinct LDS bank groups in step 2.
 //     gather (when W changed since the last call): tile row p of group g = W_g
 //     column of p's slot, transposed (WT[pos][label]); a duplicated index gets
 //     sum_j W[l, j] (fp32, ascending j) split into its 16-bit rounding (hi)
@@ -25,10 +26,11 @@
 //     group the range's WT tiles are staged once into an LDS ring shared by
 //     the waves; each wave multiplies its dY rows with them (MFMA, M = batch
 //     rows, N = 16 positions, K = labels) and, one group later, a lane adds
-//     four consecutive batch values of one position into the partial row of
-//     the position's feature (one 16-byte read and one 16-byte write).  A
-//     wave's LDS accesses complete in program order, so layer 1 and later
-//     groups see the earlier writes.
+//     four consecutive batch values of one position -- the layer-0 product
+//     plus the paired layer-1 product -- into the partial row of the
+//     position's feature (one 16-byte read and one 16-byte write).  A wave's
+//     LDS accesses complete in program order, so later groups see the
+//     earlier writes.
 //  3. reduce: dXT = sum over slices s = 0..S-1 in ascending order (fp32 out), or
 //     fused with the bf16 stochastic rounding of shared_ffi/bindings.py:44-48.
 #include <algorithm>
@@ -45,6 +47,28 @@ int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, 
 namespace {
 
 // --------------------------------------------------------------- plan ------
+// Layer-0 slots of a range with T0 layer-0 tiles, T1 layer-1 tiles and nd
+// duplicated features: duplicated feature k sits at (tile k % T1, position
+// k / T1), as its layer-1 row does, so at position p the tiles [0,
+// dup_tiles_at(p)) hold duplicated features.  The other ("free") slots are
+// numbered position by position, tile by tile.
+__device__ __forceinline__ int dup_tiles_at(int p, int T1, int nd) {
+    return min(max(nd - p * T1, 0), T1);
+}
+__device__ __forceinline__ int dup_free_index(int t, int p, int T0, int T1, int nd) {
+    int n = 0;
+    for (int s = 0; s < p; ++s) n += T0 - dup_tiles_at(s, T1, nd);
+    return n + t - dup_tiles_at(p, T1, nd);
+}
+__device__ __forceinline__ void dup_free_slot(int k, int T0, int T1, int nd, int& t, int& p) {
+    for (p = 0; p < 15; ++p) {
+        const int fr = T0 - dup_tiles_at(p, T1, nd);
+        if (k < fr) break;
+        k -= fr;
+    }
+    t = dup_tiles_at(p, T1, nd) + k;
+}
+
 // Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*2 + 0..1]
 // = (tb | tm << 16, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative
 // to g*Tcap); meta[(g*ndr + ndr-1)*2 + 1] is the group's tile count.  For tile row
@@ -90,13 +114,13 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
     const int r = f / Dc;
     const int r_lo = r * Dc;
     const int key = (((f - r_lo) & 15) << 16) | (f - r_lo);
-    int pu = 0, pd = 0;  // order of the feature among the range's distinct / duplicated ones
+    int pn = 0, pd = 0;  // order of the feature among the range's single / duplicated ones
     if (tid < F && first) {
         for (int k = 0; k < F; ++k) {
             const int v = s_idx[k], fl = s_flag[k];
             const int kk = (((v - r_lo) & 15) << 16) | (v - r_lo);
             const bool in = (fl & 1) && v >= r_lo && v < r_lo + Dc && kk < key;
-            pu += in;
+            pn += in && !(fl & 2);
             pd += in && (fl & 2);
         }
         atomicAdd(&s_cnt[0][r], 1);
@@ -122,13 +146,23 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
     }
     const int64_t tbase = g * Tcap;
     if (tid < F && first) {
-        const int T0 = s_tile[r][1] - s_tile[r][0];
-        const int64_t row0 = (tbase + s_tile[r][0] + pu % T0) * 16 + pu / T0;
+        const int T0 = s_tile[r][1] - s_tile[r][0], T1 = s_tile[r][2] - s_tile[r][1];
+        // layer-0 slot: a duplicated feature takes the same (tile, position) as
+        // its layer-1 row, so the main kernel can add the two products before
+        // one partial update; single features fill the other slots position by
+        // position over the tiles
+        int t, p;
+        if (cnt > 1) {
+            t = pd % T1;
+            p = pd / T1;
+        } else {
+            dup_free_slot(pn, T0, T1, s_cnt[1][r], t, p);
+        }
+        const int64_t row0 = (tbase + s_tile[r][0] + t) * 16 + p;
         tfeat[row0] = (f - r_lo) * row_bytes;
         tsrc[row0] = (rank << 10) | (cnt << 1);
         if (cnt > 1) {
-            const int T1 = s_tile[r][2] - s_tile[r][1];
-            const int64_t row1 = (tbase + s_tile[r][1] + pd % T1) * 16 + pd / T1;
+            const int64_t row1 = (tbase + s_tile[r][1] + t) * 16 + p;
             tfeat[row1] = (f - r_lo) * row_bytes;
             tsrc[row1] = (rank << 10) | (cnt << 1) | 1;
         }
@@ -139,11 +173,17 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         const int t = i / 16, p = i % 16;
         int rr = 0;
         while (t >= s_tile[rr][2]) ++rr;  // empty ranges have tb == te and are skipped
-        const bool lay1 = t >= s_tile[rr][1];
-        const int used = lay1 ? s_cnt[1][rr] : s_cnt[0][rr];
-        const int tl0 = s_tile[rr][lay1 ? 1 : 0];
-        const int nt = (lay1 ? s_tile[rr][2] : s_tile[rr][1]) - tl0;
-        if (p * nt + (t - tl0) < used) continue;
+        const int nd = s_cnt[1][rr];
+        const int T0 = s_tile[rr][1] - s_tile[rr][0], T1 = s_tile[rr][2] - s_tile[rr][1];
+        bool used;
+        if (t >= s_tile[rr][1]) {
+            used = p * T1 + (t - s_tile[rr][1]) < nd;
+        } else {
+            const int tt = t - s_tile[rr][0];
+            const int occ = dup_tiles_at(p, T1, nd);
+            used = tt < occ || dup_free_index(tt, p, T0, T1, nd) < s_cnt[0][rr] - nd;
+        }
+        if (used) continue;
         tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
         tsrc[(tbase + t) * 16 + p] = 0;
     }
@@ -199,14 +239,17 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
 //    the tiles (MFMA, M = batch rows, N = 16 positions, K = labels); a lane then
 //    holds four consecutive batch values of one position and adds them into
 //    the partial row of the position's feature with one 16-byte read and one
-//    16-byte write.  Within a layer the tiles' features are distinct, so all
-//    reads of a layer are issued before its writes; a wave's LDS accesses
-//    complete in order, so layer 1 (the second rows of duplicated indices)
-//    and later groups see the earlier writes.  Padding positions add into
-//    trash rows that are never read.
+//    16-byte write.  A layer-1 tile (the second rows of duplicated indices)
+//    shares its positions' features with the layer-0 tile it pairs with, so
+//    its products are added to that tile's before the update.  Within a layer
+//    the tiles' features are distinct, so all reads of the update are issued
+//    before its writes; a wave's LDS accesses complete in order, so later
+//    groups see the earlier writes.  Padding positions add into trash rows
+//    that are never read.
 //  - one barrier per group publishes the next group's ring buffer.
 // Ranges holding more than RT tiles in a group process the rest in further
-// rounds staged synchronously (rare: a range's share of F is usually ~F/ndr).
+// rounds staged synchronously (rare: a range's share of F is usually ~F/ndr),
+// layer by layer.
 template <int G, int WAVES>
 struct BwdFCfg {
     static constexpr int KS = G >= 32 ? G / 32 : 1;  // MFMA k-steps over labels
@@ -378,12 +421,46 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
             r.c[t] = v;
         }
     };
-    // Partial update of the first NTL tiles of round pr: layer 0 (layer-1 tiles
-    // add into trash rows), then layer 1 if any; a pass issues all its reads
-    // before its writes (a layer's features are distinct), and a wave's LDS
-    // accesses complete in order, so later passes and rounds see the writes.
-    // The MFMAs of round cur (if given) are issued between the first pass's
-    // reads and writes.
+    // Partial update of a group's first round pr, whose first N0 tiles are
+    // layer 0: layer-1 tile t of the group is the round's tile N0 + t and pairs
+    // with its tile t (a round starting at the group's first tile holds
+    // layer-1 tiles only when all layer-0 tiles fit), so one pass adds both.
+    // Tiles past the range's are zero rows (zero products).  The MFMAs of the
+    // next round (mma) are issued between the reads and the writes.
+    auto update_first_n = [&](const Round& pr, auto n0, auto mma) __attribute__((always_inline)) {
+        constexpr int N0 = decltype(n0)::value;
+        f32x4 old[N0 > 0 ? N0 : 1];
+#pragma unroll
+        for (int t = 0; t < N0; ++t) old[t] = *reinterpret_cast<const f32x4*>(acc_b + pr.f[t]);
+        mma();
+#pragma unroll
+        for (int t = 0; t < N0; ++t) {
+            f32x4 v = pr.c[t];
+            if (N0 + t < RT) v += pr.c[N0 + t];
+            *reinterpret_cast<f32x4*>(acc_b + pr.f[t]) = old[t] + v;
+        }
+        // every LDS op of the wave but the N0 writes has completed
+        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(N0));
+    };
+    auto update_first = [&](const Round& pr, auto mma) __attribute__((always_inline)) {
+        static_assert(RT <= 8, "ring tiles");
+        using std::integral_constant;
+        switch (min(pr.n0, pr.nt)) {
+        case 0: update_first_n(pr, integral_constant<int, 0>{}, mma); break;
+        case 1: update_first_n(pr, integral_constant<int, 1>{}, mma); break;
+        case 2: update_first_n(pr, integral_constant<int, (RT >= 2 ? 2 : 1)>{}, mma); break;
+        case 3: update_first_n(pr, integral_constant<int, (RT >= 3 ? 3 : 1)>{}, mma); break;
+        case 4: update_first_n(pr, integral_constant<int, (RT >= 4 ? 4 : 1)>{}, mma); break;
+        case 5: update_first_n(pr, integral_constant<int, (RT >= 5 ? 5 : 1)>{}, mma); break;
+        case 6: update_first_n(pr, integral_constant<int, (RT >= 6 ? 6 : 1)>{}, mma); break;
+        case 7: update_first_n(pr, integral_constant<int, (RT >= 7 ? 7 : 1)>{}, mma); break;
+        default: update_first_n(pr, integral_constant<int, RT>{}, mma); break;
+        }
+    };
+    // Partial update of a further round: layer 0 (layer-1 tiles add into trash
+    // rows), then layer 1 if any; a pass issues all its reads before its writes
+    // (a layer's features are distinct), and a wave's LDS accesses complete in
+    // order, so later passes and rounds see the writes.
     auto update_n = [&](const Round& pr, auto ntiles, auto mma) __attribute__((always_inline)) {
         constexpr int NTL = decltype(ntiles)::value;
         f32x4 old[NTL > 0 ? NTL : 1];
@@ -408,7 +485,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         // every LDS op of the wave but the last pass's NTL writes has completed
         __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(NTL));
     };
-    // update of round pr specialised for its tile count (a uniform switch), with mma()
+    // update of a further round pr, specialised for its tile count (a uniform switch)
     auto update = [&](const Round& pr, auto mma) __attribute__((always_inline)) {
         static_assert(RT <= 8, "ring tiles");
         using std::integral_constant;
@@ -497,11 +574,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         u32x4 bf[RT][KS];
         read_round(P, bf, rd[P]);
         asm volatile("" ::: "memory");  // the update's LDS ops stay after the stage and reads
-        update(rd[1 - P], [&]() __attribute__((always_inline)) { mma_round(ya[Q], bf, rd[P]); });
+        update_first(rd[1 - P], [&]() __attribute__((always_inline)) { mma_round(ya[Q], bf, rd[P]); });
         round_counts(mu[0], 0, rd[P]);
         if ((int)mu[0][1] - (int)(mu[0][0] & 0xFFFF) > RT) {  // uniform, rare
             // add this round now, then the group's further rounds in order
-            update(rd[P], no_mma);
+            update_first(rd[P], no_mma);
             rd[P].nt = 0;
             __syncthreads();
             extra_rounds(i, mu[0], P, ya[Q]);
@@ -530,7 +607,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         body(i + 5, std::integral_constant<int, 5>{});
     }
     static_assert(kGroupUnroll % 2 == 0, "the last iteration's round is in rd[1]");
-    update(rd[1], no_mma);
+    update_first(rd[1], no_mma);
     __syncthreads();
 
     // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----

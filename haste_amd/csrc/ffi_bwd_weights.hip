@@ -188,6 +188,29 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
 
     const rsrc_t wr = make_rsrc(SGD ? sg.W + l0 * F : nullptr, SGD ? (int64_t)nl * F * 2 : 0);
     constexpr int CPR = C::CPR, WPT = C::WPT;
+    // Fused step: the weights and bias the epilogue updates are loaded now, so
+    // their latency hides behind the batch loop (when the gradient tile is
+    // processed in one pass, the thread's chunks are known: chunk tid + q*256
+    // is row it / CPR, slots (it % CPR) * 8 .. +7).  Not for F > 128, where the
+    // extra registers would cost a wave per SIMD.
+    constexpr bool kWPre = SGD && PR == G && FP <= 128;
+    u32x4 wpre[kWPre ? WPT : 1];
+    uint32_t bpre[NT];
+    if constexpr (SGD) {
+#pragma unroll
+        for (int q = 0; q < (kWPre ? WPT : 0); ++q) {
+            const int it = tid + q * kThreads;
+            const int j0 = (it % CPR) * 8;
+            wpre[q] = buf_load16(wr, it < PR * CPR && j0 < F ? (uint32_t)((it / CPR) * F + j0) * 2 : kOOB);
+        }
+        const rsrc_t bbr = make_rsrc(sg.bias != nullptr ? sg.bias + l0 : nullptr,
+                                     sg.bias != nullptr ? (int64_t)nl * 2 : 0);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int ll = (wn * NT + nt) * 16 + col;
+            bpre[nt] = __builtin_amdgcn_raw_buffer_load_b16(bbr, (do_bias && kq == 0 ? ll * 2 : (int)kOOB), 0, 0);
+        }
+    }
 
     // Ping-pong register sets by chunk parity (the loop body is unrolled twice),
     // so no register copy waits on a load: dY pieces are fetched two chunks
@@ -257,7 +280,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
             if constexpr (SGD) {
                 if (sg.bias != nullptr) {
                     float mv = sg.use_mom ? sg.mb[l] : 0.f;
-                    sg.bias[l] = (uint16_t)sgd_one(bf16_bits_to_f32(sg.bias[l]), v, &mv,
+                    sg.bias[l] = (uint16_t)sgd_one(bf16_bits_to_f32(bpre[nt]), v, &mv,
                                                    sg.use_mom, sg.lr, sg.wd, sg.mu, sg.do_sr,
                                                    (uint64_t)l, sg.k0, sg.k1);
                     if (sg.use_mom) sg.mb[l] = mv;
@@ -329,7 +352,9 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                 }
             }
             if constexpr (SGD) {
-                const u32x4 wv = buf_load16(wr, in ? e * 2 : kOOB);
+                u32x4 wv;
+                if constexpr (kWPre) wv = wpre[q];
+                else wv = buf_load16(wr, in ? e * 2 : kOOB);
                 float gv[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
                 float mv[8];
                 if (sg.use_mom) {
