@@ -52,9 +52,36 @@ struct FwdCfg {
     static_assert(MTILES % WM == 0 && PPT >= 1, "tile shape");
 };
 
+// Fused sparse-BCE epilogue (BCE = true): out receives dY = sigma(x) - y instead of
+// the logits x, where x is the bf16-rounded logit and y the label bit; logits,
+// when not null, receives x as well.  part[w] = workgroup w's sum over its valid
+// elements of max(x, 0) - y*x + log(1 + exp(-|x|)) (the loss of
+// src/runner.py:469-478, whose gradient in x is sigma(x) - y).  ybits holds one
+// bit per (row, label), ldyw 32-bit words per row.
+struct BceArgs {
+    const uint32_t* ybits;
+    int64_t ldyw;
+    uint16_t* logits;
+    float* part;
+};
+
+// dY = sigma(x) - y and the loss term of one element with label bit y (0 or 1),
+// in fp32 from the hardware exp2 / log2 / reciprocal (about 1 ulp each).  With
+// e = exp(-|x|) and r = 1 / (1 + e), sigma(x) and 1 - sigma(x) are r and e*r in
+// some order, so sigma(x) - 1 needs no cancelling subtraction.
+__device__ __forceinline__ float bce_term(float x, uint32_t y, float* dy) {
+    const float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(x) * 1.44269504088896341f);
+    const float d = 1.0f + e;
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float er = e * r;
+    const bool pos = x >= 0.0f;
+    *dy = y ? -(pos ? er : r) : (pos ? r : er);
+    return __builtin_fmaxf(x, 0.0f) - (y ? x : 0.0f) + __builtin_amdgcn_logf(d) * 0.693147180559945309f;
+}
+
 // LAST: the workgroup's group is the last one and holds fewer than G labels;
 // its stores are per element so that no column >= O is written.
-template <typename T, int G, int FP, bool LAST>
+template <typename T, int G, int FP, bool LAST, bool BCE>
 __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                                           const uint16_t* __restrict__ xT, int64_t ldx,
                                           const uint16_t* __restrict__ W,
@@ -62,7 +89,8 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                                           uint16_t* __restrict__ out, int64_t ldo, int B, int D,
                                           int F, int64_t O, int64_t g, int b_chunk0, int ntiles,
                                           char (*Xg)[FP * FwdCfg<G, FP>::RB], int32_t* sidx,
-                                          char (*stg)[FwdCfg<G, FP>::STG]) {
+                                          char (*stg)[FwdCfg<G, FP>::STG], const BceArgs& bce,
+                                          float* s_red) {
     using C = FwdCfg<G, FP>;
     constexpr int KS = C::KS, MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SRB = C::SRB;
     const int tid = threadIdx.x;
@@ -141,9 +169,32 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
     // lane's tr-read address: slot 8*kq + col/4 (+4 for the second half), batch
     // columns n0 + 4*(col%4)
     const int tr_off = (kq * 8 + col / 4) * RB + (col % 4) * 8;
+    // BCE: label words of the group for each of the lane's rows (the words
+    // holding labels l0 .. l0+G-1 start at word l0/32, bit l0 % 32)
+    constexpr int YW = G >= 64 ? G / 32 : 2;
+    const uint32_t ybit0 = (uint32_t)(l0 % 32);
+    float lsum = 0.0f;
     for (int t = 0; t < ntiles; ++t) {
         const int b_base = b_chunk0 + t * kBT;
         const char* xs = Xg[t & 1];
+        uint32_t yw[NT][YW];
+        if constexpr (BCE) {
+            const rsrc_t yr = make_rsrc(bce.ybits + (int64_t)b_base * bce.ldyw,
+                                        (int64_t)std::min(kBT, B - b_base) * bce.ldyw * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const uint32_t o = (uint32_t)(((wn * NT + nt) * 16 + col) * bce.ldyw + l0 / 32) * 4;
+                if constexpr (YW == 2) {
+                    const u32x2 v = buf_load8(yr, o);
+                    yw[nt][0] = v[0];
+                    yw[nt][1] = v[1];
+                } else {
+                    const u32x4 v = buf_load16(yr, o);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) yw[nt][k] = v[k];
+                }
+            }
+        }
         f32x4 acc[MT][NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -171,6 +222,7 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
         // stores per element instead, so no column >= O is written. ----
         const rsrc_t orr = make_rsrc(out + (int64_t)b_base * ldo + l0,
                                      (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2);
+        u32x2 hx[NT][MT];  // BCE: the rounded logits, when they are also written
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int rb = (wn * NT + nt) * 16 + col;  // row within the tile
@@ -178,8 +230,22 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
             for (int mt = 0; mt < MT; ++mt) {
                 const int ll = (wm * MT + mt) * 16 + kq * 4;  // label within the group
                 const f32x4 v = acc[mt][nt];
-                const u32x2 h = u32x2{pack2_rne<T>(v[0] + bv[mt][0], v[1] + bv[mt][1]),
-                                      pack2_rne<T>(v[2] + bv[mt][2], v[3] + bv[mt][3])};
+                u32x2 h = u32x2{pack2_rne<T>(v[0] + bv[mt][0], v[1] + bv[mt][1]),
+                                pack2_rne<T>(v[2] + bv[mt][2], v[3] + bv[mt][3])};
+                if constexpr (BCE) {
+                    hx[nt][mt] = h;
+                    const uint32_t bit = ybit0 + (uint32_t)ll;
+                    const uint32_t y4 = (yw[nt][bit >> 5] >> (bit & 31)) & 0xFu;
+                    const bool row_ok = b_base + rb < B;
+                    float dy[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t xb = (h[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu;
+                        const float term = bce_term(bits_to_f32<T>(xb), (y4 >> i) & 1u, &dy[i]);
+                        lsum += (row_ok && ll + i < nl) ? term : 0.0f;
+                    }
+                    h = u32x2{pack2_rne<T>(dy[0], dy[1]), pack2_rne<T>(dy[2], dy[3])};
+                }
                 const uint32_t off = (uint32_t)((int64_t)rb * ldo + ll) * 2;
                 if constexpr (!LAST) {
                     *reinterpret_cast<u32x2*>(&stg[wave][(nt * 16 + col) * SRB + (mt * 16 + kq * 4) * 2]) = h;
@@ -198,30 +264,73 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
         // staged rows go out as 16-byte stores, whole row segments per
         // instruction (full 128-byte lines at MT = 4); the wave reads back only
         // what it wrote, and a wave's LDS accesses complete in order
-        if constexpr (!LAST) {
+        auto flush = [&](const rsrc_t& dst) {
             constexpr int LPR = MT * 2;     // lanes per staged row (MT*32 bytes)
             constexpr int RPI = 64 / LPR;   // rows per instruction
 #pragma unroll
             for (int r0 = 0; r0 < NT * 16; r0 += RPI) {
+                // at G = 16 an instruction spans more rows than the wave staged
+                // (RPI = 32 > 16): the lanes past them store nothing
                 const int rr = r0 + lane / LPR, cb = (lane % LPR) * 16;
-                const u32x4 v = *reinterpret_cast<const u32x4*>(&stg[wave][rr * SRB + cb]);
-                const int rb = wn * NT * 16 + rr;
-                buf_store16(v, orr, (uint32_t)((int64_t)rb * ldo * 2 + (wm * MT * 16) * 2 + cb));
+                const bool own = RPI <= NT * 16 || rr < NT * 16;
+                const int rs = own ? rr : 0;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(&stg[wave][rs * SRB + cb]);
+                const int rb = wn * NT * 16 + rs;
+                buf_store16(v, dst, own ? (uint32_t)((int64_t)rb * ldo * 2 + (wm * MT * 16) * 2 + cb) : kOOB);
+            }
+        };
+        if constexpr (!LAST) flush(orr);
+        if constexpr (BCE) {
+            if (bce.logits != nullptr) {
+                // the rounded logits too: staged again (this wave's earlier reads
+                // of its staging rows complete first) or stored per element
+                const rsrc_t lr = make_rsrc(bce.logits + (int64_t)b_base * ldo + l0,
+                                            (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int rb = (wn * NT + nt) * 16 + col;
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const int ll = (wm * MT + mt) * 16 + kq * 4;
+                        if constexpr (!LAST) {
+                            *reinterpret_cast<u32x2*>(&stg[wave][(nt * 16 + col) * SRB + (mt * 16 + kq * 4) * 2]) =
+                                hx[nt][mt];
+                        } else {
+                            const uint32_t off = (uint32_t)((int64_t)rb * ldo + ll) * 2;
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                buf_store2((uint16_t)(hx[nt][mt][i >> 1] >> ((i & 1) * 16)), lr,
+                                           ll + i < nl ? off + 2 * i : kOOB);
+                        }
+                    }
+                }
+                if constexpr (!LAST) flush(lr);
             }
         }
         __syncthreads();
     }
+    if constexpr (BCE) {
+        // workgroup sum of the loss terms in a fixed order: lanes by xor
+        // butterfly, then the four waves in order
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) lsum += __shfl_xor(lsum, m, 64);
+        if (lane == 0) s_red[wave] = lsum;
+        __syncthreads();
+        if (tid == 0) *bce.part = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    }
 }
 
-template <typename T, int G, int FP>
+template <typename T, int G, int FP, bool BCE>
 __global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
-    int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk) {
+    int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk,
+    BceArgs bce) {
     using C = FwdCfg<G, FP>;
     __shared__ __attribute__((aligned(16))) char Xg[2][FP * C::RB];
     __shared__ int32_t sidx[FP];
     __shared__ __attribute__((aligned(16))) char stg[4][C::STG];
+    __shared__ float s_red[4];
 
     const int64_t work = xcd_remap(blockIdx.x, Gc * nchunks);
     if (work < 0) return;
@@ -229,26 +338,33 @@ __global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
     const int chunk = (int)(work % nchunks);
     const int b_chunk0 = chunk * tiles_per_chunk * kBT;
     const int ntiles = min(tiles_per_chunk, (B - b_chunk0 + kBT - 1) / kBT);
+    if constexpr (BCE) bce.part += work;
     if ((g + 1) * G > O)
-        fwd_group<T, G, FP, true>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
-                                  ntiles, Xg, sidx, stg);
+        fwd_group<T, G, FP, true, BCE>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
+                                       ntiles, Xg, sidx, stg, bce, s_red);
     else
-        fwd_group<T, G, FP, false>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
-                                   ntiles, Xg, sidx, stg);
+        fwd_group<T, G, FP, false, BCE>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
+                                        ntiles, Xg, sidx, stg, bce, s_red);
+}
+
+// Batch chunks per group: the whole batch per workgroup (up to kMaxTilesPerWG
+// tiles), split further only when there are too few groups to fill the GPU.
+// Returns the chunk count; *tpc = tiles per chunk.
+int64_t fwd_chunks(int64_t B, int64_t Gc, int64_t* tpc) {
+    const int64_t ntiles = ceil_div(B, kBT);
+    int64_t nchunks = ceil_div(ntiles, kMaxTilesPerWG);
+    while (Gc * nchunks < 2048 && nchunks < ntiles) ++nchunks;
+    *tpc = ceil_div(ntiles, nchunks);
+    return ceil_div(ntiles, *tpc);
 }
 
 template <typename T, int G, int FP>
 int launch_fwd(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
                const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
-               int64_t O, hipStream_t st) {
+               int64_t O, const BceArgs* bce, hipStream_t st) {
     const int64_t Gc = ceil_div(O, G);
-    const int64_t ntiles = ceil_div(B, kBT);
-    // whole batch per workgroup (up to kMaxTilesPerWG tiles); split further only
-    // when there are too few groups to fill the GPU
-    int64_t nchunks = ceil_div(ntiles, kMaxTilesPerWG);
-    while (Gc * nchunks < 2048 && nchunks < ntiles) ++nchunks;
-    const int64_t tpc = ceil_div(ntiles, nchunks);
-    nchunks = ceil_div(ntiles, tpc);
+    int64_t tpc = 1;
+    const int64_t nchunks = fwd_chunks(B, Gc, &tpc);
     const int64_t nlogical = Gc * nchunks;
     const int64_t grid = 8 * ceil_div(nlogical, 8);
     if (grid > 0x7FFFFFFF || (int64_t)kBT * ldo * 2 > kMaxRsrcBytes ||
@@ -257,8 +373,14 @@ int launch_fwd(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16
                   (long long)grid, (long long)ldo, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
-    ffi_fwd_kernel<T, G, FP><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
-        idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks, (int)tpc);
+    if (bce != nullptr)
+        ffi_fwd_kernel<T, G, FP, true><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
+            idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks,
+            (int)tpc, *bce);
+    else
+        ffi_fwd_kernel<T, G, FP, false><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
+            idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks,
+            (int)tpc, BceArgs{nullptr, 0, nullptr, nullptr});
     HASTE_CHECK_LAUNCH("haste_ffi_forward");
     return HASTE_OK;
 }
@@ -266,27 +388,75 @@ int launch_fwd(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16
 template <typename T, int G>
 int dispatch_fp(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
                 const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
-                int64_t O, hipStream_t st) {
-    if (F <= 32) return launch_fwd<T, G, 32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
-    if (F <= 64) return launch_fwd<T, G, 64>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
-    if (F <= 128) return launch_fwd<T, G, 128>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
-    return launch_fwd<T, G, 256>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
+                int64_t O, const BceArgs* bce, hipStream_t st) {
+    if (F <= 32) return launch_fwd<T, G, 32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    if (F <= 64) return launch_fwd<T, G, 64>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    if (F <= 128) return launch_fwd<T, G, 128>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    return launch_fwd<T, G, 256>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
 }
 
 template <typename T>
 int dispatch_g(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
                const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
-               int64_t O, int64_t G, hipStream_t st) {
+               int64_t O, int64_t G, const BceArgs* bce, hipStream_t st) {
     switch (G) {
-    case 16: return dispatch_fp<T, 16>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
-    case 32: return dispatch_fp<T, 32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
-    case 64: return dispatch_fp<T, 64>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
-    case 128: return dispatch_fp<T, 128>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, st);
+    case 16: return dispatch_fp<T, 16>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    case 32: return dispatch_fp<T, 32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    case 64: return dispatch_fp<T, 64>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    case 128: return dispatch_fp<T, 128>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
     default: break;
     }
     set_error("Unsupported group size for FFI kernel. choose from 16,32,64,128 (got %lld)",
               (long long)G);
     return HASTE_ERR_UNSUPPORTED;
+}
+
+// Label bits of the COO positives (row, label) pairs: SET ors the bits in, else
+// the words holding them are cleared (the whole word: the bitmap is all zero
+// between calls).  Pairs outside [0, B) x [0, O) are ignored.
+template <bool SET>
+__global__ __launch_bounds__(256) void label_bits_kernel(const int32_t* __restrict__ labels,
+                                                         int64_t nnz, uint32_t* __restrict__ ybits,
+                                                         int64_t ldyw, int B, int64_t O) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nnz) return;
+    const int r = labels[2 * i], c = labels[2 * i + 1];
+    if (r < 0 || r >= B || c < 0 || c >= O) return;
+    uint32_t* w = ybits + (int64_t)r * ldyw + c / 32;
+    if constexpr (SET)
+        atomicOr(w, 1u << (c % 32));
+    else
+        *w = 0u;
+}
+
+// loss = sum of the n workgroup partials: each thread sums a strided subset in
+// order, then a fixed tree over the threads.
+__global__ __launch_bounds__(256) void loss_sum_kernel(const float* __restrict__ part, int64_t n,
+                                                       float* __restrict__ loss) {
+    __shared__ float s[256];
+    float v = 0.0f;
+    for (int64_t i = threadIdx.x; i < n; i += 256) v += part[i];
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int m = 128; m >= 1; m >>= 1) {
+        if ((int)threadIdx.x < m) s[threadIdx.x] += s[threadIdx.x + m];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *loss = s[0];
+}
+
+struct BceLayout {
+    int64_t ldyw, bits_bytes, nparts, bytes;
+};
+BceLayout bce_layout(int64_t B, int64_t O, int64_t G) {
+    BceLayout L;
+    const int64_t Gc = ceil_div(O, G);
+    int64_t tpc = 1;
+    L.ldyw = ceil_div(Gc * G, 32);
+    L.bits_bytes = (B * L.ldyw * 4 + 255) / 256 * 256;
+    L.nparts = Gc * fwd_chunks(B, Gc, &tpc);
+    L.bytes = L.bits_bytes + L.nparts * 4;
+    return L;
 }
 
 }  // namespace
@@ -346,6 +516,63 @@ extern "C" int haste_ffi_forward(const int32_t* idx, const void* xT, int64_t ldx
     auto* o = static_cast<uint16_t*>(out);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (dtype == HASTE_DTYPE_BF16)
-        return haste::dispatch_g<haste::BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, st);
-    return haste::dispatch_g<haste::F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, st);
+        return haste::dispatch_g<haste::BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, nullptr, st);
+    return haste::dispatch_g<haste::F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, nullptr, st);
+}
+
+extern "C" int64_t haste_ffi_forward_bce_workspace_size(int64_t B, int64_t O, int64_t G) {
+    if (B <= 0 || O <= 0 || (G != 16 && G != 32 && G != 64 && G != 128)) return -1;
+    return haste::bce_layout(B, O, G).bytes;
+}
+
+extern "C" int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t ldx,
+                                     const void* W, const void* bias, const int32_t* labels,
+                                     int64_t nnz, void* dY, int64_t ldo, void* logits,
+                                     float* loss, void* workspace, int64_t ws_bytes, int64_t B,
+                                     int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype,
+                                     void* stream) {
+    int rc = haste::check_ffi_shape("haste_ffi_forward_bce", B, D, F, O, G, dtype);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(idx && xT && W && dY && loss && workspace && (labels || nnz == 0) && nnz >= 0,
+                    "haste_ffi_forward_bce: null pointer or negative nnz");
+    HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
+                    "haste_ffi_forward_bce: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)",
+                    (long long)ldx, (long long)B);
+    HASTE_CHECK_ARG(ldo >= O && ldo % 8 == 0,
+                    "haste_ffi_forward_bce: ldo must be >= O and a multiple of 8 (ldo=%lld O=%lld)",
+                    (long long)ldo, (long long)O);
+    HASTE_CHECK_ARG(haste::aligned16(xT) && haste::aligned16(W) && haste::aligned16(dY) &&
+                        (logits == nullptr || haste::aligned16(logits)) &&
+                        haste::aligned16(workspace),
+                    "haste_ffi_forward_bce: xT, W, dY, logits and workspace must be 16-byte aligned");
+    const haste::BceLayout L = haste::bce_layout(B, O, G);
+    HASTE_CHECK_ARG(ws_bytes >= L.bytes,
+                    "haste_ffi_forward_bce: workspace too small (%lld < %lld bytes)",
+                    (long long)ws_bytes, (long long)L.bytes);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    auto* ybits = static_cast<uint32_t*>(workspace);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.bits_bytes);
+    const int64_t lblocks = (nnz + 255) / 256;
+    if (lblocks > 0) {
+        haste::label_bits_kernel<true><<<dim3((unsigned)lblocks), dim3(256), 0, st>>>(
+            labels, nnz, ybits, L.ldyw, (int)B, O);
+        HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
+    }
+    const haste::BceArgs bce{ybits, L.ldyw, static_cast<uint16_t*>(logits), part};
+    auto* x = static_cast<const uint16_t*>(xT);
+    auto* w = static_cast<const uint16_t*>(W);
+    auto* bb = static_cast<const uint16_t*>(bias);
+    auto* o = static_cast<uint16_t*>(dY);
+    rc = dtype == HASTE_DTYPE_BF16
+             ? haste::dispatch_g<haste::BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st)
+             : haste::dispatch_g<haste::F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st);
+    if (rc != HASTE_OK) return rc;
+    if (lblocks > 0) {
+        haste::label_bits_kernel<false><<<dim3((unsigned)lblocks), dim3(256), 0, st>>>(
+            labels, nnz, ybits, L.ldyw, (int)B, O);
+        HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
+    }
+    haste::loss_sum_kernel<<<dim3(1), dim3(256), 0, st>>>(part, L.nparts, loss);
+    HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
+    return HASTE_OK;
 }

@@ -50,6 +50,9 @@ class FFITrainStep:
         # (written by backward_features, or by backward_weights_sgd for the weights
         # it updates); None when stale
         self._wt_version = None
+        self.bce_ws = None   # forward_bce's label bits + loss partials (allocated on first use)
+        self.dY_buf = None
+        self.loss_buf = None
         self.code = _lib.DTYPE_BF16
         self.gcode = _C.dtype_code(grad_dtype)
         self._sgd_args = None
@@ -97,6 +100,50 @@ class FFITrainStep:
                   self.logits_buf.data_ptr(), self.ldo, self.B, self.D, self.F, self.O, self.G,
                   self.code, _C.stream_of(self.W))
         return self.logits
+
+    def forward_bce(self, x: torch.Tensor, labels: torch.Tensor,
+                    write_logits: bool = False) -> torch.Tensor:
+        """Forward fused with the sparse BCE loss (src/runner.py:469-478): ``labels``
+        is the COO [nnz, 2] int32 (row, label) list of positives.  Writes
+        dY = sigma(logits) - Y into ``dY_buf`` ([B, ldo]; the logits into
+        ``logits_buf`` too when ``write_logits``) and returns the summed loss as a
+        0-d fp32 tensor (computed on the device, no host sync)."""
+        if tuple(x.shape) != (self.B, self.D) or x.dtype != torch.bfloat16:
+            raise ValueError(f"FFITrainStep.forward_bce: x must be bf16 [{self.B}, {self.D}] "
+                             f"(got {x.dtype} {list(x.shape)})")
+        _C.require_device(x, "x")
+        _C.require_device(labels, "labels")
+        if labels.dtype != torch.int32 or labels.dim() != 2 or labels.shape[1] != 2:
+            raise ValueError("FFITrainStep.forward_bce: labels must be int32 [nnz, 2] (row, label)")
+        labels = labels.contiguous()
+        if x.stride(1) != 1:
+            x = x.contiguous()
+        if self.bce_ws is None:
+            n = _lib.lib().haste_ffi_forward_bce_workspace_size(self.B, self.O, self.G)
+            if n < 0:
+                raise ValueError("FFITrainStep.forward_bce: unsupported shape")
+            self.bce_ws = torch.zeros(n, dtype=torch.uint8, device=self.W.device)
+            self.dY_buf = torch.zeros(self.B, self.ldo, dtype=torch.bfloat16, device=self.W.device)
+            self.loss_buf = torch.zeros((), dtype=torch.float32, device=self.W.device)
+        st = _C.stream_of(self.W)
+        _lib.call("haste_transpose_features", x.data_ptr(), x.stride(0), self.xT_buf.data_ptr(),
+                  self.ldx, self.B, self.D, st)
+        _lib.call("haste_ffi_forward_bce", self.idx.data_ptr(), self.xT_buf.data_ptr(), self.ldx,
+                  self.W.data_ptr(), None if self.bias is None else self.bias.data_ptr(),
+                  labels.data_ptr(), labels.shape[0], self.dY_buf.data_ptr(), self.ldo,
+                  self.logits_buf.data_ptr() if write_logits else None, self.loss_buf.data_ptr(),
+                  self.bce_ws.data_ptr(), self.bce_ws.numel(), self.B, self.D, self.F, self.O,
+                  self.G, self.code, st)
+        return self.loss_buf
+
+    def step_bce(self, x: torch.Tensor, labels: torch.Tensor) -> torch.Tensor:
+        """A training step with the loss fused into the forward: forward + BCE
+        gradient -> backward to features (dX) -> fused weight/bias gradient +
+        SR-SGD.  Returns the loss (0-d fp32 device tensor) of the step's forward."""
+        loss = self.forward_bce(x, labels)
+        self.backward_features(self.dY_buf, self.ldo)
+        self.backward_weights_sgd(self.dY_buf, self.ldo)
+        return loss
 
     def _check_dY(self, dY: torch.Tensor, lddy: int) -> None:
         _C.require_device(dY, "dY")

@@ -59,6 +59,32 @@ int haste_ffi_forward(const int32_t* idx, const void* xT, int64_t ldx, const voi
                       int64_t O, int64_t G, int32_t dtype, void* stream);
 
 /*
+ * Grouped FFI forward fused with the sparse BCE loss of the application's
+ * training loop (src/runner.py:469-478, labels in the COO [nnz, 2] int32
+ * (row, label) form of src/data.py:26-46):
+ *   x[b, l]  = the forward's bf16 logit (RNE of the fp32 sum + bias);
+ *   dY[b, l] = RNE(sigma(x) - y[b, l]), the gradient of the loss in x (the
+ *              autograd of the reference formula through PyTorch's bf16 ops is
+ *              this up to rounding);
+ *   *loss    = sum over b < B, l < O of max(x, 0) - y*x + log(1 + exp(-|x|)),
+ *              fp32, summed in a fixed order (deterministic).
+ * y is 1 at the listed (row, label) pairs (duplicates count once; pairs
+ * outside [0, B) x [0, O) are ignored).  dY has the layout of haste_ffi_forward's
+ * out (columns >= O of the last group are zero); logits, if not NULL, also
+ * receives x.  loss is a device pointer to one float.  The workspace
+ * (haste_ffi_forward_bce_workspace_size bytes, 16-byte aligned) must be zero
+ * before its first use; every call leaves it zero again.  No counterpart in
+ * shared_ffi: replaces the application's logits -> _bce_loss -> autograd
+ * sequence, so the logits need not make a round trip through HBM.
+ */
+int64_t haste_ffi_forward_bce_workspace_size(int64_t B, int64_t O, int64_t G);
+int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t ldx, const void* W,
+                          const void* bias, const int32_t* labels, int64_t nnz, void* dY,
+                          int64_t ldo, void* logits, float* loss, void* workspace,
+                          int64_t ws_bytes, int64_t B, int64_t D, int64_t F, int64_t O,
+                          int64_t G, int32_t dtype, void* stream);
+
+/*
  * Workspace bytes needed by haste_ffi_bwd_features / haste_ffi_bwd_features_sr.
  * Returns a negative HASTE_ERR_* code for unsupported shapes.
  */

@@ -93,3 +93,23 @@ def ffi_backward_weights(idx: torch.Tensor, xT: torch.Tensor, dY: torch.Tensor,
 def bias_grad(dY: torch.Tensor) -> torch.Tensor:
     """torch.sum(grad_output, dim=0) (bindings.py:40), fp32."""
     return dY.float().sum(0)
+
+
+def bce_loss_grad(logits: torch.Tensor, labels: torch.Tensor):
+    """Sparse BCE of the application's training loop (src/runner.py:469-478) on
+    logits x [B, O] (bf16 values, upcast exactly) with positives given as COO
+    int32 [nnz, 2] (row, label) pairs (src/data.py:26-46; y = 1 there, a repeated
+    pair counts once, pairs outside [0, B) x [0, O) are ignored):
+      loss = sum max(x, 0) - sum_pos x + sum log(1 + exp(-|x|))   (fp64 here)
+      dY   = sigmoid(x) - y, rounded to bf16 (RNE)
+    Returns (loss as a Python float, dY bf16 [B, O], y fp32 [B, O])."""
+    x = logits.double()
+    B, O = x.shape
+    y = torch.zeros(B, O, dtype=torch.float64)
+    lab = labels.long()
+    ok = (lab[:, 0] >= 0) & (lab[:, 0] < B) & (lab[:, 1] >= 0) & (lab[:, 1] < O)
+    lab = lab[ok]
+    y[lab[:, 0], lab[:, 1]] = 1.0
+    loss = (x.clamp(min=0.0) - y * x + torch.log1p(torch.exp(-x.abs()))).sum().item()
+    dY = (torch.sigmoid(x) - y).to(torch.bfloat16)
+    return loss, dY, y.float()

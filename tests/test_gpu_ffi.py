@@ -183,3 +183,22 @@ def test_forward_leaves_columns_past_O_untouched(dev, B, O, G, F):
     torch.testing.assert_close(out[:B, :O].float().cpu(), ref, **TOL16)
     assert bool((out[:B, O:] == 7.0).all()), "columns >= O were written"
     assert bool((out[B:] == 7.0).all()), "rows >= B were written"
+
+
+@pytest.mark.parametrize("B", [37, 64, 100, 130])
+def test_forward_g16_rows_written_once(dev, B):
+    """G = 16: every wave stores only the rows it staged (an instruction spans 32
+    rows, a wave stages 16); each call rewrites a NaN-filled output the same."""
+    D, O, G, F = 200, 513, 16, 64
+    x, W, bias, idx, _ = make_case(B, D, O, G, F)
+    ref = oracle.ffi_forward(idx, x.t().contiguous(), W, bias, G)
+    ldx, ldo = (B + 7) // 8 * 8, (O + 7) // 8 * 8
+    xT = torch.zeros(D, ldx, dtype=torch.bfloat16)
+    xT[:, :B] = x.t()
+    xT, idx_d, W_d, bias_d = xT.to(dev), idx.to(dev), W.to(dev), bias.to(dev)
+    for _ in range(3):
+        out = torch.full((B, ldo), float("nan"), dtype=torch.bfloat16, device=dev)
+        _lib.call("haste_ffi_forward", idx_d.data_ptr(), xT.data_ptr(), ldx, W_d.data_ptr(),
+                  bias_d.data_ptr(), out.data_ptr(), ldo, B, D, F, O, G, _lib.DTYPE_BF16,
+                  torch.cuda.current_stream().cuda_stream)
+        torch.testing.assert_close(out[:, :O].float().cpu(), ref, **TOL16)

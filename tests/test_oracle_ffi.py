@@ -97,3 +97,60 @@ def test_duplicate_indices_sum():
     dY = torch.tensor([[1.0, 0.0], [0.0, 1.0]])
     dXT = oracle.ffi_backward_features(idx, W, dY, G, D)
     assert np.allclose(dXT[3].numpy(), [11.0, 22.0]) and dXT[:3].abs().sum() == 0
+
+
+# ---- sparse BCE (fused into the forward by haste_ffi_forward_bce) ----
+def _bce_case(B=5, O=37, nnz=12, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(B, O, generator=g) * 4).to(torch.bfloat16)
+    rows = torch.randint(0, B, (nnz,), generator=g)
+    cols = torch.randint(0, O, (nnz,), generator=g)
+    labels = torch.stack([rows, cols], 1).to(torch.int32)
+    return x, labels
+
+
+def test_bce_matches_library_bce_with_logits():
+    """The loss is torch's binary_cross_entropy_with_logits (sum) on the same
+    binary targets, and dY its autograd gradient, rounded to bf16."""
+    x, labels = _bce_case()
+    loss, dY, y = oracle.ffi.bce_loss_grad(x, labels)
+    xd = x.double().requires_grad_(True)
+    ref = torch.nn.functional.binary_cross_entropy_with_logits(xd, y.double(), reduction="sum")
+    ref.backward()
+    assert abs(loss - ref.item()) <= 1e-12 * abs(ref.item())
+    assert torch.equal(dY, xd.grad.to(torch.bfloat16))
+
+
+def test_bce_closed_forms():
+    """x = 0 everywhere: loss = B*O*ln 2 and dY = 1/2 - y; a repeated positive
+    counts once; pairs out of range are ignored; large |x| gives exact 0/1 terms."""
+    B, O = 3, 10
+    x = torch.zeros(B, O, dtype=torch.bfloat16)
+    labels = torch.tensor([[0, 1], [0, 1], [2, 9], [3, 0], [-1, 2], [1, 10]], dtype=torch.int32)
+    loss, dY, y = oracle.ffi.bce_loss_grad(x, labels)
+    assert abs(loss - B * O * np.log(2.0)) < 1e-9
+    expect = torch.full((B, O), 0.5)
+    expect[0, 1] = -0.5
+    expect[2, 9] = -0.5
+    assert torch.equal(dY.float(), expect)
+    assert y.sum().item() == 2
+    big = torch.tensor([[100.0, -100.0]], dtype=torch.bfloat16)
+    loss, dY, _ = oracle.ffi.bce_loss_grad(big, torch.tensor([[0, 0]], dtype=torch.int32))
+    assert 0.0 <= loss < 1e-40  # two terms of log1p(exp(-100))
+    assert dY.float().tolist() == [[0.0, 0.0]]
+
+
+def test_bce_gradient_is_loss_derivative():
+    """Central finite differences of the fp64 loss in x match sigma(x) - y."""
+    x, labels = _bce_case(B=2, O=6, nnz=4, seed=5)
+    loss, dY, y = oracle.ffi.bce_loss_grad(x, labels)
+    xd = x.double()
+    h = 1e-6
+    for b in range(2):
+        for l in range(6):
+            xp, xm = xd.clone(), xd.clone()
+            xp[b, l] += h
+            xm[b, l] -= h
+            f = lambda t: (t.clamp(min=0) - y.double() * t + torch.log1p(torch.exp(-t.abs()))).sum()
+            num = (f(xp) - f(xm)).item() / (2 * h)
+            assert abs(num - (torch.sigmoid(xd[b, l]) - y[b, l]).item()) < 1e-6
