@@ -222,7 +222,12 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
         // stores per element instead, so no column >= O is written. ----
         const rsrc_t orr = make_rsrc(out + (int64_t)b_base * ldo + l0,
                                      (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2);
-        u32x2 hx[NT][MT];  // BCE: the rounded logits, when they are also written
+        // BCE with logits wanted: the rounded logits go out directly, 8 bytes per
+        // lane (rows past B and labels past O outside the resource)
+        const rsrc_t lgr = BCE && bce.logits != nullptr
+            ? make_rsrc(bce.logits + (int64_t)b_base * ldo + l0,
+                        (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2)
+            : make_rsrc(out, 0);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int rb = (wn * NT + nt) * 16 + col;  // row within the tile
@@ -233,7 +238,17 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                 u32x2 h = u32x2{pack2_rne<T>(v[0] + bv[mt][0], v[1] + bv[mt][1]),
                                 pack2_rne<T>(v[2] + bv[mt][2], v[3] + bv[mt][3])};
                 if constexpr (BCE) {
-                    hx[nt][mt] = h;
+                    if (bce.logits != nullptr) {
+                        const uint32_t lo = (uint32_t)((int64_t)rb * ldo + ll) * 2;
+                        if (ll + 4 <= nl) {
+                            buf_store8(h, lgr, lo);
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                buf_store2((uint16_t)(h[i >> 1] >> ((i & 1) * 16)), lgr,
+                                           ll + i < nl ? lo + 2 * i : kOOB);
+                        }
+                    }
                     const uint32_t bit = ybit0 + (uint32_t)ll;
                     const uint32_t y4 = (yw[nt][bit >> 5] >> (bit & 31)) & 0xFu;
                     const bool row_ok = b_base + rb < B;
@@ -280,33 +295,6 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
             }
         };
         if constexpr (!LAST) flush(orr);
-        if constexpr (BCE) {
-            if (bce.logits != nullptr) {
-                // the rounded logits too: staged again (this wave's earlier reads
-                // of its staging rows complete first) or stored per element
-                const rsrc_t lr = make_rsrc(bce.logits + (int64_t)b_base * ldo + l0,
-                                            (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const int rb = (wn * NT + nt) * 16 + col;
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const int ll = (wm * MT + mt) * 16 + kq * 4;
-                        if constexpr (!LAST) {
-                            *reinterpret_cast<u32x2*>(&stg[wave][(nt * 16 + col) * SRB + (mt * 16 + kq * 4) * 2]) =
-                                hx[nt][mt];
-                        } else {
-                            const uint32_t off = (uint32_t)((int64_t)rb * ldo + ll) * 2;
-#pragma unroll
-                            for (int i = 0; i < 4; ++i)
-                                buf_store2((uint16_t)(hx[nt][mt][i >> 1] >> ((i & 1) * 16)), lr,
-                                           ll + i < nl ? off + 2 * i : kOOB);
-                        }
-                    }
-                }
-                if constexpr (!LAST) flush(lr);
-            }
-        }
         __syncthreads();
     }
     if constexpr (BCE) {
@@ -320,8 +308,13 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
     }
 }
 
+// The BCE epilogue's extra registers would cost a wave per SIMD at G*F = 64*128;
+// the bound keeps three (the plain kernel fits them as is).
+template <int G, int FP, bool BCE>
+constexpr int fwd_waves_per_simd() { return BCE && G * FP == 64 * 128 ? 3 : 2; }
+
 template <typename T, int G, int FP, bool BCE>
-__global__ __launch_bounds__(kThreads, 2) void ffi_fwd_kernel(
+__global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE>())) void ffi_fwd_kernel(
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
     int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk,
