@@ -35,6 +35,55 @@ def _grad_dtype(p: torch.Tensor) -> torch.dtype:
     return gd if gd is not None else p.dtype
 
 
+def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.Tensor,
+               gsize: int, grad_output: torch.Tensor, need_x: bool, need_w: bool, need_b: bool,
+               w_grad_dtype: torch.dtype, bias_dtype: Optional[torch.dtype]):
+    """(grad_x, grad_w, grad_b) of the grouped FFI layer for grad_output [B, O]
+    (any row stride; rows are copied to aligned storage only when needed)."""
+    D, B = xT.shape
+    O, F = weights.shape
+    dtype = weights.dtype
+    dev = weights.device
+    if grad_output.dtype != dtype:
+        grad_output = grad_output.to(dtype)
+    dY, lddy = _C.rows_aligned(grad_output)
+    locs = group_locations.contiguous()
+    W = weights.contiguous()
+    stream = _C.stream_of(W)
+    code = _C.dtype_code(dtype)
+
+    grad_x = None
+    if need_x:
+        ws = _C.bwd_features_workspace(B, D, F, O, gsize, dtype, dev)
+        if dtype == torch.bfloat16:
+            grad_x = torch.empty(B, D, dtype=dtype, device=dev)
+            _lib.call("haste_ffi_bwd_features_sr", locs.data_ptr(), W.data_ptr(),
+                      dY.data_ptr(), lddy, grad_x.data_ptr(), SR_SEED_GRAD_X, ws.data_ptr(),
+                      ws.numel(), B, D, F, O, gsize, code, 0, stream)
+        else:
+            dxt = torch.empty(D, B, dtype=torch.float32, device=dev)
+            _lib.call("haste_ffi_bwd_features", locs.data_ptr(), W.data_ptr(), dY.data_ptr(),
+                      lddy, dxt.data_ptr(), ws.data_ptr(), ws.numel(), B, D, F, O, gsize,
+                      code, 0, stream)
+            grad_x = dxt.t().to(dtype).contiguous()
+
+    grad_w = grad_b = None
+    if need_w or need_b:
+        ldx = xT.stride(0)
+        grad_w = torch.empty(O, F, dtype=w_grad_dtype, device=dev) if need_w else None
+        grad_b = torch.empty(O, dtype=bias_dtype, device=dev) if need_b else None
+        if need_w:
+            dw_ptr, dw_code = grad_w.data_ptr(), _C.dtype_code(w_grad_dtype)
+        else:  # bias only: the kernel still needs a dW target
+            scratch = torch.empty(O, F, dtype=dtype, device=dev)
+            dw_ptr, dw_code = scratch.data_ptr(), code
+        _lib.call("haste_ffi_bwd_weights", locs.data_ptr(), xT.data_ptr(), ldx, dY.data_ptr(),
+                  lddy, dw_ptr, dw_code, None if grad_b is None else grad_b.data_ptr(),
+                  0 if grad_b is None else _C.dtype_code(bias_dtype), B, D, F, O, gsize,
+                  code, stream)
+    return grad_x, grad_w, grad_b
+
+
 class GroupFFIMulFunction(torch.autograd.Function):
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
@@ -59,49 +108,69 @@ class GroupFFIMulFunction(torch.autograd.Function):
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, grad_output):
         xT, weights, group_locations = ctx.saved_tensors
-        gsize = ctx.gsize
-        D, B = xT.shape
-        O, F = weights.shape
-        dtype = weights.dtype
-        dev = weights.device
-        if grad_output.dtype != dtype:
-            grad_output = grad_output.to(dtype)
-        dY, lddy = _C.rows_aligned(grad_output)
-        locs = group_locations.contiguous()
-        W = weights.contiguous()
-        stream = _C.stream_of(W)
-        code = _C.dtype_code(dtype)
-
-        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        need_b = ctx.use_bias and ctx.needs_input_grad[3]
-
-        grad_x = None
-        if need_x:
-            ws = _C.bwd_features_workspace(B, D, F, O, gsize, dtype, dev)
-            if dtype == torch.bfloat16:
-                grad_x = torch.empty(B, D, dtype=dtype, device=dev)
-                _lib.call("haste_ffi_bwd_features_sr", locs.data_ptr(), W.data_ptr(),
-                          dY.data_ptr(), lddy, grad_x.data_ptr(), SR_SEED_GRAD_X, ws.data_ptr(),
-                          ws.numel(), B, D, F, O, gsize, code, 0, stream)
-            else:
-                dxt = torch.empty(D, B, dtype=torch.float32, device=dev)
-                _lib.call("haste_ffi_bwd_features", locs.data_ptr(), W.data_ptr(), dY.data_ptr(),
-                          lddy, dxt.data_ptr(), ws.data_ptr(), ws.numel(), B, D, F, O, gsize,
-                          code, 0, stream)
-                grad_x = dxt.t().to(dtype).contiguous()
-
-        grad_w = grad_b = None
-        if need_w or need_b:
-            ldx = xT.stride(0)
-            grad_w = torch.empty(O, F, dtype=ctx.w_grad_dtype, device=dev) if need_w else None
-            grad_b = torch.empty(O, dtype=ctx.bias_dtype, device=dev) if need_b else None
-            if need_w:
-                dw_ptr, dw_code = grad_w.data_ptr(), _C.dtype_code(ctx.w_grad_dtype)
-            else:  # bias only: the kernel still needs a dW target
-                scratch = torch.empty(O, F, dtype=dtype, device=dev)
-                dw_ptr, dw_code = scratch.data_ptr(), code
-            _lib.call("haste_ffi_bwd_weights", locs.data_ptr(), xT.data_ptr(), ldx, dY.data_ptr(),
-                      lddy, dw_ptr, dw_code, None if grad_b is None else grad_b.data_ptr(),
-                      0 if grad_b is None else _C.dtype_code(ctx.bias_dtype), B, D, F, O, gsize,
-                      code, stream)
+        grad_x, grad_w, grad_b = _ffi_grads(
+            xT, weights, group_locations, ctx.gsize, grad_output, ctx.needs_input_grad[0],
+            ctx.needs_input_grad[1], ctx.use_bias and ctx.needs_input_grad[3], ctx.w_grad_dtype,
+            ctx.bias_dtype)
         return grad_x, grad_w, None, grad_b, None
+
+
+class HeadTailFFIFunction(torch.autograd.Function):
+    """torch.cat((head(x_head), ffi(x_tail)), dim=1) of the head/tail split model
+    (src/model.py:227-232,245-248: a dense nn.Linear head and an FFI tail), built
+    in one [B, H + O] buffer: the FFI kernel writes the tail logits in place (the
+    view starts at the column that puts the tail's rows on 16-byte boundaries)
+    and the backward reads the tail's columns of grad_output in place when their
+    rows are so aligned, so the B x O tail is never copied.  Values are those of
+    the torch.cat formulation: the same head op (F.linear) and FFI kernels."""
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
+    def forward(ctx: Any, x_head: torch.Tensor, head_weight: torch.Tensor,
+                head_bias: Optional[torch.Tensor], x_tail: torch.Tensor, weights: torch.Tensor,
+                group_locations: torch.Tensor, bias: Optional[torch.Tensor],
+                gsize: int = 32) -> torch.Tensor:
+        _C.require_device(x_tail, "x_tail")
+        if x_tail.dim() != 2 or x_head.dim() != 2 or x_head.shape[0] != x_tail.shape[0]:
+            raise RuntimeError("x_head and x_tail must be 2-D with the same batch size")
+        B, D = x_tail.shape
+        O, F = weights.shape
+        H = head_weight.shape[0]
+        dt = x_tail.dtype
+        head = torch.nn.functional.linear(x_head, head_weight, head_bias).to(dt)
+        s0 = (8 - H % 8) % 8                       # tail columns start on a multiple of 8
+        ld = _C.round8(s0 + H + O)
+        buf = torch.empty(B, ld, dtype=dt, device=x_tail.device)
+        out = buf[:, s0: s0 + H + O]
+        out[:, :H].copy_(head)
+        xT, ldx = _C.padded_transpose(x_tail)
+        locs = _C._check_locations(group_locations, O, F, gsize)
+        if weights.dtype != dt or (bias is not None and bias.dtype != dt):
+            raise RuntimeError("weights and bias dtype must match x_tail's")
+        W = weights.contiguous()
+        b = None if bias is None else bias.contiguous()
+        _lib.call("haste_ffi_forward", locs.data_ptr(), xT.data_ptr(), ldx, W.data_ptr(),
+                  None if b is None else b.data_ptr(), buf[:, s0 + H:].data_ptr(), ld, B, D, F, O,
+                  gsize, _C.dtype_code(dt), _C.stream_of(x_tail))
+        ctx.save_for_backward(x_head, head_weight, xT, weights, group_locations)
+        ctx.H, ctx.gsize = H, int(gsize)
+        ctx.head_has_bias = head_bias is not None
+        ctx.use_bias = bias is not None
+        ctx.w_grad_dtype = _grad_dtype(weights)
+        ctx.bias_dtype = _grad_dtype(bias) if bias is not None else None
+        return out
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, grad_output):
+        x_head, head_weight, xT, weights, group_locations = ctx.saved_tensors
+        H = ctx.H
+        gh = grad_output[:, :H]
+        n = ctx.needs_input_grad
+        gx_h = gh.to(head_weight.dtype) @ head_weight if n[0] else None
+        gw_h = gh.t().to(x_head.dtype) @ x_head if n[1] else None
+        gb_h = gh.sum(0) if (ctx.head_has_bias and n[2]) else None
+        gx_t, gw_t, gb_t = _ffi_grads(xT, weights, group_locations, ctx.gsize,
+                                      grad_output[:, H:], n[3], n[4], ctx.use_bias and n[6],
+                                      ctx.w_grad_dtype, ctx.bias_dtype)
+        return gx_h, gw_h, gb_h, gx_t, gw_t, None, gb_t, None

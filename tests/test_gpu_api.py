@@ -204,3 +204,40 @@ def test_train_step_replans_after_rewire(dev):
     layer.rewire(seed=3)
     assert layer.group_locations._version != v0
     check()  # plan rebuilt for the new indices
+
+
+@pytest.mark.parametrize("H", [1000, 1001])
+def test_head_tail_logits_match_cat(dev, H):
+    """ops.head_tail_logits equals torch.cat((head(x), group_ffi_mul(x, ...)), 1) of
+    src/model.py:245-248 in values and gradients; the tail lands in place on
+    16-byte aligned rows of the concatenated buffer."""
+    B, D, O, G, F = 64, 256, 3000, 32, 64
+    torch.manual_seed(3)
+    x = torch.randn(B, D, device=dev).to(torch.bfloat16)
+    head = torch.nn.Linear(D, H).to(dev).to(torch.bfloat16)
+    W = (torch.randn(O, F, device=dev) * 0.1).to(torch.bfloat16)
+    bias = (torch.randn(O, device=dev) * 0.1).to(torch.bfloat16)
+    idx = torch.randint(0, D, ((O + G - 1) // G, F), dtype=torch.int32, device=dev)
+    g_out = (torch.randn(B, H + O, device=dev) * 0.1).to(torch.bfloat16)
+
+    def run(fused):
+        xr = x.clone().requires_grad_(True)
+        hd = torch.nn.Linear(D, H).to(dev).to(torch.bfloat16)
+        hd.load_state_dict(head.state_dict())
+        Wr, br = W.clone().requires_grad_(True), bias.clone().requires_grad_(True)
+        if fused:
+            out = ops.head_tail_logits(xr, hd, xr, Wr, idx, br, G)
+        else:
+            out = torch.cat((hd(xr), ops.group_ffi_mul(xr, Wr, idx, br, G)), dim=1)
+        out.backward(g_out)
+        return out.detach(), xr.grad, hd.weight.grad, hd.bias.grad, Wr.grad, br.grad
+
+    o_ref, gx_ref, ghw_ref, ghb_ref, gw_ref, gb_ref = run(False)
+    o, gx, ghw, ghb, gw, gb = run(True)
+    assert o.shape == (B, H + O)
+    assert (o[:, H:].data_ptr() % 16 == 0) and o.stride(0) % 8 == 0
+    assert np.array_equal(bits(o), bits(o_ref))
+    assert np.array_equal(bits(gw), bits(gw_ref)) and np.array_equal(bits(gb), bits(gb_ref))
+    torch.testing.assert_close(ghw.float(), ghw_ref.float(), **TOL16)
+    torch.testing.assert_close(ghb.float(), ghb_ref.float(), **TOL16)
+    torch.testing.assert_close(gx.float(), gx_ref.float(), **TOL16)
