@@ -15,6 +15,11 @@ Difference: the fp32 momentum buffer is allocated only once momentum is
 actually used (the reference always allocates it, optim_sr.py:35-44); a
 buffer created later starts at zero, which is what the reference's unused
 buffer holds.
+
+Checkpoints: ``state_dict()`` holds each group's current ``seed`` and the fp32
+momentum buffers.  ``load_state_dict`` keeps the buffers in fp32 (torch's
+default casts floating-point state to the parameter's dtype, which would round
+them to bf16), so a restored optimizer continues bit-identically.
 """
 from __future__ import annotations
 
@@ -34,6 +39,18 @@ class SRSgd(Optimizer):
                         use_momentum=use_momentum, stochastic_rounding=stochastic_rounding,
                         seed=seed)
         super().__init__(params, defaults)
+
+    def load_state_dict(self, state_dict) -> None:
+        # torch casts floating-point state to the parameter's dtype; the momentum
+        # buffers are fp32 whatever the parameter's dtype, so they are put back
+        saved = {k: v.get("momentum_buf") for k, v in state_dict["state"].items()}
+        saved_ids = [i for g in state_dict["param_groups"] for i in g["params"]]
+        super().load_state_dict(state_dict)
+        params = [p for g in self.param_groups for p in g["params"]]
+        for pid, p in zip(saved_ids, params):
+            m = saved.get(pid)
+            if isinstance(m, torch.Tensor):
+                self.state[p]["momentum_buf"] = m.to(dtype=torch.float32, device=p.device).clone()
 
     @staticmethod
     def _uses_momentum(group) -> bool:

@@ -27,7 +27,7 @@ INIT_MODES = ["random", "zero"]
 REGROW_MODES = ["random", "unused"]
 GROUP_SIZES = [16, 32, 64, 128]
 
-__all__ = ["GroupFixedFanIn"]
+__all__ = ["GroupFixedFanIn", "inflate_group_locations"]
 
 
 class GroupFixedFanIn(torch.nn.Module):
@@ -140,3 +140,12 @@ class GroupFixedFanIn(torch.nn.Module):
         # keyed on the version counter) that both tensors changed
         torch.autograd.graph.increment_version(self.weights)
         torch.autograd.graph.increment_version(self.group_locations)
+
+
+@torch.no_grad()
+def inflate_group_locations(group_locations: torch.Tensor, out_features: int,
+                            group_size: int) -> torch.Tensor:
+    """[ceil(L/G), F] group indices -> [L, F] per-label indices (each group row
+    repeated group_size times, truncated to L), the checkpoint conversion of
+    src/runner.py:323-334 from a grouped layer to a per-label fixed fan-in one."""
+    return group_locations.repeat_interleave(int(group_size), dim=0)[: int(out_features)]

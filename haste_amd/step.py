@@ -57,6 +57,14 @@ class FFITrainStep:
         self.gcode = _C.dtype_code(grad_dtype)
         self._sgd_args = None
 
+    def state_dict(self) -> dict:
+        """The step's own state (the parameters W, bias and idx belong to the caller):
+        the SR seed the next update will use."""
+        return {"seed": int(self.seed)}
+
+    def load_state_dict(self, state: dict) -> None:
+        self.seed = int(state["seed"])
+
     @property
     def dW(self) -> torch.Tensor:
         """[O, F] weight gradient of the last ``backward_weights`` call."""

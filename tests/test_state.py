@@ -1,0 +1,97 @@
+"""Checkpoint / state format of the FFI layer and its optimizer (SURVEY 8(f)4 row:
+shared_ffi/rewire.py:110,115,127 keys, src/runner.py:304-334)."""
+import io
+
+import pytest
+import torch
+
+from haste_amd.optim_sr import SRSgd
+from haste_amd.rewire import GroupFixedFanIn, inflate_group_locations
+
+
+def test_layer_state_dict_keys_and_dtypes():
+    """Keys, shapes and dtypes of the reference layer: weights [O, F] and bias [O]
+    parameters, group_locations int32 [ceil(O/G), F] persistent buffer; a state
+    dict loads into a fresh layer unchanged."""
+    torch.manual_seed(0)
+    layer = GroupFixedFanIn(300, 1001, 64, group_size=32, prune_mode="fraction", rewire_fraction=0.15,
+                            dtype=torch.bfloat16)
+    sd = layer.state_dict()
+    assert list(sd) == ["weights", "bias", "group_locations"]
+    assert sd["weights"].shape == (1001, 64) and sd["weights"].dtype == torch.bfloat16
+    assert sd["bias"].shape == (1001,) and sd["bias"].dtype == torch.bfloat16
+    assert sd["group_locations"].shape == (32, 64) and sd["group_locations"].dtype == torch.int32
+    buf = io.BytesIO()
+    torch.save(sd, buf)
+    buf.seek(0)
+    other = GroupFixedFanIn(300, 1001, 64, group_size=32, prune_mode="fraction", rewire_fraction=0.15,
+                            dtype=torch.bfloat16)
+    other.load_state_dict(torch.load(buf, weights_only=True))
+    for k, v in other.state_dict().items():
+        assert torch.equal(v, sd[k])
+
+
+def test_inflate_group_locations():
+    """Each group row repeated group_size times, truncated to L (src/runner.py:323-334)."""
+    g = torch.arange(12, dtype=torch.int32).view(3, 4)
+    out = inflate_group_locations(g, 7, 3)
+    assert out.shape == (7, 4)
+    for l in range(7):
+        assert torch.equal(out[l], g[l // 3])
+
+
+def test_optimizer_state_keeps_fp32_momentum_and_seed():
+    """SRSgd.state_dict carries the current seed and the fp32 momentum buffer, and
+    load_state_dict restores the buffer in fp32 (torch's default would cast it to
+    the bf16 parameter dtype)."""
+    p = torch.nn.Parameter(torch.zeros(10, dtype=torch.bfloat16))
+    opt = SRSgd([p], lr=0.1, momentum=0.9, seed=77)
+    m = torch.linspace(-1, 1, 10, dtype=torch.float32) / 3  # not representable in bf16
+    opt.state[p]["momentum_buf"] = m.clone()
+    opt.param_groups[0]["seed"] = 81
+    buf = io.BytesIO()
+    torch.save(opt.state_dict(), buf)
+    buf.seek(0)
+    q = torch.nn.Parameter(torch.zeros(10, dtype=torch.bfloat16))
+    opt2 = SRSgd([q], lr=0.1, momentum=0.9, seed=5)
+    opt2.load_state_dict(torch.load(buf, weights_only=True))
+    assert opt2.param_groups[0]["seed"] == 81
+    mb = opt2.state[q]["momentum_buf"]
+    assert mb.dtype == torch.float32 and torch.equal(mb, m)
+
+
+@pytest.mark.gpu
+def test_resume_is_bit_identical(dev):
+    """Train, checkpoint layer + optimizer, keep training; a fresh layer and
+    optimizer loaded from the checkpoint produce the same weights bit for bit."""
+    B, D, O, G, F = 32, 256, 2000, 32, 64
+
+    def make():
+        torch.manual_seed(0)
+        layer = GroupFixedFanIn(D, O, F, group_size=G, prune_mode="fraction", rewire_fraction=0.15,
+                                dtype=torch.bfloat16).to(dev)
+        return layer, SRSgd(layer.parameters(), lr=0.05, weight_decay=1e-4, momentum=0.9, seed=42)
+
+    def train(layer, opt, k, seed):
+        g = torch.Generator().manual_seed(seed)
+        for _ in range(k):
+            x = torch.randn(B, D, generator=g).to(torch.bfloat16).to(dev)
+            dY = (torch.randn(B, O, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+            opt.zero_grad()
+            layer(x).backward(dY)
+            opt.step()
+
+    layer, opt = make()
+    train(layer, opt, 3, seed=1)
+    ck = io.BytesIO()
+    torch.save({"state_dict": layer.state_dict(), "optimizer": opt.state_dict()}, ck)
+    train(layer, opt, 2, seed=2)
+    ck.seek(0)
+    st = torch.load(ck, weights_only=True)
+    layer2, opt2 = make()
+    layer2.load_state_dict(st["state_dict"])
+    opt2.load_state_dict(st["optimizer"])
+    train(layer2, opt2, 2, seed=2)
+    torch.cuda.synchronize()
+    for a, b in zip(layer.state_dict().values(), layer2.state_dict().values()):
+        assert torch.equal(a, b)
