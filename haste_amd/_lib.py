@@ -21,7 +21,8 @@ HASTE_ERR_WORKSPACE = -3
 HASTE_ERR_HIP = -4
 
 DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
-PRUNE_THRESHOLD, PRUNE_FRACTION = 0, 1
+PRUNE_THRESHOLD, PRUNE_FRACTION, PRUNE_GLOBAL_FRACTION = 0, 1, 2
+SCORE_MEAN, SCORE_MAX = 0, 1
 REGROW_RANDOM, REGROW_UNUSED = 0, 1
 INIT_ZERO, INIT_RANDOM = 0, 1
 
@@ -68,6 +69,9 @@ SIGNATURES = {
     "haste_transpose_features": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I64, _P]),
     "haste_rewire": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _F32, _I64,
                                     _I32, _I32, _F32, _U64, _P]),
+    "haste_rewire_scores": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I64, _I64, _I64, _P]),
+    "haste_rewire_ex": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _I64,
+                                       _I64, _I32, _F32, _I64, _I32, _I32, _F32, _U64, _P]),
 }
 
 _lib = None

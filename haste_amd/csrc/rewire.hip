@@ -7,6 +7,15 @@
 // is fixed here (and restated bit-for-bit by the CPU oracle):
 //   score[g, j] = (fp32 sum over rows l of g, ascending, of |W[l, j]|) / rows
 //   prune:  THRESHOLD -> score < threshold;  FRACTION -> k smallest (score, j)
+// haste_rewire_scores / haste_rewire_ex add the application's variant
+// (GroupFixedFanInReal.rewire, src/group_fanin_real.py:150-286):
+//   value v[l, j] = |W| or, with a gradient, the saliency |W * grad| (the
+//           product rounded to bf16 when grad is bf16, as the reference's bf16
+//           tensor product, or fp32 when grad is fp32)
+//   score  MEAN -> fp32 sum over rows (ascending) / rows;  MAX -> max over rows
+//   prune  GLOBAL_FRACTION -> the k smallest keys (bits(score) << 32 | g*F + j)
+//           over all slots of the layer, i.e. key <= the k-th smallest key,
+//           which the caller selects on the device from the scores
 //   regrow: RANDOM -> d = (philox(seed; g*F+j, 1, 0).w0 * D) >> 32
 //           UNUSED -> attempts t = 0..63 with counter (g*F+j, 1, t); first
 //           candidate not used by the group (kept slots and slots regrown
@@ -21,10 +30,46 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnusedTries = 64;
 
+// score of slot j of group g over rows [l0, l1): mean or max of |W| or of the
+// saliency |W * grad| (grad_dtype: HASTE_DTYPE_BF16 or _F32; grad may be null)
+__device__ __forceinline__ float slot_score(const uint16_t* __restrict__ W, const void* grad,
+                                            int grad_dtype, int score_mode, int64_t l0,
+                                            int64_t l1, int F, int j) {
+    float acc = score_mode == HASTE_SCORE_MAX ? -__builtin_inff() : 0.0f;
+    for (int64_t l = l0; l < l1; ++l) {
+        const float w = bf16_bits_to_f32(W[l * F + j]);
+        float v;
+        if (grad == nullptr) {
+            v = fabsf(w);
+        } else if (grad_dtype == HASTE_DTYPE_F32) {
+            v = fabsf(w * static_cast<const float*>(grad)[l * F + j]);
+        } else {  // bf16 x bf16 is exact in fp32; the tensor product rounds it to bf16
+            const float gv = bf16_bits_to_f32(static_cast<const uint16_t*>(grad)[l * F + j]);
+            v = fabsf(bf16_bits_to_f32(f32_to_bf16_rne(w * gv)));
+        }
+        acc = score_mode == HASTE_SCORE_MAX ? fmaxf(acc, v) : acc + v;
+    }
+    return score_mode == HASTE_SCORE_MAX ? acc : acc / (float)(l1 - l0);
+}
+
+__global__ __launch_bounds__(kThreads) void rewire_scores_kernel(
+    const uint16_t* __restrict__ W, const void* grad, int grad_dtype, int score_mode,
+    float* __restrict__ scores, int64_t O, int F, int G) {
+    const int64_t g = blockIdx.x;
+    const int j = threadIdx.x;
+    if (j >= F) return;
+    const int64_t l0 = g * G, l1 = min(O, l0 + G);
+    scores[g * F + j] = slot_score(W, grad, grad_dtype, score_mode, l0, l1, F, j);
+}
+
+// scores_in: the layer's scores (GLOBAL_FRACTION, written by rewire_scores_kernel
+// with the same value and score modes); key_thr: the k-th smallest key.
 __global__ __launch_bounds__(kThreads) void rewire_kernel(
     uint16_t* __restrict__ W, int32_t* __restrict__ idx, float* __restrict__ scores_out,
     int32_t* __restrict__ n_pruned, int64_t O, int F, int G, int D, int prune_mode, float thr,
-    int k, int regrow_mode, int init_mode, float bound, uint32_t k0, uint32_t k1) {
+    int k, int regrow_mode, int init_mode, float bound, uint32_t k0, uint32_t k1,
+    const void* grad, int grad_dtype, int score_mode, const float* __restrict__ scores_in,
+    const int64_t* __restrict__ key_thr) {
     __shared__ float sc[256];
     __shared__ int32_t sidx[256];
     __shared__ int mask[256];
@@ -37,8 +82,8 @@ __global__ __launch_bounds__(kThreads) void rewire_kernel(
 
     float score = 0.0f;
     if (jv) {
-        for (int64_t l = l0; l < l1; ++l) score += fabsf(bf16_bits_to_f32(W[l * F + j]));
-        score = score / (float)(l1 - l0);
+        score = scores_in != nullptr ? scores_in[g * F + j]
+                                     : slot_score(W, grad, grad_dtype, score_mode, l0, l1, F, j);
         sc[j] = score;
         sidx[j] = idx[g * F + j];
         if (scores_out) scores_out[g * F + j] = score;
@@ -49,6 +94,9 @@ __global__ __launch_bounds__(kThreads) void rewire_kernel(
     if (jv) {
         if (prune_mode == HASTE_PRUNE_THRESHOLD) {
             m = score < thr;
+        } else if (prune_mode == HASTE_PRUNE_GLOBAL_FRACTION) {
+            const int64_t key = ((int64_t)__float_as_uint(score) << 32) | (int64_t)(uint32_t)(g * F + j);
+            m = key <= *key_thr;
         } else {
             int rank = 0;
             for (int q = 0; q < F; ++q) {
@@ -123,7 +171,72 @@ extern "C" int haste_rewire(uint16_t* W, int32_t* idx, float* scores_out, int32_
     hipStream_t st = static_cast<hipStream_t>(stream);
     haste::rewire_kernel<<<dim3((unsigned)Gc), dim3(haste::kThreads), 0, st>>>(
         W, idx, scores_out, n_pruned, O, (int)F, (int)G, (int)D, prune_mode, threshold, (int)k,
-        regrow_mode, init_mode, bound, (uint32_t)seed, (uint32_t)(seed >> 32));
+        regrow_mode, init_mode, bound, (uint32_t)seed, (uint32_t)(seed >> 32), nullptr,
+        HASTE_DTYPE_BF16, HASTE_SCORE_MEAN, nullptr, nullptr);
     HASTE_CHECK_LAUNCH("haste_rewire");
+    return HASTE_OK;
+}
+
+namespace {
+int check_scores_args(const char* fn, const void* W, int64_t O, int64_t F, int64_t G,
+                      const void* grad, int32_t grad_dtype, int32_t score_mode) {
+    HASTE_CHECK_ARG(W != nullptr, "%s: null pointer", fn);
+    HASTE_CHECK_ARG(F >= 1 && F <= 256, "%s: fan_in must be in [1, 256] (got %lld)", fn,
+                    (long long)F);
+    HASTE_CHECK_ARG(G >= 1 && O >= 1, "%s: invalid sizes O=%lld G=%lld", fn, (long long)O,
+                    (long long)G);
+    HASTE_CHECK_ARG(O * F < ((int64_t)1 << 32), "%s: O*F must be < 2^32", fn);
+    HASTE_CHECK_ARG(score_mode == HASTE_SCORE_MEAN || score_mode == HASTE_SCORE_MAX,
+                    "%s: bad score mode %d", fn, (int)score_mode);
+    HASTE_CHECK_ARG(grad == nullptr || grad_dtype == HASTE_DTYPE_BF16 ||
+                        grad_dtype == HASTE_DTYPE_F32,
+                    "%s: grad dtype must be bf16 or fp32 (got %d)", fn, (int)grad_dtype);
+    return HASTE_OK;
+}
+}  // namespace
+
+extern "C" int haste_rewire_scores(const uint16_t* W, const void* grad, int32_t grad_dtype,
+                                   int32_t score_mode, float* scores, int64_t O, int64_t F,
+                                   int64_t G, void* stream) {
+    int rc = check_scores_args("haste_rewire_scores", W, O, F, G, grad, grad_dtype, score_mode);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(scores != nullptr, "haste_rewire_scores: null scores");
+    const int64_t Gc = haste::ceil_div(O, G);
+    haste::rewire_scores_kernel<<<dim3((unsigned)Gc), dim3(haste::kThreads), 0,
+                                  static_cast<hipStream_t>(stream)>>>(
+        W, grad, grad_dtype, score_mode, scores, O, (int)F, (int)G);
+    HASTE_CHECK_LAUNCH("haste_rewire_scores");
+    return HASTE_OK;
+}
+
+extern "C" int haste_rewire_ex(uint16_t* W, int32_t* idx, const void* grad, int32_t grad_dtype,
+                               int32_t score_mode, const float* scores_in,
+                               const int64_t* key_thr, float* scores_out, int32_t* n_pruned,
+                               int64_t O, int64_t F, int64_t G, int64_t D, int32_t prune_mode,
+                               float threshold, int64_t k, int32_t regrow_mode,
+                               int32_t init_mode, float bound, uint64_t seed, void* stream) {
+    int rc = check_scores_args("haste_rewire_ex", W, O, F, G, grad, grad_dtype, score_mode);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(idx != nullptr, "haste_rewire_ex: null idx");
+    HASTE_CHECK_ARG(D >= 1 && D <= 0x7FFFFFFF, "haste_rewire_ex: invalid D=%lld", (long long)D);
+    HASTE_CHECK_ARG(prune_mode == HASTE_PRUNE_THRESHOLD || prune_mode == HASTE_PRUNE_FRACTION ||
+                        prune_mode == HASTE_PRUNE_GLOBAL_FRACTION,
+                    "haste_rewire_ex: bad prune mode %d", (int)prune_mode);
+    HASTE_CHECK_ARG(prune_mode != HASTE_PRUNE_GLOBAL_FRACTION ||
+                        (scores_in != nullptr && key_thr != nullptr),
+                    "haste_rewire_ex: GLOBAL_FRACTION needs scores_in and key_thr");
+    HASTE_CHECK_ARG(regrow_mode == HASTE_REGROW_RANDOM || regrow_mode == HASTE_REGROW_UNUSED,
+                    "haste_rewire_ex: bad regrow mode %d", (int)regrow_mode);
+    HASTE_CHECK_ARG(init_mode == HASTE_INIT_ZERO || init_mode == HASTE_INIT_RANDOM,
+                    "haste_rewire_ex: bad init mode %d", (int)init_mode);
+    HASTE_CHECK_ARG(prune_mode != HASTE_PRUNE_FRACTION || (k >= 0 && k <= F),
+                    "haste_rewire_ex: k must be in [0, F] (got %lld)", (long long)k);
+    const int64_t Gc = haste::ceil_div(O, G);
+    haste::rewire_kernel<<<dim3((unsigned)Gc), dim3(haste::kThreads), 0,
+                           static_cast<hipStream_t>(stream)>>>(
+        W, idx, scores_out, n_pruned, O, (int)F, (int)G, (int)D, prune_mode, threshold, (int)k,
+        regrow_mode, init_mode, bound, (uint32_t)seed, (uint32_t)(seed >> 32), grad, grad_dtype,
+        score_mode, scores_in, key_thr);
+    HASTE_CHECK_LAUNCH("haste_rewire_ex");
     return HASTE_OK;
 }

@@ -27,7 +27,8 @@ INIT_MODES = ["random", "zero"]
 REGROW_MODES = ["random", "unused"]
 GROUP_SIZES = [16, 32, 64, 128]
 
-__all__ = ["GroupFixedFanIn", "inflate_group_locations"]
+__all__ = ["GroupFixedFanIn", "GroupFixedFanInReal", "inflate_group_locations"]
+SCORE_MODES = ["mean", "max"]
 
 
 class GroupFixedFanIn(torch.nn.Module):
@@ -138,6 +139,89 @@ class GroupFixedFanIn(torch.nn.Module):
                   float(1.0 / math.sqrt(F)), int(seed), _C.stream_of(W))
         # the kernel wrote through raw pointers: tell torch (and index-plan caches
         # keyed on the version counter) that both tensors changed
+        torch.autograd.graph.increment_version(self.weights)
+        torch.autograd.graph.increment_version(self.group_locations)
+
+
+
+class GroupFixedFanInReal(GroupFixedFanIn):
+    """The application's grouped layer (src/group_fanin_real.py, ``GroupFixedFanInReal``):
+    the same parameters and forward, and its rewire variant (:150-286):
+      * scores per (group, slot): the mean (``score_mode="mean"``) or max
+        (``"max"``) over the group's rows of |w|, or of the saliency |w * grad|
+        when ``use_grad`` is set (the product in the tensors' dtype, as the
+        reference; fp32 gradients are used as they are);
+      * ``prune_mode="fraction"`` prunes the ``int(num_groups * fan_in * fraction)``
+        smallest scores of the whole layer (the reference's global topk; ties go
+        to the lower slot), ``"threshold"`` every score below the threshold;
+      * regrowth and initialisation as GroupFixedFanIn (Philox streams keyed by one
+        seed per call; ``regrow_mode="unused"`` is also available).
+    Runs as two kernels and one device-side k-th-value selection, no host sync."""
+
+    def __init__(self, in_features: int, out_features: int, fan_in: int, bias: bool = True,
+                 device=None, dtype=None, *, group_size=32, prune_mode="threshold",
+                 rewire_threshold=None, rewire_fraction=None, growth_mode="random",
+                 init_mode="random", score_mode="mean", regrow_mode="random",
+                 fp32_grads=False, **kwargs):
+        assert score_mode in SCORE_MODES, f"Invalid score_mode={score_mode}; supported: {SCORE_MODES}"
+        super().__init__(in_features, out_features, fan_in, bias, device, dtype,
+                         group_size=group_size, prune_mode=prune_mode,
+                         rewire_threshold=rewire_threshold, rewire_fraction=rewire_fraction,
+                         growth_mode=growth_mode, init_mode=init_mode, regrow_mode=regrow_mode,
+                         fp32_grads=fp32_grads, **kwargs)
+        self.score_mode = score_mode
+        self.use_grad = False
+
+    @torch.no_grad()
+    def rewire(self, seed: int = None):
+        W = self.weights
+        if self.out_features == 0:
+            return
+        _C.require_device(W, "weights")
+        if W.dtype != torch.bfloat16:
+            raise NotImplementedError(f"rewire: weights must be bfloat16 (got {W.dtype})")
+        if not W.is_contiguous() or not self.group_locations.is_contiguous():
+            raise RuntimeError("rewire: weights and group_locations must be contiguous")
+        O, F, G = self.out_features, self.fan_in, self.group_size
+        Gc = self.num_groups
+        grad = W.grad if self.use_grad else None
+        if self.use_grad and grad is None:
+            raise RuntimeError("rewire: use_grad is set but weights.grad is None")
+        if grad is not None:
+            if grad.dtype not in (torch.bfloat16, torch.float32):
+                raise NotImplementedError("rewire: grad must be bf16 or fp32")
+            grad = grad.contiguous()
+        gptr = None if grad is None else grad.data_ptr()
+        gcode = _lib.DTYPE_F32 if (grad is not None and grad.dtype == torch.float32) else _lib.DTYPE_BF16
+        smode = _lib.SCORE_MAX if self.score_mode == "max" else _lib.SCORE_MEAN
+        st = _C.stream_of(W)
+        scores = key_thr = None
+        if self.prune_mode == "threshold":
+            mode, thr, k = _lib.PRUNE_THRESHOLD, float(self.rewire_threshold), 0
+        else:
+            k = int(Gc * F * self.rewire_fraction)
+            if k == 0:
+                return
+            mode, thr = _lib.PRUNE_GLOBAL_FRACTION, 0.0
+            scores = torch.empty(Gc, F, dtype=torch.float32, device=W.device)
+            _lib.call("haste_rewire_scores", W.data_ptr(), gptr, gcode, smode, scores.data_ptr(),
+                      O, F, G, st)
+            # unique keys (scores are >= 0, so their bits order them): the k-th
+            # smallest is the last pruned slot; ties go to the lower slot
+            keys = (scores.view(-1).view(torch.int32).to(torch.int64) << 32) | torch.arange(
+                Gc * F, dtype=torch.int64, device=W.device)
+            key_thr = torch.kthvalue(keys, k).values.contiguous()
+        if seed is None:
+            seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+        if self._pruned_total is None or self._pruned_total.device != W.device:
+            self._pruned_total = torch.zeros(1, dtype=torch.int32, device=W.device)
+        _lib.call("haste_rewire_ex", W.data_ptr(), self.group_locations.data_ptr(), gptr, gcode,
+                  smode, None if scores is None else scores.data_ptr(),
+                  None if key_thr is None else key_thr.data_ptr(), None,
+                  self._pruned_total.data_ptr(), O, F, G, self.in_features, mode, thr, k,
+                  _lib.REGROW_UNUSED if self.regrow_mode == "unused" else _lib.REGROW_RANDOM,
+                  _lib.INIT_RANDOM if self.init_mode == "random" else _lib.INIT_ZERO,
+                  float(1.0 / math.sqrt(F)), int(seed), st)
         torch.autograd.graph.increment_version(self.weights)
         torch.autograd.graph.increment_version(self.group_locations)
 

@@ -38,7 +38,8 @@ enum {
 
 enum { HASTE_DTYPE_BF16 = 0, HASTE_DTYPE_F16 = 1, HASTE_DTYPE_F32 = 2 };
 
-enum { HASTE_PRUNE_THRESHOLD = 0, HASTE_PRUNE_FRACTION = 1 };
+enum { HASTE_PRUNE_THRESHOLD = 0, HASTE_PRUNE_FRACTION = 1, HASTE_PRUNE_GLOBAL_FRACTION = 2 };
+enum { HASTE_SCORE_MEAN = 0, HASTE_SCORE_MAX = 1 };
 enum { HASTE_REGROW_RANDOM = 0, HASTE_REGROW_UNUSED = 1 };
 enum { HASTE_INIT_ZERO = 0, HASTE_INIT_RANDOM = 1 };
 
@@ -229,6 +230,30 @@ int haste_rewire(uint16_t* W, int32_t* idx, float* scores_out, int32_t* n_pruned
                  int64_t F, int64_t G, int64_t D, int32_t prune_mode, float threshold, int64_t k,
                  int32_t regrow_mode, int32_t init_mode, float bound, uint64_t seed,
                  void* stream);
+
+/*
+ * The application's rewire variant, GroupFixedFanInReal.rewire
+ * (src/group_fanin_real.py:150-286).  haste_rewire_scores writes the fp32
+ * scores [ceil(O/G), F]: per slot, the mean (HASTE_SCORE_MEAN, fp32 sum over the
+ * group's rows in ascending order / rows) or the max (HASTE_SCORE_MAX) of |W|,
+ * or, with grad (bf16 or fp32, [O, F]) not NULL, of the saliency |W * grad| (the
+ * product rounded to bf16 for a bf16 grad, as the reference's tensor product).
+ * haste_rewire_ex is haste_rewire with those score modes and one more prune
+ * mode, HASTE_PRUNE_GLOBAL_FRACTION: prune the slots whose key
+ * (bits(score) << 32 | g*F + j) is <= *key_thr, the k-th smallest key of the
+ * layer (so exactly k slots, the smallest scores, ties to the lower slot),
+ * selected by the caller on the device from scores_in (the scores of
+ * haste_rewire_scores with the same modes).  Regrow and init as haste_rewire.
+ */
+int haste_rewire_scores(const uint16_t* W, const void* grad, int32_t grad_dtype,
+                        int32_t score_mode, float* scores, int64_t O, int64_t F, int64_t G,
+                        void* stream);
+int haste_rewire_ex(uint16_t* W, int32_t* idx, const void* grad, int32_t grad_dtype,
+                    int32_t score_mode, const float* scores_in, const int64_t* key_thr,
+                    float* scores_out, int32_t* n_pruned, int64_t O, int64_t F, int64_t G,
+                    int64_t D, int32_t prune_mode, float threshold, int64_t k,
+                    int32_t regrow_mode, int32_t init_mode, float bound, uint64_t seed,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -70,6 +70,10 @@ def lib() -> ctypes.CDLL:
         L.ho_rewire_scores.argtypes = [P, P, i64, i64, i64]
         L.ho_rewire.argtypes = [P, P, i64, i64, i64, i64, c_int, f32, i64, c_int, c_int, f32, u64, P, P]
         L.ho_rewire.restype = i64
+        L.ho_rewire_scores_ex.argtypes = [P, P, c_int, c_int, P, i64, i64, i64]
+        L.ho_rewire_ex.argtypes = [P, P, P, c_int, c_int, i64, i64, i64, i64, c_int, f32, i64,
+                                   c_int, c_int, f32, u64, P, P]
+        L.ho_rewire_ex.restype = i64
         L.ho_num_threads.restype = c_int
         L.ho_set_num_threads.argtypes = [c_int]
         _lib = L
@@ -165,6 +169,54 @@ def rewire(w_bits: np.ndarray, idx: np.ndarray, G: int, D: int, *, prune_mode: i
     mask = np.empty((Gc, F), dtype=np.uint8)
     n = lib().ho_rewire(_ptr(w), _ptr(ix), O, F, G, D, prune_mode, np.float32(threshold), k,
                         regrow_mode, init_mode, np.float32(bound), seed, _ptr(scores), _ptr(mask))
+    return w, ix, int(n), scores, mask.astype(bool)
+
+
+PRUNE_GLOBAL_FRACTION = 2
+SCORE_MEAN, SCORE_MAX = 0, 1
+
+
+def _grad_f32(grad):
+    """grad as an fp32 array and whether it was bf16 (uint16 bit patterns)."""
+    if grad is None:
+        return None, 0
+    if grad.dtype == np.uint16:
+        return np.ascontiguousarray(bf16_bits_to_f32(grad), dtype=np.float32), 1
+    return np.ascontiguousarray(grad, dtype=np.float32), 0
+
+
+def rewire_scores_ex(w_bits: np.ndarray, G: int, score_mode: int = SCORE_MEAN,
+                     grad: np.ndarray | None = None) -> np.ndarray:
+    """Scores of the application's rewire variant (haste_oracle.c:ho_rewire_scores_ex);
+    grad is None, bf16 bit patterns (uint16) or fp32."""
+    O, F = w_bits.shape
+    Gc = (O + G - 1) // G
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    gf, gb = _grad_f32(grad)
+    s = np.empty((Gc, F), dtype=np.float32)
+    lib().ho_rewire_scores_ex(_ptr(w_bits), None if gf is None else _ptr(gf), gb, score_mode,
+                              _ptr(s), O, F, G)
+    return s
+
+
+def rewire_ex(w_bits: np.ndarray, idx: np.ndarray, G: int, D: int, *, prune_mode: int,
+              score_mode: int = SCORE_MEAN, grad: np.ndarray | None = None,
+              threshold: float = 0.0, k: int = 0, regrow_mode: int = REGROW_RANDOM,
+              init_mode: int = INIT_ZERO, bound: float = 0.0, seed: int = 0):
+    """The application's rewire variant (GroupFixedFanInReal.rewire,
+    src/group_fanin_real.py:150-286) under the contract of haste_oracle.c;
+    k is per group for PRUNE_FRACTION and for the whole layer for
+    PRUNE_GLOBAL_FRACTION.  Returns (weight bits, idx, n_pruned, scores, mask)."""
+    w = np.array(w_bits, dtype=np.uint16, copy=True, order="C")
+    ix = np.array(idx, dtype=np.int32, copy=True, order="C")
+    O, F = w.shape
+    Gc = ix.shape[0]
+    gf, gb = _grad_f32(grad)
+    scores = np.empty((Gc, F), dtype=np.float32)
+    mask = np.empty((Gc, F), dtype=np.uint8)
+    n = lib().ho_rewire_ex(_ptr(w), _ptr(ix), None if gf is None else _ptr(gf), gb, score_mode,
+                           O, F, G, D, prune_mode, np.float32(threshold), k, regrow_mode,
+                           init_mode, np.float32(bound), seed, _ptr(scores), _ptr(mask))
     return w, ix, int(n), scores, mask.astype(bool)
 
 

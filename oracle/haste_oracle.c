@@ -227,18 +227,107 @@ void ho_rewire_scores(const uint16_t* W, float* scores, int64_t O, int64_t F, in
     }
 }
 
+/* ---------------------------------------------------------------------------
+ * The application's variant, GroupFixedFanInReal.rewire
+ * (src/group_fanin_real.py:150-286):
+ *  value v[l][j] = |W| or, with grad, the saliency |W * grad|
+ *          (group_fanin_real.py:199-204); with grad_bf16 the product (exact in
+ *          fp32 for two bf16 values) is rounded to bf16, as the reference's bf16
+ *          tensor product; with an fp32 grad it is the fp32 product.
+ *  score  MEAN: fp32 sum over the group's rows in ascending order / rows
+ *         (group_fanin_real.py:206-212,226-228); MAX: max over the rows
+ *         (group_fanin_real.py:213-220).
+ *  prune  GLOBAL_FRACTION: the k slots of the whole layer with the smallest
+ *         (score, g*F + j) pairs (group_fanin_real.py:234-251, topk over all
+ *         slots; its tie order is unspecified, fixed here to the lower slot).
+ * --------------------------------------------------------------------------- */
+enum { HO_PRUNE_GLOBAL_FRACTION = 2 };
+enum { HO_SCORE_MEAN = 0, HO_SCORE_MAX = 1 };
+
+void ho_rewire_scores_ex(const uint16_t* W, const float* grad, int grad_bf16, int score_mode,
+                         float* scores, int64_t O, int64_t F, int64_t G) {
+    int64_t Gc = (O + G - 1) / G;
+    for (int64_t g = 0; g < Gc; ++g) {
+        int64_t l0 = g * G, l1 = l0 + G < O ? l0 + G : O;
+        for (int64_t j = 0; j < F; ++j) {
+            float acc = score_mode == HO_SCORE_MAX ? -INFINITY : 0.0f;
+            for (int64_t l = l0; l < l1; ++l) {
+                float w = ho_bf16_to_f32(W[l * F + j]);
+                float v;
+                if (!grad) {
+                    v = fabsf(w);
+                } else if (grad_bf16) {
+                    v = fabsf(ho_bf16_to_f32(ho_f32_to_bf16_rne(w * grad[l * F + j])));
+                } else {
+                    v = fabsf(w * grad[l * F + j]);
+                }
+                acc = score_mode == HO_SCORE_MAX ? (v > acc ? v : acc) : acc + v;
+            }
+            scores[g * F + j] = score_mode == HO_SCORE_MAX ? acc : acc / (float)(l1 - l0);
+        }
+    }
+}
+
+static int cmp_u64(const void* a, const void* b) {
+    uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+static int64_t rewire_apply(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G,
+                            int64_t D, int prune_mode, float thr, int64_t k, int regrow_mode,
+                            int init_mode, float bound, uint64_t seed, const float* scores,
+                            uint8_t* mask);
+
+int64_t ho_rewire_ex(uint16_t* W, int32_t* idx, const float* grad, int grad_bf16,
+                     int score_mode, int64_t O, int64_t F, int64_t G, int64_t D,
+                     int prune_mode, float thr, int64_t k, int regrow_mode, int init_mode,
+                     float bound, uint64_t seed, float* scores_out, uint8_t* mask_out) {
+    int64_t Gc = (O + G - 1) / G, n = Gc * F;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)n);
+    uint8_t* mask = (uint8_t*)calloc((size_t)n, 1);
+    ho_rewire_scores_ex(W, grad, grad_bf16, score_mode, scores, O, F, G);
+    if (prune_mode == HO_PRUNE_GLOBAL_FRACTION) {
+        /* keys (bits(score) << 32 | slot) order the scores (>= 0) with ties to the lower slot */
+        uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)n);
+        for (int64_t i = 0; i < n; ++i) {
+            uint32_t b;
+            memcpy(&b, &scores[i], 4);
+            keys[i] = ((uint64_t)b << 32) | (uint64_t)i;
+        }
+        qsort(keys, (size_t)n, sizeof(uint64_t), cmp_u64);
+        for (int64_t r = 0; r < k && r < n; ++r) mask[keys[r] & 0xFFFFFFFFu] = 1;
+        free(keys);
+    }
+    int64_t total = rewire_apply(W, idx, O, F, G, D, prune_mode, thr, k, regrow_mode, init_mode,
+                                 bound, seed, scores, mask);
+    if (scores_out) memcpy(scores_out, scores, sizeof(float) * (size_t)n);
+    if (mask_out) memcpy(mask_out, mask, (size_t)n);
+    free(scores);
+    free(mask);
+    return total;
+}
+
 int64_t ho_rewire(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G, int64_t D,
                   int prune_mode, float thr, int64_t k, int regrow_mode, int init_mode,
                   float bound, uint64_t seed, float* scores_out, uint8_t* mask_out) {
+    return ho_rewire_ex(W, idx, NULL, 0, HO_SCORE_MEAN, O, F, G, D, prune_mode, thr, k,
+                        regrow_mode, init_mode, bound, seed, scores_out, mask_out);
+}
+
+/* prune (threshold / per-group fraction into mask; global fraction: mask given),
+ * regrow and re-initialise; returns the number of pruned slots */
+static int64_t rewire_apply(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G,
+                            int64_t D, int prune_mode, float thr, int64_t k, int regrow_mode,
+                            int init_mode, float bound, uint64_t seed, const float* scores,
+                            uint8_t* mask) {
     int64_t Gc = (O + G - 1) / G;
-    float* scores = (float*)malloc(sizeof(float) * (size_t)(Gc * F));
-    uint8_t* mask = (uint8_t*)calloc((size_t)(Gc * F), 1);
-    ho_rewire_scores(W, scores, O, F, G);
     int64_t total = 0;
     for (int64_t g = 0; g < Gc; ++g) {
-        float* s = scores + g * F;
+        const float* s = scores + g * F;
         uint8_t* mk = mask + g * F;
-        if (prune_mode == HO_PRUNE_THRESHOLD) {
+        if (prune_mode == HO_PRUNE_GLOBAL_FRACTION) {
+            /* mask already set */
+        } else if (prune_mode == HO_PRUNE_THRESHOLD) {
             for (int64_t j = 0; j < F; ++j) mk[j] = s[j] < thr;
         } else {
             /* rank of slot j = #slots with (score, slot) lexicographically smaller */
@@ -282,9 +371,5 @@ int64_t ho_rewire(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G, in
             }
         }
     }
-    if (scores_out) memcpy(scores_out, scores, sizeof(float) * (size_t)(Gc * F));
-    if (mask_out) memcpy(mask_out, mask, (size_t)(Gc * F));
-    free(scores);
-    free(mask);
     return total;
 }

@@ -173,3 +173,57 @@ def test_rewire(dev, O, F, G, D, prune, kt, regrow, init):
     assert np.array_equal(idxd.cpu().numpy(), ref_idx)
     assert np.array_equal(bits(Wd), ref_w)
     assert int(cnt.item()) == ref_n
+
+
+# ---- the application's variant (GroupFixedFanInReal.rewire) against the oracle ----
+APP_CASES = [
+    # O, F, G, D, score, grad, prune, regrow, init
+    (1000, 64, 32, 300, "mean", None, "fraction", "random", "zero"),
+    (1000, 64, 32, 300, "max", None, "fraction", "unused", "random"),
+    (777, 128, 64, 768, "mean", "bf16", "fraction", "random", "random"),
+    (777, 128, 64, 768, "max", "f32", "threshold", "random", "zero"),
+    (300, 16, 16, 50, "max", "bf16", "fraction", "unused", "zero"),
+    (513, 256, 128, 1000, "mean", "f32", "fraction", "random", "zero"),
+]
+
+
+@pytest.mark.parametrize("O,F,G,D,score,gk,prune,regrow,init", APP_CASES)
+def test_app_rewire(dev, O, F, G, D, score, gk, prune, regrow, init):
+    from haste_amd.rewire import GroupFixedFanInReal
+    torch.manual_seed(O + F)
+    layer = GroupFixedFanInReal(D, O, F, group_size=G, prune_mode=prune,
+                                rewire_threshold=0.0 if prune == "threshold" else None,
+                                rewire_fraction=0.15 if prune == "fraction" else None,
+                                init_mode=init, score_mode=score, regrow_mode=regrow,
+                                fp32_grads=gk == "f32", dtype=torch.bfloat16)
+    w = bits(layer.weights)
+    idx = layer.group_locations.numpy().copy()
+    sm = oracle.SCORE_MAX if score == "max" else oracle.SCORE_MEAN
+    g_np = None
+    if gk is not None:
+        gt = torch.randn(O, F, generator=torch.Generator().manual_seed(5)) * 1e-2
+        gt = gt.to(torch.bfloat16) if gk == "bf16" else gt
+        g_np = bits(gt) if gk == "bf16" else gt.numpy()
+    if prune == "threshold":  # prune about half: the median score
+        layer.rewire_threshold = float(np.median(oracle.rewire_scores_ex(w, G, sm, g_np)))
+    layer = layer.to(dev)
+    if gk is not None:
+        layer.use_grad = True
+        layer.weights.grad = gt.to(dev)
+    Gc = (O + G - 1) // G
+    seed = 0xABCDEF + O
+    pm = oracle.PRUNE_THRESHOLD if prune == "threshold" else oracle.PRUNE_GLOBAL_FRACTION
+    k = 0 if prune == "threshold" else int(Gc * F * 0.15)
+    ref_w, ref_idx, ref_n, _, _ = oracle.rewire_ex(
+        w, idx, G, D, prune_mode=pm, score_mode=sm, grad=g_np,
+        threshold=getattr(layer, "rewire_threshold", 0.0), k=k,
+        regrow_mode=oracle.REGROW_UNUSED if regrow == "unused" else oracle.REGROW_RANDOM,
+        init_mode=oracle.INIT_RANDOM if init == "random" else oracle.INIT_ZERO,
+        bound=1.0 / math.sqrt(F), seed=seed)
+    layer.rewire(seed=seed)
+    torch.cuda.synchronize()
+    assert layer.pruned_total == ref_n
+    assert np.array_equal(layer.group_locations.cpu().numpy(), ref_idx)
+    assert np.array_equal(bits(layer.weights), ref_w)
+    if prune == "fraction":
+        assert ref_n == k

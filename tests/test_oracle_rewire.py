@@ -3,6 +3,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 import oracle
 from oracle import bf16_bits_to_f32, f32_to_bf16_bits
@@ -103,3 +104,86 @@ def test_random_init_bounds():
                                       init_mode=oracle.INIT_RANDOM, bound=b, seed=10)
     vals = bf16_bits_to_f32(w2[mask[np.arange(O) // G]])
     assert np.all(np.abs(vals) <= b * (1 + 2**-8)) and np.unique(vals).size > 10
+
+
+# ---- the application's variant (GroupFixedFanInReal.rewire, src/group_fanin_real.py:150-286) ----
+def _app_case(O=300, F=32, G=16, seed=11):
+    g = torch.Generator().manual_seed(seed)
+    W = (torch.rand(O, F, generator=g) * 2 - 1).to(torch.bfloat16)
+    grad = (torch.randn(O, F, generator=g) * 1e-2).to(torch.bfloat16)
+    return W, grad
+
+
+def _ref_scores(W, grad, G, mode):
+    """The reference's own steps in torch: |w| or (w * grad).abs() in the tensors'
+    dtype, then index_add_ (mean) or scatter_reduce amax (max) per group."""
+    O, F = W.shape
+    Gc = (O + G - 1) // G
+    gid = torch.arange(O) // G
+    val = (W.abs() if grad is None else (W * grad).abs()).to(torch.float32)
+    if mode == "mean":
+        s = torch.zeros(Gc, F).index_add_(0, gid, val)
+        cnt = torch.zeros(Gc).index_add_(0, gid, torch.ones(O)).clamp_min(1).unsqueeze(1)
+        return s / cnt
+    s = torch.full((Gc, F), -float("inf"))
+    return s.scatter_reduce(0, gid[:, None].expand(-1, F), val, reduce="amax", include_self=True)
+
+
+@pytest.mark.parametrize("mode", ["mean", "max"])
+@pytest.mark.parametrize("gkind", [None, "bf16", "f32"])
+def test_app_scores_match_reference_steps(mode, gkind):
+    W, grad = _app_case()
+    if gkind == "f32":
+        grad = grad.float() * 1.37
+    g_np = None if gkind is None else (grad.view(torch.int16).numpy().view(np.uint16)
+                                       if gkind == "bf16" else grad.numpy())
+    wb = W.view(torch.int16).numpy().view(np.uint16)
+    sm = oracle.SCORE_MEAN if mode == "mean" else oracle.SCORE_MAX
+    got = torch.from_numpy(oracle.rewire_scores_ex(wb, 16, sm, g_np))
+    ref = _ref_scores(W, None if gkind is None else grad, 16, mode)
+    if mode == "max":
+        assert torch.equal(got, ref)            # a max does not depend on the order
+    else:
+        torch.testing.assert_close(got, ref, rtol=2e-6, atol=0)  # summation order differs
+    if gkind is None and mode == "mean":
+        assert np.array_equal(got.numpy(), oracle.rewire_scores(wb, 16))
+
+
+def test_app_global_fraction_selects_k_smallest():
+    """GLOBAL_FRACTION prunes exactly k = int(Gc*F*fraction) slots of the layer: the
+    smallest scores (torch.topk(largest=False) when scores are distinct), ties to
+    the lower flat slot (brute-force lexicographic order)."""
+    W, _ = _app_case(O=250, F=16, G=16)
+    wb = W.view(torch.int16).numpy().view(np.uint16)
+    Gc = 16
+    idx = np.zeros((Gc, 16), dtype=np.int32)
+    k = int(Gc * 16 * 0.15)
+    _, _, n, scores, mask = oracle.rewire_ex(wb, idx, 16, 100, prune_mode=oracle.PRUNE_GLOBAL_FRACTION,
+                                             score_mode=oracle.SCORE_MAX, k=k, seed=3)
+    assert n == k and mask.sum() == k
+    flat = scores.reshape(-1)
+    order = np.lexsort((np.arange(flat.size), flat))
+    assert set(np.flatnonzero(mask.reshape(-1))) == set(order[:k].tolist())
+    if len(np.unique(flat)) == flat.size:
+        _, ti = torch.topk(torch.from_numpy(flat), k, largest=False)
+        assert set(ti.tolist()) == set(order[:k].tolist())
+    # ties: all scores equal -> the k lowest flat slots
+    z = np.zeros_like(wb)
+    _, _, n, _, mask = oracle.rewire_ex(z, idx, 16, 100, prune_mode=oracle.PRUNE_GLOBAL_FRACTION, k=k)
+    assert np.array_equal(np.flatnonzero(mask.reshape(-1)), np.arange(k))
+
+
+def test_app_rewire_invariants():
+    """Zero init: every row of a pruned slot is zero, other weights untouched; new
+    indices in [0, D); kept indices unchanged."""
+    W, grad = _app_case(O=200, F=32, G=16, seed=5)
+    wb = W.view(torch.int16).numpy().view(np.uint16)
+    Gc, D = 13, 77
+    idx = np.random.default_rng(0).integers(0, D, (Gc, 32)).astype(np.int32)
+    g_np = grad.view(torch.int16).numpy().view(np.uint16)
+    w2, ix2, n, _, mask = oracle.rewire_ex(wb, idx, 16, D, prune_mode=oracle.PRUNE_GLOBAL_FRACTION,
+                                           score_mode=oracle.SCORE_MEAN, grad=g_np, k=60, seed=9)
+    assert n == 60
+    rows_mask = np.repeat(mask, 16, axis=0)[:200]
+    assert np.all(w2[rows_mask] == 0) and np.array_equal(w2[~rows_mask], wb[~rows_mask])
+    assert np.array_equal(ix2[~mask], idx[~mask]) and ix2.min() >= 0 and ix2.max() < D
