@@ -107,6 +107,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     constexpr int MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SP = C::SP, PR = C::PR;
     __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
     __shared__ int s_perm[SGD ? FP : 1];
+    __shared__ float s_bg[SGD ? G : 1];  // fused step: the bias gradient of the group
     char (*Ys)[kKC * RB] = reinterpret_cast<char (*)[kKC * RB]>(lds);
     float* stg = reinterpret_cast<float*>(lds);
 
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     // extra registers would cost a wave per SIMD.
     constexpr bool kWPre = SGD && PR == G && FP <= 128;
     u32x4 wpre[kWPre ? WPT : 1];
-    uint32_t bpre[NT];
+    uint32_t bpre = 0;  // fused step: bias bits of label tid (tid < nl)
     if constexpr (SGD) {
 #pragma unroll
         for (int q = 0; q < (kWPre ? WPT : 0); ++q) {
@@ -205,11 +206,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
         }
         const rsrc_t bbr = make_rsrc(sg.bias != nullptr ? sg.bias + l0 : nullptr,
                                      sg.bias != nullptr ? (int64_t)nl * 2 : 0);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int ll = (wn * NT + nt) * 16 + col;
-            bpre[nt] = __builtin_amdgcn_raw_buffer_load_b16(bbr, (do_bias && kq == 0 ? ll * 2 : (int)kOOB), 0, 0);
-        }
+        bpre = __builtin_amdgcn_raw_buffer_load_b16(bbr, (tid < G ? tid * 2 : (int)kOOB), 0, 0);
     }
 
     // Ping-pong register sets by chunk parity (the loop body is unrolled twice),
@@ -277,15 +274,9 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                 else
                     static_cast<uint16_t*>(dbias)[l] = (uint16_t)f32_to_f16_rne(v);
             }
-            if constexpr (SGD) {
-                if (sg.bias != nullptr) {
-                    float mv = sg.use_mom ? sg.mb[l] : 0.f;
-                    sg.bias[l] = (uint16_t)sgd_one(bf16_bits_to_f32(bpre[nt]), v, &mv,
-                                                   sg.use_mom, sg.lr, sg.wd, sg.mu, sg.do_sr,
-                                                   (uint64_t)l, sg.k0, sg.k1);
-                    if (sg.use_mom) sg.mb[l] = mv;
-                }
-            }
+            // fused step: staged, and applied below by thread ll (in parallel with
+            // the weights, instead of by these 16 lanes while the other waves wait)
+            if constexpr (SGD) s_bg[ll] = v;
         }
     }
 
@@ -329,6 +320,16 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
             }
         }
         __syncthreads();
+        if constexpr (SGD) {
+            if (p0 == 0 && sg.bias != nullptr && tid < nl) {
+                const int64_t l = l0 + tid;
+                float mv = sg.use_mom ? sg.mb[l] : 0.f;
+                sg.bias[l] = (uint16_t)sgd_one(bf16_bits_to_f32(bpre), s_bg[tid], &mv, sg.use_mom,
+                                               sg.lr, sg.wd, sg.mu, sg.do_sr, (uint64_t)l, sg.k0,
+                                               sg.k1);
+                if (sg.use_mom) sg.mb[l] = mv;
+            }
+        }
 #pragma unroll
         for (int q = 0; q < WPT; ++q) {
             const int it = tid + q * kThreads;
