@@ -96,6 +96,22 @@ def make_inputs(cfg, dev):
             torch.from_numpy(idx).to(dev), Y.to(dev))
 
 
+def make_labels(cfg, dev):
+    """The positives of make_inputs' Y as COO int32 [nnz, 2] (row, label) pairs
+    (the application's label format, src/data.py:26-46)."""
+    import numpy as np
+    import torch
+
+    B, O = cfg["B"], cfg["O"]
+    rng_y = np.random.default_rng(3)
+    n_pos = B * cfg["pos"]
+    lab = rng_y.zipf(1.1, size=4 * n_pos)
+    lab = lab[lab <= O][:n_pos] - 1
+    rows = np.repeat(np.arange(B), cfg["pos"])[: len(lab)]
+    coo = np.unique(np.stack([rows, lab], 1).astype(np.int32), axis=0)  # Y is binary
+    return torch.from_numpy(coo).to(dev)
+
+
 def cpu_baseline(cfg, budget_s=20.0):
     """Times the CPU oracle (PyTorch-CPU gather+bmm fwd/bwd + C SR-SGD) on a
     slice of the label groups, scaled to the full label count."""
@@ -181,7 +197,7 @@ def main():
     ldy = st.ldo
     dY_buf = torch.zeros(B, ldy, dtype=torch.bfloat16, device=dev)
     dY_buf[:, :O] = (torch.sigmoid(logits.float()) - Y).to(torch.bfloat16)
-    labels = Y.nonzero().to(torch.int32).contiguous()  # COO (row, label) positives
+    labels = make_labels(cfg, dev)  # the same positives as COO (row, label) pairs
     del Y
     torch.cuda.synchronize()
 

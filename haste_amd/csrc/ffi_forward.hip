@@ -404,10 +404,9 @@ int dispatch_g(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16
     return HASTE_ERR_UNSUPPORTED;
 }
 
-// Label bits of the COO positives (row, label) pairs: SET ors the bits in, else
-// the words holding them are cleared (the whole word: the bitmap is all zero
-// between calls).  Pairs outside [0, B) x [0, O) are ignored.
-template <bool SET>
+// Label bits of the COO positives (row, label) pairs, ored into the (all zero)
+// bitmap; loss_sum_kernel clears the words again after the forward.  Pairs
+// outside [0, B) x [0, O) are ignored.
 __global__ __launch_bounds__(256) void label_bits_kernel(const int32_t* __restrict__ labels,
                                                          int64_t nnz, uint32_t* __restrict__ ybits,
                                                          int64_t ldyw, int B, int64_t O) {
@@ -415,18 +414,22 @@ __global__ __launch_bounds__(256) void label_bits_kernel(const int32_t* __restri
     if (i >= nnz) return;
     const int r = labels[2 * i], c = labels[2 * i + 1];
     if (r < 0 || r >= B || c < 0 || c >= O) return;
-    uint32_t* w = ybits + (int64_t)r * ldyw + c / 32;
-    if constexpr (SET)
-        atomicOr(w, 1u << (c % 32));
-    else
-        *w = 0u;
+    atomicOr(ybits + (int64_t)r * ldyw + c / 32, 1u << (c % 32));
 }
 
 // loss = sum of the n workgroup partials: each thread sums a strided subset in
-// order, then a fixed tree over the threads.
+// order, then a fixed tree over the threads.  The same workgroup clears the
+// label words the call set (one launch instead of two small ones).
 __global__ __launch_bounds__(256) void loss_sum_kernel(const float* __restrict__ part, int64_t n,
-                                                       float* __restrict__ loss) {
+                                                       float* __restrict__ loss,
+                                                       const int32_t* __restrict__ labels,
+                                                       int64_t nnz, uint32_t* __restrict__ ybits,
+                                                       int64_t ldyw, int B, int64_t O) {
     __shared__ float s[256];
+    for (int64_t i = threadIdx.x; i < nnz; i += 256) {
+        const int r = labels[2 * i], c = labels[2 * i + 1];
+        if (r >= 0 && r < B && c >= 0 && c < O) ybits[(int64_t)r * ldyw + c / 32] = 0u;
+    }
     float v = 0.0f;
     for (int64_t i = threadIdx.x; i < n; i += 256) v += part[i];
     s[threadIdx.x] = v;
@@ -547,7 +550,7 @@ extern "C" int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.bits_bytes);
     const int64_t lblocks = (nnz + 255) / 256;
     if (lblocks > 0) {
-        haste::label_bits_kernel<true><<<dim3((unsigned)lblocks), dim3(256), 0, st>>>(
+        haste::label_bits_kernel<<<dim3((unsigned)lblocks), dim3(256), 0, st>>>(
             labels, nnz, ybits, L.ldyw, (int)B, O);
         HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
     }
@@ -560,12 +563,8 @@ extern "C" int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t
              ? haste::dispatch_g<haste::BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st)
              : haste::dispatch_g<haste::F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st);
     if (rc != HASTE_OK) return rc;
-    if (lblocks > 0) {
-        haste::label_bits_kernel<false><<<dim3((unsigned)lblocks), dim3(256), 0, st>>>(
-            labels, nnz, ybits, L.ldyw, (int)B, O);
-        HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
-    }
-    haste::loss_sum_kernel<<<dim3(1), dim3(256), 0, st>>>(part, L.nparts, loss);
+    haste::loss_sum_kernel<<<dim3(1), dim3(256), 0, st>>>(part, L.nparts, loss, labels, nnz,
+                                                          ybits, L.ldyw, (int)B, O);
     HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
     return HASTE_OK;
 }
