@@ -88,7 +88,7 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                                           const uint16_t* __restrict__ bias,
                                           uint16_t* __restrict__ out, int64_t ldo, int B, int D,
                                           int F, int64_t O, int64_t g, int b_chunk0, int ntiles,
-                                          char (*Xg)[FP * FwdCfg<G, FP>::RB], int32_t* sidx,
+                                          char (*Xg)[FP * FwdCfg<G, FP>::RB],
                                           char (*stg)[FwdCfg<G, FP>::STG], const BceArgs& bce,
                                           float* s_red) {
     using C = FwdCfg<G, FP>;
@@ -101,10 +101,22 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
     const int64_t l0 = g * G;
     const int nl = (int)std::min<int64_t>(G, O - l0);  // labels of this group
 
-    // Indices outside [0, D) are clamped (the reference leaves them undefined);
-    // slots >= F gather row 0 (their W columns read as zero).
-    for (int j = tid; j < FP; j += kThreads)
-        sidx[j] = j < F ? min(max(idx[g * F + j], 0), D - 1) : 0;
+    // piece p of a tile: slot p / 8, batch columns 8 * (p % 8) .. +7.  The
+    // thread's slots' indices are loaded first, straight into registers (they
+    // start the gather chain); indices outside [0, D) are clamped (the
+    // reference leaves them undefined), slots >= F gather row 0 (their W
+    // columns read as zero).
+    int pj[PPT], pc[PPT], pidx[PPT];
+    {
+        const rsrc_t ir = make_rsrc(idx + g * F, (int64_t)F * 4);
+#pragma unroll
+        for (int q = 0; q < PPT; ++q) {
+            const int p = tid + q * kThreads;
+            pj[q] = p / (kBT / 8);
+            pc[q] = (p % (kBT / 8)) * 8;
+            pidx[q] = (int)buf_load4(ir, pj[q] < F ? (uint32_t)pj[q] * 4 : kOOB);
+        }
+    }
 
     // W fragments (A operand) and bias of this wave's label tiles; rows >= O and
     // slots >= F are outside the resources and read as zero.
@@ -125,22 +137,13 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
         for (int i = 0; i < 4; ++i)
             bv[mt][i] = bits_to_f32<T>(__builtin_amdgcn_raw_buffer_load_b16(br, (lb + i) * 2, 0, 0));
     }
-    __syncthreads();
 
-    // piece p of a tile: slot p / 8, batch columns 8 * (p % 8) .. +7; chunks
-    // starting at or past B read as zero, columns >= B of a partial chunk are
-    // masked when stashed
+    // chunks starting at or past B read as zero, columns >= B of a partial chunk
+    // are masked when stashed
     const rsrc_t xr = make_rsrc(xT, (int64_t)D * ldx * 2);
-    int pj[PPT], pc[PPT];
-#pragma unroll
-    for (int q = 0; q < PPT; ++q) {
-        const int p = tid + q * kThreads;
-        pj[q] = p / (kBT / 8);
-        pc[q] = (p % (kBT / 8)) * 8;
-    }
     int64_t prow[PPT];
 #pragma unroll
-    for (int q = 0; q < PPT; ++q) prow[q] = (int64_t)sidx[pj[q]] * ldx;
+    for (int q = 0; q < PPT; ++q) prow[q] = (int64_t)min(max(pidx[q], 0), D - 1) * ldx;
     auto fetch = [&](int b_base, u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
@@ -321,7 +324,6 @@ __global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE>())) void 
     BceArgs bce) {
     using C = FwdCfg<G, FP>;
     __shared__ __attribute__((aligned(16))) char Xg[2][FP * C::RB];
-    __shared__ int32_t sidx[FP];
     __shared__ __attribute__((aligned(16))) char stg[4][C::STG];
     __shared__ float s_red[4];
 
@@ -334,10 +336,10 @@ __global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE>())) void 
     if constexpr (BCE) bce.part += work;
     if ((g + 1) * G > O)
         fwd_group<T, G, FP, true, BCE>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
-                                       ntiles, Xg, sidx, stg, bce, s_red);
+                                       ntiles, Xg, stg, bce, s_red);
     else
         fwd_group<T, G, FP, false, BCE>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
-                                        ntiles, Xg, sidx, stg, bce, s_red);
+                                        ntiles, Xg, stg, bce, s_red);
 }
 
 // Batch chunks per group: the whole batch per workgroup (up to kMaxTilesPerWG
