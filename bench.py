@@ -207,25 +207,32 @@ def main():
            lambda: st.backward_weights_sgd(dY_buf, ldy)]
 
     def timed(fn_list, steps, warmup):
+        """(ms per step, per-phase ms, wall s).  The step time comes from K steps with
+        nothing but the two bracketing events; the per-phase times from a second
+        pass of K steps with an event between phases (recording events between
+        kernels adds gaps, so those phases sum to more than the step time)."""
         for _ in range(warmup):
             for fn in fn_list:
                 fn()
         torch.cuda.synchronize()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fn_list) + 1)]
-               for _ in range(steps)]
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
         t0.record(stream)
         w0 = time.perf_counter()
+        for _ in range(steps):
+            for fn in fn_list:
+                fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - w0
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fn_list) + 1)]
+               for _ in range(steps)]
         for k in range(steps):
             evs[k][0].record(stream)
             for i, fn in enumerate(fn_list):
                 fn()
                 evs[k][i + 1].record(stream)
-        t1.record(stream)
         torch.cuda.synchronize()
-        wall_s = time.perf_counter() - w0
         per = [sum(e[i].elapsed_time(e[i + 1]) for e in evs) / steps for i in range(len(fn_list))]
         return t0.elapsed_time(t1) / steps, per, wall_s
 
