@@ -20,6 +20,8 @@ tensor, so backward does no device->host sync.
 """
 from __future__ import annotations
 
+import collections
+import weakref
 from typing import Any, Optional
 
 import torch
@@ -33,6 +35,32 @@ def _grad_dtype(p: torch.Tensor) -> torch.dtype:
     """dtype autograd will store for p.grad: p.grad_dtype if set (torch >= 2.10), else p.dtype."""
     gd = getattr(p, "grad_dtype", None)
     return gd if gd is not None else p.dtype
+
+
+# Feature-gradient workspaces reused across backward calls.  The index plan in a
+# workspace depends on group_locations only, so a call with the same index
+# tensor (same object, unchanged version counter: a rewire bumps it) skips
+# rebuilding it.  Keyed by shape, dtype, device and stream too: a workspace's
+# partial sums are written and read in stream order.
+_WS_CACHE: "collections.OrderedDict[tuple, list]" = collections.OrderedDict()
+_WS_CACHE_SIZE = 2
+
+
+def _bwdf_workspace(locs: torch.Tensor, B: int, D: int, F: int, O: int, gsize: int,
+                    dtype: torch.dtype, stream: int):
+    """(workspace, plan_ready, entry): plan_ready = 1 when the cached workspace holds
+    the plan of these indices; the caller marks ``entry`` valid after its call."""
+    key = (locs.device, B, D, F, O, gsize, dtype, stream)
+    ent = _WS_CACHE.get(key)
+    if ent is None:
+        ent = [_C.bwd_features_workspace(B, D, F, O, gsize, dtype, locs.device), None, -1, 0]
+        _WS_CACHE[key] = ent
+        while len(_WS_CACHE) > _WS_CACHE_SIZE:
+            _WS_CACHE.popitem(last=False)
+    _WS_CACHE.move_to_end(key)
+    ready = 1 if (ent[1] is not None and ent[1]() is locs and ent[2] == locs._version
+                  and ent[3] == locs.data_ptr()) else 0
+    return ent[0], ready, ent
 
 
 def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.Tensor,
@@ -54,18 +82,19 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
 
     grad_x = None
     if need_x:
-        ws = _C.bwd_features_workspace(B, D, F, O, gsize, dtype, dev)
+        ws, ready, ent = _bwdf_workspace(locs, B, D, F, O, gsize, dtype, stream)
         if dtype == torch.bfloat16:
             grad_x = torch.empty(B, D, dtype=dtype, device=dev)
             _lib.call("haste_ffi_bwd_features_sr", locs.data_ptr(), W.data_ptr(),
                       dY.data_ptr(), lddy, grad_x.data_ptr(), SR_SEED_GRAD_X, ws.data_ptr(),
-                      ws.numel(), B, D, F, O, gsize, code, 0, stream)
+                      ws.numel(), B, D, F, O, gsize, code, ready, stream)
         else:
             dxt = torch.empty(D, B, dtype=torch.float32, device=dev)
             _lib.call("haste_ffi_bwd_features", locs.data_ptr(), W.data_ptr(), dY.data_ptr(),
                       lddy, dxt.data_ptr(), ws.data_ptr(), ws.numel(), B, D, F, O, gsize,
-                      code, 0, stream)
+                      code, ready, stream)
             grad_x = dxt.t().to(dtype).contiguous()
+        ent[1], ent[2], ent[3] = weakref.ref(locs), locs._version, locs.data_ptr()
 
     grad_w = grad_b = None
     if need_w or need_b:

@@ -241,3 +241,32 @@ def test_head_tail_logits_match_cat(dev, H):
     torch.testing.assert_close(ghw.float(), ghw_ref.float(), **TOL16)
     torch.testing.assert_close(ghb.float(), ghb_ref.float(), **TOL16)
     torch.testing.assert_close(gx.float(), gx_ref.float(), **TOL16)
+
+
+def test_autograd_reuses_plan_until_indices_change(dev):
+    """The drop-in backward keeps the index plan of its workspace across calls and
+    rebuilds it after the indices change (rewire, in-place edit): gradients match
+    the oracle every time."""
+    B, D, O, G, F = 64, 300, 1000, 32, 64
+    torch.manual_seed(5)
+    layer = GroupFixedFanIn(D, O, F, group_size=G, prune_mode="fraction", rewire_fraction=0.2,
+                            dtype=torch.bfloat16).to(dev)
+    x = torch.randn(B, D).to(torch.bfloat16)
+    dY = (torch.randn(B, O) * 0.1).to(torch.bfloat16)
+
+    def check():
+        xd = x.to(dev).requires_grad_(True)
+        layer.zero_grad()
+        layer(xd).backward(dY.to(dev))
+        idx = layer.group_locations.cpu()
+        W = layer.weights.detach().cpu()
+        ref = oracle.ffi_backward_features(idx, W, dY, G, D).t().contiguous()
+        torch.testing.assert_close(xd.grad.float().cpu(), ref, **TOL16)
+
+    check()
+    check()                         # plan reused
+    layer.rewire(seed=1)            # indices change (version bump)
+    check()
+    with torch.no_grad():
+        layer.group_locations[0].copy_(torch.arange(F, dtype=torch.int32, device=dev))
+    check()
