@@ -35,7 +35,7 @@ constexpr int kGroupUnroll = 6;   // groups per unrolled iteration of the main k
 // in a double-buffered LDS ring of ring_tiles(G) tiles of 16 rows; a W^T row is
 // 2G bytes, stored with 32 bytes of padding (conflict-free 16-byte reads of 16
 // rows).  Ranges with more tiles take the rest from global memory.
-__host__ __device__ constexpr int ring_tiles(int G) { return G <= 16 ? 8 : G <= 32 ? 6 : G <= 64 ? 4 : 2; }
+__host__ __device__ constexpr int ring_tiles(int G) { return G <= 16 ? 8 : G <= 32 ? 6 : G <= 64 ? 4 : 3; }
 __host__ __device__ constexpr int ring_row_bytes(int G) { return 2 * G + 32; }
 __host__ __device__ constexpr int ring_bytes(int G) {
     return 2 * ring_tiles(G) * 16 * (ring_row_bytes(G) + 4);

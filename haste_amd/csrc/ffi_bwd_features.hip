@@ -533,7 +533,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // stages group i+1 into ring[1 - i % 2] (read by every wave before the
     // last barrier), reads and multiplies group i's first round and adds
     // group i-1's products into the partial. ----
-    constexpr int DEPTH = 5, NS = DEPTH + 1;
+    // G = 128 groups take about twice as long per iteration, so two groups of
+    // look-ahead cover the load latency; the shallower pipeline leaves room in
+    // the register budget for the larger dY fragments and ring rounds.
+    constexpr int DEPTH = G >= 128 ? 2 : 5, NS = DEPTH + 1;
     static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0, "unroll");
     Stage stg[NS];
     u32x4 ya[NS][KS];
@@ -562,9 +565,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
-    auto body = [&](int i, auto q) __attribute__((always_inline)) {
-        constexpr int Q = decltype(q)::value;  // i % NS
-        constexpr int P = Q % 2;               // ring buffer of group i
+    auto body = [&](int i, auto kc) __attribute__((always_inline)) {
+        constexpr int K = decltype(kc)::value;  // i % kGroupUnroll
+        constexpr int Q = K % NS;               // i % NS
+        constexpr int P = K % 2;                // ring buffer of group i
         const u32x2 mn = uniform_meta(mraw[(Q + 1 + DEPTH) % NS]);
         load_stage(i + 1 + DEPTH, mn, 0, stg[(Q + 1 + DEPTH) % NS]);
         load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS]);

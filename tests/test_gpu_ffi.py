@@ -58,6 +58,8 @@ CASES = [
     (64, 4096, 3000, 32, 256, "random"),  # wide input, F = 256 (config 3 family)
     (40, 768, 2100, 128, 128, "random"),  # G = 128 (config 4 family)
     (33, 200, 700, 128, 256, "dups"),
+    (200, 768, 3000, 128, 128, "dups"),   # G = 128, batch tiles of 128 (8 waves), 4 ranges
+    (150, 200, 1500, 128, 256, "random"), # G = 128, 8 waves, one range: rounds past the ring
     (1, 64, 64, 64, 64, "random"),
 ]
 
