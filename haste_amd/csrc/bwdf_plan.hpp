@@ -17,6 +17,7 @@
 #pragma once
 
 #include <algorithm>
+#include <cmath>
 
 #include "common.hpp"
 
@@ -32,22 +33,42 @@ constexpr int kLdsMisc = 1024;    // LDS the main kernel keeps for other things
 constexpr int kGroupUnroll = 6;   // groups per unrolled iteration of the main kernel's loop
 
 // The main kernel stages each group's W^T tiles (and their partial-row offsets)
-// in a double-buffered LDS ring of ring_tiles(G) tiles of 16 rows; a W^T row is
-// 2G bytes, stored with 32 bytes of padding (conflict-free 16-byte reads of 16
-// rows).  Ranges with more tiles take the rest from global memory.
+// in a double-buffered LDS ring of RT tiles of 16 rows; a W^T row is 2G bytes,
+// stored with 32 bytes of padding (conflict-free 16-byte reads of 16 rows).
+// Ranges with more tiles take the rest from global memory.  Every wave
+// multiplies all RT ring tiles of a round, so the kernel is built for RT in
+// {2, 3, ring_tiles(G)} and the plan picks the smallest ring that a range's
+// tiles fit in 99 % of rounds (ring_overflow below); a smaller ring also
+// leaves more LDS for the partial.
 __host__ __device__ constexpr int ring_tiles(int G) { return G <= 16 ? 8 : G <= 32 ? 6 : G <= 64 ? 4 : 3; }
 __host__ __device__ constexpr int ring_row_bytes(int G) { return 2 * G + 32; }
-__host__ __device__ constexpr int ring_bytes(int G) {
-    return 2 * ring_tiles(G) * 16 * (ring_row_bytes(G) + 4);
+__host__ __device__ constexpr int ring_bytes(int G, int rt) {
+    return 2 * rt * 16 * (ring_row_bytes(G) + 4);
 }
 __host__ __device__ constexpr int acc_stride(int bt) { return bt + kAccPad; }
 // Features per range: the LDS partial holds (Dc + kTrashRows) rows of bt fp32.
-__host__ __device__ constexpr int max_dc(int bt, int G) {
-    return (kLdsBytes - kLdsMisc - ring_bytes(G)) / 4 / acc_stride(bt) - kTrashRows;
+__host__ __device__ constexpr int max_dc(int bt, int G, int rt) {
+    return (kLdsBytes - kLdsMisc - ring_bytes(G, rt)) / 4 / acc_stride(bt) - kTrashRows;
+}
+
+// Probability that a range holds more than rt layer-0 tiles when its share of
+// a group's F indices is Binomial(F, q) -- an upper bound for indices drawn
+// uniformly without replacement, whose share is hypergeometric.
+inline double ring_overflow(int64_t F, double q, int rt) {
+    const int64_t cap = 16 * (int64_t)rt;
+    if (cap >= F) return 0.0;
+    if (q >= 1.0) return 1.0;
+    const double lf = std::lgamma((double)F + 1.0), lq = std::log(q), lr = std::log1p(-q);
+    double s = 0.0;
+    for (int64_t n = cap + 1; n <= F; ++n)
+        s += std::exp(lf - std::lgamma((double)n + 1.0) - std::lgamma((double)(F - n) + 1.0) +
+                      (double)n * lq + (double)(F - n) * lr);
+    return s;
 }
 
 struct BwdFPlan {
     int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;
+    int64_t RT, DCMAX;  // ring tiles of the main kernel; its partial's trash rows start at DCMAX
     int64_t tfeat_off, tsrc_off, perm_off, meta_off, twt_off, prep_bytes, ws_bytes;
 };
 
@@ -57,7 +78,17 @@ inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G)
     p.BT = B <= 64 ? 64 : 128;
     p.nbt = ceil_div(B, p.BT);
     p.Bp = p.nbt * p.BT;
-    p.ndr = ceil_div(D, max_dc((int)p.BT, (int)G));
+    // the smallest ring whose rounds overflow for under 1 % of (group, range) pairs
+    p.RT = ring_tiles((int)G);
+    for (int rt = 2; rt <= 3 && rt < p.RT; ++rt) {
+        const int64_t dc = ceil_div(D, ceil_div(D, max_dc((int)p.BT, (int)G, rt)));
+        if (ring_overflow(F, std::min(1.0, (double)dc / (double)D), rt) < 0.01) {
+            p.RT = rt;
+            break;
+        }
+    }
+    p.DCMAX = max_dc((int)p.BT, (int)G, (int)p.RT);
+    p.ndr = ceil_div(D, p.DCMAX);
     p.Dc = ceil_div(D, p.ndr);
     int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
     S = std::min<int64_t>(S, std::max<int64_t>(1, ceil_div(p.Gc, 8)));

@@ -250,27 +250,27 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
 // Ranges holding more than RT tiles in a group process the rest in further
 // rounds staged synchronously (rare: a range's share of F is usually ~F/ndr),
 // layer by layer.
-template <int G, int WAVES>
+template <int G, int WAVES, int RT_>
 struct BwdFCfg {
     static constexpr int KS = G >= 32 ? G / 32 : 1;  // MFMA k-steps over labels
     static constexpr int BT = 16 * WAVES;            // batch columns per workgroup
     static constexpr int AS = acc_stride(BT);
-    static constexpr int RT = ring_tiles(G);
+    static constexpr int RT = RT_;
     static constexpr int RB = ring_row_bytes(G);
     static constexpr int RING = RT * 16 * RB;        // bytes per ring buffer
     static constexpr int THREADS = 64 * WAVES;
     static constexpr int CH = G / 8;                 // 16-byte chunks per W^T row
     static constexpr int SPT = (RT * 16 * CH + THREADS - 1) / THREADS;  // staged chunks per thread
-    static constexpr int DCMAX = max_dc(BT, G);
+    static constexpr int DCMAX = max_dc(BT, G, RT);
     static_assert(DCMAX > 0, "LDS budget");
 };
 
-template <typename T, int G, int WAVES>
+template <typename T, int G, int WAVES, int RT_>
 __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
     const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
     int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
-    using C = BwdFCfg<G, WAVES>;
+    using C = BwdFCfg<G, WAVES, RT_>;
     constexpr int KS = C::KS, BT = C::BT, AS = C::AS, RT = C::RT, RB = C::RB, CH = C::CH;
     constexpr int SPT = C::SPT, NTH = C::THREADS;
     __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
@@ -679,7 +679,7 @@ __global__ __launch_bounds__(256) void bwdf_reduce_sr_kernel(const float* __rest
     }
 }
 
-template <typename T, int G, int WAVES>
+template <typename T, int G, int WAVES, int RT>
 int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                 int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
                 hipStream_t st) {
@@ -689,11 +689,24 @@ int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const ui
         set_error("haste_ffi_bwd_features: lddy = %lld too large", (long long)lddy);
         return HASTE_ERR_UNSUPPORTED;
     }
-    bwdf_main_kernel<T, G, WAVES><<<dim3((unsigned)grid), dim3(64 * WAVES), 0, st>>>(
+    bwdf_main_kernel<T, G, WAVES, RT><<<dim3((unsigned)grid), dim3(64 * WAVES), 0, st>>>(
         tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
         (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
     return HASTE_OK;
+}
+
+// the plan's ring size: 2, 3 or ring_tiles(G) tiles
+template <typename T, int G, int WAVES>
+int launch_ring(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
+                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
+                hipStream_t st) {
+    constexpr int R = ring_tiles(G);
+    if (p.RT == 2) return launch_main<T, G, WAVES, 2>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    if constexpr (R > 3) {
+        if (p.RT == 3) return launch_main<T, G, WAVES, 3>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    }
+    return launch_main<T, G, WAVES, R>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
 template <typename T, int G>
@@ -701,8 +714,8 @@ int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint1
              int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
              int64_t O, hipStream_t st) {
     (void)F;
-    if (p.BT == 64) return launch_main<T, G, 4>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-    return launch_main<T, G, 8>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    if (p.BT == 64) return launch_ring<T, G, 4>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    return launch_ring<T, G, 8>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
 // Checks the arguments and the workspace size; returns the plan.
@@ -713,7 +726,7 @@ int check_bwdf(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, int64
     const BwdFPlan p = make_plan(B, D, F, O, G);
     if (p.ndr > kMaxRanges) {
         set_error("%s: D = %lld is too large (at most %lld features)", fn, (long long)D,
-                  (long long)kMaxRanges * max_dc((int)p.BT, (int)G));
+                  (long long)kMaxRanges * p.DCMAX);
         return HASTE_ERR_UNSUPPORTED;
     }
     HASTE_CHECK_ARG(aligned16(workspace), "%s: workspace must be 16-byte aligned", fn);
@@ -754,7 +767,7 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     if (!plan_ready) {
         bwdf_plan_kernel<<<pgrid, dim3(256), 0, st>>>(
             idx, tfeat, tsrc, perm, meta, (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap,
-            acc_stride((int)p.BT) * 4, max_dc((int)p.BT, (int)G));
+            acc_stride((int)p.BT) * 4, (int)p.DCMAX);
         HASTE_CHECK_LAUNCH(fn);
     }
     const bool gather = plan_ready != 2;
@@ -816,7 +829,7 @@ extern "C" int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace,
         idx, reinterpret_cast<int*>(base + p.tfeat_off), reinterpret_cast<int*>(base + p.tsrc_off),
         reinterpret_cast<int*>(base + p.perm_off), reinterpret_cast<int*>(base + p.meta_off),
         (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap, haste::acc_stride((int)p.BT) * 4,
-        haste::max_dc((int)p.BT, (int)G));
+        (int)p.DCMAX);
     HASTE_CHECK_LAUNCH(fn);
     return HASTE_OK;
 }

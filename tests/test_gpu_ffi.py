@@ -60,6 +60,8 @@ CASES = [
     (33, 200, 700, 128, 256, "dups"),
     (200, 768, 3000, 128, 128, "dups"),   # G = 128, batch tiles of 128 (8 waves), 4 ranges
     (150, 200, 1500, 128, 256, "random"), # G = 128, 8 waves, one range: rounds past the ring
+    (256, 768, 5000, 64, 64, "dups"),     # 2-tile ring (config 2 family); duplicates overflow it
+    (160, 4096, 1000, 32, 256, "random"), # 2-tile ring, 15 ranges (config 3 family), 8 waves
     (1, 64, 64, 64, 64, "random"),
 ]
 
