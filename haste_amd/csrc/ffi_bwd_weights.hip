@@ -190,19 +190,24 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     const rsrc_t wr = make_rsrc(SGD ? sg.W + l0 * F : nullptr, SGD ? (int64_t)nl * F * 2 : 0);
     constexpr int CPR = C::CPR, WPT = C::WPT;
     // Fused step: the weights and bias the epilogue updates are loaded now, so
-    // their latency hides behind the batch loop (when the gradient tile is
-    // processed in one pass, the thread's chunks are known: chunk tid + q*256
-    // is row it / CPR, slots (it % CPR) * 8 .. +7).  Not for F > 128, where the
-    // extra registers would cost a wave per SIMD.
-    constexpr bool kWPre = SGD && PR == G && FP <= 128;
-    u32x4 wpre[kWPre ? WPT : 1];
+    // their latency hides behind the batch loop (the thread's chunks are known:
+    // in pass pp, chunk tid + q*256 is row pp*PR + it / CPR, slots (it % CPR) * 8
+    // .. +7).  For at most two passes and F <= 128: beyond that the extra
+    // registers would cost a wave per SIMD.
+    constexpr int NPASS = G / PR;
+    constexpr bool kWPre = SGD && NPASS <= 2 && FP <= 128;
+    u32x4 wpre[kWPre ? NPASS * WPT : 1];
     uint32_t bpre = 0;  // fused step: bias bits of label tid (tid < nl)
     if constexpr (SGD) {
 #pragma unroll
-        for (int q = 0; q < (kWPre ? WPT : 0); ++q) {
-            const int it = tid + q * kThreads;
-            const int j0 = (it % CPR) * 8;
-            wpre[q] = buf_load16(wr, it < PR * CPR && j0 < F ? (uint32_t)((it / CPR) * F + j0) * 2 : kOOB);
+        for (int pp = 0; pp < (kWPre ? NPASS : 0); ++pp) {
+#pragma unroll
+            for (int q = 0; q < WPT; ++q) {
+                const int it = tid + q * kThreads;
+                const int j0 = (it % CPR) * 8;
+                wpre[pp * WPT + q] = buf_load16(
+                    wr, it < PR * CPR && j0 < F ? (uint32_t)((pp * PR + it / CPR) * F + j0) * 2 : kOOB);
+            }
         }
         const rsrc_t bbr = make_rsrc(sg.bias != nullptr ? sg.bias + l0 : nullptr,
                                      sg.bias != nullptr ? (int64_t)nl * 2 : 0);
@@ -354,7 +359,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
             }
             if constexpr (SGD) {
                 u32x4 wv;
-                if constexpr (kWPre) wv = wpre[q];
+                if constexpr (kWPre) wv = p0 == 0 ? wpre[q] : wpre[(NPASS - 1) * WPT + q];
                 else wv = buf_load16(wr, in ? e * 2 : kOOB);
                 float gv[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
                 float mv[8];

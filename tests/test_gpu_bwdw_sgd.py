@@ -24,6 +24,8 @@ CASES = [
     (100, 300, 1000, 16, 48, True, True, True),      # B % 8 != 0, F % 32 != 0, momentum
     (96, 512, 2050, 64, 64, False, False, True),     # no bias, partial last group
     (40, 768, 2100, 128, 128, True, True, False),    # G = 128, RNE instead of SR
+    (130, 768, 3001, 128, 128, True, False, True),   # G = 128, SR: two prefetched epilogue passes
+    (70, 768, 2000, 128, 96, True, True, True),      # G = 128, F < 128 slots, momentum
     (33, 200, 700, 128, 256, True, False, True),     # G = 128, F = 256 (several epilogue passes)
     (64, 4096, 3000, 32, 256, True, True, True),     # wide input, F = 256
 ]
