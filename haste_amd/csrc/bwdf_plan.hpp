@@ -66,6 +66,26 @@ inline double ring_overflow(int64_t F, double q, int rt) {
     return s;
 }
 
+// The smallest ring whose rounds overflow for under 1 % of (group, range)
+// pairs.  Plans are made on every call, so the last shape's choice is kept
+// (per host thread) instead of summing the binomial tail again.
+inline int64_t pick_ring(int64_t BT, int64_t D, int64_t F, int64_t G) {
+    thread_local int64_t key[4] = {-1, -1, -1, -1};
+    thread_local int64_t last = 0;
+    if (key[0] == BT && key[1] == D && key[2] == F && key[3] == G) return last;
+    int64_t ring = ring_tiles((int)G);
+    for (int rt = 2; rt <= 3 && rt < ring; ++rt) {
+        const int64_t dc = ceil_div(D, ceil_div(D, (int64_t)max_dc((int)BT, (int)G, rt)));
+        if (ring_overflow(F, std::min(1.0, (double)dc / (double)D), rt) < 0.01) {
+            ring = rt;
+            break;
+        }
+    }
+    key[0] = BT; key[1] = D; key[2] = F; key[3] = G;
+    last = ring;
+    return ring;
+}
+
 struct BwdFPlan {
     int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;
     int64_t RT, DCMAX;  // ring tiles of the main kernel; its partial's trash rows start at DCMAX
@@ -78,15 +98,7 @@ inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G)
     p.BT = B <= 64 ? 64 : 128;
     p.nbt = ceil_div(B, p.BT);
     p.Bp = p.nbt * p.BT;
-    // the smallest ring whose rounds overflow for under 1 % of (group, range) pairs
-    p.RT = ring_tiles((int)G);
-    for (int rt = 2; rt <= 3 && rt < p.RT; ++rt) {
-        const int64_t dc = ceil_div(D, ceil_div(D, max_dc((int)p.BT, (int)G, rt)));
-        if (ring_overflow(F, std::min(1.0, (double)dc / (double)D), rt) < 0.01) {
-            p.RT = rt;
-            break;
-        }
-    }
+    p.RT = pick_ring(p.BT, D, F, G);
     p.DCMAX = max_dc((int)p.BT, (int)G, (int)p.RT);
     p.ndr = ceil_div(D, p.DCMAX);
     p.Dc = ceil_div(D, p.ndr);
