@@ -32,6 +32,7 @@ namespace haste {
 namespace {
 
 constexpr int kBT = 64;        // batch columns per tile
+constexpr int kStoreNT = 2;    // buffer-store cache policy: nt (non-temporal) on gfx950
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kMaxTilesPerWG = 8;
 
@@ -294,7 +295,12 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                 const int rs = own ? rr : 0;
                 const u32x4 v = *reinterpret_cast<const u32x4*>(&stg[wave][rs * SRB + cb]);
                 const int rb = wn * NT * 16 + rs;
-                buf_store16(v, dst, own ? (uint32_t)((int64_t)rb * ldo * 2 + (wm * MT * 16) * 2 + cb) : kOOB);
+                // logits are non-temporal stores (cache-policy bit nt), so the
+                // stream of them does not evict the gathered rows and weights;
+                // dY (BCE) is read back by the backward kernels and stays cached
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v, dst, own ? (uint32_t)((int64_t)rb * ldo * 2 + (wm * MT * 16) * 2 + cb) : kOOB, 0,
+                    BCE ? 0 : kStoreNT);
             }
         };
         if constexpr (!LAST) flush(orr);
