@@ -98,7 +98,13 @@ struct SgdArgs {
 template <int G, int FP>
 constexpr int bwdw_waves_per_simd() { return G * FP >= 128 * 256 ? 1 : 2; }
 
-template <typename T, int G, int FP, bool SGD>
+// dY larger than the 256 MB last-level cache (MALL) of an MI355X: this kernel,
+// its last reader in a training step, streams it with non-temporal loads (YNT),
+// so it does not evict the weights that the next step's forward reads.
+constexpr int64_t kMallBytes = 256ll << 20;
+constexpr int kLoadNT = 2;  // buffer-load cache policy: nt on gfx950
+
+template <typename T, int G, int FP, bool SGD, bool YNT>
 __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_bwd_w_kernel(
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
     const uint16_t* __restrict__ dY, int64_t lddy, void* __restrict__ dW, int dW_dtype,
@@ -152,7 +158,8 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
             const bool ok = tid + q * kThreads < C::PIECES && pcc[q] < nl;
-            v[q] = buf_load16(yr, ok ? (uint32_t)((int64_t)pr[q] * lddy + pcc[q]) * 2 : kOOB);
+            v[q] = __builtin_amdgcn_raw_buffer_load_b128(
+                yr, ok ? (uint32_t)((int64_t)pr[q] * lddy + pcc[q]) * 2 : kOOB, 0, YNT ? kLoadNT : 0);
         }
     };
     auto stash = [&](int buf, const u32x4 (&v)[PPT]) {
@@ -423,7 +430,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     }
 }
 
-template <typename T, int G, int FP, bool SGD>
+template <typename T, int G, int FP, bool SGD, bool YNT>
 int launch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY, int64_t lddy,
            void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B, int64_t D, int64_t F,
            int64_t O, const SgdArgs& sg, hipStream_t st) {
@@ -434,25 +441,25 @@ int launch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* 
                   (long long)Gc, (long long)lddy, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
-    ffi_bwd_w_kernel<T, G, FP, SGD><<<dim3((unsigned)Gc), dim3(kThreads), 0, st>>>(
+    ffi_bwd_w_kernel<T, G, FP, SGD, YNT><<<dim3((unsigned)Gc), dim3(kThreads), 0, st>>>(
         idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, (int)B, (int)D, (int)F, O, sg);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_weights");
     return HASTE_OK;
 }
 
-template <typename T, bool SGD>
-int dispatch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY,
+template <typename T, bool SGD, bool YNT>
+int dispatch_g(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY,
              int64_t lddy, void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B,
              int64_t D, int64_t F, int64_t O, int64_t G, const SgdArgs& sg, hipStream_t st) {
 #define HASTE_BWDW_FP(GG)                                                                        \
     do {                                                                                         \
-        if (F <= 32) return launch<T, GG, 32, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,  \
+        if (F <= 32) return launch<T, GG, 32, SGD, YNT>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,  \
                                                    dbias_dtype, B, D, F, O, sg, st);             \
-        if (F <= 64) return launch<T, GG, 64, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,  \
+        if (F <= 64) return launch<T, GG, 64, SGD, YNT>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,  \
                                                    dbias_dtype, B, D, F, O, sg, st);             \
-        if (F <= 128) return launch<T, GG, 128, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype,       \
+        if (F <= 128) return launch<T, GG, 128, SGD, YNT>(idx, xT, ldx, dY, lddy, dW, dW_dtype,       \
                                                      dbias, dbias_dtype, B, D, F, O, sg, st);    \
-        return launch<T, GG, 256, SGD>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, \
+        return launch<T, GG, 256, SGD, YNT>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, \
                                        B, D, F, O, sg, st);                                      \
     } while (0)
     switch (G) {
@@ -465,6 +472,19 @@ int dispatch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t
 #undef HASTE_BWDW_FP
     set_error("haste_ffi_bwd_weights: unsupported group size %lld", (long long)G);
     return HASTE_ERR_UNSUPPORTED;
+}
+
+template <typename T, bool SGD>
+int dispatch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY,
+             int64_t lddy, void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B,
+             int64_t D, int64_t F, int64_t O, int64_t G, const SgdArgs& sg, hipStream_t st) {
+    if constexpr (std::is_same_v<T, BF16>) {
+        if (B * lddy * 2 > kMallBytes)
+            return dispatch_g<T, SGD, true>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,
+                                            dbias_dtype, B, D, F, O, G, sg, st);
+    }
+    return dispatch_g<T, SGD, false>(idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, B,
+                                     D, F, O, G, sg, st);
 }
 
 int check_bwdw(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, const void* dY,

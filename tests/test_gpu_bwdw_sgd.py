@@ -107,7 +107,8 @@ def test_fused_matches_separate_and_oracle(dev, B, D, O, G, F, has_bias, use_mom
         assert np.array_equal(mW2.cpu().numpy().reshape(-1), m_ref)
 
 
-@pytest.mark.parametrize("B,D,O,G,F", [(128, 768, 8193, 64, 128), (72, 500, 3001, 32, 64)])
+@pytest.mark.parametrize("B,D,O,G,F", [(128, 768, 8193, 64, 128), (72, 500, 3001, 32, 64),
+                                       (512, 768, 270001, 64, 128)])  # dY > 256 MB: streamed
 def test_train_step_fused_equals_unfused(dev, B, D, O, G, F):
     """FFITrainStep.step (fused weight-gradient + SGD, which also hands the next
     step's bwd-features the transposed updated weights) gives dX, W and bias

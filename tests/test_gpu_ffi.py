@@ -206,3 +206,32 @@ def test_forward_g16_rows_written_once(dev, B):
                   bias_d.data_ptr(), out.data_ptr(), ldo, B, D, F, O, G, _lib.DTYPE_BF16,
                   torch.cuda.current_stream().cuda_stream)
         torch.testing.assert_close(out[:, :O].float().cpu(), ref, **TOL16)
+
+
+def test_backward_weights_streaming_dY(dev):
+    """dY above 256 MB (the MI355X last-level cache) is read with non-temporal
+    loads, a separate instantiation of the weight-gradient kernel: dW and dbias
+    of the first, a middle and the last (partial) group match the oracle."""
+    B, D, O, G, F = 512, 768, 270001, 64, 128
+    g = torch.Generator(device=dev).manual_seed(12)
+    x = torch.randn(B, D, generator=g, device=dev).to(torch.bfloat16)
+    Gc = (O + G - 1) // G
+    idx = torch.randint(0, D, (Gc, F), generator=g, device=dev, dtype=torch.int32)
+    lddy = (O + 7) // 8 * 8
+    assert B * lddy * 2 > 256 << 20
+    dY = torch.zeros(B, lddy, dtype=torch.bfloat16, device=dev)
+    dY[:, :O] = torch.randn(B, O, generator=g, device=dev).mul_(0.1).to(torch.bfloat16)
+    xT, ldx = _C.padded_transpose(x)
+    dW = torch.empty(O, F, dtype=torch.float32, device=dev)
+    db = torch.empty(O, dtype=torch.float32, device=dev)
+    _lib.call("haste_ffi_bwd_weights", idx.data_ptr(), xT.data_ptr(), ldx, dY.data_ptr(), lddy,
+              dW.data_ptr(), _lib.DTYPE_F32, db.data_ptr(), _lib.DTYPE_F32, B, D, F, O, G,
+              _lib.DTYPE_BF16, _C.stream_of(dY))
+    torch.cuda.synchronize()
+    x_t = x.t().contiguous().cpu()
+    for grp in (0, Gc // 2, Gc - 1):
+        l0, l1 = grp * G, min(O, (grp + 1) * G)
+        dy = dY[:, l0:l1].cpu()
+        ref_w = oracle.ffi_backward_weights(idx[grp:grp + 1].cpu(), x_t, dy, G)
+        torch.testing.assert_close(dW[l0:l1].cpu(), ref_w, **TOL32)
+        torch.testing.assert_close(db[l0:l1].cpu(), oracle.bias_grad(dy), **TOL32)
