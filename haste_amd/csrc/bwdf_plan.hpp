@@ -58,12 +58,15 @@ inline double ring_overflow(int64_t F, double q, int rt) {
     const int64_t cap = 16 * (int64_t)rt;
     if (cap >= F) return 0.0;
     if (q >= 1.0) return 1.0;
-    const double lf = std::lgamma((double)F + 1.0), lq = std::log(q), lr = std::log1p(-q);
-    double s = 0.0;
-    for (int64_t n = cap + 1; n <= F; ++n)
-        s += std::exp(lf - std::lgamma((double)n + 1.0) - std::lgamma((double)(F - n) + 1.0) +
-                      (double)n * lq + (double)(F - n) * lr);
-    return s;
+    // log pmf by the ratio pmf(n+1) / pmf(n) = (F-n)/(n+1) * q/(1-q), from
+    // pmf(0) = (1-q)^F (no lgamma: it writes the global signgam)
+    const double lodds = std::log(q) - std::log1p(-q);
+    double lp = (double)F * std::log1p(-q), s = 0.0;
+    for (int64_t n = 0; n < F; ++n) {
+        if (n > cap) s += std::exp(lp);
+        lp += std::log((double)(F - n) / (double)(n + 1)) + lodds;
+    }
+    return s + std::exp(lp);  // n = F
 }
 
 // The smallest ring whose rounds overflow for under 1 % of (group, range)
