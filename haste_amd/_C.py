@@ -8,8 +8,8 @@ input's device; kernels run on torch's current stream (the reference used the
 legacy default stream).
 
 Also holds the layout helpers shared by bindings.py / step.py: the HIP kernels
-need 16-byte aligned rows (row pitch a multiple of 8 elements) for X^T, dY and
-the logits.
+need 16-byte aligned rows (row pitch a multiple of 8 elements) for X^T and the
+logits; the grad of the logits may have any row pitch.
 """
 from __future__ import annotations
 
@@ -64,6 +64,18 @@ def rows_aligned(t: torch.Tensor) -> Tuple[torch.Tensor, int]:
     buf = torch.empty(t.shape[0], ld, dtype=t.dtype, device=t.device)
     buf[:, : t.shape[1]].copy_(t)
     return buf[:, : t.shape[1]], ld
+
+
+def grad_rows(t: torch.Tensor) -> Tuple[torch.Tensor, int]:
+    """(t2, ld) for a grad-of-logits matrix [B, O] read by the backward kernels:
+    any row stride works (rows may start on 2-byte boundaries), so ``t`` is used
+    in place when its columns are contiguous; it is copied only otherwise, or
+    when O < 8 and the row stride is not a multiple of 8."""
+    assert t.dim() == 2
+    if (t.stride(1) == 1 or t.shape[1] == 1) and t.stride(0) >= t.shape[1] and \
+            t.data_ptr() % 2 == 0 and (t.shape[1] >= 8 or t.stride(0) % 8 == 0):
+        return t, t.stride(0)
+    return rows_aligned(t)
 
 
 def padded_transpose(features: torch.Tensor) -> Tuple[torch.Tensor, int]:
@@ -151,7 +163,7 @@ def ffi_backward_features_cuda(features: torch.Tensor, weights: torch.Tensor,
         raise RuntimeError(f"grad_outputs must be [B={B}, L={L}] (got {list(grad_outputs.shape)})")
     if grad_outputs.dtype != weights.dtype:
         raise RuntimeError("grad_outputs dtype must match weights dtype")
-    dY, lddy = rows_aligned(grad_outputs)
+    dY, lddy = grad_rows(grad_outputs)
     W = weights.contiguous()
     ws = bwd_features_workspace(B, H, FANIN, L, gsize, weights.dtype, weights.device)
     out = torch.empty(H, B, dtype=torch.float32, device=weights.device)
@@ -175,7 +187,7 @@ def ffi_backward_weights_cuda(features: torch.Tensor, weights: torch.Tensor,
     if tuple(grad_outputs.shape) != (B, L):
         raise RuntimeError(f"grad_outputs must be [B={B}, L={L}] (got {list(grad_outputs.shape)})")
     xT, ldx = rows_aligned(features)
-    dY, lddy = rows_aligned(grad_outputs)
+    dY, lddy = grad_rows(grad_outputs)
     dW = torch.empty(L, FANIN, dtype=features.dtype, device=features.device)
     _lib.call("haste_ffi_bwd_weights", locations.data_ptr(), xT.data_ptr(), ldx, dY.data_ptr(),
               lddy, dW.data_ptr(), dtype_code(features.dtype), None, 0, B, H, FANIN, L, gsize,

@@ -67,14 +67,14 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
                gsize: int, grad_output: torch.Tensor, need_x: bool, need_w: bool, need_b: bool,
                w_grad_dtype: torch.dtype, bias_dtype: Optional[torch.dtype]):
     """(grad_x, grad_w, grad_b) of the grouped FFI layer for grad_output [B, O]
-    (any row stride; rows are copied to aligned storage only when needed)."""
+    (read in place at any row stride when its columns are contiguous)."""
     D, B = xT.shape
     O, F = weights.shape
     dtype = weights.dtype
     dev = weights.device
     if grad_output.dtype != dtype:
         grad_output = grad_output.to(dtype)
-    dY, lddy = _C.rows_aligned(grad_output)
+    dY, lddy = _C.grad_rows(grad_output)
     locs = group_locations.contiguous()
     W = weights.contiguous()
     stream = _C.stream_of(W)
@@ -149,8 +149,8 @@ class HeadTailFFIFunction(torch.autograd.Function):
     (src/model.py:227-232,245-248: a dense nn.Linear head and an FFI tail), built
     in one [B, H + O] buffer: the FFI kernel writes the tail logits in place (the
     view starts at the column that puts the tail's rows on 16-byte boundaries)
-    and the backward reads the tail's columns of grad_output in place when their
-    rows are so aligned, so the B x O tail is never copied.  Values are those of
+    and the backward reads the tail's columns of grad_output in place, so the
+    B x O tail is never copied.  Values are those of
     the torch.cat formulation: the same head op (F.linear) and FFI kernels."""
 
     @staticmethod

@@ -241,6 +241,24 @@ __device__ __forceinline__ void buf_store2(uint16_t v, rsrc_t r, uint32_t off) {
     __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
 }
 
+// Rows of a [rows, ld] 16-bit matrix with any ld start on 2-byte boundaries;
+// 16-byte loads of 8 elements need no more alignment than that on gfx950
+// (unaligned buffer access).  The 8-element piece that straddles the end of
+// the matrix's last row is the one exception: it would cross the end of the
+// tensor, so it is loaded sh elements early (ending at the row's end) and moved
+// back into place with shift_down16.  Elements sh .. 7 of v go to positions
+// 0 .. 7 - sh; the top sh positions are unspecified.  sh in [0, 7], per lane.
+__device__ __forceinline__ u32x4 shift_down16(u32x4 v, int sh) {
+    const int ws = sh >> 1;
+    const uint32_t w0 = ws == 0 ? v[0] : ws == 1 ? v[1] : ws == 2 ? v[2] : v[3];
+    const uint32_t w1 = ws == 0 ? v[1] : ws == 1 ? v[2] : v[3];
+    const uint32_t w2 = ws == 0 ? v[2] : v[3];
+    const uint32_t w3 = v[3];
+    const uint32_t bs = (uint32_t)(sh & 1) * 2;  // bytes
+    return u32x4{__builtin_amdgcn_alignbyte(w1, w0, bs), __builtin_amdgcn_alignbyte(w2, w1, bs),
+                 __builtin_amdgcn_alignbyte(w3, w2, bs), __builtin_amdgcn_alignbyte(0u, w3, bs)};
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of
 // the 8-byte rows addressed by lanes 4k + i/4 (k = 0..3) as its element k.
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));

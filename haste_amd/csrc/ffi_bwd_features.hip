@@ -269,7 +269,7 @@ template <typename T, int G, int WAVES, int RT_>
 __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
     const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
-    int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
+    int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap, int yshort) {
     using C = BwdFCfg<G, WAVES, RT_>;
     constexpr int KS = C::KS, BT = C::BT, AS = C::AS, RT = C::RT, RB = C::RB, CH = C::CH;
     constexpr int SPT = C::SPT, NTH = C::THREADS;
@@ -299,10 +299,24 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     for (int i = tid * 4; i < dn * AS; i += NTH * 4)
         *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // dY of this lane's row (rows >= B read as zero; labels >= O are masked at use)
+    // dY of this lane's row (rows >= B read as zero; labels >= O are masked at
+    // use).  A row is read up to the 8-label piece boundary past O: inside the
+    // row when lddy >= O is a multiple of 8, else inside the next row.  dY's
+    // last row may end at label O (yshort): there the resource ends at O and
+    // the piece that straddles O is loaded early and shifted back
+    // (shift_down16; O >= 8 keeps the early load inside the resource).
     const int b0 = bt * BT;
+    const int rows = min(BT, B - b0);
     const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy,
-                                ((int64_t)(min(BT, B - b0) - 1) * lddy + (O + 7) / 8 * 8) * 2);
+                                ((int64_t)(rows - 1) * lddy +
+                                 ((yshort && b0 + rows == B) ? O : (O + 7) / 8 * 8)) * 2);
+    const bool last_row = yshort && b0 + wave * 16 + col == B - 1;
+    // elements the lane's piece ks of group g is loaded early by (0 unless it
+    // straddles O in dY's last row)
+    auto tail_shift = [&](int64_t g, int ks) __attribute__((always_inline)) -> int {
+        const int64_t over = g * G + kofs + ks * 32 + 8 - O;
+        return (last_row && over > 0 && over < 8) ? (int)over : 0;
+    };
     // byte offset of the lane's first label in the tile (32 bits: the tile's
     // resource spans at most kMaxRsrcBytes; g * G * 2 < 2 * lddy for real groups)
     const uint32_t yoff2 = (uint32_t)(((int64_t)(wave * 16 + col) * lddy + kofs) * 2);
@@ -310,7 +324,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-            a[ks] = buf_load16(yr, kq_ok ? yoff2 + go + ks * 64 : kOOB);
+            a[ks] = buf_load16(yr, kq_ok ? yoff2 + go + ks * 64 - 2 * tail_shift(g, ks) : kOOB);
     };
     // labels >= O read as zero: only the last group has any (a uniform branch)
     auto mask_y = [&](int64_t g, u32x4 (&a)[KS]) __attribute__((always_inline)) {
@@ -319,6 +333,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
         const int nr = (int)max<int64_t>(rem, 0);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
+            const int sh = tail_shift(g, ks);
+            if (sh) a[ks] = shift_down16(a[ks], sh);
             const int nv = nr - (ks * 32 + kofs);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -685,13 +701,13 @@ int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const ui
                 hipStream_t st) {
     const int64_t nlog = p.S * p.ndr * p.nbt;
     const int64_t grid = 8 * ceil_div(nlog, 8);
-    if ((int64_t)p.BT * lddy * 2 > kMaxRsrcBytes) {
+    if (((int64_t)p.BT * lddy + 8) * 2 > kMaxRsrcBytes) {
         set_error("haste_ffi_bwd_features: lddy = %lld too large", (long long)lddy);
         return HASTE_ERR_UNSUPPORTED;
     }
     bwdf_main_kernel<T, G, WAVES, RT><<<dim3((unsigned)grid), dim3(64 * WAVES), 0, st>>>(
         tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
-        (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
+        (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap, lddy % 8 != 0);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
     return HASTE_OK;
 }
@@ -748,10 +764,11 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     int rc = check_bwdf(fn, B, D, F, O, G, dtype, workspace, workspace_bytes, &p);
     if (rc != HASTE_OK) return rc;
     HASTE_CHECK_ARG(idx && W && dY, "%s: null pointer", fn);
-    HASTE_CHECK_ARG(lddy >= O && lddy % 8 == 0,
-                    "%s: lddy must be >= O and a multiple of 8 (lddy=%lld O=%lld)", fn,
-                    (long long)lddy, (long long)O);
-    HASTE_CHECK_ARG(aligned16(W) && aligned16(dY), "%s: W and dY must be 16-byte aligned", fn);
+    HASTE_CHECK_ARG(lddy >= O && (lddy % 8 == 0 || O >= 8),
+                    "%s: lddy must be >= O, and a multiple of 8 when O < 8 (lddy=%lld O=%lld)",
+                    fn, (long long)lddy, (long long)O);
+    HASTE_CHECK_ARG(aligned16(W) && (reinterpret_cast<uintptr_t>(dY) & 1) == 0,
+                    "%s: W must be 16-byte aligned and dY 2-byte aligned", fn);
     HASTE_CHECK_ARG(plan_ready >= 0 && plan_ready <= 2, "%s: plan_ready must be 0, 1 or 2 (got %d)",
                     fn, (int)plan_ready);
     char* base = static_cast<char*>(workspace);
@@ -812,6 +829,19 @@ extern "C" int64_t haste_ffi_bwd_features_workspace_size(int64_t B, int64_t D, i
     if (rc != HASTE_OK) return rc;
     const haste::BwdFPlan p = haste::make_plan(B, D, F, O, G);
     return p.prep_bytes + p.ws_bytes;
+}
+
+extern "C" int haste_ffi_bwd_features_config(int64_t B, int64_t D, int64_t F, int64_t O,
+                                             int64_t G, int32_t dtype, int64_t* cfg) {
+    int rc = haste::check_ffi_shape("haste_ffi_bwd_features_config", B, D, F, O, G, dtype);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(cfg != nullptr, "haste_ffi_bwd_features_config: null pointer");
+    const haste::BwdFPlan p = haste::make_plan(B, D, F, O, G);
+    cfg[0] = p.BT;
+    cfg[1] = p.RT;
+    cfg[2] = p.ndr;
+    cfg[3] = p.S;
+    return HASTE_OK;
 }
 
 extern "C" int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace,

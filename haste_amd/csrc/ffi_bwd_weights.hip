@@ -108,7 +108,8 @@ template <typename T, int G, int FP, bool SGD, bool YNT>
 __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_bwd_w_kernel(
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
     const uint16_t* __restrict__ dY, int64_t lddy, void* __restrict__ dW, int dW_dtype,
-    void* __restrict__ dbias, int dbias_dtype, int B, int D, int F, int64_t O, SgdArgs sg) {
+    void* __restrict__ dbias, int dbias_dtype, int B, int D, int F, int64_t O, int yshort,
+    SgdArgs sg) {
     using C = BwdWCfg<G, FP>;
     constexpr int MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SP = C::SP, PR = C::PR;
     __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
@@ -142,8 +143,10 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     // dY chunk c (rows c*64 ..) -> registers; rows >= B and labels >= O read as
     // zero (labels of a partial 8-label piece are masked when stashed).  An
     // access that crosses the end of a resource reads as zero as a whole, so the
-    // resource covers the last row up to the 8-label piece boundary (inside the
-    // row: lddy is a multiple of 8 and >= O).
+    // resource covers a row up to the 8-label piece boundary: inside the row
+    // when lddy >= O is a multiple of 8, else inside the next row.  dY's last
+    // row may end at label O (yshort): there the resource ends at O and the
+    // piece that straddles O is loaded early and shifted back (shift_down16).
     int pr[PPT], pcc[PPT];
 #pragma unroll
     for (int q = 0; q < PPT; ++q) {
@@ -151,23 +154,35 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
         pr[q] = p / (G / 8);
         pcc[q] = (p % (G / 8)) * 8;
     }
+    // elements piece q of chunk c is loaded early by (0 unless it straddles O in row B-1)
+    auto tail_shift = [&](int c, int q) -> int {
+        const int over = pcc[q] + 8 - nl;  // > 0 only in the last group
+        return (yshort && over > 0 && over < 8 && c * kKC + pr[q] == B - 1) ? over : 0;
+    };
+    // (the resource starts at the chunk's first row, not at label l0, so that an
+    // early load of the last group stays inside it: l0 + pcc - sh >= O - 8 >= 0)
     auto fetch = [&](int c, u32x4 (&v)[PPT]) {
         const int b0 = c * kKC;
-        const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy + l0,
-                                    ((int64_t)(std::min(kKC, B - b0) - 1) * lddy + (nl + 7) / 8 * 8) * 2);
+        const int rows = std::min(kKC, B - b0);
+        const int64_t lend = l0 + ((yshort && b0 + rows == B) ? nl : (nl + 7) / 8 * 8);
+        const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy, ((int64_t)(rows - 1) * lddy + lend) * 2);
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
             const bool ok = tid + q * kThreads < C::PIECES && pcc[q] < nl;
+            const int sh = tail_shift(c, q);
             v[q] = __builtin_amdgcn_raw_buffer_load_b128(
-                yr, ok ? (uint32_t)((int64_t)pr[q] * lddy + pcc[q]) * 2 : kOOB, 0, YNT ? kLoadNT : 0);
+                yr, ok ? (uint32_t)((int64_t)pr[q] * lddy + l0 + pcc[q] - sh) * 2 : kOOB, 0,
+                YNT ? kLoadNT : 0);
         }
     };
-    auto stash = [&](int buf, const u32x4 (&v)[PPT]) {
+    auto stash = [&](int c, int buf, const u32x4 (&v)[PPT]) {
 #pragma unroll
         for (int q = 0; q < PPT; ++q) {
-            if (tid + q * kThreads < C::PIECES)
+            if (tid + q * kThreads < C::PIECES) {
+                const int sh = tail_shift(c, q);
                 *reinterpret_cast<u32x4*>(&Ys[buf][pr[q] * RB + pcc[q] * 2]) =
-                    keep_first(v[q], nl - pcc[q]);
+                    keep_first(sh ? shift_down16(v[q], sh) : v[q], nl - pcc[q]);
+            }
         }
     };
     // A fragments of chunk c: 8 consecutive batch entries of each slot row
@@ -230,7 +245,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     fetch(0, yr[0]);
     fetch(1, yr[1]);
     fetch_a(0, ar[0]);
-    stash(0, yr[0]);
+    stash(0, 0, yr[0]);
     fetch(2, yr[0]);
     __syncthreads();
 
@@ -260,7 +275,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                 }
             }
         }
-        stash(1 - P, yr[1 - P]);  // chunk c + 1 (zeros past the end)
+        stash(c + 1, 1 - P, yr[1 - P]);  // chunk c + 1 (zeros past the end)
         fetch(c + 3, yr[1 - P]);
         __syncthreads();
     };
@@ -435,14 +450,15 @@ int launch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* 
            void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B, int64_t D, int64_t F,
            int64_t O, const SgdArgs& sg, hipStream_t st) {
     const int64_t Gc = ceil_div(O, G);
-    if (Gc > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes || (int64_t)kKC * lddy * 2 > kMaxRsrcBytes ||
-        (int64_t)G * F * 4 > kMaxRsrcBytes) {
+    if (Gc > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes ||
+        ((int64_t)kKC * lddy + 8) * 2 > kMaxRsrcBytes || (int64_t)G * F * 4 > kMaxRsrcBytes) {
         set_error("haste_ffi_bwd_weights: problem too large (Gc %lld, lddy %lld, D*ldx %lld)",
                   (long long)Gc, (long long)lddy, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
     ffi_bwd_w_kernel<T, G, FP, SGD, YNT><<<dim3((unsigned)Gc), dim3(kThreads), 0, st>>>(
-        idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, (int)B, (int)D, (int)F, O, sg);
+        idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, (int)B, (int)D, (int)F, O,
+        lddy % 8 != 0, sg);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_weights");
     return HASTE_OK;
 }
@@ -496,10 +512,11 @@ int check_bwdw(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, 
     HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
                     "%s: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)", fn,
                     (long long)ldx, (long long)B);
-    HASTE_CHECK_ARG(lddy >= O && lddy % 8 == 0,
-                    "%s: lddy must be >= O and a multiple of 8 (lddy=%lld O=%lld)", fn,
-                    (long long)lddy, (long long)O);
-    HASTE_CHECK_ARG(aligned16(xT) && aligned16(dY), "%s: xT and dY must be 16-byte aligned", fn);
+    HASTE_CHECK_ARG(lddy >= O && (lddy % 8 == 0 || O >= 8),
+                    "%s: lddy must be >= O, and a multiple of 8 when O < 8 (lddy=%lld O=%lld)",
+                    fn, (long long)lddy, (long long)O);
+    HASTE_CHECK_ARG(aligned16(xT) && (reinterpret_cast<uintptr_t>(dY) & 1) == 0,
+                    "%s: xT must be 16-byte aligned and dY 2-byte aligned", fn);
     HASTE_CHECK_ARG(dW_dtype == HASTE_DTYPE_F32 || dW_dtype == HASTE_DTYPE_BF16 ||
                         dW_dtype == HASTE_DTYPE_F16,
                     "%s: bad dW dtype %d", fn, (int)dW_dtype);

@@ -359,21 +359,32 @@ int64_t fwd_chunks(int64_t B, int64_t Gc, int64_t* tpc) {
     return ceil_div(ntiles, *tpc);
 }
 
-template <typename T, int G, int FP>
-int launch_fwd(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
-               const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
-               int64_t O, const BceArgs* bce, hipStream_t st) {
+// The host-side limits of launch_fwd: the grid and the 32-bit buffer offsets.
+// haste_ffi_forward_bce checks them before it marks any label bits, so a call
+// that fails here leaves the workspace zero.
+int check_fwd_size(int64_t B, int64_t D, int64_t ldx, int64_t ldo, int64_t O, int64_t G) {
     const int64_t Gc = ceil_div(O, G);
     int64_t tpc = 1;
-    const int64_t nchunks = fwd_chunks(B, Gc, &tpc);
-    const int64_t nlogical = Gc * nchunks;
-    const int64_t grid = 8 * ceil_div(nlogical, 8);
+    const int64_t grid = 8 * ceil_div(Gc * fwd_chunks(B, Gc, &tpc), 8);
     if (grid > 0x7FFFFFFF || (int64_t)kBT * ldo * 2 > kMaxRsrcBytes ||
         D * ldx * 2 > kMaxRsrcBytes) {
         set_error("haste_ffi_forward: problem too large (grid %lld, ldo %lld, D*ldx %lld)",
                   (long long)grid, (long long)ldo, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
+    return HASTE_OK;
+}
+
+template <typename T, int G, int FP>
+int launch_fwd(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
+               const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
+               int64_t O, const BceArgs* bce, hipStream_t st) {
+    const int rc = check_fwd_size(B, D, ldx, ldo, O, G);
+    if (rc != HASTE_OK) return rc;
+    const int64_t Gc = ceil_div(O, G);
+    int64_t tpc = 1;
+    const int64_t nchunks = fwd_chunks(B, Gc, &tpc);
+    const int64_t grid = 8 * ceil_div(Gc * nchunks, 8);
     if (bce != nullptr)
         ffi_fwd_kernel<T, G, FP, true><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
             idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks,
@@ -553,6 +564,8 @@ extern "C" int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t
     HASTE_CHECK_ARG(ws_bytes >= L.bytes,
                     "haste_ffi_forward_bce: workspace too small (%lld < %lld bytes)",
                     (long long)ws_bytes, (long long)L.bytes);
+    rc = haste::check_fwd_size(B, D, ldx, ldo, O, G);
+    if (rc != HASTE_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     auto* ybits = static_cast<uint32_t*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.bits_bytes);

@@ -11,10 +11,9 @@ Semantics kept from the reference:
     (g' = fma(wd, w, g); m' = fma(mu, m, g'); w' = fma(-lr, m' or g', w);
     SR to bf16 with tl.randint(seed, i), or RNE when SR is off);
   * non-contiguous params are updated through a contiguous copy.
-Difference: the fp32 momentum buffer is allocated only once momentum is
-actually used (the reference always allocates it, optim_sr.py:35-44); a
-buffer created later starts at zero, which is what the reference's unused
-buffer holds.
+  * every parameter that requires a gradient gets its fp32 ``momentum_buf``
+    at construction, zero, whether or not momentum is used (optim_sr.py:35-44),
+    so a checkpoint carries the same state keys as the reference's.
 
 Checkpoints: ``state_dict()`` holds each group's current ``seed`` and the fp32
 momentum buffers.  ``load_state_dict`` keeps the buffers in fp32 (torch's
@@ -39,6 +38,10 @@ class SRSgd(Optimizer):
                         use_momentum=use_momentum, stochastic_rounding=stochastic_rounding,
                         seed=seed)
         super().__init__(params, defaults)
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.requires_grad:
+                    self._momentum_buf(p)
 
     def load_state_dict(self, state_dict) -> None:
         # torch casts floating-point state to the parameter's dtype; the momentum

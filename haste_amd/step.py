@@ -10,6 +10,11 @@ and, in ``step``, never leave the chip (the SGD update is applied in the
 epilogue of the weight-gradient kernel; the result is bit-identical to
 ``backward_weights`` followed by ``sgd``), and the grad of the logits ``dY`` is
 an input.
+
+The step keeps the transposed weights of the bwd-features workspace valid
+across steps by the version counter of ``weights``: pass the tensor through
+which the weights are changed (the Parameter itself, not ``.data``, whose
+version counter is separate) so that a change made outside the step is seen.
 """
 from __future__ import annotations
 
@@ -155,11 +160,11 @@ class FFITrainStep:
 
     def _check_dY(self, dY: torch.Tensor, lddy: int) -> None:
         _C.require_device(dY, "dY")
-        if (dY.dtype != torch.bfloat16 or lddy % 8 or lddy < self.O
+        if (dY.dtype != torch.bfloat16 or lddy < self.O or (lddy % 8 and self.O < 8)
                 or dY.numel() < (self.B - 1) * lddy + self.O):
             raise ValueError(f"FFITrainStep: dY must be a bf16 buffer of {self.B} rows of "
-                             f"stride lddy >= {self.O}, lddy % 8 == 0 (got {dY.dtype}, "
-                             f"{dY.numel()} elements, lddy={lddy})")
+                             f"stride lddy >= {self.O} (a multiple of 8 when O < 8; got "
+                             f"{dY.dtype}, {dY.numel()} elements, lddy={lddy})")
 
     def backward_features(self, dY: torch.Tensor, lddy: int) -> None:
         """dX [B, D] bf16 = SR(feature gradient, seed 123) (bindings.py:44-48)."""
@@ -186,7 +191,7 @@ class FFITrainStep:
                   self.D, self.F, self.O, self.G, self.code, _C.stream_of(self.W))
 
     def backward(self, dY: torch.Tensor, lddy: int) -> None:
-        """dY: [B, lddy] bf16 buffer (lddy % 8 == 0) holding grad of the logits."""
+        """dY: [B, lddy] bf16 buffer holding grad of the logits (the last row may end at O)."""
         self.backward_features(dY, lddy)
         self.backward_weights(dY, lddy)
 
@@ -198,6 +203,7 @@ class FFITrainStep:
         self._sgd_args[-2] = self.seed
         self._sgd_args[-1] = _C.stream_of(self.W)
         _lib.call("haste_sgd_sr_step_multi", *self._sgd_args)
+        torch.autograd.graph.increment_version(self.W)
         self._wt_version = None  # W changed, W^T not refreshed
         self.seed += 1
 
@@ -217,7 +223,9 @@ class FFITrainStep:
                   _lib.DTYPE_F32, None, _lib.DTYPE_F32, self.lr, self.wd, 0.0, 0, 1, self.seed,
                   self.ws.data_ptr() if plan_ok else None, self.ws.numel() if plan_ok else 0,
                   self.B, self.D, self.F, self.O, self.G, self.code, _C.stream_of(self.W))
-        # the kernel writes W in place (torch's version counter does not move)
+        # the kernel wrote W in place: move torch's version counter, as an in-place
+        # torch op would, and record that the workspace holds W^T of this version
+        torch.autograd.graph.increment_version(self.W)
         self._wt_version = self.W._version if plan_ok else None
         self.seed += 1
 

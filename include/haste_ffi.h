@@ -13,8 +13,10 @@
  *   xT    [D, ldx]        features transposed, columns 0..B-1 used, ldx % 8 == 0
  *   W     [O, F]          weights
  *   out   [B, ldo]        logits, columns 0..O-1 written, ldo % 8 == 0
- *   dY    [B, lddy]       grad of logits, lddy % 8 == 0
- * Element types are HASTE_DTYPE_* codes; 16-bit tensors must be 16-byte aligned.
+ *   dY    [B, lddy]       grad of logits, lddy >= O; any lddy when O >= 8 (else a
+ *                         multiple of 8), 2-byte aligned.  When lddy % 8 != 0 the
+ *                         last row need only hold O elements (a [B, O] tensor)
+ * Element types are HASTE_DTYPE_* codes; other 16-bit tensors must be 16-byte aligned.
  * Supported: dtype bf16 or f16; G in {16, 32, 64, 128}; F % 16 == 0, 16 <= F <= 256.
  * The reference envelope is G in {16,32,64}, F <= 128 (F <= 256 for G = 16);
  * this library accepts the wider set.
@@ -91,6 +93,15 @@ int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t ldx, const
  */
 int64_t haste_ffi_bwd_features_workspace_size(int64_t B, int64_t D, int64_t F, int64_t O,
                                               int64_t G, int32_t dtype);
+
+/*
+ * How haste_ffi_bwd_features splits the work for these sizes (host-only, no
+ * GPU call): cfg[0] = batch columns per workgroup, cfg[1] = W^T tiles of 16
+ * positions per LDS ring round, cfg[2] = feature ranges, cfg[3] = group
+ * slices.  For tuning and tests; no counterpart in the reference.
+ */
+int haste_ffi_bwd_features_config(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+                                  int32_t dtype, int64_t* cfg);
 
 /*
  * Writes the index-dependent part of the bwd-features workspace (the "plan":

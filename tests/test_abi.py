@@ -126,3 +126,18 @@ def test_bwd_weights_sgd_rejects_bad_arguments():
     assert _bwdw_sgd(G=48) == _lib.HASTE_ERR_UNSUPPORTED
     assert _bwdw_sgd(lddy=4092) == _lib.HASTE_ERR_INVALID_ARG
     assert _bwdw_sgd(ws=64, ws_bytes=16) == _lib.HASTE_ERR_INVALID_ARG  # workspace too small
+
+
+def test_ring_cases_reach_every_bwd_features_build():
+    """tests/bwdf_cases.RING_CASES maps onto every (G, BT, RT) build of the
+    bwd-features main kernel, each with more than one feature range, so the GPU
+    parity test over them covers every build (no GPU call: the plan's shape
+    is computed on the host)."""
+    from bwdf_cases import RING_CASES, all_variants, kernel_config
+
+    seen = set()
+    for B, D, O, G, F, _ in RING_CASES:
+        BT, RT, ndr, _S = kernel_config(_lib.lib(), B, D, O, G, F)
+        assert ndr >= 2, (B, D, O, G, F)
+        seen.add((G, BT, RT))
+    assert seen == all_variants()

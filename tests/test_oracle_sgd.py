@@ -1,5 +1,10 @@
-"""Pins the oracle's fused SGD step (shared_ffi/sr_triton.py:109-168) by an
-exact-rational evaluation of the FMA contract on small arrays."""
+"""Pins the oracle's fused SGD step (shared_ffi/sr_triton.py:109-168):
+
+* torch.optim.SGD's update on inputs where every operation is exact, which fixes
+  the terms, their signs and their order independently of the oracle;
+* hand-derived closed forms;
+* an exact-rational evaluation of the FMA contraction on general inputs, which
+  fixes the rounding (where fused and unfused evaluation differ)."""
 from fractions import Fraction
 
 import numpy as np
@@ -101,3 +106,66 @@ def test_seed_changes_rounding(oracle_mod):
     # every output is one of the two bf16 neighbours of the RNE result
     c, _ = oracle_mod.sgd_sr_step(w, g, None, 0.05, 1e-4, 0.0, False, False, seed=0)
     assert np.all(np.abs(a.astype(np.int32) - c.astype(np.int32)) <= 1)
+
+
+# ---- independent pins of the update's terms, signs and order ----------------
+# torch.optim.SGD (dampening 0, no Nesterov) performs d = g + wd*p;
+# buf = mu*buf + d; p = p - lr*buf.  On dyadic inputs with short numerators
+# every product and sum is exact in fp32 (so fusing or not cannot matter) and
+# every result is exact in bf16 (so RNE and SR are the identity): the oracle
+# must then equal torch's fp32 update bit for bit.  A swapped sign, a weight
+# decay applied to the wrong operand or momentum applied in the wrong order
+# changes the value.
+
+def _exact_inputs(n, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.integers(-15, 16, n).astype(np.float32) / 16      # a / 16
+    g = rng.integers(-31, 32, n).astype(np.float32) / 64      # b / 64
+    m = rng.integers(-31, 32, n).astype(np.float32) / 32      # c / 32
+    return w, g, m
+
+
+@pytest.mark.parametrize("use_mom", [False, True])
+@pytest.mark.parametrize("do_sr", [False, True])
+def test_sgd_equals_torch_optim_sgd_on_exact_inputs(oracle_mod, use_mom, do_sr):
+    import torch
+
+    lr, wd, mu = 0.5, 0.25, 0.5
+    w, g, m = _exact_inputs(4096, seed=11 + use_mom)
+    p = torch.nn.Parameter(torch.from_numpy(w.copy()))
+    opt = torch.optim.SGD([p], lr=lr, momentum=mu if use_mom else 0.0, dampening=0.0,
+                          weight_decay=wd)
+    p.grad = torch.from_numpy(g.copy())
+    if use_mom:
+        opt.state[p]["momentum_buffer"] = torch.from_numpy(m.copy())
+    opt.step()
+    exp = p.detach().numpy()
+    w_bits = f32_to_bf16_bits(w)
+    assert np.array_equal(bf16_bits_to_f32(w_bits), w)  # inputs exact in bf16
+    got, gm = oracle_mod.sgd_sr_step(w_bits, g, m.copy() if use_mom else None, lr, wd, mu,
+                                     use_mom, do_sr, seed=42)
+    assert np.array_equal(bf16_bits_to_f32(got), exp)
+    if use_mom:
+        assert np.array_equal(gm, opt.state[p]["momentum_buffer"].numpy())
+
+
+def test_sgd_closed_forms(oracle_mod):
+    """Hand-derived single-element updates (all values exact in bf16)."""
+    def one(w, g, m, lr, wd, mu, use_mom):
+        wb = f32_to_bf16_bits(np.array([w], np.float32))
+        out, mo = oracle_mod.sgd_sr_step(wb, np.array([g], np.float32),
+                                         np.array([m], np.float32) if use_mom else None,
+                                         lr, wd, mu, use_mom, False, seed=0)
+        return float(bf16_bits_to_f32(out)[0]), (None if mo is None else float(mo[0]))
+
+    # w' = w - lr*(g + wd*w) = 1 - 0.5*(0.5 + 0.25) = 0.625
+    assert one(1.0, 0.5, 0.0, 0.5, 0.25, 0.0, False) == (0.625, None)
+    # m' = mu*m + (g + wd*w) = 0.25 + 0.75 = 1; w' = 1 - 0.5*1 = 0.5
+    assert one(1.0, 0.5, 0.5, 0.5, 0.25, 0.5, True) == (0.5, 1.0)
+    # the decay term scales w, not g: w = 2, g = 0 -> w' = 2 - 0.5*0.5 = 1.75
+    assert one(2.0, 0.0, 0.0, 0.5, 0.25, 0.0, False) == (1.75, None)
+    # a negative gradient raises the weight: w' = 0 - 0.25*(-1) = 0.25
+    assert one(0.0, -1.0, 0.0, 0.25, 0.0, 0.0, False) == (0.25, None)
+    # momentum scales the old buffer, not the new gradient: m = 1, g = 1, mu = 0.25
+    # -> m' = 1.25, w' = 0 - 1 * 1.25
+    assert one(0.0, 1.0, 1.0, 1.0, 0.0, 0.25, True) == (-1.25, 1.25)

@@ -60,6 +60,29 @@ def test_optimizer_state_keeps_fp32_momentum_and_seed():
     assert mb.dtype == torch.float32 and torch.equal(mb, m)
 
 
+def test_momentum_buffers_always_in_state():
+    """As the reference's SRSgd.__init__ (shared_ffi/optim_sr.py:35-44), every
+    parameter that requires a gradient has a zero fp32 momentum_buf from the
+    start, also with momentum 0, so a checkpoint has the state keys that the
+    reference's step reads unconditionally (optim_sr.py:70)."""
+    p = torch.nn.Parameter(torch.zeros(6, 4, dtype=torch.bfloat16))
+    b = torch.nn.Parameter(torch.zeros(6, dtype=torch.bfloat16))
+    frozen = torch.nn.Parameter(torch.zeros(3), requires_grad=False)
+    opt = SRSgd([p, b, frozen], lr=0.1, momentum=0.0, seed=1)
+    sd = opt.state_dict()
+    assert set(sd["state"]) == {0, 1}
+    for i, t in ((0, p), (1, b)):
+        m = sd["state"][i]["momentum_buf"]
+        assert m.dtype == torch.float32 and m.shape == t.shape and not m.any()
+    # a reference-shaped consumer: every listed parameter's state has the key
+    buf = io.BytesIO()
+    torch.save(sd, buf)
+    buf.seek(0)
+    loaded = torch.load(buf, weights_only=True)
+    for i in loaded["param_groups"][0]["params"][:2]:
+        assert "momentum_buf" in loaded["state"][i]
+
+
 @pytest.mark.gpu
 def test_resume_is_bit_identical(dev):
     """Train, checkpoint layer + optimizer, keep training; a fresh layer and
