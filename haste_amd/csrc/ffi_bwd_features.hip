@@ -310,12 +310,16 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy,
                                 ((int64_t)(rows - 1) * lddy +
                                  ((yshort && b0 + rows == B) ? O : (O + 7) / 8 * 8)) * 2);
-    const bool last_row = yshort && b0 + wave * 16 + col == B - 1;
-    // elements the lane's piece ks of group g is loaded early by (0 unless it
-    // straddles O in dY's last row)
+    // elements the lane's piece ks of group g is loaded early by: 0 unless it
+    // straddles O in dY's last row (then g is the last group)
+    int sh_last[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int64_t over = (Gc - 1) * G + kofs + ks * 32 + 8 - O;
+        sh_last[ks] = (yshort && b0 + wave * 16 + col == B - 1 && over > 0 && over < 8) ? (int)over : 0;
+    }
     auto tail_shift = [&](int64_t g, int ks) __attribute__((always_inline)) -> int {
-        const int64_t over = g * G + kofs + ks * 32 + 8 - O;
-        return (last_row && over > 0 && over < 8) ? (int)over : 0;
+        return g == Gc - 1 ? sh_last[ks] : 0;
     };
     // byte offset of the lane's first label in the tile (32 bits: the tile's
     // resource spans at most kMaxRsrcBytes; g * G * 2 < 2 * lddy for real groups)
