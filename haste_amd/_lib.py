@@ -48,6 +48,8 @@ SIGNATURES = {
     "haste_ffi_forward_bce_workspace_size": (_I64, [_I64, _I64, _I64]),
     "haste_ffi_forward_bce": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P, _P,
                                              _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
+    "haste_ffi_forward_bce_noalloc": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P,
+                                                     _P, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
     "haste_ffi_bwd_features_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I32]),
     "haste_ffi_bwd_features_config": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I32, _P]),
     "haste_ffi_bwd_features_plan": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64,

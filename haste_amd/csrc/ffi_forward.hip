@@ -25,6 +25,7 @@
 // result rounded to nearest even (as dump_and_store_tile,
 // shared_ffi/ffi_forward_kernels.cu:85-101).
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -540,52 +541,163 @@ extern "C" int64_t haste_ffi_forward_bce_workspace_size(int64_t B, int64_t O, in
     return haste::bce_layout(B, O, G).bytes;
 }
 
+namespace haste {
+namespace {
+
+// Launches of haste_ffi_forward_bce on a checked workspace: label bits, the
+// forward with the BCE epilogue, the loss sum (which clears the label bits).
+int run_forward_bce(const int32_t* idx, const void* xT, int64_t ldx, const void* W,
+                    const void* bias, const int32_t* labels, int64_t nnz, void* dY, int64_t ldo,
+                    void* logits, float* loss, void* workspace, const BceLayout& L, int64_t B,
+                    int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype, hipStream_t st) {
+    auto* ybits = static_cast<uint32_t*>(workspace);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.bits_bytes);
+    const int64_t lblocks = (nnz + 255) / 256;
+    if (lblocks > 0) {
+        label_bits_kernel<<<dim3((unsigned)lblocks), dim3(256), 0, st>>>(labels, nnz, ybits,
+                                                                          L.ldyw, (int)B, O);
+        HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
+    }
+    const BceArgs bce{ybits, L.ldyw, static_cast<uint16_t*>(logits), part};
+    auto* x = static_cast<const uint16_t*>(xT);
+    auto* w = static_cast<const uint16_t*>(W);
+    auto* bb = static_cast<const uint16_t*>(bias);
+    auto* o = static_cast<uint16_t*>(dY);
+    int rc = dtype == HASTE_DTYPE_BF16
+                 ? dispatch_g<BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st)
+                 : dispatch_g<F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st);
+    if (rc != HASTE_OK) return rc;
+    loss_sum_kernel<<<dim3(1), dim3(256), 0, st>>>(part, L.nparts, loss, labels, nnz, ybits,
+                                                   L.ldyw, (int)B, O);
+    HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
+    return HASTE_OK;
+}
+
+// Host-side checks of haste_ffi_forward_bce[_noalloc] except the workspace.
+int check_forward_bce(const char* fn, const int32_t* idx, const void* xT, int64_t ldx,
+                      const void* W, const int32_t* labels, int64_t nnz, const void* dY,
+                      int64_t ldo, const void* logits, const float* loss, int64_t B, int64_t D,
+                      int64_t F, int64_t O, int64_t G, int32_t dtype) {
+    int rc = check_ffi_shape(fn, B, D, F, O, G, dtype);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(idx && xT && W && dY && loss && (labels || nnz == 0) && nnz >= 0,
+                    "%s: null pointer or negative nnz", fn);
+    HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
+                    "%s: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)", fn,
+                    (long long)ldx, (long long)B);
+    HASTE_CHECK_ARG(ldo >= O && ldo % 8 == 0,
+                    "%s: ldo must be >= O and a multiple of 8 (ldo=%lld O=%lld)", fn,
+                    (long long)ldo, (long long)O);
+    HASTE_CHECK_ARG(aligned16(xT) && aligned16(W) && aligned16(dY) &&
+                        (logits == nullptr || aligned16(logits)),
+                    "%s: xT, W, dY and logits must be 16-byte aligned", fn);
+    return check_fwd_size(B, D, ldx, ldo, O, G);
+}
+
+// Zeroes n16 16-byte words (a fill kernel: no memset node, so a caller may
+// capture the call in a HIP graph).
+__global__ __launch_bounds__(256) void zero16_kernel(u32x4* __restrict__ p, int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+        p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+}  // namespace haste
+
+// The workspace of haste_ffi_forward_bce_noalloc: one array per GPU (every
+// device that runs the library holds its own copy, at its own address, until
+// the process ends).  Host code never passes this name to a kernel: it is a
+// host-side stand-in, not the device address; the per-device address comes
+// from hipGetSymbolAddress below.
+static __device__ __align__(256) uint8_t scratch[HASTE_FORWARD_BCE_SCRATCH_BYTES];
+
+namespace haste {
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the device of stream st (looked up once per
+// device, with that device current).
+int scratch_for(hipStream_t st, void** out) {
+    int dev = -1;
+    if (st != nullptr)
+        HASTE_HIP_TRY(hipStreamGetDevice(st, &dev), "haste_ffi_forward_bce_noalloc: stream device");
+    else
+        HASTE_HIP_TRY(hipGetDevice(&dev), "haste_ffi_forward_bce_noalloc: current device");
+    HASTE_CHECK_ARG(dev >= 0 && dev < kMaxDevices,
+                    "haste_ffi_forward_bce_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = -1;
+        HASTE_HIP_TRY(hipGetDevice(&cur), "haste_ffi_forward_bce_noalloc: current device");
+        if (cur != dev) HASTE_HIP_TRY(hipSetDevice(dev), "haste_ffi_forward_bce_noalloc: set device");
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) HASTE_HIP_TRY(hipSetDevice(cur), "haste_ffi_forward_bce_noalloc: set device");
+        HASTE_HIP_TRY(e, "haste_ffi_forward_bce_noalloc: hipGetSymbolAddress(scratch)");
+        HASTE_CHECK_ARG(p != nullptr && aligned16(p),
+                        "haste_ffi_forward_bce_noalloc: bad scratch address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return HASTE_OK;
+}
+
+}  // namespace
+}  // namespace haste
+
 extern "C" int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t ldx,
                                      const void* W, const void* bias, const int32_t* labels,
                                      int64_t nnz, void* dY, int64_t ldo, void* logits,
                                      float* loss, void* workspace, int64_t ws_bytes, int64_t B,
                                      int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype,
                                      void* stream) {
-    int rc = haste::check_ffi_shape("haste_ffi_forward_bce", B, D, F, O, G, dtype);
+    const char* fn = "haste_ffi_forward_bce";
+    int rc = haste::check_forward_bce(fn, idx, xT, ldx, W, labels, nnz, dY, ldo, logits, loss, B,
+                                      D, F, O, G, dtype);
     if (rc != HASTE_OK) return rc;
-    HASTE_CHECK_ARG(idx && xT && W && dY && loss && workspace && (labels || nnz == 0) && nnz >= 0,
-                    "haste_ffi_forward_bce: null pointer or negative nnz");
-    HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
-                    "haste_ffi_forward_bce: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)",
-                    (long long)ldx, (long long)B);
-    HASTE_CHECK_ARG(ldo >= O && ldo % 8 == 0,
-                    "haste_ffi_forward_bce: ldo must be >= O and a multiple of 8 (ldo=%lld O=%lld)",
-                    (long long)ldo, (long long)O);
-    HASTE_CHECK_ARG(haste::aligned16(xT) && haste::aligned16(W) && haste::aligned16(dY) &&
-                        (logits == nullptr || haste::aligned16(logits)) &&
-                        haste::aligned16(workspace),
-                    "haste_ffi_forward_bce: xT, W, dY, logits and workspace must be 16-byte aligned");
+    HASTE_CHECK_ARG(workspace != nullptr && haste::aligned16(workspace),
+                    "%s: workspace must be a 16-byte aligned pointer", fn);
     const haste::BceLayout L = haste::bce_layout(B, O, G);
-    HASTE_CHECK_ARG(ws_bytes >= L.bytes,
-                    "haste_ffi_forward_bce: workspace too small (%lld < %lld bytes)",
+    HASTE_CHECK_ARG(ws_bytes >= L.bytes, "%s: workspace too small (%lld < %lld bytes)", fn,
                     (long long)ws_bytes, (long long)L.bytes);
-    rc = haste::check_fwd_size(B, D, ldx, ldo, O, G);
+    return haste::run_forward_bce(idx, xT, ldx, W, bias, labels, nnz, dY, ldo, logits, loss,
+                                  workspace, L, B, D, F, O, G, dtype,
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int haste_ffi_forward_bce_noalloc(const int32_t* idx, const void* xT, int64_t ldx,
+                                             const void* W, const void* bias,
+                                             const int32_t* labels, int64_t nnz, void* dY,
+                                             int64_t ldo, void* logits, float* loss, int64_t B,
+                                             int64_t D, int64_t F, int64_t O, int64_t G,
+                                             int32_t dtype, void* stream) {
+    const char* fn = "haste_ffi_forward_bce_noalloc";
+    int rc = haste::check_forward_bce(fn, idx, xT, ldx, W, labels, nnz, dY, ldo, logits, loss, B,
+                                      D, F, O, G, dtype);
     if (rc != HASTE_OK) return rc;
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    auto* ybits = static_cast<uint32_t*>(workspace);
-    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.bits_bytes);
-    const int64_t lblocks = (nnz + 255) / 256;
-    if (lblocks > 0) {
-        haste::label_bits_kernel<<<dim3((unsigned)lblocks), dim3(256), 0, st>>>(
-            labels, nnz, ybits, L.ldyw, (int)B, O);
-        HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
+    const haste::BceLayout L = haste::bce_layout(B, O, G);
+    if (L.bytes > HASTE_FORWARD_BCE_SCRATCH_BYTES) {
+        haste::set_error("%s: B = %lld, O = %lld need %lld bytes of scratch, above the "
+                         "library's %lld (use haste_ffi_forward_bce with a workspace)",
+                         fn, (long long)B, (long long)O, (long long)L.bytes,
+                         (long long)HASTE_FORWARD_BCE_SCRATCH_BYTES);
+        return HASTE_ERR_WORKSPACE;
     }
-    const haste::BceArgs bce{ybits, L.ldyw, static_cast<uint16_t*>(logits), part};
-    auto* x = static_cast<const uint16_t*>(xT);
-    auto* w = static_cast<const uint16_t*>(W);
-    auto* bb = static_cast<const uint16_t*>(bias);
-    auto* o = static_cast<uint16_t*>(dY);
-    rc = dtype == HASTE_DTYPE_BF16
-             ? haste::dispatch_g<haste::BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st)
-             : haste::dispatch_g<haste::F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = nullptr;
+    rc = haste::scratch_for(st, &ws);
     if (rc != HASTE_OK) return rc;
-    haste::loss_sum_kernel<<<dim3(1), dim3(256), 0, st>>>(part, L.nparts, loss, labels, nnz,
-                                                          ybits, L.ldyw, (int)B, O);
-    HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
-    return HASTE_OK;
+    // the label bitmap must start at zero; the previous call on this GPU left
+    // its own layout in the scratch, so this call's part is cleared here
+    const int64_t n16 = L.bits_bytes / 16;
+    haste::zero16_kernel<<<dim3((unsigned)std::min<int64_t>(haste::ceil_div(n16, 256), 2048)),
+                           dim3(256), 0, st>>>(static_cast<haste::u32x4*>(ws), n16);
+    HASTE_CHECK_LAUNCH(fn);
+    return haste::run_forward_bce(idx, xT, ldx, W, bias, labels, nnz, dY, ldo, logits, loss, ws,
+                                  L, B, D, F, O, G, dtype, st);
 }

@@ -88,6 +88,26 @@ int haste_ffi_forward_bce(const int32_t* idx, const void* xT, int64_t ldx, const
                           int64_t G, int32_t dtype, void* stream);
 
 /*
+ * haste_ffi_forward_bce that allocates nothing and takes no workspace: the
+ * workspace is the library's own device scratch array, HASTE_FORWARD_BCE_SCRATCH_BYTES
+ * (64 MiB) on every GPU the library runs on, held until the process ends.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc); no counterpart in the
+ * reference.  Shapes whose haste_ffi_forward_bce_workspace_size exceeds the
+ * scratch are rejected with HASTE_ERR_WORKSPACE (BASELINE configs 0-3 fit;
+ * config 4's 384 MB label bitmap does not).  Results are bit-identical to
+ * haste_ffi_forward_bce.  All calls on one GPU share its scratch, so calls that
+ * overlap in time on one GPU (on different streams) race; calls on one stream
+ * are ordered.  Each call clears the part of the scratch it needs (a fill
+ * kernel, no memset node).
+ */
+#define HASTE_FORWARD_BCE_SCRATCH_BYTES (64ll << 20)
+int haste_ffi_forward_bce_noalloc(const int32_t* idx, const void* xT, int64_t ldx, const void* W,
+                                  const void* bias, const int32_t* labels, int64_t nnz, void* dY,
+                                  int64_t ldo, void* logits, float* loss, int64_t B, int64_t D,
+                                  int64_t F, int64_t O, int64_t G, int32_t dtype, void* stream);
+
+/*
  * Workspace bytes needed by haste_ffi_bwd_features / haste_ffi_bwd_features_sr.
  * Returns a negative HASTE_ERR_* code for unsupported shapes.
  */

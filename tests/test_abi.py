@@ -141,3 +141,18 @@ def test_ring_cases_reach_every_bwd_features_build():
         assert ndr >= 2, (B, D, O, G, F)
         seen.add((G, BT, RT))
     assert seen == all_variants()
+
+
+def test_forward_bce_noalloc_rejects_shapes_beyond_its_scratch():
+    """The no-allocation forward+loss refuses, before any HIP call, a shape whose
+    workspace exceeds the library's fixed per-GPU scratch (64 MiB): BASELINE
+    config 4's label bitmap alone is 384 MB."""
+    L = _lib.lib()
+    B, D, F, O, G = 1024, 768, 128, 3_000_000, 128
+    assert L.haste_ffi_forward_bce_workspace_size(B, O, G) > 64 << 20
+    rc = L.haste_ffi_forward_bce_noalloc(16, 16, 1024, 16, None, 16, 10, 16, 3000064, None, 16,
+                                         B, D, F, O, G, _lib.DTYPE_BF16, None)
+    assert rc == _lib.HASTE_ERR_WORKSPACE
+    assert "scratch" in _lib.last_error()
+    # config 2 fits
+    assert L.haste_ffi_forward_bce_workspace_size(512, 670091, 64) <= 64 << 20
