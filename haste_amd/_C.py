@@ -67,13 +67,15 @@ def rows_aligned(t: torch.Tensor) -> Tuple[torch.Tensor, int]:
 
 
 def grad_rows(t: torch.Tensor) -> Tuple[torch.Tensor, int]:
-    """(t2, ld) for a grad-of-logits matrix [B, O] read by the backward kernels:
-    any row stride works (rows may start on 2-byte boundaries), so ``t`` is used
-    in place when its columns are contiguous; it is copied only otherwise, or
-    when O < 8 and the row stride is not a multiple of 8."""
+    """(t2, ld) for the grad of the logits [B, O] handed to a backward: used in
+    place when its columns are contiguous (any row stride and alignment; rows
+    that do not start on 16-byte boundaries take the kernels' two-chunk loads,
+    which cost about what a realigning copy would, without the copy's buffer),
+    copied into aligned rows otherwise or when O < 16."""
     assert t.dim() == 2
     if (t.stride(1) == 1 or t.shape[1] == 1) and t.stride(0) >= t.shape[1] and \
-            t.data_ptr() % 2 == 0 and (t.shape[1] >= 8 or t.stride(0) % 8 == 0):
+            t.data_ptr() % 2 == 0 and (t.shape[1] >= 16 or
+                                        (t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0)):
         return t, t.stride(0)
     return rows_aligned(t)
 
@@ -117,7 +119,8 @@ def ffi_forward_cuda(locations: torch.Tensor, features: torch.Tensor, weights: t
                      bias: Optional[torch.Tensor] = None, B: int = None, H: int = None,
                      FANIN: int = None, L: int = None, gsize: int = 32) -> torch.Tensor:
     """Grouped FFI forward.  ``features`` is X^T [H, B]; returns logits [B, L]
-    as a view of a [B, ceil8(L)] buffer (as the reference)."""
+    as a view of a [B, ceil64(L)] buffer (the reference's view is of a
+    [B, ceil8(L)] buffer; the values and the view's shape are the same)."""
     require_device(features, "features")
     require_device(weights, "weights")
     _check_sizes(features, weights, B, H, FANIN, L)
@@ -132,7 +135,9 @@ def ffi_forward_cuda(locations: torch.Tensor, features: torch.Tensor, weights: t
         bias = bias.contiguous()
     xT, ldx = rows_aligned(features)
     W = weights.contiguous()
-    L_pad = round8(L)
+    # rows padded to 128-byte lines (the reference pads to 8 labels): a group's
+    # logit row segment is then one line, written whole
+    L_pad = round64(L)
     out = torch.empty(B, L_pad, dtype=features.dtype, device=features.device)
     _lib.call("haste_ffi_forward", locations.data_ptr(), xT.data_ptr(), ldx, W.data_ptr(),
               None if bias is None else bias.data_ptr(), out.data_ptr(), L_pad, B, H, FANIN, L,

@@ -148,10 +148,10 @@ class HeadTailFFIFunction(torch.autograd.Function):
     """torch.cat((head(x_head), ffi(x_tail)), dim=1) of the head/tail split model
     (src/model.py:227-232,245-248: a dense nn.Linear head and an FFI tail), built
     in one [B, H + O] buffer: the FFI kernel writes the tail logits in place (the
-    view starts at the column that puts the tail's rows on 16-byte boundaries)
-    and the backward reads the tail's columns of grad_output in place, so the
-    B x O tail is never copied.  Values are those of
-    the torch.cat formulation: the same head op (F.linear) and FFI kernels."""
+    view starts at the column that puts the tail's rows on 128-byte lines), so
+    the forward never copies the B x O tail, and the backward reads the tail's
+    columns of grad_output in place.  Values are those of the torch.cat
+    formulation: the same head op (F.linear) and FFI kernels."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
@@ -167,8 +167,8 @@ class HeadTailFFIFunction(torch.autograd.Function):
         H = head_weight.shape[0]
         dt = x_tail.dtype
         head = torch.nn.functional.linear(x_head, head_weight, head_bias).to(dt)
-        s0 = (8 - H % 8) % 8                       # tail columns start on a multiple of 8
-        ld = _C.round8(s0 + H + O)
+        s0 = (64 - H % 64) % 64                    # tail rows start on 128-byte lines
+        ld = _C.round64(s0 + H + O)
         buf = torch.empty(B, ld, dtype=dt, device=x_tail.device)
         out = buf[:, s0: s0 + H + O]
         out[:, :H].copy_(head)

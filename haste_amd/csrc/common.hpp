@@ -259,6 +259,20 @@ __device__ __forceinline__ u32x4 shift_down16(u32x4 v, int sh) {
                  __builtin_amdgcn_alignbyte(w3, w2, bs), __builtin_amdgcn_alignbyte(0u, w3, bs)};
 }
 
+// Bytes mb .. mb+15 of the 32 bytes a || b (mb even, per lane, in [0, 14]): an
+// 8-element piece that starts mb bytes into the aligned chunk a.
+__device__ __forceinline__ u32x4 shift_pair16(u32x4 a, u32x4 b, uint32_t mb) {
+    const uint32_t ws = mb >> 2;
+    const uint32_t x0 = ws == 0 ? a[0] : ws == 1 ? a[1] : ws == 2 ? a[2] : a[3];
+    const uint32_t x1 = ws == 0 ? a[1] : ws == 1 ? a[2] : ws == 2 ? a[3] : b[0];
+    const uint32_t x2 = ws == 0 ? a[2] : ws == 1 ? a[3] : ws == 2 ? b[0] : b[1];
+    const uint32_t x3 = ws == 0 ? a[3] : ws == 1 ? b[0] : ws == 2 ? b[1] : b[2];
+    const uint32_t x4 = ws == 0 ? b[0] : ws == 1 ? b[1] : ws == 2 ? b[2] : b[3];
+    const uint32_t bs = mb & 3u;
+    return u32x4{__builtin_amdgcn_alignbyte(x1, x0, bs), __builtin_amdgcn_alignbyte(x2, x1, bs),
+                 __builtin_amdgcn_alignbyte(x3, x2, bs), __builtin_amdgcn_alignbyte(x4, x3, bs)};
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4 of
 // the 8-byte rows addressed by lanes 4k + i/4 (k = 0..3) as its element k.
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));

@@ -37,7 +37,7 @@
 
 #include <type_traits>
 
-#include "bwdf_plan.hpp"
+#include "bwdf_main.hpp"
 
 
 namespace haste {
@@ -227,422 +227,6 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
     }
 }
 
-// --------------------------------------------------------------- main ------
-// A workgroup owns (group slice s, feature range r, batch tile of BT = 16*WAVES
-// columns) and keeps dXT[range, tile] as an fp32 partial in LDS.  Wave w owns
-// batch rows [16w, 16w+16) of the tile, so no two waves touch the same LDS
-// word of the partial.  Per group:
-//  - the group's W^T tiles for the range (and the partial-row offsets of their
-//    positions) are staged once into a double-buffered LDS ring, shared by all
-//    waves: each thread copies 16-byte chunks loaded two groups ahead;
-//  - each wave multiplies its dY rows (16 x G, loaded one group ahead) with
-//    the tiles (MFMA, M = batch rows, N = 16 positions, K = labels); a lane then
-//    holds four consecutive batch values of one position and adds them into
-//    the partial row of the position's feature with one 16-byte read and one
-//    16-byte write.  A layer-1 tile (the second rows of duplicated indices)
-//    shares its positions' features with the layer-0 tile it pairs with, so
-//    its products are added to that tile's before the update.  Within a layer
-//    the tiles' features are distinct, so all reads of the update are issued
-//    before its writes; a wave's LDS accesses complete in order, so later
-//    groups see the earlier writes.  Padding positions add into trash rows
-//    that are never read.
-//  - one barrier per group publishes the next group's ring buffer.
-// Ranges holding more than RT tiles in a group process the rest in further
-// rounds staged synchronously (rare: a range's share of F is usually ~F/ndr),
-// layer by layer.
-template <int G, int WAVES, int RT_>
-struct BwdFCfg {
-    static constexpr int KS = G >= 32 ? G / 32 : 1;  // MFMA k-steps over labels
-    static constexpr int BT = 16 * WAVES;            // batch columns per workgroup
-    static constexpr int AS = acc_stride(BT);
-    static constexpr int RT = RT_;
-    static constexpr int RB = ring_row_bytes(G);
-    static constexpr int RING = RT * 16 * RB;        // bytes per ring buffer
-    static constexpr int THREADS = 64 * WAVES;
-    static constexpr int CH = G / 8;                 // 16-byte chunks per W^T row
-    static constexpr int SPT = (RT * 16 * CH + THREADS - 1) / THREADS;  // staged chunks per thread
-    static constexpr int DCMAX = max_dc(BT, G, RT);
-    static_assert(DCMAX > 0, "LDS budget");
-};
-
-template <typename T, int G, int WAVES, int RT_>
-__global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
-    const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
-    const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
-    int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap, int yshort) {
-    using C = BwdFCfg<G, WAVES, RT_>;
-    constexpr int KS = C::KS, BT = C::BT, AS = C::AS, RT = C::RT, RB = C::RB, CH = C::CH;
-    constexpr int SPT = C::SPT, NTH = C::THREADS;
-    __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
-    __shared__ __attribute__((aligned(16))) char ring[2][C::RING];
-    __shared__ int fring[2][RT * 16];
-
-    const int64_t work = xcd_remap(blockIdx.x, (int64_t)S * ndr * nbt);
-    if (work < 0) return;
-    const int bt = (int)(work % nbt);
-    const int r = (int)((work / nbt) % ndr);
-    const int s = (int)(work / ((int64_t)nbt * ndr));
-    const int d_lo = r * Dc;
-    const int dn = min(Dc, D - d_lo);
-    const int64_t g_lo = (int64_t)s * gps;
-    const int64_t g_hi = min<int64_t>(Gc, g_lo + gps);
-    const int ng = (int)(g_hi - g_lo);
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int col = lane & 15;  // A row within the M tile / B column (tile position)
-    const int kq = lane >> 4;   // which 8 of the 32 K elements
-    const bool kq_ok = G >= 32 || kq < 2;
-    const int kofs = kq_ok ? kq * 8 : 0;
-    const int trash_f = (C::DCMAX + (col & (kTrashRows - 1))) * AS * 4;
-
-    for (int i = tid * 4; i < dn * AS; i += NTH * 4)
-        *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // dY of this lane's row (rows >= B read as zero; labels >= O are masked at
-    // use).  A row is read up to the 8-label piece boundary past O: inside the
-    // row when lddy >= O is a multiple of 8, else inside the next row.  dY's
-    // last row may end at label O (yshort): there the resource ends at O and
-    // the piece that straddles O is loaded early and shifted back
-    // (shift_down16; O >= 8 keeps the early load inside the resource).
-    const int b0 = bt * BT;
-    const int rows = min(BT, B - b0);
-    const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy,
-                                ((int64_t)(rows - 1) * lddy +
-                                 ((yshort && b0 + rows == B) ? O : (O + 7) / 8 * 8)) * 2);
-    // elements the lane's piece ks of group g is loaded early by: 0 unless it
-    // straddles O in dY's last row (then g is the last group)
-    int sh_last[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const int64_t over = (Gc - 1) * G + kofs + ks * 32 + 8 - O;
-        sh_last[ks] = (yshort && b0 + wave * 16 + col == B - 1 && over > 0 && over < 8) ? (int)over : 0;
-    }
-    auto tail_shift = [&](int64_t g, int ks) __attribute__((always_inline)) -> int {
-        return g == Gc - 1 ? sh_last[ks] : 0;
-    };
-    // byte offset of the lane's first label in the tile (32 bits: the tile's
-    // resource spans at most kMaxRsrcBytes; g * G * 2 < 2 * lddy for real groups)
-    const uint32_t yoff2 = (uint32_t)(((int64_t)(wave * 16 + col) * lddy + kofs) * 2);
-    auto load_y = [&](int64_t g, u32x4 (&a)[KS]) __attribute__((always_inline)) {
-        const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            a[ks] = buf_load16(yr, kq_ok ? yoff2 + go + ks * 64 - 2 * tail_shift(g, ks) : kOOB);
-    };
-    // labels >= O read as zero: only the last group has any (a uniform branch)
-    auto mask_y = [&](int64_t g, u32x4 (&a)[KS]) __attribute__((always_inline)) {
-        const int64_t rem = O - g * G;  // labels of group g below O
-        if (rem >= G) return;
-        const int nr = (int)max<int64_t>(rem, 0);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int sh = tail_shift(g, ks);
-            if (sh) a[ks] = shift_down16(a[ks], sh);
-            const int nv = nr - (ks * 32 + kofs);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                a[ks][e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
-        }
-    };
-
-    // Tile range of group g_lo + i in range r: tb | tm << 16, te (layer-0 tiles
-    // [tb, tm), layer-1 tiles [tm, te)).  A buffer load, i.e. a vector-memory op
-    // consumed DEPTH iterations later: a scalar load would hold up every later
-    // LDS wait of the wave until it returns; both words are used, so no register
-    // of the load is free for reuse (which would wait for it).  Groups past the
-    // slice read as zero (no tiles), so iterations past them do nothing.
-    const rsrc_t mr = make_rsrc(meta + (g_lo * ndr + r) * kMetaStride,
-                                ((int64_t)(max(ng, 1) - 1) * ndr + 1) * kMetaStride * 4);
-    auto load_meta = [&](int i) __attribute__((always_inline)) -> u32x2 {
-        return buf_load8(mr, i < ng ? (uint32_t)(i * ndr * kMetaStride * 4) : kOOB);
-    };
-    // wave-uniform (SGPR) form
-    auto uniform_meta = [](const u32x2& m) __attribute__((always_inline)) -> u32x2 {
-        return u32x2{(uint32_t)__builtin_amdgcn_readfirstlane((int)m[0]),
-                     (uint32_t)__builtin_amdgcn_readfirstlane((int)m[1])};
-    };
-    // Stage tiles [tb + t0, tb + t0 + RT) of group g_lo + i into registers: W^T
-    // chunks and the positions' partial-row offsets (past the range's tiles:
-    // zero W^T rows, trash offsets).  m is uniform.
-    struct Stage {
-        u32x4 w[SPT];
-        int f;
-    };
-    auto load_stage = [&](int i, u32x2 m, int t0, Stage& st) __attribute__((always_inline)) {
-        // wave-uniform (SGPR) values, so the buffer descriptors below are scalar
-        const int tb = __builtin_amdgcn_readfirstlane((int)(m[0] & 0xFFFF) + t0);
-        const int nrow = __builtin_amdgcn_readfirstlane(max(0, min(RT, (int)m[1] - tb)) * 16);
-        const int64_t row0 = ((g_lo + __builtin_amdgcn_readfirstlane(i)) * Tcap + tb) * 16;
-        const rsrc_t wr = make_rsrc_u32(twt + row0 * G, (uint32_t)nrow * G * 2);
-#pragma unroll
-        for (int k = 0; k < SPT; ++k) {
-            const int c = tid + k * NTH;
-            st.w[k] = buf_load16(wr, c < RT * 16 * CH ? (uint32_t)c * 16 : kOOB);
-        }
-        const rsrc_t fr = make_rsrc_u32(tfeat + row0, (uint32_t)nrow * 4);
-        // used as loaded (rows past nrow are selected away in store_stage): an
-        // operation on a pending load would wait for it here
-        st.f = (int)buf_load4(fr, tid < RT * 16 ? (uint32_t)tid * 4 : kOOB);
-    };
-    auto store_stage = [&](int buf, const Stage& st, u32x2 m, int t0) __attribute__((always_inline)) {
-        const int tb = (int)(m[0] & 0xFFFF) + t0;
-        const int nt = max(0, min(RT, (int)m[1] - tb));  // tiles of this round
-#pragma unroll
-        for (int k = 0; k < SPT; ++k) {
-            const int c = tid + k * NTH;
-            if (c < RT * 16 * CH)
-                *reinterpret_cast<u32x4*>(&ring[buf][(c / CH) * RB + (c % CH) * 16]) = st.w[k];
-        }
-        if (tid < RT * 16) fring[buf][tid] = tid < nt * 16 ? st.f : (C::DCMAX + (tid & (kTrashRows - 1))) * AS * 4;
-    };
-
-    // Batch columns of a partial row are permuted: the 4 columns a lane adds (its
-    // wave's rows 4kq .. 4kq+3) sit at column (kq & 1) * BT/2 + 8*wave + 4*(kq >> 1),
-    // so in one 16-byte RMW instruction the lanes of kq = 0 and 1 are 256 bytes
-    // apart: reads (32 lanes, 512-byte bank window) and writes (16 lanes, 256
-    // bytes) are conflict-free when a tile's features differ mod 16, which the
-    // plan's dealing arranges.
-    auto perm_col = [](int w, int q) { return (q & 1) * (BT / 2) + w * 8 + (q >> 1) * 4; };
-    char* const acc_b = reinterpret_cast<char*>(acc) + perm_col(wave, kq) * 4;
-    // A round is up to RT staged tiles of one group.  Its MFMAs run on all RT
-    // ring tiles (rows past the round's tiles are zero) and the products stay
-    // in registers; the partial update (read, add, write) of a round runs in
-    // the next iteration, in the same code as the next round's MFMAs, so the
-    // products' latency and the update's LDS traffic overlap the next group.
-    struct Round {
-        f32x4 c[RT];  // dY rows x W^T tile t
-        int f[RT];    // partial-row byte offset of the lane's position in tile t
-        int n0, nt;   // uniform: layer-0 tiles and tiles of the round (nt 0: nothing to add)
-    };
-    auto round_counts = [](u32x2 m, int t0, Round& r) __attribute__((always_inline)) {
-        const int tb = (int)(m[0] & 0xFFFF) + t0;
-        r.n0 = max(0, (int)(m[0] >> 16) - tb);
-        r.nt = max(0, min(RT, (int)m[1] - tb));
-    };
-    // ring and offset reads of the round staged in ring[buf]
-    auto read_round = [&](int buf, u32x4 (&bf)[RT][KS], Round& r) __attribute__((always_inline)) {
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            r.f[t] = fring[buf][t * 16 + col];
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                bf[t][ks] = *reinterpret_cast<const u32x4*>(&ring[buf][(t * 16 + col) * RB + ks * 64 + kq * 16]);
-                if (!kq_ok) bf[t][ks] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
-    auto mma_round = [&](const u32x4 (&a)[KS], const u32x4 (&bf)[RT][KS], Round& r) __attribute__((always_inline)) {
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(a[ks], bf[t][ks], v);
-            r.c[t] = v;
-        }
-    };
-    // Partial update of a group's first round pr, whose first N0 tiles are
-    // layer 0: layer-1 tile t of the group is the round's tile N0 + t and pairs
-    // with its tile t (a round starting at the group's first tile holds
-    // layer-1 tiles only when all layer-0 tiles fit), so one pass adds both.
-    // Tiles past the range's are zero rows (zero products).  The MFMAs of the
-    // next round (mma) are issued between the reads and the writes.
-    auto update_first_n = [&](const Round& pr, auto n0, auto mma) __attribute__((always_inline)) {
-        constexpr int N0 = decltype(n0)::value;
-        f32x4 old[N0 > 0 ? N0 : 1];
-#pragma unroll
-        for (int t = 0; t < N0; ++t) old[t] = *reinterpret_cast<const f32x4*>(acc_b + pr.f[t]);
-        mma();
-#pragma unroll
-        for (int t = 0; t < N0; ++t) {
-            f32x4 v = pr.c[t];
-            if (N0 + t < RT) v += pr.c[N0 + t];
-            *reinterpret_cast<f32x4*>(acc_b + pr.f[t]) = old[t] + v;
-        }
-        // every LDS op of the wave but the N0 writes has completed
-        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(N0));
-    };
-    auto update_first = [&](const Round& pr, auto mma) __attribute__((always_inline)) {
-        static_assert(RT <= 8, "ring tiles");
-        using std::integral_constant;
-        switch (min(pr.n0, pr.nt)) {
-        case 0: update_first_n(pr, integral_constant<int, 0>{}, mma); break;
-        case 1: update_first_n(pr, integral_constant<int, 1>{}, mma); break;
-        case 2: update_first_n(pr, integral_constant<int, (RT >= 2 ? 2 : 1)>{}, mma); break;
-        case 3: update_first_n(pr, integral_constant<int, (RT >= 3 ? 3 : 1)>{}, mma); break;
-        case 4: update_first_n(pr, integral_constant<int, (RT >= 4 ? 4 : 1)>{}, mma); break;
-        case 5: update_first_n(pr, integral_constant<int, (RT >= 5 ? 5 : 1)>{}, mma); break;
-        case 6: update_first_n(pr, integral_constant<int, (RT >= 6 ? 6 : 1)>{}, mma); break;
-        case 7: update_first_n(pr, integral_constant<int, (RT >= 7 ? 7 : 1)>{}, mma); break;
-        default: update_first_n(pr, integral_constant<int, RT>{}, mma); break;
-        }
-    };
-    // Partial update of a further round: layer 0 (layer-1 tiles add into trash
-    // rows), then layer 1 if any; a pass issues all its reads before its writes
-    // (a layer's features are distinct), and a wave's LDS accesses complete in
-    // order, so later passes and rounds see the writes.
-    auto update_n = [&](const Round& pr, auto ntiles, auto mma) __attribute__((always_inline)) {
-        constexpr int NTL = decltype(ntiles)::value;
-        f32x4 old[NTL > 0 ? NTL : 1];
-        int fa[NTL > 0 ? NTL : 1];
-#pragma unroll
-        for (int t = 0; t < NTL; ++t) {
-            fa[t] = t < pr.n0 ? pr.f[t] : trash_f;
-            old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
-        }
-        mma();
-#pragma unroll
-        for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + pr.c[t];
-        if (pr.n0 < NTL) {
-#pragma unroll
-            for (int t = 0; t < NTL; ++t) {
-                fa[t] = t >= pr.n0 ? pr.f[t] : trash_f;
-                old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
-            }
-#pragma unroll
-            for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + pr.c[t];
-        }
-        // every LDS op of the wave but the last pass's NTL writes has completed
-        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(NTL));
-    };
-    // update of a further round pr, specialised for its tile count (a uniform switch)
-    auto update = [&](const Round& pr, auto mma) __attribute__((always_inline)) {
-        static_assert(RT <= 8, "ring tiles");
-        using std::integral_constant;
-        switch (pr.nt) {
-        case 0: update_n(pr, integral_constant<int, 0>{}, mma); break;
-        case 1: update_n(pr, integral_constant<int, 1>{}, mma); break;
-        case 2: update_n(pr, integral_constant<int, (RT >= 2 ? 2 : 1)>{}, mma); break;
-        case 3: update_n(pr, integral_constant<int, (RT >= 3 ? 3 : 1)>{}, mma); break;
-        case 4: update_n(pr, integral_constant<int, (RT >= 4 ? 4 : 1)>{}, mma); break;
-        case 5: update_n(pr, integral_constant<int, (RT >= 5 ? 5 : 1)>{}, mma); break;
-        case 6: update_n(pr, integral_constant<int, (RT >= 6 ? 6 : 1)>{}, mma); break;
-        case 7: update_n(pr, integral_constant<int, (RT >= 7 ? 7 : 1)>{}, mma); break;
-        default: update_n(pr, integral_constant<int, RT>{}, mma); break;
-        }
-    };
-    auto no_mma = []() __attribute__((always_inline)) {};
-    // Further rounds of a group whose range holds more than RT tiles, done
-    // synchronously after the group's first round: staged into ring[buf] (not
-    // in use by any wave at this point), multiplied and added at once.
-    auto extra_rounds = [&](int i, u32x2 m, int buf, const u32x4 (&a)[KS]) __attribute__((always_inline)) {
-        const int ntot = (int)m[1] - (int)(m[0] & 0xFFFF);
-        for (int t0 = RT; t0 < ntot; t0 += RT) {
-            Stage st;
-            load_stage(i, m, t0, st);
-            store_stage(buf, st, m, t0);
-            __syncthreads();
-            Round r;
-            u32x4 bf[RT][KS];
-            read_round(buf, bf, r);
-            mma_round(a, bf, r);
-            round_counts(m, t0, r);
-            update(r, no_mma);
-            __syncthreads();
-        }
-    };
-
-    // ---- pipeline: ring[i % 2] holds group i.  Every global load is issued
-    // DEPTH iterations before its use, in the same order every iteration (W^T
-    // stage of group i+1+DEPTH, dY of group i+DEPTH, meta of group i+1+2*DEPTH),
-    // so the one wait of an iteration (on the meta it converts) covers exactly
-    // the loads of iteration i-DEPTH.  Register sets rotate over NS slots
-    // (group h in slot h % NS), resolved at compile time by unrolling
-    // kGroupUnroll iterations (a multiple of NS and of the 2 ring buffers);
-    // the loop runs whole unrolled iterations without guards.  Iteration i
-    // stages group i+1 into ring[1 - i % 2] (read by every wave before the
-    // last barrier), reads and multiplies group i's first round and adds
-    // group i-1's products into the partial. ----
-    // G = 128 groups take about twice as long per iteration, so two groups of
-    // look-ahead cover the load latency; the shallower pipeline leaves room in
-    // the register budget for the larger dY fragments and ring rounds.
-    constexpr int DEPTH = G >= 128 ? 2 : 5, NS = DEPTH + 1;
-    static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0, "unroll");
-    Stage stg[NS];
-    u32x4 ya[NS][KS];
-    u32x2 mraw[NS];
-    u32x2 mu[DEPTH + 1];  // uniform meta of groups i .. i+DEPTH
-    Round rd[2];          // round of group i in rd[i % 2]
-    rd[0].nt = rd[1].nt = 0;
-    rd[0].n0 = rd[1].n0 = 0;
-    {
-        u32x2 m0[DEPTH + 1];
-#pragma unroll
-        for (int k = 0; k <= DEPTH; ++k) m0[k] = load_meta(k);
-#pragma unroll
-        for (int k = 0; k <= DEPTH; ++k) mu[k] = uniform_meta(m0[k]);
-        load_stage(0, mu[0], 0, stg[0]);
-        store_stage(0, stg[0], mu[0], 0);
-        // iterations -DEPTH .. -1 of the steady-state load sequence, kept in
-        // that order (the loop's wait counts assume it)
-#pragma unroll
-        for (int k = 1; k <= DEPTH; ++k) {
-            __builtin_amdgcn_sched_barrier(0);
-            load_stage(k, mu[k], 0, stg[k % NS]);
-            load_y(g_lo + k - 1, ya[(k - 1) % NS]);
-            mraw[(k + DEPTH) % NS] = load_meta(k + DEPTH);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-    auto body = [&](int i, auto kc) __attribute__((always_inline)) {
-        constexpr int K = decltype(kc)::value;  // i % kGroupUnroll
-        constexpr int Q = K % NS;               // i % NS
-        constexpr int P = K % 2;                // ring buffer of group i
-        const u32x2 mn = uniform_meta(mraw[(Q + 1 + DEPTH) % NS]);
-        load_stage(i + 1 + DEPTH, mn, 0, stg[(Q + 1 + DEPTH) % NS]);
-        load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS]);
-        mraw[(Q + 1 + 2 * DEPTH) % NS] = load_meta(i + 1 + 2 * DEPTH);
-        store_stage(1 - P, stg[(Q + 1) % NS], mu[1], 0);
-        mask_y(g_lo + i, ya[Q]);
-        u32x4 bf[RT][KS];
-        read_round(P, bf, rd[P]);
-        asm volatile("" ::: "memory");  // the update's LDS ops stay after the stage and reads
-        update_first(rd[1 - P], [&]() __attribute__((always_inline)) { mma_round(ya[Q], bf, rd[P]); });
-        round_counts(mu[0], 0, rd[P]);
-        if ((int)mu[0][1] - (int)(mu[0][0] & 0xFFFF) > RT) {  // uniform, rare
-            // add this round now, then the group's further rounds in order
-            update_first(rd[P], no_mma);
-            rd[P].nt = 0;
-            __syncthreads();
-            extra_rounds(i, mu[0], P, ya[Q]);
-            // the rounds consumed their loads (only some threads use a stage's
-            // position offsets); say so, so later code need not wait for them
-            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        }
-#pragma unroll
-        for (int k = 0; k < DEPTH; ++k) mu[k] = mu[k + 1];
-        mu[DEPTH] = mn;
-        // Barrier without draining the wave's LDS queue: other waves next write
-        // ring[P] and read ring[1 - P], and this wave's reads of ring[P] and
-        // fring[P] and writes of ring[1 - P] have completed (the update's wait);
-        // only its last partial writes may still be in flight, and no other
-        // wave touches those words.
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-    };
-    for (int i = 0; i < ng; i += kGroupUnroll) {
-        body(i, std::integral_constant<int, 0>{});
-        body(i + 1, std::integral_constant<int, 1>{});
-        body(i + 2, std::integral_constant<int, 2>{});
-        body(i + 3, std::integral_constant<int, 3>{});
-        body(i + 4, std::integral_constant<int, 4>{});
-        body(i + 5, std::integral_constant<int, 5>{});
-    }
-    static_assert(kGroupUnroll % 2 == 0, "the last iteration's round is in rd[1]");
-    update_first(rd[1], no_mma);
-    __syncthreads();
-
-    // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----
-    float* out = ws + ((int64_t)s * D + d_lo) * Bp + (int64_t)bt * BT;
-    for (int i = tid; i < dn * (BT / 4); i += NTH) {
-        const int d = i / (BT / 4), q = i % (BT / 4);  // natural columns 4q .. 4q+3
-        *reinterpret_cast<f32x4*>(out + (int64_t)d * Bp + q * 4) =
-            *reinterpret_cast<const f32x4*>(&acc[d * AS + perm_col(q / 4, q % 4)]);
-    }
-}
-
 // ------------------------------------------------------------- reduce ------
 // Both reduce kernels read the partials as 16-byte rows of 4 batch columns
 // (Bp is a multiple of 64, so every such read is in bounds and aligned).
@@ -699,45 +283,6 @@ __global__ __launch_bounds__(256) void bwdf_reduce_sr_kernel(const float* __rest
     }
 }
 
-template <typename T, int G, int WAVES, int RT>
-int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
-                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
-                hipStream_t st) {
-    const int64_t nlog = p.S * p.ndr * p.nbt;
-    const int64_t grid = 8 * ceil_div(nlog, 8);
-    if (((int64_t)p.BT * lddy + 8) * 2 > kMaxRsrcBytes) {
-        set_error("haste_ffi_bwd_features: lddy = %lld too large", (long long)lddy);
-        return HASTE_ERR_UNSUPPORTED;
-    }
-    bwdf_main_kernel<T, G, WAVES, RT><<<dim3((unsigned)grid), dim3(64 * WAVES), 0, st>>>(
-        tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
-        (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap, lddy % 8 != 0);
-    HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
-    return HASTE_OK;
-}
-
-// the plan's ring size: 2, 3 or ring_tiles(G) tiles
-template <typename T, int G, int WAVES>
-int launch_ring(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
-                int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
-                hipStream_t st) {
-    constexpr int R = ring_tiles(G);
-    if (p.RT == 2) return launch_main<T, G, WAVES, 2>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-    if constexpr (R > 3) {
-        if (p.RT == 3) return launch_main<T, G, WAVES, 3>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-    }
-    return launch_main<T, G, WAVES, R>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-}
-
-template <typename T, int G>
-int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
-             int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
-             int64_t O, hipStream_t st) {
-    (void)F;
-    if (p.BT == 64) return launch_ring<T, G, 4>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-    return launch_ring<T, G, 8>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-}
-
 // Checks the arguments and the workspace size; returns the plan.
 int check_bwdf(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
                int32_t dtype, const void* workspace, int64_t workspace_bytes, BwdFPlan* out) {
@@ -768,9 +313,12 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     int rc = check_bwdf(fn, B, D, F, O, G, dtype, workspace, workspace_bytes, &p);
     if (rc != HASTE_OK) return rc;
     HASTE_CHECK_ARG(idx && W && dY, "%s: null pointer", fn);
-    HASTE_CHECK_ARG(lddy >= O && (lddy % 8 == 0 || O >= 8),
-                    "%s: lddy must be >= O, and a multiple of 8 when O < 8 (lddy=%lld O=%lld)",
-                    fn, (long long)lddy, (long long)O);
+    // rows that all start on 16-byte boundaries take the plain build, any other
+    // rows the YA build (which needs O >= 16)
+    const bool ya = lddy % 8 != 0 || !aligned16(dY);
+    HASTE_CHECK_ARG(lddy >= O && (!ya || O >= 16),
+                    "%s: lddy must be >= O, and dY's rows must start on 16-byte boundaries "
+                    "when O < 16 (lddy=%lld O=%lld)", fn, (long long)lddy, (long long)O);
     HASTE_CHECK_ARG(aligned16(W) && (reinterpret_cast<uintptr_t>(dY) & 1) == 0,
                     "%s: W must be 16-byte aligned and dY 2-byte aligned", fn);
     HASTE_CHECK_ARG(plan_ready >= 0 && plan_ready <= 2, "%s: plan_ready must be 0, 1 or 2 (got %d)",
@@ -801,14 +349,16 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
                     w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);              \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
-            rc = run_main<BF16, GG>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);          \
+            rc = ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)   \
+                    : run_main<BF16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st); \
         } else {                                                                                \
             if (gather) {                                                                       \
                 bwdf_gather_kernel<F16, GG><<<pgrid, dim3(256), 0, st>>>(                       \
                     w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);              \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
-            rc = run_main<F16, GG>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);           \
+            rc = ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)   \
+                    : run_main<F16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);  \
         }                                                                                       \
         break;
         HASTE_BWDF_G(16)

@@ -10,7 +10,7 @@ template <typename T, bool SGD>
 int dispatch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* dY,
              int64_t lddy, void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B,
              int64_t D, int64_t F, int64_t O, int64_t G, const SgdArgs& sg, hipStream_t st) {
-    if (lddy % 8 != 0)
+    if (lddy % 8 != 0 || !aligned16(dY))
         return bwdw_dispatch_ys(T::code, SGD, idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias,
                                 dbias_dtype, B, D, F, O, G, sg, st);
     if constexpr (std::is_same_v<T, BF16>) {
@@ -31,9 +31,9 @@ int check_bwdw(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, 
     HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
                     "%s: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)", fn,
                     (long long)ldx, (long long)B);
-    HASTE_CHECK_ARG(lddy >= O && (lddy % 8 == 0 || O >= 8),
-                    "%s: lddy must be >= O, and a multiple of 8 when O < 8 (lddy=%lld O=%lld)",
-                    fn, (long long)lddy, (long long)O);
+    HASTE_CHECK_ARG(lddy >= O && ((lddy % 8 == 0 && aligned16(dY)) || O >= 16),
+                    "%s: lddy must be >= O, and dY's rows must start on 16-byte boundaries "
+                    "when O < 16 (lddy=%lld O=%lld)", fn, (long long)lddy, (long long)O);
     HASTE_CHECK_ARG(aligned16(xT) && (reinterpret_cast<uintptr_t>(dY) & 1) == 0,
                     "%s: xT must be 16-byte aligned and dY 2-byte aligned", fn);
     HASTE_CHECK_ARG(dW_dtype == HASTE_DTYPE_F32 || dW_dtype == HASTE_DTYPE_BF16 ||

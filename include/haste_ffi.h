@@ -13,9 +13,11 @@
  *   xT    [D, ldx]        features transposed, columns 0..B-1 used, ldx % 8 == 0
  *   W     [O, F]          weights
  *   out   [B, ldo]        logits, columns 0..O-1 written, ldo % 8 == 0
- *   dY    [B, lddy]       grad of logits, lddy >= O; any lddy when O >= 8 (else a
- *                         multiple of 8), 2-byte aligned.  When lddy % 8 != 0 the
- *                         last row need only hold O elements (a [B, O] tensor)
+ *   dY    [B, lddy]       grad of logits, lddy >= O, 2-byte aligned.  Rows that do
+ *                         not all start on 16-byte boundaries (lddy % 8 != 0, or dY
+ *                         not 16-byte aligned) need O >= 16, and then the last row
+ *                         need only hold O elements (a [B, O] tensor, or a column
+ *                         block of a wider one); they are read at some extra cost
  * Element types are HASTE_DTYPE_* codes; other 16-bit tensors must be 16-byte aligned.
  * Supported: dtype bf16 or f16; G in {16, 32, 64, 128}; F % 16 == 0, 16 <= F <= 256.
  * The reference envelope is G in {16,32,64}, F <= 128 (F <= 256 for G = 16);

@@ -250,27 +250,29 @@ def test_backward_weights_streaming_dY(dev):
         torch.testing.assert_close(db[l0:l1].cpu(), oracle.bias_grad(dy), **TOL32)
 
 
-@pytest.mark.parametrize("B,D,O,G,F,pad", [
-    (37, 300, 2003, 64, 64, 0),    # [B, O] contiguous, O odd
-    (64, 768, 4133, 32, 32, 4),    # odd row stride past O
-    (7, 50, 130, 16, 48, 5),       # tiny batch: the last row is the tile's first row at B = 1..
-    (100, 768, 2100, 128, 128, 0),
-    (65, 200, 1001, 16, 32, 1),    # B = 65: the last row sits alone in a 64-row chunk
-    (1, 64, 67, 64, 64, 0),        # one row, last group of 3 labels
+@pytest.mark.parametrize("B,D,O,G,F,pad,col0", [
+    (37, 300, 2003, 64, 64, 0, 0),    # [B, O] contiguous, O odd
+    (64, 768, 4133, 32, 32, 4, 0),    # odd row stride past O
+    (7, 50, 130, 16, 48, 5, 0),       # tiny batch
+    (100, 768, 2100, 128, 128, 0, 0),
+    (65, 200, 1001, 16, 32, 1, 0),    # B = 65: the last row sits alone in a 64-row chunk
+    (1, 64, 67, 64, 64, 0, 0),        # one row, last group of 3 labels
+    (130, 300, 5000, 64, 64, 3, 5),   # the view starts 5 columns into a row of 5008
+    (70, 300, 3001, 32, 32, 0, 1001), # the tail columns of a head/tail concat
 ])
-def test_backward_reads_rows_at_any_stride(dev, oracle_mod, B, D, O, G, F, pad):
-    """The backward kernels read grad-of-logits rows in place at any row stride
-    (rows start on 2-byte boundaries) and read nothing past label O of the last
-    row: the tensor here ends there, with NaN in the stride's padding.  Results
-    are bit-identical to the same data at an aligned stride, and match the
-    oracle."""
+def test_backward_reads_rows_at_any_stride(dev, oracle_mod, B, D, O, G, F, pad, col0):
+    """The backward kernels read grad-of-logits rows in place whatever their
+    alignment (rows start on 2-byte boundaries) and read nothing past label O
+    of the last row: the tensor here ends there, with NaN in the rest of each
+    row.  Results are bit-identical to the same data in 16-byte aligned rows,
+    and match the oracle."""
     x, W, bias, idx, dY = make_case(B, D, O, G, F, idx_mode="random", seed=13)
-    lddy = O + pad
-    buf = torch.full(((B - 1) * lddy + O,), float("nan"), dtype=torch.bfloat16, device=dev)
-    dYo = buf.as_strided((B, O), (lddy, 1))
+    lddy = col0 + O + pad
+    buf = torch.full(((B - 1) * lddy + col0 + O,), float("nan"), dtype=torch.bfloat16, device=dev)
+    dYo = buf.as_strided((B, O), (lddy, 1), col0)
     dYo.copy_(dY.to(dev))
     dYa, ldda = _C.rows_aligned(dY.to(dev))            # aligned copy, stride % 8 == 0
-    assert lddy % 8 != 0 and ldda % 8 == 0
+    assert (lddy % 8 != 0 or col0 % 8 != 0) and ldda % 8 == 0
     idx_d, W_d = idx.to(dev), W.to(dev)
     xT, ldx = _C.padded_transpose(x.to(dev))
     st = _C.stream_of(W_d)
