@@ -42,25 +42,74 @@ def _grad_dtype(p: torch.Tensor) -> torch.dtype:
 # tensor (same object, unchanged version counter: a rewire bumps it) skips
 # rebuilding it.  Keyed by shape, dtype, device and stream too: a workspace's
 # partial sums are written and read in stream order.
-_WS_CACHE: "collections.OrderedDict[tuple, list]" = collections.OrderedDict()
+class _Workspace:
+    __slots__ = ("ws", "dims", "stream", "locs", "locs_version", "locs_ptr", "wt_ptr",
+                 "wt_version", "__weakref__")
+
+    def __init__(self, ws, dims, stream):
+        self.ws, self.dims, self.stream = ws, dims, stream
+        self.locs = None          # weakref to the index tensor of the plan
+        self.locs_version = -1
+        self.locs_ptr = 0
+        self.wt_ptr = 0           # (data_ptr, version) of the weights whose W^T an
+        self.wt_version = -1      # optimizer step wrote into the workspace, if any
+
+    def plan_valid(self, locs) -> bool:
+        return (self.locs is not None and self.locs() is locs
+                and self.locs_version == locs._version and self.locs_ptr == locs.data_ptr())
+
+    def wt_valid(self, W) -> bool:
+        return self.wt_ptr == W.data_ptr() and self.wt_version == W._version
+
+
+_WS_CACHE: "collections.OrderedDict[tuple, _Workspace]" = collections.OrderedDict()
 _WS_CACHE_SIZE = 2
+# weights data_ptr -> the workspace whose plan was last used with them, so that
+# SRSgd can refresh its transposed weights while it updates them (the next
+# backward then skips the gather)
+_WT_TARGETS: "weakref.WeakValueDictionary[int, _Workspace]" = weakref.WeakValueDictionary()
 
 
 def _bwdf_workspace(locs: torch.Tensor, B: int, D: int, F: int, O: int, gsize: int,
-                    dtype: torch.dtype, stream: int):
-    """(workspace, plan_ready, entry): plan_ready = 1 when the cached workspace holds
-    the plan of these indices; the caller marks ``entry`` valid after its call."""
+                    dtype: torch.dtype, stream: int) -> _Workspace:
     key = (locs.device, B, D, F, O, gsize, dtype, stream)
     ent = _WS_CACHE.get(key)
     if ent is None:
-        ent = [_C.bwd_features_workspace(B, D, F, O, gsize, dtype, locs.device), None, -1, 0]
+        ent = _Workspace(_C.bwd_features_workspace(B, D, F, O, gsize, dtype, locs.device),
+                         (B, D, F, O, gsize), stream)
         _WS_CACHE[key] = ent
         while len(_WS_CACHE) > _WS_CACHE_SIZE:
             _WS_CACHE.popitem(last=False)
     _WS_CACHE.move_to_end(key)
-    ready = 1 if (ent[1] is not None and ent[1]() is locs and ent[2] == locs._version
-                  and ent[3] == locs.data_ptr()) else 0
-    return ent[0], ready, ent
+    return ent
+
+
+def mark_wt_refreshed(ent: _Workspace, weights: torch.Tensor) -> None:
+    """The workspace now holds the transposed weights of ``weights`` as they are."""
+    ent.wt_ptr, ent.wt_version = weights.data_ptr(), weights._version
+
+
+def clear_wt_refreshed() -> None:
+    """Forget every refreshed transposed-weight copy (the next backward gathers)."""
+    for ent in _WS_CACHE.values():
+        ent.wt_ptr, ent.wt_version = 0, -1
+
+
+def wt_target(weights: torch.Tensor):
+    """The workspace (if any) whose plan the last backward of ``weights`` used and
+    whose index tensor is unchanged since: an optimizer that updates these
+    weights may refresh its transposed weights (haste_sgd_sr_step_wt) and then
+    call ``mark_wt_refreshed``.  The reuse is keyed on the weights' version
+    counter: changes made through ``.data`` do not move it, so code that edits
+    the weights that way between an optimizer step and the next backward must
+    call ``clear_wt_refreshed`` (or build SRSgd with refresh_transposed=False)."""
+    ent = _WT_TARGETS.get(weights.data_ptr())
+    if ent is None or ent.locs is None:
+        return None
+    locs = ent.locs()
+    if locs is None or not ent.plan_valid(locs):
+        return None
+    return ent
 
 
 def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.Tensor,
@@ -82,7 +131,14 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
 
     grad_x = None
     if need_x:
-        ws, ready, ent = _bwdf_workspace(locs, B, D, F, O, gsize, dtype, stream)
+        ent = _bwdf_workspace(locs, B, D, F, O, gsize, dtype, stream)
+        ws = ent.ws
+        # 1: the plan is current; 2: the transposed weights too (written by the
+        # SRSgd step that last updated these weights, haste_sgd_sr_step_wt, and
+        # the weights' version counter has not moved since)
+        ready = 0
+        if ent.plan_valid(locs):
+            ready = 2 if ent.wt_valid(W) else 1
         if dtype == torch.bfloat16:
             grad_x = torch.empty(B, D, dtype=dtype, device=dev)
             _lib.call("haste_ffi_bwd_features_sr", locs.data_ptr(), W.data_ptr(),
@@ -94,7 +150,9 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
                       lddy, dxt.data_ptr(), ws.data_ptr(), ws.numel(), B, D, F, O, gsize,
                       code, ready, stream)
             grad_x = dxt.t().to(dtype).contiguous()
-        ent[1], ent[2], ent[3] = weakref.ref(locs), locs._version, locs.data_ptr()
+        ent.locs, ent.locs_version, ent.locs_ptr = weakref.ref(locs), locs._version, locs.data_ptr()
+        if W is weights and dtype == torch.bfloat16:
+            _WT_TARGETS[W.data_ptr()] = ent
 
     grad_w = grad_b = None
     if need_w or need_b:

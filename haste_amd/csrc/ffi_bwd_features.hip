@@ -190,16 +190,49 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
 }
 
 // ------------------------------------------------------------- gather ------
+// The SGD step that haste_sgd_sr_step_wt applies to W while gathering it: the
+// update of haste_sgd_sr_step on the tensor W [O, F] (element offsets l*F + j
+// from 0, the same FMA chain and Philox words), so W^T is built from the
+// updated weights.
+struct GatherSgd {
+    const void* g;  // gradient [O, F], g_dtype
+    float* m;       // fp32 momentum [O, F] (use_mom)
+    int g_dtype, use_mom, do_sr;
+    float lr, wd, mu;
+    uint32_t k0, k1;
+};
+
+template <int GD>
+__device__ __forceinline__ void grad8(const void* g, int64_t i, float out[8]) {
+    if constexpr (GD == HASTE_DTYPE_F32) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(g) + i);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(g) + i + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { out[e] = a[e]; out[4 + e] = b[e]; }
+    } else {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(g) + i);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = v[q] & 0xFFFFu, hi = v[q] >> 16;
+            out[2 * q] = GD == HASTE_DTYPE_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+            out[2 * q + 1] = GD == HASTE_DTYPE_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        }
+    }
+}
+
 // One workgroup per group: W_g is staged in LDS ([label][slot], row stride
 // F + 2 halves so the 8 label rows a wave reads at once sit in distinct banks),
-// then each thread writes 8 labels (16 bytes) of one tile row.
-template <typename T, int G>
+// then each thread writes 8 labels (16 bytes) of one tile row.  SGD: the
+// staged rows are W_g after the SGD step (GatherSgd), which is also written
+// back to W (16-bit weights, bf16 only).
+template <typename T, int G, bool SGD>
 __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __restrict__ W,
                                                           const int* __restrict__ tsrc,
                                                           const int* __restrict__ perm,
                                                           const int* __restrict__ meta,
                                                           uint16_t* __restrict__ twt, int F,
-                                                          int64_t O, int ndr, int Tcap) {
+                                                          int64_t O, int ndr, int Tcap,
+                                                          GatherSgd sg) {
     __shared__ uint32_t s_w[G * 129];  // G rows of (F + 2) halves, F <= 256
     __shared__ int s_perm[256];
     const int64_t g = blockIdx.x;
@@ -208,7 +241,36 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
     for (int it = tid; it < G * (F / 8); it += 256) {
         const int l = it / (F / 8), j0 = (it % (F / 8)) * 8;
         u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (g * G + l < O) v = *reinterpret_cast<const u32x4*>(W + (g * G + l) * F + j0);
+        if (g * G + l < O) {
+            const int64_t e = (g * G + l) * F + j0;
+            v = *reinterpret_cast<const u32x4*>(W + e);
+            if constexpr (SGD) {
+                float gv[8], mv[8];
+                if (sg.g_dtype == HASTE_DTYPE_F32) grad8<HASTE_DTYPE_F32>(sg.g, e, gv);
+                else if (sg.g_dtype == HASTE_DTYPE_BF16) grad8<HASTE_DTYPE_BF16>(sg.g, e, gv);
+                else grad8<HASTE_DTYPE_F16>(sg.g, e, gv);
+                if (sg.use_mom) {
+                    const f32x4 m0 = *reinterpret_cast<const f32x4*>(sg.m + e);
+                    const f32x4 m1 = *reinterpret_cast<const f32x4*>(sg.m + e + 4);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) { mv[k] = m0[k]; mv[4 + k] = m1[k]; }
+                }
+                uint32_t ob[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t wb = (k & 1) ? (v[k >> 1] >> 16) : (v[k >> 1] & 0xFFFFu);
+                    ob[k] = sgd_one(bf16_bits_to_f32(wb), gv[k], &mv[k], sg.use_mom, sg.lr, sg.wd,
+                                    sg.mu, sg.do_sr, (uint64_t)(e + k), sg.k0, sg.k1);
+                }
+                v = u32x4{ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16), ob[4] | (ob[5] << 16),
+                          ob[6] | (ob[7] << 16)};
+                *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(W) + e) = v;
+                if (sg.use_mom) {
+                    *reinterpret_cast<f32x4*>(sg.m + e) = f32x4{mv[0], mv[1], mv[2], mv[3]};
+                    *reinterpret_cast<f32x4*>(sg.m + e + 4) = f32x4{mv[4], mv[5], mv[6], mv[7]};
+                }
+            }
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) s_w[l * ldw + j0 / 2 + q] = v[q];
     }
@@ -345,16 +407,16 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     case GG:                                                                                    \
         if (dtype == HASTE_DTYPE_BF16) {                                                        \
             if (gather) {                                                                       \
-                bwdf_gather_kernel<BF16, GG><<<pgrid, dim3(256), 0, st>>>(                      \
-                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);              \
+                bwdf_gather_kernel<BF16, GG, false><<<pgrid, dim3(256), 0, st>>>(               \
+                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, GatherSgd{}); \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
             rc = ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)   \
                     : run_main<BF16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st); \
         } else {                                                                                \
             if (gather) {                                                                       \
-                bwdf_gather_kernel<F16, GG><<<pgrid, dim3(256), 0, st>>>(                       \
-                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap);              \
+                bwdf_gather_kernel<F16, GG, false><<<pgrid, dim3(256), 0, st>>>(                \
+                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, GatherSgd{}); \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
             rc = ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)   \
@@ -455,5 +517,50 @@ extern "C" int haste_ffi_bwd_features_sr(const int32_t* idx, const void* W, cons
                                                             (int)p.S, (uint32_t)seed,
                                                             (uint32_t)(seed >> 32));
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features_sr");
+    return HASTE_OK;
+}
+
+extern "C" int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype, float* m,
+                                    float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
+                                    uint64_t seed, void* workspace, int64_t workspace_bytes,
+                                    int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+                                    int32_t dtype, void* stream) {
+    const char* fn = "haste_sgd_sr_step_wt";
+    haste::BwdFPlan p;
+    int rc = haste::check_bwdf(fn, B, D, F, O, G, dtype, workspace, workspace_bytes, &p);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(dtype == HASTE_DTYPE_BF16, "%s: weights must be bf16", fn);
+    HASTE_CHECK_ARG(W && g && haste::aligned16(W) && haste::aligned16(g),
+                    "%s: W and g must be 16-byte aligned pointers", fn);
+    HASTE_CHECK_ARG(g_dtype == HASTE_DTYPE_BF16 || g_dtype == HASTE_DTYPE_F16 ||
+                        g_dtype == HASTE_DTYPE_F32,
+                    "%s: bad gradient dtype %d", fn, (int)g_dtype);
+    HASTE_CHECK_ARG(!use_mom || (m != nullptr && haste::aligned16(m)),
+                    "%s: momentum buffer must be a 16-byte aligned pointer", fn);
+    char* base = static_cast<char*>(workspace);
+    const haste::GatherSgd sg{g, m, (int)g_dtype, use_mom ? 1 : 0, do_sr ? 1 : 0, lr, wd, mu,
+                              (uint32_t)seed, (uint32_t)(seed >> 32)};
+    const int* tsrc = reinterpret_cast<const int*>(base + p.tsrc_off);
+    const int* perm = reinterpret_cast<const int*>(base + p.perm_off);
+    const int* meta = reinterpret_cast<const int*>(base + p.meta_off);
+    uint16_t* twt = reinterpret_cast<uint16_t*>(base + p.twt_off);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)p.Gc);
+    switch (G) {
+#define HASTE_SGD_WT(GG)                                                                            \
+    case GG:                                                                                        \
+        haste::bwdf_gather_kernel<haste::BF16, GG, true><<<grid, dim3(256), 0, st>>>(               \
+            W, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, sg);                      \
+        break;
+        HASTE_SGD_WT(16)
+        HASTE_SGD_WT(32)
+        HASTE_SGD_WT(64)
+        HASTE_SGD_WT(128)
+#undef HASTE_SGD_WT
+    default:
+        haste::set_error("%s: unsupported group size %lld", fn, (long long)G);
+        return HASTE_ERR_UNSUPPORTED;
+    }
+    HASTE_CHECK_LAUNCH(fn);
     return HASTE_OK;
 }

@@ -11,6 +11,12 @@ Semantics kept from the reference:
     (g' = fma(wd, w, g); m' = fma(mu, m, g'); w' = fma(-lr, m' or g', w);
     SR to bf16 with tl.randint(seed, i), or RNE when SR is off);
   * non-contiguous params are updated through a contiguous copy.
+The weights of a grouped FFI layer whose last backward used an index plan
+(``bindings.wt_target``) are updated by haste_sgd_sr_step_wt instead: the same
+update, bit for bit, which also writes the transposed weights that layer's
+next backward reads, so the backward skips gathering them
+(``refresh_transposed=False`` turns this off).  Every updated parameter's
+version counter is moved, as an in-place torch op would move it.
   * every parameter that requires a gradient gets its fp32 ``momentum_buf``
     at construction, zero, whether or not momentum is used (optim_sr.py:35-44),
     so a checkpoint carries the same state keys as the reference's.
@@ -25,6 +31,8 @@ from __future__ import annotations
 import torch
 from torch.optim import Optimizer
 
+from . import _C, _lib
+from . import bindings as _bindings
 from .sr import sgd_update_multi
 
 __all__ = ["SRSgd", "SGD_SR"]
@@ -33,11 +41,13 @@ __all__ = ["SRSgd", "SGD_SR"]
 class SRSgd(Optimizer):
     def __init__(self, params, lr: float = 1e-3, weight_decay: float = 0.0,
                  momentum: float = 0.0, use_momentum: bool = True,
-                 stochastic_rounding: bool = True, seed: int = 123):
+                 stochastic_rounding: bool = True, seed: int = 123,
+                 refresh_transposed: bool = True):
         defaults = dict(lr=lr, weight_decay=weight_decay, momentum=momentum,
                         use_momentum=use_momentum, stochastic_rounding=stochastic_rounding,
                         seed=seed)
         super().__init__(params, defaults)
+        self.refresh_transposed = bool(refresh_transposed)
         for group in self.param_groups:
             for p in group["params"]:
                 if p.requires_grad:
@@ -104,8 +114,23 @@ class SRSgd(Optimizer):
                     continue
 
                 w = p.data
-                w_contig = w if w.is_contiguous() else w.contiguous()
                 g_contig = grad if grad.is_contiguous() else grad.contiguous()
+                ent = (_bindings.wt_target(p) if self.refresh_transposed and w.is_contiguous()
+                       and p.dtype == torch.bfloat16 and p.dim() == 2 else None)
+                if ent is not None and ent.dims[2:4] == (p.shape[1], p.shape[0]):
+                    # an FFI layer's weights: the same update, which also writes the
+                    # transposed weights its next backward reads (no gather there)
+                    B, D, F, O, G = ent.dims
+                    m = self._momentum_buf(p) if mom_on else None
+                    _lib.call("haste_sgd_sr_step_wt", w.data_ptr(), g_contig.data_ptr(),
+                              _C.dtype_code(g_contig.dtype), None if m is None else m.data_ptr(),
+                              float(lr), float(wd), float(mu), int(mom_on), int(bool(sr)),
+                              int(seed), ent.ws.data_ptr(), ent.ws.numel(), B, D, F, O, G,
+                              _lib.DTYPE_BF16, _C.stream_of(w))
+                    torch.autograd.graph.increment_version(p)
+                    _bindings.mark_wt_refreshed(ent, p)
+                    continue
+                w_contig = w if w.is_contiguous() else w.contiguous()
                 b = batches.setdefault(grad.dtype, ([], [], [], []))
                 b[0].append(w_contig)
                 b[1].append(g_contig)
@@ -118,6 +143,9 @@ class SRSgd(Optimizer):
                 for w_contig, p in zip(ws, ps):
                     if w_contig.data_ptr() != p.data.data_ptr():
                         p.data.copy_(w_contig)
+                    # the kernel wrote through a raw pointer: move the version counter
+                    # as an in-place torch op would
+                    torch.autograd.graph.increment_version(p)
         return loss
 
 

@@ -202,6 +202,22 @@ int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx, c
                               int64_t O, int64_t G, int32_t dtype, void* stream);
 
 /*
+ * haste_sgd_sr_step on the weights W [O, F] (bf16) of an FFI layer (element
+ * offsets l*F + j from 0; bit-identical), which also writes the transposed
+ * weights of the UPDATED W into a haste_ffi_bwd_features workspace holding the
+ * plan of the layer's idx for these sizes (B, D, F, O, G), so that the next
+ * haste_ffi_bwd_features[_sr] call may pass plan_ready = 2 and skip gathering
+ * them.  g: gradient [O, F] (bf16, f16 or f32); m: fp32 momentum [O, F], read
+ * and written when use_mom.  Replaces, for an FFI weight matrix, SRSgd.step's
+ * sgd_update call (shared_ffi/optim_sr.py:99-109, shared_ffi/sr_triton.py:172-213);
+ * the transposed weights have no counterpart in the reference.
+ */
+int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype, float* m, float lr,
+                         float wd, float mu, int32_t use_mom, int32_t do_sr, uint64_t seed,
+                         void* workspace, int64_t workspace_bytes, int64_t B, int64_t D, int64_t F,
+                         int64_t O, int64_t G, int32_t dtype, void* stream);
+
+/*
  * Stochastic rounding fp32 -> bf16: out[i] = SR(x[i], tl.randint(seed, offset0 + i)).
  * Replaces stochastic_rounding (shared_ffi/sr_triton.py:51-59).
  */
