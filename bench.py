@@ -319,22 +319,30 @@ def time_dropin(cfg, steps, warmup, dev):
 
 
 def cpu_info():
-    model = None
+    """The host CPU as /proc/cpuinfo names it (model name, family/model/stepping)
+    and how many logical CPUs the host has."""
+    fields, n = {}, 0
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k == "processor":
+                    n += 1
+                elif k in ("model name", "cpu family", "model", "stepping") and k not in fields:
+                    fields[k] = v.strip()
     except OSError:
-        pass
-    return model
+        return None
+    return (f"{fields.get('model name')} (family {fields.get('cpu family')} model "
+            f"{fields.get('model')} stepping {fields.get('stepping')}; {n} logical CPUs on the host)")
 
 
-def cpu_baseline(cfg, budget_s=25.0):
+def cpu_baseline(cfg, budget_s=10.0, max_steps=40):
     """Times the CPU oracle (PyTorch-CPU gather+bmm fwd/bwd + C/OpenMP SR-SGD,
-    the reference formulation restated) on a slice of the label groups, scaled
-    to the full label count, on every core in this process's affinity."""
+    the reference formulation restated) on the full workload of `cfg` (all
+    label groups, no scaling), on every core in this process's affinity: two
+    warm-up steps, then steps until `budget_s` seconds of timed work (at least
+    3, at most `max_steps`); the median step is reported."""
     import numpy as np
     import torch
 
@@ -345,17 +353,15 @@ def cpu_baseline(cfg, budget_s=25.0):
     oracle.set_num_threads(ncores)
     B, D, O, G, F = cfg["B"], cfg["D"], cfg["O"], cfg["G"], cfg["F"]
     Gc = (O + G - 1) // G
-    frac = 1
-    while Gc // frac > 256 and frac < 64:
-        frac *= 2
-    Gs = max(1, Gc // frac)
-    Os = Gs * G
+    Op = Gc * G  # the oracle works on whole groups; the padding labels are W = 0 columns
     g = torch.Generator().manual_seed(0)
     x = torch.randn(B, D, generator=g).to(torch.bfloat16)
-    W = ((torch.rand(Os, F, generator=g) * 2 - 1) / math.sqrt(F)).to(torch.bfloat16)
-    bias = torch.zeros(Os, dtype=torch.bfloat16)
-    idx = torch.randint(0, D, (Gs, F), generator=g, dtype=torch.int32)
-    dY = (torch.randn(B, Os, generator=g) * 0.1).to(torch.bfloat16)
+    W = ((torch.rand(Op, F, generator=g) * 2 - 1) / math.sqrt(F)).to(torch.bfloat16)
+    W[O:] = 0
+    bias = torch.zeros(Op, dtype=torch.bfloat16)
+    idx = torch.randint(0, D, (Gc, F), generator=g, dtype=torch.int32)
+    dY = (torch.randn(B, Op, generator=g) * 0.1).to(torch.bfloat16)
+    dY[:, O:] = 0
 
     def one_step(seed):
         t = [time.perf_counter()]
@@ -379,20 +385,19 @@ def cpu_baseline(cfg, budget_s=25.0):
     one_step(0)
     steps = []
     t_start = time.perf_counter()
-    while len(steps) < 5 and (time.perf_counter() - t_start) < budget_s:
+    while len(steps) < max_steps and (len(steps) < 3 or time.perf_counter() - t_start < budget_s):
         steps.append(one_step(len(steps) + 1))
-    scale = O / Os
-    tot = sorted(sum(s) for s in steps)[len(steps) // 2] * scale
-    ph = [sorted(s[i] for s in steps)[len(steps) // 2] * scale * 1e3 for i in range(4)]
+    timed_s = time.perf_counter() - t_start
+    tot = sorted(sum(s) for s in steps)[len(steps) // 2]
+    ph = [sorted(s[i] for s in steps)[len(steps) // 2] * 1e3 for i in range(4)]
     return {"value": B / tot, "unit": "samples/s", "cores": ncores, "kind": "port",
             "cpu_model": cpu_info(),
-            "sample": (f"oracle (torch-CPU gather+bmm fwd/bwd + C/OpenMP SR-SGD) on {Gs} of {Gc} "
-                       f"label groups (O_s={Os}), median of {len(steps)} steps after 2 warm-ups, "
-                       f"times scaled by O/O_s={scale:.1f}"),
-            "step_ms_full_scaled": tot * 1e3,
-            "phases_ms_full_scaled": {"fwd": round(ph[0], 2), "bwd_features_sr": round(ph[1], 2),
-                                      "bwd_weights_dbias": round(ph[2], 2),
-                                      "sr_sgd": round(ph[3], 2)}}
+            "sample": (f"oracle (torch-CPU gather+bmm fwd/bwd + C/OpenMP SR-SGD) on the full workload "
+                       f"({Gc} label groups, B={B}), median of {len(steps)} steps ({timed_s:.1f} s "
+                       f"timed) after 2 warm-ups"),
+            "step_ms": round(tot * 1e3, 2),
+            "phases_ms": {"fwd": round(ph[0], 2), "bwd_features_sr": round(ph[1], 2),
+                          "bwd_weights_dbias": round(ph[2], 2), "sr_sgd": round(ph[3], 2)}}
 
 
 def main():
