@@ -284,12 +284,14 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const char* p) {
 }
 
 // Workgroup-id remap so that consecutive logical ids land on the same XCD
-// (the hardware dispatches workgroup i to XCD i % 8).  Returns -1 for the
-// padding ids of a grid rounded up to a multiple of 8.
+// (the hardware dispatches workgroup i to XCD i % 8), the ids split as evenly
+// as the count allows (XCD x holds nlogical / 8 ids, one more when x <
+// nlogical % 8).  Returns -1 for the padding ids of a grid rounded up to a
+// multiple of 8.
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nlogical) {
-    const int64_t per = (nlogical + 7) / 8;
-    const int64_t w = (bid % 8) * per + bid / 8;
-    return w < nlogical ? w : -1;
+    const int64_t lo = nlogical / 8, rem = nlogical % 8;
+    const int64_t x = bid % 8, k = bid / 8;
+    return k < lo + (x < rem ? 1 : 0) ? x * lo + min(x, rem) + k : -1;
 }
 
 }  // namespace haste

@@ -13,7 +13,8 @@
 //    (16-byte copies, Xg[slot][batch]; xT is small and L2 resident) and read
 //    back with ds_read_b64_tr_b16, which hands each lane 4 consecutive slots of
 //    one batch column.  Tile t+2's rows are fetched into registers while tile
-//    t's MFMAs run (two LDS buffers).
+//    t's MFMAs run (two LDS buffers, or one where LDS limits the workgroups
+//    per CU).
 //  - Epilogue: results are staged per wave in LDS and stored as whole 128-byte
 //    row segments (a lane's MFMA output covers only 8 bytes of a row; 8-byte
 //    stores spread over 16 rows cost four times the L2 write requests).
@@ -41,8 +42,15 @@ template <int G, int FP>
 struct FwdCfg {
     static constexpr int KS = FP / 32;     // MFMA k-steps
     static constexpr int MTILES = G / 16;  // label tiles in the group
-    // waves along labels: a wave keeps MT*KS W fragments (<= 16, 64 VGPRs)
-    static constexpr int WM = MTILES * KS <= 16 ? 1 : (MTILES * KS <= 32 ? 2 : 4);
+    // Gathered-row LDS buffers: two (tile t+1 is stashed while tile t is read)
+    // unless their size caps the workgroups per CU below what the registers
+    // allow; with one, a barrier separates a tile's reads from the next stash.
+    static constexpr int NB = (FP == 256 || (FP == 128 && (G == 32 || G == 64))) ? 1 : 2;
+    // Waves along labels: a wave keeps MT*KS W fragments (<= 16, 64 VGPRs).  At
+    // G = 64, FP = 128 two waves share the labels (32 W registers each, twice
+    // the LDS reads of the gathered rows), so that four workgroups fit a CU:
+    // the 2049 groups of a 131K-label layer then run in two rounds, not three.
+    static constexpr int WM = (G == 64 && FP == 128) ? 2 : MTILES * KS <= 16 ? 1 : (MTILES * KS <= 32 ? 2 : 4);
     static constexpr int WN = 4 / WM;             // waves along the batch
     static constexpr int MT = MTILES / WM;        // label tiles per wave
     static constexpr int NT = (kBT / 16) / WN;    // 16-column batch tiles per wave
@@ -181,7 +189,7 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
     float lsum = 0.0f;
     for (int t = 0; t < ntiles; ++t) {
         const int b_base = b_chunk0 + t * kBT;
-        const char* xs = Xg[t & 1];
+        const char* xs = Xg[C::NB == 1 ? 0 : t & 1];
         uint32_t yw[NT][YW];
         if constexpr (BCE) {
             const rsrc_t yr = make_rsrc(bce.ybits + (int64_t)b_base * bce.ldyw,
@@ -216,8 +224,9 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                 for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16x16x32<T>(wf[mt][ks], bf, acc[mt][nt]);
             }
         }
+        if (C::NB == 1) __syncthreads();  // every wave is done reading the buffer
         if (t + 1 < ntiles) {
-            stash((t + 1) & 1, b_base + kBT, xv);
+            stash(C::NB == 1 ? 0 : (t + 1) & 1, b_base + kBT, xv);
             if (t + 2 < ntiles) fetch(b_base + 2 * kBT, xv);
         }
 
@@ -318,10 +327,11 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
     }
 }
 
-// The BCE epilogue's extra registers would cost a wave per SIMD at G*F = 64*128;
-// the bound keeps three (the plain kernel fits them as is).
+// Register bound: four waves per SIMD at G = 64, FP = 128 (the split labels
+// above), three there for the BCE epilogue, whose extra registers would
+// otherwise cost a wave; two elsewhere.
 template <int G, int FP, bool BCE>
-constexpr int fwd_waves_per_simd() { return BCE && G * FP == 64 * 128 ? 3 : 2; }
+constexpr int fwd_waves_per_simd() { return G == 64 && FP == 128 ? (BCE ? 3 : 4) : 2; }
 
 template <typename T, int G, int FP, bool BCE>
 __global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE>())) void ffi_fwd_kernel(
@@ -330,14 +340,18 @@ __global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE>())) void 
     int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk,
     BceArgs bce) {
     using C = FwdCfg<G, FP>;
-    __shared__ __attribute__((aligned(16))) char Xg[2][FP * C::RB];
+    __shared__ __attribute__((aligned(16))) char Xg[C::NB][FP * C::RB];
     __shared__ __attribute__((aligned(16))) char stg[4][C::STG];
     __shared__ float s_red[4];
 
     const int64_t work = xcd_remap(blockIdx.x, Gc * nchunks);
     if (work < 0) return;
-    const int64_t g = work / nchunks;
-    const int chunk = (int)(work % nchunks);
+    // the last group's chunks are the first work items: when the work does not
+    // split evenly over the XCDs, XCD 0 holds one item more than the others,
+    // and it is then the last group, the smallest one when O % G != 0
+    const int64_t wr = work < nchunks ? work + (Gc - 1) * nchunks : work - nchunks;
+    const int64_t g = wr / nchunks;
+    const int chunk = (int)(wr % nchunks);
     const int b_chunk0 = chunk * tiles_per_chunk * kBT;
     const int ntiles = min(tiles_per_chunk, (B - b_chunk0 + kBT - 1) / kBT);
     if constexpr (BCE) bce.part += work;
