@@ -100,9 +100,12 @@ __device__ __forceinline__ u32x4 keep_first(u32x4 v, int nv) {
 
 
 // Two waves per SIMD (at most 256 registers each) hide the chunk pipeline's load
-// latency; the largest tile set (G = 128, 256 slots) needs more registers.
+// latency; the largest tile set (G = 128, 256 slots) needs more registers.  At
+// G = 64, FP = 128 four fit (the fused update then loads W in its epilogue):
+// the 2049 groups of a 131K-label layer run in two rounds of 1024, not three
+// of 768.
 template <int G, int FP>
-constexpr int bwdw_waves_per_simd() { return G * FP >= 128 * 256 ? 1 : 2; }
+constexpr int bwdw_waves_per_simd() { return G == 64 && FP == 128 ? 4 : G * FP >= 128 * 256 ? 1 : 2; }
 
 // dY larger than the 256 MB last-level cache (MALL) of an MI355X: this kernel,
 // its last reader in a training step, streams it with non-temporal loads (YNT),
@@ -124,9 +127,15 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     char (*Ys)[kKC * RB] = reinterpret_cast<char (*)[kKC * RB]>(lds);
     float* stg = reinterpret_cast<float*>(lds);
 
-    const int64_t g = blockIdx.x;
+    // the last group (partial when O % G != 0, the shortest workgroup) is
+    // dispatched first: with Gc = 8k + 1 groups, XCD 0 holds one workgroup
+    // more than the others, and it is then that one
+    const int64_t g = blockIdx.x == 0 ? (int64_t)gridDim.x - 1 : (int64_t)blockIdx.x - 1;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    // the wave index as a scalar: branches on wm / wn / active are then scalar
+    // branches that skip their MFMAs (an MFMA under an EXEC mask still runs and
+    // writes every lane)
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % C::WM, wn = wave / C::WM;
     const bool active = wn < C::WN;
     const int col = lane & 15, kq = lane >> 4;
@@ -210,17 +219,22 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
         }
     };
 
+    // The bias MFMA of label tile nt runs on the wave with wm == nt % WM, into
+    // its accumulator accb[nt / WM]: the waves share the work and hold
+    // ceil(NT / WM) accumulators each, not NT.
+    constexpr int NBW = (NT + C::WM - 1) / C::WM;
     f32x4 acc[MT][NT];
-    f32x4 accb[NT];
+    f32x4 accb[NBW];
+#pragma unroll
+    for (int k = 0; k < NBW; ++k) accb[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        accb[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const uint32_t op = one_pair<T>();
     const u32x4 ones = u32x4{op, op, op, op};
-    const bool do_bias = (dbias != nullptr || (SGD && sg.bias != nullptr)) && wm == 0 && active;
+    const bool do_bias = (dbias != nullptr || (SGD && sg.bias != nullptr)) && active;
 
     const rsrc_t wr = make_rsrc(SGD ? sg.W + l0 * F : nullptr, SGD ? (int64_t)nl * F * 2 : 0);
     constexpr int CPR = C::CPR, WPT = C::WPT;
@@ -228,9 +242,9 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     // their latency hides behind the batch loop (the thread's chunks are known:
     // in pass pp, chunk tid + q*256 is row pp*PR + it / CPR, slots (it % CPR) * 8
     // .. +7).  For at most two passes and F <= 128: beyond that the extra
-    // registers would cost a wave per SIMD.
+    // registers would cost a wave per SIMD (so would they at four waves).
     constexpr int NPASS = G / PR;
-    constexpr bool kWPre = SGD && NPASS <= 2 && FP <= 128;
+    constexpr bool kWPre = SGD && NPASS <= 2 && FP <= 128 && bwdw_waves_per_simd<G, FP>() < 4;
     u32x4 wpre[kWPre ? NPASS * WPT : 1];
     uint32_t bpre = 0;  // fused step: bias bits of label tid (tid < nl)
     if constexpr (SGD) {
@@ -284,7 +298,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
                         acc[mt][nt] = mfma16x16x32<T>(ar[P][ks][mt], bf, acc[mt][nt]);
-                    if (do_bias) accb[nt] = mfma16x16x32<T>(ones, bf, accb[nt]);
+                    if (do_bias && nt % C::WM == wm) accb[nt / C::WM] = mfma16x16x32<T>(ones, bf, accb[nt / C::WM]);
                 }
             }
         }
@@ -297,15 +311,15 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
         body(c + 1, std::integral_constant<int, 1>{});
     }
 
-    // ---- bias: lane (col, kq = 0) of a wave with wm == 0 holds the column sum of
-    // label (wn*NT + nt)*16 + col in accb[nt][0] ----
+    // ---- bias: lane (col, kq = 0) of the wave with wm == nt % WM holds the
+    // column sum of label (wn*NT + nt)*16 + col in accb[nt / WM][0] ----
     if (do_bias && kq == 0) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int ll = (wn * NT + nt) * 16 + col;
-            if (ll >= nl) continue;
+            if (nt % C::WM != wm || ll >= nl) continue;
             const int64_t l = l0 + ll;
-            const float v = accb[nt][0];
+            const float v = accb[nt / C::WM][0];
             if (dbias != nullptr) {
                 if (dbias_dtype == HASTE_DTYPE_F32)
                     static_cast<float*>(dbias)[l] = v;
