@@ -13,13 +13,15 @@ namespace {
 
 // --------------------------------------------------------------- main ------
 // A workgroup owns (group slice s, feature range r, batch tile of BT = 16*WAVES
-// columns) and keeps dXT[range, tile] as an fp32 partial in LDS.  Wave w owns
-// batch rows [16w, 16w+16) of the tile, so no two waves touch the same LDS
-// word of the partial.  Per group:
+// columns) and keeps dXT[range, tile] as an fp32 partial in LDS.  The tile's
+// rows are WAVES blocks of 16; a wave owns MT consecutive blocks (MT = 2 for
+// the 128-column build: four waves, one per SIMD, each reading the ring once
+// for two blocks), so no two waves touch the same LDS word of the partial.
+// Per group:
 //  - the group's W^T tiles for the range (and the partial-row offsets of their
 //    positions) are staged once into a double-buffered LDS ring, shared by all
 //    waves: each thread copies 16-byte chunks loaded two groups ahead;
-//  - each wave multiplies its dY rows (16 x G, loaded one group ahead) with
+//  - each wave multiplies its dY rows (MT blocks of 16 x G) with
 //    the tiles (MFMA, M = batch rows, N = 16 positions, K = labels); a lane then
 //    holds four consecutive batch values of one position and adds them into
 //    the partial row of the position's feature with one 16-byte read and one
@@ -34,15 +36,16 @@ namespace {
 // Ranges holding more than RT tiles in a group process the rest in further
 // rounds staged synchronously (rare: a range's share of F is usually ~F/ndr),
 // layer by layer.
-template <int G, int WAVES, int RT_>
+template <int G, int WAVES, int RT_, int MT_>
 struct BwdFCfg {
     static constexpr int KS = G >= 32 ? G / 32 : 1;  // MFMA k-steps over labels
     static constexpr int BT = 16 * WAVES;            // batch columns per workgroup
     static constexpr int AS = acc_stride(BT);
     static constexpr int RT = RT_;
+    static constexpr int MT = MT_;                   // 16-row M tiles per wave
     static constexpr int RB = ring_row_bytes(G);
     static constexpr int RING = RT * 16 * RB;        // bytes per ring buffer
-    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int THREADS = 64 * WAVES / MT;
     static constexpr int CH = G / 8;                 // 16-byte chunks per W^T row
     static constexpr int SPT = (RT * 16 * CH + THREADS - 1) / THREADS;  // staged chunks per thread
     static constexpr int DCMAX = max_dc(BT, G, RT);
@@ -55,13 +58,13 @@ struct BwdFCfg {
 // loads cost the kernel about twice its time); dY's last row, which may end at
 // label O, is read by plain (unaligned) loads, its piece across O loaded early
 // and shifted back.
-template <typename T, int G, int WAVES, int RT_, bool YA>
-__global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
+template <typename T, int G, int WAVES, int RT_, bool YA, int MT_>
+__global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
     const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
     const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
     int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
-    using C = BwdFCfg<G, WAVES, RT_>;
-    constexpr int KS = C::KS, BT = C::BT, AS = C::AS, RT = C::RT, RB = C::RB, CH = C::CH;
+    using C = BwdFCfg<G, WAVES, RT_, MT_>;
+    constexpr int KS = C::KS, BT = C::BT, AS = C::AS, RT = C::RT, RB = C::RB, CH = C::CH, MT = C::MT;
     constexpr int SPT = C::SPT, NTH = C::THREADS;
     __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
     __shared__ __attribute__((aligned(16))) char ring[2][C::RING];
@@ -79,7 +82,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     const int ng = (int)(g_hi - g_lo);
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15;  // A row within the M tile / B column (tile position)
     const int kq = lane >> 4;   // which 8 of the 32 K elements
     const bool kq_ok = G >= 32 || kq < 2;
@@ -97,8 +100,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // resource).
     const int b0 = bt * BT;
     const int rows = min(BT, B - b0);
-    const int lrow = wave * 16 + col;
-    const bool last_row = YA && b0 + lrow == B - 1;
+    // M tile mt of the wave covers the tile's rows 16 * (wave * MT + mt) ..
+    int lrow[MT];
+    bool last_row[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        lrow[mt] = (wave * MT + mt) * 16 + col;
+        last_row[mt] = YA && b0 + lrow[mt] == B - 1;
+    }
     // (YA: the resource starts at the 16-byte boundary at or below the tile's
     // first row, delta bytes before it)
     const uintptr_t tile = reinterpret_cast<uintptr_t>(dY + (int64_t)b0 * lddy);
@@ -108,53 +117,67 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
                                  (!YA ? (O + 7) / 8 * 8 : b0 + rows == B ? O : (O + 7) / 8 * 8 + 8)) * 2 +
                                     delta);
     // YA: bytes by which the lane's row starts past a 16-byte boundary
-    const uint32_t mb = YA ? (uint32_t)((delta + (uint64_t)lrow * (uint64_t)lddy * 2) & 15) : 0u;
+    uint32_t mb[MT];
     // elements the lane's piece ks of group g is loaded early by: 0 unless it
     // straddles O in dY's last row (then g is the last group)
-    int sh_last[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const int64_t over = (Gc - 1) * G + kofs + ks * 32 + 8 - O;
-        sh_last[ks] = (last_row && over > 0 && over < 8) ? (int)over : 0;
-    }
-    auto tail_shift = [&](int64_t g, int ks) __attribute__((always_inline)) -> int {
-        return g == Gc - 1 ? sh_last[ks] : 0;
-    };
+    int sh_last[MT][KS];
     // byte offset of the lane's first label in the tile (32 bits: the tile's
     // resource spans at most kMaxRsrcBytes; g * G * 2 < 2 * lddy for real groups)
-    const uint32_t yoff2 = delta + (uint32_t)(((int64_t)lrow * lddy + kofs) * 2);
-    // a: the fragment (YA: the aligned chunk holding its start); YA b: the next chunk
-    auto load_y = [&](int64_t g, u32x4 (&a)[KS], u32x4 (&b)[KS]) __attribute__((always_inline)) {
-        const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
+    uint32_t yoff2[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        mb[mt] = YA ? (uint32_t)((delta + (uint64_t)lrow[mt] * (uint64_t)lddy * 2) & 15) : 0u;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            const uint32_t o = yoff2 + go + ks * 64;
-            if constexpr (YA) {
-                a[ks] = buf_load16(yr, !kq_ok ? kOOB : last_row ? o - 2 * tail_shift(g, ks) : o - mb);
-                b[ks] = buf_load16(yr, !kq_ok || last_row ? kOOB : o - mb + 16);
-            } else {
-                a[ks] = buf_load16(yr, kq_ok ? o : kOOB);
+            const int64_t over = (Gc - 1) * G + kofs + ks * 32 + 8 - O;
+            sh_last[mt][ks] = (last_row[mt] && over > 0 && over < 8) ? (int)over : 0;
+        }
+        yoff2[mt] = delta + (uint32_t)(((int64_t)lrow[mt] * lddy + kofs) * 2);
+    }
+    auto tail_shift = [&](int64_t g, int mt, int ks) __attribute__((always_inline)) -> int {
+        return g == Gc - 1 ? sh_last[mt][ks] : 0;
+    };
+    // a: the fragment (YA: the aligned chunk holding its start); YA b: the next chunk
+    auto load_y = [&](int64_t g, u32x4 (&a)[MT][KS], u32x4 (&b)[MT][KS]) __attribute__((always_inline)) {
+        const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint32_t o = yoff2[mt] + go + ks * 64;
+                if constexpr (YA) {
+                    a[mt][ks] = buf_load16(yr, !kq_ok ? kOOB : last_row[mt] ? o - 2 * tail_shift(g, mt, ks) : o - mb[mt]);
+                    b[mt][ks] = buf_load16(yr, !kq_ok || last_row[mt] ? kOOB : o - mb[mt] + 16);
+                } else {
+                    a[mt][ks] = buf_load16(yr, kq_ok ? o : kOOB);
+                }
             }
         }
     };
     // The fragments of group g as the MFMA takes them: YA chunks joined; labels
     // >= O zeroed (only the last group has any: a uniform branch)
-    auto prep_y = [&](int64_t g, u32x4 (&a)[KS], const u32x4 (&b)[KS]) __attribute__((always_inline)) {
+    auto prep_y = [&](int64_t g, u32x4 (&a)[MT][KS], const u32x4 (&b)[MT][KS]) __attribute__((always_inline)) {
         if constexpr (YA) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) a[ks] = shift_pair16(a[ks], b[ks], last_row ? 0u : mb);
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    a[mt][ks] = shift_pair16(a[mt][ks], b[mt][ks], last_row[mt] ? 0u : mb[mt]);
         }
         const int64_t rem = O - g * G;  // labels of group g below O
         if (rem >= G) return;
         const int nr = (int)max<int64_t>(rem, 0);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int sh = tail_shift(g, ks);
-            if (sh) a[ks] = shift_down16(a[ks], sh);
-            const int nv = nr - (ks * 32 + kofs);
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                a[ks][e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
+            for (int ks = 0; ks < KS; ++ks) {
+                const int sh = tail_shift(g, mt, ks);
+                if (sh) a[mt][ks] = shift_down16(a[mt][ks], sh);
+                const int nv = nr - (ks * 32 + kofs);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    a[mt][ks][e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
+            }
         }
     };
 
@@ -219,14 +242,17 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // bytes) are conflict-free when a tile's features differ mod 16, which the
     // plan's dealing arranges.
     auto perm_col = [](int w, int q) { return (q & 1) * (BT / 2) + w * 8 + (q >> 1) * 4; };
-    char* const acc_b = reinterpret_cast<char*>(acc) + perm_col(wave, kq) * 4;
+    // (M tile mt of a wave adds the columns of the 16-row block wave * MT + mt)
+    char* acc_b[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc_b[mt] = reinterpret_cast<char*>(acc) + perm_col(wave * MT + mt, kq) * 4;
     // A round is up to RT staged tiles of one group.  Its MFMAs run on all RT
     // ring tiles (rows past the round's tiles are zero) and the products stay
     // in registers; the partial update (read, add, write) of a round runs in
     // the next iteration, in the same code as the next round's MFMAs, so the
     // products' latency and the update's LDS traffic overlap the next group.
     struct Round {
-        f32x4 c[RT];  // dY rows x W^T tile t
+        f32x4 c[MT][RT];  // dY rows of M tile mt x W^T tile t
         int f[RT];    // partial-row byte offset of the lane's position in tile t
         int n0, nt;   // uniform: layer-0 tiles and tiles of the round (nt 0: nothing to add)
     };
@@ -247,13 +273,16 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
             }
         }
     };
-    auto mma_round = [&](const u32x4 (&a)[KS], const u32x4 (&bf)[RT][KS], Round& r) __attribute__((always_inline)) {
+    auto mma_round = [&](const u32x4 (&a)[MT][KS], const u32x4 (&bf)[RT][KS], Round& r) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(a[ks], bf[t][ks], v);
-            r.c[t] = v;
+            for (int mt = 0; mt < MT; ++mt) {
+                f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(a[mt][ks], bf[t][ks], v);
+                r.c[mt][t] = v;
+            }
         }
     };
     // Partial update of a group's first round pr, whose first N0 tiles are
@@ -264,18 +293,24 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // next round (mma) are issued between the reads and the writes.
     auto update_first_n = [&](const Round& pr, auto n0, auto mma) __attribute__((always_inline)) {
         constexpr int N0 = decltype(n0)::value;
-        f32x4 old[N0 > 0 ? N0 : 1];
+        f32x4 old[MT][N0 > 0 ? N0 : 1];
 #pragma unroll
-        for (int t = 0; t < N0; ++t) old[t] = *reinterpret_cast<const f32x4*>(acc_b + pr.f[t]);
+        for (int t = 0; t < N0; ++t)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) old[mt][t] = *reinterpret_cast<const f32x4*>(acc_b[mt] + pr.f[t]);
         mma();
 #pragma unroll
         for (int t = 0; t < N0; ++t) {
-            f32x4 v = pr.c[t];
-            if (N0 + t < RT) v += pr.c[N0 + t];
-            *reinterpret_cast<f32x4*>(acc_b + pr.f[t]) = old[t] + v;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                f32x4 v = pr.c[mt][t];
+                if (N0 + t < RT) v += pr.c[mt][N0 + t];
+                *reinterpret_cast<f32x4*>(acc_b[mt] + pr.f[t]) = old[mt][t] + v;
+            }
         }
-        // every LDS op of the wave but the N0 writes has completed
-        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(N0));
+        // every LDS op of the wave but the MT*N0 writes has completed (a count
+        // above the counter's maximum waits for a little more)
+        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(MT * N0 < 15 ? MT * N0 : 15));
     };
     auto update_first = [&](const Round& pr, auto mma) __attribute__((always_inline)) {
         static_assert(RT <= 8, "ring tiles");
@@ -298,27 +333,35 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // order, so later passes and rounds see the writes.
     auto update_n = [&](const Round& pr, auto ntiles, auto mma) __attribute__((always_inline)) {
         constexpr int NTL = decltype(ntiles)::value;
-        f32x4 old[NTL > 0 ? NTL : 1];
+        f32x4 old[MT][NTL > 0 ? NTL : 1];
         int fa[NTL > 0 ? NTL : 1];
 #pragma unroll
         for (int t = 0; t < NTL; ++t) {
             fa[t] = t < pr.n0 ? pr.f[t] : trash_f;
-            old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) old[mt][t] = *reinterpret_cast<const f32x4*>(acc_b[mt] + fa[t]);
         }
         mma();
 #pragma unroll
-        for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + pr.c[t];
+        for (int t = 0; t < NTL; ++t)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                *reinterpret_cast<f32x4*>(acc_b[mt] + fa[t]) = old[mt][t] + pr.c[mt][t];
         if (pr.n0 < NTL) {
 #pragma unroll
             for (int t = 0; t < NTL; ++t) {
                 fa[t] = t >= pr.n0 ? pr.f[t] : trash_f;
-                old[t] = *reinterpret_cast<const f32x4*>(acc_b + fa[t]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) old[mt][t] = *reinterpret_cast<const f32x4*>(acc_b[mt] + fa[t]);
             }
 #pragma unroll
-            for (int t = 0; t < NTL; ++t) *reinterpret_cast<f32x4*>(acc_b + fa[t]) = old[t] + pr.c[t];
+            for (int t = 0; t < NTL; ++t)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    *reinterpret_cast<f32x4*>(acc_b[mt] + fa[t]) = old[mt][t] + pr.c[mt][t];
         }
-        // every LDS op of the wave but the last pass's NTL writes has completed
-        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(NTL));
+        // every LDS op of the wave but the last pass's MT*NTL writes has completed
+        __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(MT * NTL < 15 ? MT * NTL : 15));
     };
     // update of a further round pr, specialised for its tile count (a uniform switch)
     auto update = [&](const Round& pr, auto mma) __attribute__((always_inline)) {
@@ -340,7 +383,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     // Further rounds of a group whose range holds more than RT tiles, done
     // synchronously after the group's first round: staged into ring[buf] (not
     // in use by any wave at this point), multiplied and added at once.
-    auto extra_rounds = [&](int i, u32x2 m, int buf, const u32x4 (&a)[KS]) __attribute__((always_inline)) {
+    auto extra_rounds = [&](int i, u32x2 m, int buf, const u32x4 (&a)[MT][KS]) __attribute__((always_inline)) {
         const int ntot = (int)m[1] - (int)(m[0] & 0xFFFF);
         for (int t0 = RT; t0 < ntot; t0 += RT) {
             Stage st;
@@ -374,8 +417,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     constexpr int DEPTH = G >= 128 ? 2 : 5, NS = DEPTH + 1;
     static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0, "unroll");
     Stage stg[NS];
-    u32x4 ya[NS][KS];
-    u32x4 yb[YA ? NS : 1][KS];  // YA: the second chunk of each fragment
+    u32x4 ya[NS][MT][KS];
+    u32x4 yb[YA ? NS : 1][MT][KS];  // YA: the second chunk of each fragment
     u32x2 mraw[NS];
     u32x2 mu[DEPTH + 1];  // uniform meta of groups i .. i+DEPTH
     Round rd[2];          // round of group i in rd[i % 2]
@@ -459,7 +502,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void bwdf_main_kernel(
     }
 }
 
-template <typename T, int G, int WAVES, int RT, bool YA>
+template <typename T, int G, int WAVES, int RT, bool YA, int MT>
 int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                 int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
                 hipStream_t st) {
@@ -469,7 +512,7 @@ int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const ui
         set_error("haste_ffi_bwd_features: lddy = %lld too large", (long long)lddy);
         return HASTE_ERR_UNSUPPORTED;
     }
-    bwdf_main_kernel<T, G, WAVES, RT, YA><<<dim3((unsigned)grid), dim3(64 * WAVES), 0, st>>>(
+    bwdf_main_kernel<T, G, WAVES, RT, YA, MT><<<dim3((unsigned)grid), dim3(64 * WAVES / MT), 0, st>>>(
         tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
         (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
@@ -477,25 +520,26 @@ int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const ui
 }
 
 // the plan's ring size: 2, 3 or ring_tiles(G) tiles
-template <typename T, int G, int WAVES, bool YA>
+template <typename T, int G, int WAVES, bool YA, int MT>
 int launch_ring(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                 int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
                 hipStream_t st) {
     constexpr int R = ring_tiles(G);
-    if (p.RT == 2) return launch_main<T, G, WAVES, 2, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    if (p.RT == 2) return launch_main<T, G, WAVES, 2, YA, MT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
     if constexpr (R > 3) {
-        if (p.RT == 3) return launch_main<T, G, WAVES, 3, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+        if (p.RT == 3) return launch_main<T, G, WAVES, 3, YA, MT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
     }
-    return launch_main<T, G, WAVES, R, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    return launch_main<T, G, WAVES, R, YA, MT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
+constexpr int kBwdfMT = 2;  // 16-row M tiles per wave of the 128-column build
 template <typename T, int G, bool YA>
 int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
              int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
              int64_t O, hipStream_t st) {
     (void)F;
-    if (p.BT == 64) return launch_ring<T, G, 4, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-    return launch_ring<T, G, 8, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    if (p.BT == 64) return launch_ring<T, G, 4, YA, 1>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    return launch_ring<T, G, 8, YA, kBwdfMT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
 }  // namespace
