@@ -89,9 +89,6 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
     const int kofs = kq_ok ? kq * 8 : 0;
     const int trash_f = (C::DCMAX + (col & (kTrashRows - 1))) * AS * 4;
 
-    for (int i = tid * 4; i < dn * AS; i += NTH * 4)
-        *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
-
     // dY of this lane's row (rows >= B read as zero; labels >= O are masked at
     // use).  A row is read up to the 8-label piece boundary past O (YA: 8 more
     // labels), inside the next row when lddy < ceil8(O) + 8; dY's last row is
@@ -428,6 +425,9 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
         u32x2 m0[DEPTH + 1];
 #pragma unroll
         for (int k = 0; k <= DEPTH; ++k) m0[k] = load_meta(k);
+        // the partial is cleared while the first tile ranges load
+        for (int i = tid * 4; i < dn * AS; i += NTH * 4)
+            *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k <= DEPTH; ++k) mu[k] = uniform_meta(m0[k]);
         load_stage(0, mu[0], 0, stg[0]);

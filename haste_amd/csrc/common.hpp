@@ -75,11 +75,13 @@ template <>
 __device__ __forceinline__ float bits_to_f32<F16>(uint32_t h) { return f16_bits_to_f32(h); }
 
 // fp32 -> bf16 round-to-nearest-even (quiet NaN keeps the sign).
+// (NaN -> quiet NaN; a select, not a branch, so a loop over elements stays
+// straight-line code)
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t qnan = ((u >> 16) | 0x40u) & 0xFFFFu;
+    const uint32_t v = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    return (u & 0x7FFFFFFFu) > 0x7F800000u ? qnan : v;
 }
 
 __device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
@@ -160,9 +162,10 @@ __device__ __forceinline__ uint32_t philox_w0_32(uint32_t c0, uint32_t k0, uint3
 // Stochastic rounding fp32 -> bf16 bits (random low 16 bits added to the fp32
 // pattern, upper half kept); NaN -> quiet NaN.
 __device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t r) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
-    return (u + (r & 0xFFFFu)) >> 16;
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t qnan = ((u >> 16) | 0x40u) & 0xFFFFu;
+    const uint32_t v = (u + (r & 0xFFFFu)) >> 16;
+    return (u & 0x7FFFFFFFu) > 0x7F800000u ? qnan : v;
 }
 
 // One element of the fused SGD step (shared_ffi/sr_triton.py:109-168) under the
