@@ -15,8 +15,9 @@ namespace {
 // A workgroup owns (group slice s, feature range r, batch tile of BT = 16*WAVES
 // columns) and keeps dXT[range, tile] as an fp32 partial in LDS.  The tile's
 // rows are WAVES blocks of 16; a wave owns MT consecutive blocks (MT = 2 for
-// the 128-column build: four waves, one per SIMD, each reading the ring once
-// for two blocks), so no two waves touch the same LDS word of the partial.
+// the 128-column build of aligned dY rows: four waves, one per SIMD, each
+// reading the ring once for two blocks), so no two waves touch the same LDS
+// word of the partial.
 // Per group:
 //  - the group's W^T tiles for the range (and the partial-row offsets of their
 //    positions) are staged once into a double-buffered LDS ring, shared by all
@@ -532,14 +533,18 @@ int launch_ring(const int* tfeat, const int* meta, const uint16_t* twt, const ui
     return launch_main<T, G, WAVES, R, YA, MT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
-constexpr int kBwdfMT = 2;  // 16-row M tiles per wave of the 128-column build
+// 16-row M tiles per wave of the 128-column build: two for 16-byte aligned dY
+// rows; one for YA, whose second chunk per fragment would double the dY
+// registers (measured: 138 us with one, 169 us with two, config 1)
+template <bool YA>
+constexpr int bwdf_mt() { return YA ? 1 : 2; }
 template <typename T, int G, bool YA>
 int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
              int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
              int64_t O, hipStream_t st) {
     (void)F;
     if (p.BT == 64) return launch_ring<T, G, 4, YA, 1>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-    return launch_ring<T, G, 8, YA, kBwdfMT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    return launch_ring<T, G, 8, YA, bwdf_mt<YA>()>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
 }  // namespace
