@@ -98,7 +98,14 @@ struct BwdFPlan {
 inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
     BwdFPlan p;
     p.Gc = ceil_div(O, G);
-    p.BT = B <= 64 ? 64 : 128;
+    // 128 batch columns per workgroup, or 64 when the batch is that small or
+    // when a 128-column partial would split D into 8 or more feature ranges
+    // (every range re-reads dY; with 64 columns a range holds twice the
+    // features: config 3, D = 4096, 15 -> 8 ranges, bwd-features 868 -> 804 us;
+    // at 3-4 ranges the 128-column build is faster: config 1 103 vs 149 us)
+    p.BT = 128;
+    if (B <= 64 || ceil_div(D, (int64_t)max_dc(128, (int)G, (int)pick_ring(128, D, F, G))) >= 8)
+        p.BT = 64;
     p.nbt = ceil_div(B, p.BT);
     p.Bp = p.nbt * p.BT;
     p.RT = pick_ring(p.BT, D, F, G);
