@@ -75,18 +75,21 @@ struct BceArgs {
     float* part;
 };
 
-// dY = sigma(x) - y and the loss term of one element with label bit y (0 or 1),
-// in fp32 from the hardware exp2 / log2 / reciprocal (about 1 ulp each).  With
-// e = exp(-|x|) and r = 1 / (1 + e), sigma(x) and 1 - sigma(x) are r and e*r in
-// some order, so sigma(x) - 1 needs no cancelling subtraction.
-__device__ __forceinline__ float bce_term(float x, uint32_t y, float* dy) {
+// dY = sigma(x) - y of one element, in fp32 from the hardware exp2 and reciprocal
+// (about 1 ulp each).  With e = exp(-|x|) and r = 1 / (1 + e), sigma(x) and
+// 1 - sigma(x) are r and e*r in some order, so sigma(x) - 1 needs no cancelling
+// subtraction.  bce_sigma is the label-free case (y = 0) and also returns
+// d = 1 + e, whose log is the element's softplus term; bce_dy_pos is y = 1.
+__device__ __forceinline__ float bce_sigma(float x, float* d) {
     const float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(x) * 1.44269504088896341f);
-    const float d = 1.0f + e;
-    const float r = __builtin_amdgcn_rcpf(d);
-    const float er = e * r;
-    const bool pos = x >= 0.0f;
-    *dy = y ? -(pos ? er : r) : (pos ? r : er);
-    return __builtin_fmaxf(x, 0.0f) - (y ? x : 0.0f) + __builtin_amdgcn_logf(d) * 0.693147180559945309f;
+    *d = 1.0f + e;
+    const float r = __builtin_amdgcn_rcpf(*d);
+    return x >= 0.0f ? r : e * r;
+}
+__device__ __forceinline__ float bce_dy_pos(float x) {
+    const float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(x) * 1.44269504088896341f);
+    const float r = __builtin_amdgcn_rcpf(1.0f + e);
+    return -(x >= 0.0f ? e * r : r);
 }
 
 // LAST: the workgroup's group is the last one and holds fewer than G labels;
@@ -186,7 +189,12 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
     // holding labels l0 .. l0+G-1 start at word l0/32, bit l0 % 32)
     constexpr int YW = G >= 64 ? G / 32 : 2;
     const uint32_t ybit0 = (uint32_t)(l0 % 32);
+    // loss of the lane's elements: the max(x, 0) - y*x parts are summed, the
+    // d = 1 + exp(-|x|) factors (each in (1, 2]) multiplied over a tile -- at most
+    // 64 per lane, so the product stays below 2^64 -- and one log2 is taken per
+    // tile instead of one per element
     float lsum = 0.0f;
+    static_assert(C::MT * C::NT * 4 <= 64, "loss product range");
     for (int t = 0; t < ntiles; ++t) {
         const int b_base = b_chunk0 + t * kBT;
         const char* xs = Xg[C::NB == 1 ? 0 : t & 1];
@@ -234,6 +242,7 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
         // one batch row; they are staged in LDS and written as row segments.
         // Rows >= B fall outside the tile's resource.  The last (partial) group
         // stores per element instead, so no column >= O is written. ----
+        float dprod = 1.0f;  // BCE: the tile's d factors of this lane
         const rsrc_t orr = make_rsrc(out + (int64_t)b_base * ldo + l0,
                                      (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2);
         // BCE with logits wanted: the rounded logits go out directly, 8 bytes per
@@ -266,13 +275,31 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                     const uint32_t bit = ybit0 + (uint32_t)ll;
                     const uint32_t y4 = (yw[nt][bit >> 5] >> (bit & 31)) & 0xFu;
                     const bool row_ok = b_base + rb < B;
-                    float dy[4];
+                    float x[4], dy[4], lin = 0.0f, dp = 1.0f;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const uint32_t xb = (h[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu;
-                        const float term = bce_term(bits_to_f32<T>(xb), (y4 >> i) & 1u, &dy[i]);
-                        lsum += (row_ok && ll + i < nl) ? term : 0.0f;
+                        x[i] = bits_to_f32<T>((h[i >> 1] >> ((i & 1) * 16)) & 0xFFFFu);
+                        float d;
+                        dy[i] = bce_sigma(x[i], &d);
+                        const bool ok = !LAST || ll + i < nl;
+                        // max(x, 0) as a select on the compare sigma already made
+                        // (fmaxf adds a canonicalising max per element)
+                        lin += ok && x[i] >= 0.0f ? x[i] : 0.0f;
+                        dp *= ok ? d : 1.0f;
                     }
+                    // positive labels are sparse: a wave takes this branch only
+                    // when one of its lanes holds one among these 4 elements
+                    if (__builtin_amdgcn_ballot_w64(y4 != 0u) != 0) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            if ((y4 >> i) & 1u) {
+                                dy[i] = bce_dy_pos(x[i]);
+                                lin -= (!LAST || ll + i < nl) ? x[i] : 0.0f;
+                            }
+                        }
+                    }
+                    lsum += row_ok ? lin : 0.0f;
+                    dprod *= row_ok ? dp : 1.0f;
                     h = u32x2{pack2_rne<T>(dy[0], dy[1]), pack2_rne<T>(dy[2], dy[3])};
                 }
                 const uint32_t off = (uint32_t)((int64_t)rb * ldo + ll) * 2;
@@ -290,6 +317,7 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                 }
             }
         }
+        if constexpr (BCE) lsum += __builtin_amdgcn_logf(dprod) * 0.693147180559945309f;
         // staged rows go out as 16-byte stores, whole row segments per
         // instruction (full 128-byte lines at MT = 4); the wave reads back only
         // what it wrote, and a wave's LDS accesses complete in order
@@ -451,21 +479,31 @@ __global__ __launch_bounds__(256) void label_bits_kernel(const int32_t* __restri
     atomicOr(ybits + (int64_t)r * ldyw + c / 32, 1u << (c % 32));
 }
 
-// loss = sum of the n workgroup partials: each thread sums a strided subset in
-// order, then a fixed tree over the threads.  The same workgroup clears the
-// label words the call set (one launch instead of two small ones).
+// loss = sum of the n workgroup partials (workgroup 0): each thread sums a
+// strided subset in order, then a fixed tree over the threads.  Every
+// workgroup also clears the label words of 256 of the call's pairs (one launch
+// instead of two small ones).
 __global__ __launch_bounds__(256) void loss_sum_kernel(const float* __restrict__ part, int64_t n,
                                                        float* __restrict__ loss,
                                                        const int32_t* __restrict__ labels,
                                                        int64_t nnz, uint32_t* __restrict__ ybits,
                                                        int64_t ldyw, int B, int64_t O) {
     __shared__ float s[256];
-    for (int64_t i = threadIdx.x; i < nnz; i += 256) {
-        const int r = labels[2 * i], c = labels[2 * i + 1];
+    const int64_t li = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (li < nnz) {
+        const int r = labels[2 * li], c = labels[2 * li + 1];
         if (r >= 0 && r < B && c >= 0 && c < O) ybits[(int64_t)r * ldyw + c / 32] = 0u;
     }
+    if (blockIdx.x != 0) return;
+    // the partials in batches of 8 loads in flight, summed in index order
     float v = 0.0f;
-    for (int64_t i = threadIdx.x; i < n; i += 256) v += part[i];
+    for (int64_t i0 = threadIdx.x; i0 < n; i0 += 8 * 256) {
+        float pv[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pv[k] = i0 + k * 256 < n ? part[i0 + k * 256] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v += pv[k];
+    }
     s[threadIdx.x] = v;
     __syncthreads();
     for (int m = 128; m >= 1; m >>= 1) {
@@ -581,8 +619,8 @@ int run_forward_bce(const int32_t* idx, const void* xT, int64_t ldx, const void*
                  ? dispatch_g<BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st)
                  : dispatch_g<F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, &bce, st);
     if (rc != HASTE_OK) return rc;
-    loss_sum_kernel<<<dim3(1), dim3(256), 0, st>>>(part, L.nparts, loss, labels, nnz, ybits,
-                                                   L.ldyw, (int)B, O);
+    loss_sum_kernel<<<dim3((unsigned)std::max<int64_t>(1, ceil_div(nnz, 256))), dim3(256), 0, st>>>(
+        part, L.nparts, loss, labels, nnz, ybits, L.ldyw, (int)B, O);
     HASTE_CHECK_LAUNCH("haste_ffi_forward_bce");
     return HASTE_OK;
 }
