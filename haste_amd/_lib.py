@@ -52,6 +52,7 @@ SIGNATURES = {
                                                      _P, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
     "haste_ffi_bwd_features_workspace_size": (_I64, [_I64, _I64, _I64, _I64, _I64, _I32]),
     "haste_ffi_bwd_features_config": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I32, _P]),
+    "haste_ffi_bwd_features_set_build": (ctypes.c_int, [_I32]),
     "haste_ffi_bwd_features_plan": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                                    _I32, _P]),
     "haste_ffi_bwd_features": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64,

@@ -228,7 +228,8 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
         for (int k = 0; k < SPT; ++k) {
             const int c = tid + k * NTH;
             if (c < RT * 16 * CH)
-                *reinterpret_cast<u32x4*>(&ring[buf][(c / CH) * RB + (c % CH) * 16]) = st.w[k];
+                // chunk c of the stage in twt storage order
+                *reinterpret_cast<u32x4*>(&ring[buf][twt_row_of(c, G) * RB + twt_chunk_of(c, G) * 16]) = st.w[k];
         }
         if (tid < RT * 16) fring[buf][tid] = tid < nt * 16 ? st.f : (C::DCMAX + (tid & (kTrashRows - 1))) * AS * 4;
     };
@@ -503,7 +504,266 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
     }
 }
 
-template <typename T, int G, int WAVES, int RT, bool YA, int MT>
+// Direct build (dY rows on 16-byte boundaries): no LDS ring and no barrier per
+// group.  Each wave loads the MFMA operand fragments of a group's W^T tiles
+// straight from the workspace -- one contiguous 1 KB block per tile and k-step
+// in the chunk-major twt layout -- with the positions' partial-row offsets and
+// its dY fragments, two groups ahead, and adds its products into its own
+// columns of the partial (the same update as the ring build: a round of up to
+// RT tiles, layer-1 tiles added with their layer-0 pairs, further rounds of
+// large ranges done at once).  The waves share nothing until the partial is
+// written out.  Every wave reads the tiles itself: four times the ring's W^T
+// reads, from L2.
+template <typename T, int G, int WAVES, int RT_, int MT_>
+__global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
+    const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
+    const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
+    int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
+    using C = BwdFCfg<G, WAVES, RT_, MT_>;
+    constexpr int KS = C::KS, BT = C::BT, AS = C::AS, RT = C::RT, MT = C::MT, NTH = C::THREADS;
+    static_assert(G >= 32, "direct build: one 32-label k-step per fragment");
+    __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
+
+    const int64_t work = xcd_remap(blockIdx.x, (int64_t)S * ndr * nbt);
+    if (work < 0) return;
+    const int bt = (int)(work % nbt);
+    const int r = (int)((work / nbt) % ndr);
+    const int s = (int)(work / ((int64_t)nbt * ndr));
+    const int d_lo = r * Dc;
+    const int dn = min(Dc, D - d_lo);
+    const int64_t g_lo = (int64_t)s * gps;
+    const int64_t g_hi = min<int64_t>(Gc, g_lo + gps);
+    const int ng = (int)(g_hi - g_lo);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15;  // A row within the M tile / B column (tile position)
+    const int kq = lane >> 4;   // which 8 of the 32 K elements
+    const int trash_f = (C::DCMAX + (col & (kTrashRows - 1))) * AS * 4;
+
+    // dY fragments: row b0 + lrow[mt], labels g*G + 32*ks + 8*kq .. +7 (rows >=
+    // B and labels past the 8-label piece holding O - 1 read as zero)
+    const int b0 = bt * BT;
+    const int rows = min(BT, B - b0);
+    const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy, ((int64_t)(rows - 1) * lddy + (O + 7) / 8 * 8) * 2);
+    uint32_t yoff2[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        yoff2[mt] = (uint32_t)(((int64_t)((wave * MT + mt) * 16 + col) * lddy + kq * 8) * 2);
+    auto load_y = [&](int64_t g, u32x4 (&a)[MT][KS]) __attribute__((always_inline)) {
+        const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) a[mt][ks] = buf_load16(yr, yoff2[mt] + go + ks * 64);
+    };
+    // labels >= O zeroed (only the last group has any: a uniform branch)
+    auto prep_y = [&](int64_t g, u32x4 (&a)[MT][KS]) __attribute__((always_inline)) {
+        const int64_t rem = O - g * G;
+        if (rem >= G) return;
+        const int nr = (int)max<int64_t>(rem, 0);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int nv = nr - (ks * 32 + kq * 8);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    a[mt][ks][e] &= (2 * e + 1 < nv) ? 0xFFFFFFFFu : (2 * e < nv ? 0xFFFFu : 0u);
+            }
+        }
+    };
+    // tile range of group g_lo + i in range r (tb | tm << 16, te), as a buffer
+    // load (a scalar load would hold up the wave's LDS waits); past the slice: zero
+    const rsrc_t mr = make_rsrc(meta + (g_lo * ndr + r) * kMetaStride,
+                                ((int64_t)(max(ng, 1) - 1) * ndr + 1) * kMetaStride * 4);
+    auto load_meta = [&](int i) __attribute__((always_inline)) -> u32x2 {
+        return buf_load8(mr, i < ng ? (uint32_t)(i * ndr * kMetaStride * 4) : kOOB);
+    };
+    auto uniform_meta = [](const u32x2& m) __attribute__((always_inline)) -> u32x2 {
+        return u32x2{(uint32_t)__builtin_amdgcn_readfirstlane((int)m[0]),
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)m[1])};
+    };
+    // A round: the lane's operand fragments of tiles [tb + t0, tb + t0 + RT) of
+    // group g_lo + i (tiles past the range's read as zero) and the partial-row
+    // byte offsets of its position in each
+    struct Frag {
+        u32x4 b[RT][KS];
+        int f[RT];
+    };
+    auto load_frag = [&](int i, u32x2 m, int t0, Frag& fr) __attribute__((always_inline)) {
+        const int tb = __builtin_amdgcn_readfirstlane((int)(m[0] & 0xFFFF) + t0);
+        const int nt = __builtin_amdgcn_readfirstlane(max(0, min(RT, (int)m[1] - tb)));
+        const int64_t row0 = ((g_lo + __builtin_amdgcn_readfirstlane(i)) * Tcap + tb) * 16;
+        const rsrc_t wr = make_rsrc_u32(twt + row0 * G, (uint32_t)nt * 16 * G * 2);
+        const rsrc_t frr = make_rsrc_u32(tfeat + row0, (uint32_t)nt * 16 * 4);
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                fr.b[t][ks] = buf_load16(wr, (uint32_t)(t * 16 * G + (ks * 64 + lane) * 8) * 2);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) fr.f[t] = (int)buf_load4(frr, (uint32_t)(t * 16 + col) * 4);
+    };
+
+    auto perm_col = [](int w, int q) { return (q & 1) * (BT / 2) + w * 8 + (q >> 1) * 4; };
+    char* acc_b[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc_b[mt] = reinterpret_cast<char*>(acc) + perm_col(wave * MT + mt, kq) * 4;
+    struct Res {
+        f32x4 c[MT][RT];
+    };
+    auto mma_round = [&](const u32x4 (&a)[MT][KS], const Frag& fr, Res& rs) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(a[mt][ks], fr.b[t][ks], v);
+                rs.c[mt][t] = v;
+            }
+        }
+    };
+    // First round of a group with N0 layer-0 tiles: layer-1 tile t is the
+    // round's tile N0 + t and adds into its pair's rows.  The partial rows are
+    // read, the MFMAs issued, then the rows written.
+    auto first_n = [&](const u32x4 (&a)[MT][KS], const Frag& fr, auto n0) __attribute__((always_inline)) {
+        constexpr int N0 = decltype(n0)::value;
+        f32x4 old[MT][N0 > 0 ? N0 : 1];
+#pragma unroll
+        for (int t = 0; t < N0; ++t)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) old[mt][t] = *reinterpret_cast<const f32x4*>(acc_b[mt] + fr.f[t]);
+        if constexpr (N0 > 0) {
+            Res rs;
+            mma_round(a, fr, rs);
+#pragma unroll
+            for (int t = 0; t < N0; ++t) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f32x4 v = rs.c[mt][t];
+                    if (N0 + t < RT) v += rs.c[mt][N0 + t];
+                    *reinterpret_cast<f32x4*>(acc_b[mt] + fr.f[t]) = old[mt][t] + v;
+                }
+            }
+        }
+    };
+    auto first = [&](const u32x4 (&a)[MT][KS], const Frag& fr, int n0) __attribute__((always_inline)) {
+        static_assert(RT <= 8, "ring tiles");
+        using std::integral_constant;
+        switch (n0) {
+        case 0: first_n(a, fr, integral_constant<int, 0>{}); break;
+        case 1: first_n(a, fr, integral_constant<int, 1>{}); break;
+        case 2: first_n(a, fr, integral_constant<int, (RT >= 2 ? 2 : 1)>{}); break;
+        case 3: first_n(a, fr, integral_constant<int, (RT >= 3 ? 3 : 1)>{}); break;
+        case 4: first_n(a, fr, integral_constant<int, (RT >= 4 ? 4 : 1)>{}); break;
+        case 5: first_n(a, fr, integral_constant<int, (RT >= 5 ? 5 : 1)>{}); break;
+        case 6: first_n(a, fr, integral_constant<int, (RT >= 6 ? 6 : 1)>{}); break;
+        case 7: first_n(a, fr, integral_constant<int, (RT >= 7 ? 7 : 1)>{}); break;
+        default: first_n(a, fr, integral_constant<int, RT>{}); break;
+        }
+    };
+    // Further rounds of a range holding more than RT tiles (rare): loaded and
+    // added at once, layer 0 first (layer-1 tiles into trash rows), then layer 1.
+    auto extra_rounds = [&](int i, u32x2 m, const u32x4 (&a)[MT][KS]) __attribute__((always_inline)) {
+        const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
+        for (int t0 = RT; t0 < te - tb; t0 += RT) {
+            Frag fr;
+            load_frag(i, m, t0, fr);
+            Res rs;
+            mma_round(a, fr, rs);
+            const int n0 = max(0, tm - (tb + t0));
+            const int nt = min(RT, te - (tb + t0));
+#pragma unroll
+            for (int pass = 0; pass < 2; ++pass) {
+                if (pass == 1 && n0 >= nt) break;
+                f32x4 old[MT][RT];
+                int fa[RT];
+#pragma unroll
+                for (int t = 0; t < RT; ++t) {
+                    const bool mine = t < nt && (pass == 0 ? t < n0 : t >= n0);
+                    fa[t] = mine ? fr.f[t] : trash_f;
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) old[mt][t] = *reinterpret_cast<const f32x4*>(acc_b[mt] + fa[t]);
+                }
+#pragma unroll
+                for (int t = 0; t < RT; ++t)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        *reinterpret_cast<f32x4*>(acc_b[mt] + fa[t]) = old[mt][t] + rs.c[mt][t];
+            }
+        }
+    };
+
+    // ---- pipeline: slot i % NS holds group i's fragments.  Iteration i
+    // converts the meta of group i+DEPTH (loaded DEPTH iterations earlier, after
+    // that iteration's fragment loads, so its wait covers the fragments of group
+    // i), issues the loads of group i+DEPTH and the meta of group i+2*DEPTH, and
+    // processes group i.  kGroupUnroll iterations are unrolled so that every
+    // slot index is a constant; the loop runs whole unrolled iterations.  Five
+    // groups of look-ahead where a slot is small (rounds of at most 4
+    // fragments: short groups need the deeper pipeline), else two. ----
+    constexpr int DEPTH = RT * KS <= 4 ? 5 : 2, NS = DEPTH + 1;
+    static_assert(kGroupUnroll % NS == 0, "unroll");
+    Frag fq[NS];
+    u32x4 ya[NS][MT][KS];
+    u32x2 mraw[NS];
+    u32x2 mq[DEPTH];  // uniform meta of groups i .. i+DEPTH-1
+    {
+        u32x2 m0[DEPTH];
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) m0[k] = load_meta(k);
+        for (int i = tid * 4; i < dn * AS; i += NTH * 4)
+            *reinterpret_cast<f32x4*>(&acc[i]) = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) mq[k] = uniform_meta(m0[k]);
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_frag(k, mq[k], 0, fq[k % NS]);
+            load_y(g_lo + k, ya[k % NS]);
+            mraw[(k + DEPTH) % NS] = load_meta(k + DEPTH);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // the partial is clear
+    auto body = [&](int i, auto kc) __attribute__((always_inline)) {
+        constexpr int K = decltype(kc)::value;  // i % kGroupUnroll
+        constexpr int Q = K % NS;
+        const u32x2 mn = uniform_meta(mraw[(Q + DEPTH) % NS]);  // group i + DEPTH
+        load_frag(i + DEPTH, mn, 0, fq[(Q + DEPTH) % NS]);
+        load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS]);
+        mraw[(Q + 2 * DEPTH) % NS] = load_meta(i + 2 * DEPTH);
+        prep_y(g_lo + i, ya[Q]);
+        const u32x2 m = mq[0];
+        const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
+        first(ya[Q], fq[Q], min(tm - tb, min(RT, te - tb)));
+        if (te - tb > RT) extra_rounds(i, m, ya[Q]);  // uniform, rare
+#pragma unroll
+        for (int k = 0; k + 1 < DEPTH; ++k) mq[k] = mq[k + 1];
+        mq[DEPTH - 1] = mn;
+    };
+    for (int i = 0; i < ng; i += kGroupUnroll) {
+        body(i, std::integral_constant<int, 0>{});
+        body(i + 1, std::integral_constant<int, 1>{});
+        body(i + 2, std::integral_constant<int, 2>{});
+        body(i + 3, std::integral_constant<int, 3>{});
+        body(i + 4, std::integral_constant<int, 4>{});
+        body(i + 5, std::integral_constant<int, 5>{});
+    }
+    __syncthreads();
+
+    // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----
+    float* out = ws + ((int64_t)s * D + d_lo) * Bp + (int64_t)bt * BT;
+    for (int i = tid; i < dn * (BT / 4); i += NTH) {
+        const int d = i / (BT / 4), q = i % (BT / 4);  // natural columns 4q .. 4q+3
+        *reinterpret_cast<f32x4*>(out + (int64_t)d * Bp + q * 4) =
+            *reinterpret_cast<const f32x4*>(&acc[d * AS + perm_col(q / 4, q % 4)]);
+    }
+}
+
+template <typename T, int G, int WAVES, int RT, bool YA, int MT, bool DIRECT = false>
 int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                 int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
                 hipStream_t st) {
@@ -513,24 +773,29 @@ int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const ui
         set_error("haste_ffi_bwd_features: lddy = %lld too large", (long long)lddy);
         return HASTE_ERR_UNSUPPORTED;
     }
-    bwdf_main_kernel<T, G, WAVES, RT, YA, MT><<<dim3((unsigned)grid), dim3(64 * WAVES / MT), 0, st>>>(
-        tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
-        (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
+    if constexpr (DIRECT)
+        bwdf_direct_kernel<T, G, WAVES, RT, MT><<<dim3((unsigned)grid), dim3(64 * WAVES / MT), 0, st>>>(
+            tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
+            (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
+    else
+        bwdf_main_kernel<T, G, WAVES, RT, YA, MT><<<dim3((unsigned)grid), dim3(64 * WAVES / MT), 0, st>>>(
+            tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
+            (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");
     return HASTE_OK;
 }
 
 // the plan's ring size: 2, 3 or ring_tiles(G) tiles
-template <typename T, int G, int WAVES, bool YA, int MT>
+template <typename T, int G, int WAVES, bool YA, int MT, bool DIRECT = false>
 int launch_ring(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                 int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
                 hipStream_t st) {
     constexpr int R = ring_tiles(G);
-    if (p.RT == 2) return launch_main<T, G, WAVES, 2, YA, MT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    if (p.RT == 2) return launch_main<T, G, WAVES, 2, YA, MT, DIRECT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
     if constexpr (R > 3) {
-        if (p.RT == 3) return launch_main<T, G, WAVES, 3, YA, MT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+        if (p.RT == 3) return launch_main<T, G, WAVES, 3, YA, MT, DIRECT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
     }
-    return launch_main<T, G, WAVES, R, YA, MT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    return launch_main<T, G, WAVES, R, YA, MT, DIRECT>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 
 // 16-row M tiles per wave of the 128-column build: two for 16-byte aligned dY
@@ -543,6 +808,17 @@ int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint1
              int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
              int64_t O, hipStream_t st) {
     (void)F;
+    // The direct build where dY fits in the last-level cache (measured: config
+    // 1, 104 -> 101 us; config 3, 802 -> 611 us).  With a dY of 686 MB (config 2)
+    // it was slower than the ring build (305 -> 361 us), which keeps the waves
+    // of a workgroup in step on each group's dY and W^T.
+    if constexpr (!YA && (G == 32 || G == 64)) {
+        const int build = bwdf_build();
+        if (build == 2 || (build == 0 && B * lddy * 2 <= kMallBytes)) {
+            if (p.BT == 64) return launch_ring<T, G, 4, YA, 1, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+            return launch_ring<T, G, 8, YA, 2, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+        }
+    }
     if (p.BT == 64) return launch_ring<T, G, 4, YA, 1>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
     return launch_ring<T, G, 8, YA, bwdf_mt<YA>()>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }

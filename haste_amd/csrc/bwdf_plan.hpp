@@ -13,6 +13,7 @@
 //   meta   int32 [Gc, ndr, 2]   tb | tm << 16, te: tiles [tb, tm) layer 0, [tm, te)
 //                               layer 1 of the range
 //   twt    16-bit [Gc, Tcap*16, G]  W^T: row p = sum of W columns of position p
+//                               (tiles of 16 rows, chunk-major: twt_elem)
 //   partials fp32 [S, D, Bp]    per-slice partial sums of dX^T
 #pragma once
 
@@ -88,6 +89,28 @@ inline int64_t pick_ring(int64_t BT, int64_t D, int64_t F, int64_t G) {
     last = ring;
     return ring;
 }
+
+// W^T for G <= 64 (the sizes with a direct bwd-features build) is stored in
+// tiles of 16 rows, chunk-major: the 16-byte chunk k (labels 8k .. 8k+7) of row
+// p of a tile is chunk k*16 + p of the tile, so the 16 rows' chunk k -- what 16
+// lanes of an MFMA operand fragment read -- are one contiguous 256-byte block.
+// For G = 128 it is row-major.  Element offset of the chunk of labels lc ..
+// lc+7 of tile row `row` (a group's rows start at a multiple of 16), and the
+// (row, chunk) of a group's it-th chunk in storage order.
+__host__ __device__ constexpr bool twt_chunk_major(int G) { return G <= 64; }
+__host__ __device__ constexpr int64_t twt_elem(int64_t row, int lc, int G) {
+    return twt_chunk_major(G) ? (row / 16) * 16 * G + ((lc / 8) * 16 + row % 16) * 8 : row * G + lc;
+}
+__host__ __device__ constexpr int twt_row_of(int it, int G) {
+    return twt_chunk_major(G) ? (it / (2 * G)) * 16 + it % 16 : it / (G / 8);
+}
+__host__ __device__ constexpr int twt_chunk_of(int it, int G) {
+    return twt_chunk_major(G) ? (it / 16) % (G / 8) : it % (G / 8);
+}
+
+// The main-kernel build selected by haste_ffi_bwd_features_set_build (0 by
+// shape, 1 LDS ring, 2 direct where built).
+int bwdf_build();
 
 struct BwdFPlan {
     int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;

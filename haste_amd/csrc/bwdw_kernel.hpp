@@ -107,10 +107,9 @@ __device__ __forceinline__ u32x4 keep_first(u32x4 v, int nv) {
 template <int G, int FP>
 constexpr int bwdw_waves_per_simd() { return G == 64 && FP == 128 ? 4 : G * FP >= 128 * 256 ? 1 : 2; }
 
-// dY larger than the 256 MB last-level cache (MALL) of an MI355X: this kernel,
-// its last reader in a training step, streams it with non-temporal loads (YNT),
-// so it does not evict the weights that the next step's forward reads.
-constexpr int64_t kMallBytes = 256ll << 20;
+// dY larger than the last-level cache (kMallBytes): this kernel, its last
+// reader in a training step, streams it with non-temporal loads (YNT), so it
+// does not evict the weights that the next step's forward reads.
 constexpr int kLoadNT = 2;  // buffer-load cache policy: nt on gfx950
 
 template <typename T, int G, int FP, bool SGD, bool YNT, bool YS>
@@ -346,8 +345,14 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
         if (do_wt)
             for (int j = tid; j < F; j += kThreads) s_perm[j] = sg.perm[g * F + j];
     }
-    // W^T chunk it = tid + k*256 (k < kWtPre) is tile row it / (PR/8) of the group:
-    // its tsrc entry is loaded here, long before the W^T pass needs it
+    // The W^T pass of labels [p0, p0 + PR) writes chunk it (of the group's
+    // rows x PR/8 chunks) in twt storage order, so consecutive threads write
+    // consecutive 16 bytes: tile row wt_row(it), chunk p0/8 + wt_chk(it).
+    // Chunk it = tid + k*256 (k < kWtPre) has its tsrc entry loaded here, long
+    // before the pass needs it.
+    constexpr int CHP = PR / 8;
+    auto wt_row = [](int it) { return twt_chunk_major(G) ? (it / (16 * CHP)) * 16 + it % 16 : it / CHP; };
+    auto wt_chk = [](int it) { return twt_chunk_major(G) ? (it / 16) % CHP : it % CHP; };
     constexpr int kWtPre = 8;
     int wsrc[SGD ? kWtPre : 1];
     int wt_rows = 0;
@@ -357,7 +362,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
             const rsrc_t tr = make_rsrc(sg.tsrc + g * sg.Tcap * 16, (int64_t)sg.Tcap * 16 * 4);
 #pragma unroll
             for (int k = 0; k < kWtPre; ++k)
-                wsrc[k] = (int)buf_load4(tr, (uint32_t)((tid + k * kThreads) / (PR / 8)) * 4);
+                wsrc[k] = (int)buf_load4(tr, (uint32_t)wt_row(tid + k * kThreads) * 4);
         }
     }
 #pragma unroll 1
@@ -451,20 +456,20 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                         &stg[(l - p0) * SP + (slot >> 3) * 8])[slot & 7];
                 };
                 const int64_t rbase = g * sg.Tcap * 16;
-                const int nch = wt_rows * (PR / 8);
+                const int nch = wt_rows * CHP;
 #pragma unroll
                 for (int k = 0; k < kWtPre; ++k) {
                     const int it = tid + k * kThreads;
                     if (it < nch) {
-                        const int row = it / (PR / 8), lc = p0 + (it % (PR / 8)) * 8;
+                        const int row = wt_row(it), lc = p0 + wt_chk(it) * 8;
                         const u32x4 v = wt_chunk<BF16>(wsrc[k], s_perm, wv, lc);
-                        *reinterpret_cast<u32x4*>(sg.twt + (rbase + row) * G + lc) = v;
+                        *reinterpret_cast<u32x4*>(sg.twt + twt_elem(rbase + row, lc, G)) = v;
                     }
                 }
                 for (int it = tid + kWtPre * kThreads; it < nch; it += kThreads) {
-                    const int row = it / (PR / 8), lc = p0 + (it % (PR / 8)) * 8;
+                    const int row = wt_row(it), lc = p0 + wt_chk(it) * 8;
                     const u32x4 v = wt_chunk<BF16>(sg.tsrc[rbase + row], s_perm, wv, lc);
-                    *reinterpret_cast<u32x4*>(sg.twt + (rbase + row) * G + lc) = v;
+                    *reinterpret_cast<u32x4*>(sg.twt + twt_elem(rbase + row, lc, G)) = v;
                 }
             }
         }

@@ -11,6 +11,9 @@
 
 namespace haste {
 
+// The last-level cache (MALL, Infinity Cache) of an MI355X: 256 MB.
+constexpr int64_t kMallBytes = 256ll << 20;
+
 // ---------------------------------------------------------------- errors ----
 // Thread-local last error, returned by haste_last_error().
 void set_error(const char* fmt, ...);

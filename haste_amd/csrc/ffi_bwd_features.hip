@@ -34,7 +34,7 @@
 //  3. reduce: dXT = sum over slices s = 0..S-1 in ascending order (fp32 out), or
 //     fused with the bf16 stochastic rounding of shared_ffi/bindings.py:44-48.
 #include <algorithm>
-
+#include <atomic>
 #include <type_traits>
 
 #include "bwdf_main.hpp"
@@ -282,10 +282,11 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
         return (slot & 1) ? (w2 >> 16) : (w2 & 0xFFFFu);
     };
     constexpr int CH = G / 8;  // 16-byte chunks per row
+    // chunk it in twt storage order (consecutive threads write consecutive 16 bytes)
     for (int it = tid; it < nrows * CH; it += 256) {
-        const int row = it / CH, lc = (it % CH) * 8;
+        const int row = twt_row_of(it, G), lc = twt_chunk_of(it, G) * 8;
         const u32x4 v = wt_chunk<T>(tsrc[(g * Tcap) * 16 + row], s_perm, wv, lc);
-        *reinterpret_cast<u32x4*>(twt + ((g * Tcap) * 16 + row) * G + lc) = v;
+        *reinterpret_cast<u32x4*>(twt + twt_elem((g * Tcap) * 16 + row, lc, G)) = v;
     }
 }
 
@@ -458,6 +459,17 @@ extern "C" int haste_ffi_bwd_features_config(int64_t B, int64_t D, int64_t F, in
     cfg[2] = p.ndr;
     cfg[3] = p.S;
     return HASTE_OK;
+}
+
+namespace haste {
+static std::atomic<int> g_bwdf_build{0};
+int bwdf_build() { return g_bwdf_build.load(std::memory_order_relaxed); }
+}  // namespace haste
+
+extern "C" int haste_ffi_bwd_features_set_build(int32_t build) {
+    HASTE_CHECK_ARG(build >= 0 && build <= 2,
+                    "haste_ffi_bwd_features_set_build: build must be 0, 1 or 2 (got %d)", (int)build);
+    return haste::g_bwdf_build.exchange(build);
 }
 
 extern "C" int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace,

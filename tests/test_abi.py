@@ -156,3 +156,13 @@ def test_forward_bce_noalloc_rejects_shapes_beyond_its_scratch():
     assert "scratch" in _lib.last_error()
     # config 2 fits
     assert L.haste_ffi_forward_bce_workspace_size(512, 670091, 64) <= 64 << 20
+
+
+def test_bwd_features_set_build():
+    L = _lib.lib()
+    assert L.haste_ffi_bwd_features_set_build(3) == _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_ffi_bwd_features_set_build(-1) == _lib.HASTE_ERR_INVALID_ARG
+    prev = L.haste_ffi_bwd_features_set_build(1)
+    assert prev == 0
+    assert L.haste_ffi_bwd_features_set_build(2) == 1
+    assert L.haste_ffi_bwd_features_set_build(prev) == 2

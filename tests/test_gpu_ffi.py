@@ -93,16 +93,28 @@ def test_backward_features(dev, B, D, O, G, F, mode):
     torch.testing.assert_close(dXT.cpu(), ref, **TOL32)
 
 
-@pytest.mark.parametrize("B,D,O,G,F,mode", RING_CASES)
-def test_backward_features_every_build(dev, B, D, O, G, F, mode):
+# every (G, BT, RT) case under the LDS-ring build (1) and, where it exists
+# (G = 32, 64 with 16-byte aligned dY rows), the direct build (2)
+BUILD_CASES = [c + (1,) for c in RING_CASES] + [c + (2,) for c in RING_CASES if c[3] in (32, 64)]
+
+
+@pytest.mark.parametrize("B,D,O,G,F,mode,build", BUILD_CASES)
+def test_backward_features_every_build(dev, B, D, O, G, F, mode, build):
     """One shape per (G, batch tile, ring tiles) build of the main kernel (the
-    coverage of RING_CASES is checked on the CPU in test_abi.py)."""
+    coverage of RING_CASES is checked on the CPU in test_abi.py), under each
+    main-kernel build."""
     BT, RT, _, _ = kernel_config(_lib.lib(), B, D, O, G, F)
     x, W, bias, idx, dY = make_case(B, D, O, G, F, idx_mode=mode, seed=11)
-    dXT = _C.ffi_backward_features_cuda(x.t().contiguous().to(dev), W.to(dev), idx.to(dev),
-                                        dY.to(dev), B, D, F, O, G)
+    prev = _lib.lib().haste_ffi_bwd_features_set_build(build)
+    try:
+        dXT = _C.ffi_backward_features_cuda(x.t().contiguous().to(dev), W.to(dev), idx.to(dev),
+                                            dY.to(dev), B, D, F, O, G)
+        torch.cuda.synchronize()
+    finally:
+        _lib.lib().haste_ffi_bwd_features_set_build(prev)
     ref = oracle.ffi_backward_features(idx, W, dY, G, D)
-    torch.testing.assert_close(dXT.cpu(), ref, **TOL32, msg=lambda m: f"G={G} BT={BT} RT={RT}: {m}")
+    torch.testing.assert_close(dXT.cpu(), ref, **TOL32,
+                               msg=lambda m: f"G={G} BT={BT} RT={RT} build={build}: {m}")
 
 
 @pytest.mark.parametrize("B,D,O,G,F,mode", CASES[:6])
