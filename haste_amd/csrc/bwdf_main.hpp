@@ -504,8 +504,7 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
     }
 }
 
-// Direct build (dY rows on 16-byte boundaries): no LDS ring and no barrier per
-// group.  Each wave loads the MFMA operand fragments of a group's W^T tiles
+// Direct build: no LDS ring and no barrier per group.  Each wave loads the MFMA operand fragments of a group's W^T tiles
 // straight from the workspace -- one contiguous 1 KB block per tile and k-step
 // in the chunk-major twt layout -- with the positions' partial-row offsets and
 // its dY fragments, two groups ahead, and adds its products into its own
@@ -513,8 +512,9 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
 // RT tiles, layer-1 tiles added with their layer-0 pairs, further rounds of
 // large ranges done at once).  The waves share nothing until the partial is
 // written out.  Every wave reads the tiles itself: four times the ring's W^T
-// reads, from L2.
-template <typename T, int G, int WAVES, int RT_, int MT_>
+// reads, from L2.  YA: dY rows off 16-byte boundaries, loaded as in the ring
+// build (two aligned chunks per fragment, joined by a funnel shift).
+template <typename T, int G, int WAVES, int RT_, int MT_, bool YA>
 __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
     const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
@@ -542,23 +542,70 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     const int trash_f = (C::DCMAX + (col & (kTrashRows - 1))) * AS * 4;
 
     // dY fragments: row b0 + lrow[mt], labels g*G + 32*ks + 8*kq .. +7 (rows >=
-    // B and labels past the 8-label piece holding O - 1 read as zero)
+    // B read as zero, labels >= O masked at use).  A row is read up to the
+    // 8-label piece boundary past O (YA: 8 more labels), inside the next row when
+    // lddy < ceil8(O) + 8; dY's last row is read up to O only (YA), the piece
+    // that straddles O loaded early and shifted back.
     const int b0 = bt * BT;
     const int rows = min(BT, B - b0);
-    const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy, ((int64_t)(rows - 1) * lddy + (O + 7) / 8 * 8) * 2);
+    int lrow[MT];
+    bool last_row[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        lrow[mt] = (wave * MT + mt) * 16 + col;
+        last_row[mt] = YA && b0 + lrow[mt] == B - 1;
+    }
+    // (YA: the resource starts at the 16-byte boundary at or below the tile's
+    // first row, delta bytes before it)
+    const uintptr_t ytile = reinterpret_cast<uintptr_t>(dY + (int64_t)b0 * lddy);
+    const uint32_t delta = YA ? (uint32_t)(ytile & 15) : 0u;
+    const rsrc_t yr = make_rsrc(reinterpret_cast<const char*>(ytile - delta),
+                                ((int64_t)(rows - 1) * lddy +
+                                 (!YA ? (O + 7) / 8 * 8 : b0 + rows == B ? O : (O + 7) / 8 * 8 + 8)) * 2 +
+                                    delta);
+    uint32_t mb[MT];  // YA: bytes by which the lane's row starts past a 16-byte boundary
+    int sh_last[MT][KS];
     uint32_t yoff2[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-        yoff2[mt] = (uint32_t)(((int64_t)((wave * MT + mt) * 16 + col) * lddy + kq * 8) * 2);
-    auto load_y = [&](int64_t g, u32x4 (&a)[MT][KS]) __attribute__((always_inline)) {
+    for (int mt = 0; mt < MT; ++mt) {
+        mb[mt] = YA ? (uint32_t)((delta + (uint64_t)lrow[mt] * (uint64_t)lddy * 2) & 15) : 0u;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int64_t over = (Gc - 1) * G + kq * 8 + ks * 32 + 8 - O;
+            sh_last[mt][ks] = (last_row[mt] && over > 0 && over < 8) ? (int)over : 0;
+        }
+        yoff2[mt] = delta + (uint32_t)(((int64_t)lrow[mt] * lddy + kq * 8) * 2);
+    }
+    auto tail_shift = [&](int64_t g, int mt, int ks) __attribute__((always_inline)) -> int {
+        return g == Gc - 1 ? sh_last[mt][ks] : 0;
+    };
+    // a: the fragment (YA: the aligned chunk holding its start); YA b: the next chunk
+    auto load_y = [&](int64_t g, u32x4 (&a)[MT][KS], u32x4 (&b)[MT][KS]) __attribute__((always_inline)) {
         const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) a[mt][ks] = buf_load16(yr, yoff2[mt] + go + ks * 64);
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint32_t o = yoff2[mt] + go + ks * 64;
+                if constexpr (YA) {
+                    a[mt][ks] = buf_load16(yr, last_row[mt] ? o - 2 * tail_shift(g, mt, ks) : o - mb[mt]);
+                    b[mt][ks] = buf_load16(yr, last_row[mt] ? kOOB : o - mb[mt] + 16);
+                } else {
+                    a[mt][ks] = buf_load16(yr, o);
+                }
+            }
+        }
     };
-    // labels >= O zeroed (only the last group has any: a uniform branch)
-    auto prep_y = [&](int64_t g, u32x4 (&a)[MT][KS]) __attribute__((always_inline)) {
+    // the fragments as the MFMA takes them: YA chunks joined; labels >= O zeroed
+    // (only the last group has any: a uniform branch)
+    auto prep_y = [&](int64_t g, u32x4 (&a)[MT][KS], const u32x4 (&b)[MT][KS]) __attribute__((always_inline)) {
+        if constexpr (YA) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    a[mt][ks] = shift_pair16(a[mt][ks], b[mt][ks], last_row[mt] ? 0u : mb[mt]);
+        }
         const int64_t rem = O - g * G;
         if (rem >= G) return;
         const int nr = (int)max<int64_t>(rem, 0);
@@ -566,6 +613,8 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
+                const int sh = tail_shift(g, mt, ks);
+                if (sh) a[mt][ks] = shift_down16(a[mt][ks], sh);
                 const int nv = nr - (ks * 32 + kq * 8);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
@@ -708,6 +757,7 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     static_assert(kGroupUnroll % NS == 0, "unroll");
     Frag fq[NS];
     u32x4 ya[NS][MT][KS];
+    u32x4 yb[YA ? NS : 1][MT][KS];  // YA: the second chunk of each fragment
     u32x2 mraw[NS];
     u32x2 mq[DEPTH];  // uniform meta of groups i .. i+DEPTH-1
     {
@@ -722,7 +772,7 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
         for (int k = 0; k < DEPTH; ++k) {
             __builtin_amdgcn_sched_barrier(0);
             load_frag(k, mq[k], 0, fq[k % NS]);
-            load_y(g_lo + k, ya[k % NS]);
+            load_y(g_lo + k, ya[k % NS], yb[YA ? k % NS : 0]);
             mraw[(k + DEPTH) % NS] = load_meta(k + DEPTH);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -733,9 +783,9 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
         constexpr int Q = K % NS;
         const u32x2 mn = uniform_meta(mraw[(Q + DEPTH) % NS]);  // group i + DEPTH
         load_frag(i + DEPTH, mn, 0, fq[(Q + DEPTH) % NS]);
-        load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS]);
+        load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS], yb[YA ? (Q + DEPTH) % NS : 0]);
         mraw[(Q + 2 * DEPTH) % NS] = load_meta(i + 2 * DEPTH);
-        prep_y(g_lo + i, ya[Q]);
+        prep_y(g_lo + i, ya[Q], yb[YA ? Q : 0]);
         const u32x2 m = mq[0];
         const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
         first(ya[Q], fq[Q], min(tm - tb, min(RT, te - tb)));
@@ -774,7 +824,7 @@ int launch_main(const int* tfeat, const int* meta, const uint16_t* twt, const ui
         return HASTE_ERR_UNSUPPORTED;
     }
     if constexpr (DIRECT)
-        bwdf_direct_kernel<T, G, WAVES, RT, MT><<<dim3((unsigned)grid), dim3(64 * WAVES / MT), 0, st>>>(
+        bwdf_direct_kernel<T, G, WAVES, RT, MT, YA><<<dim3((unsigned)grid), dim3(64 * WAVES / MT), 0, st>>>(
             tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt,
             (int)p.ndr, (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
     else
@@ -808,13 +858,15 @@ int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint1
              int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
              int64_t O, hipStream_t st) {
     (void)F;
-    // The direct build where dY fits in the last-level cache (measured: config
-    // 1, 104 -> 101 us; config 3, 802 -> 611 us).  With a dY of 686 MB (config 2)
-    // it was slower than the ring build (305 -> 361 us), which keeps the waves
-    // of a workgroup in step on each group's dY and W^T.
-    if constexpr (!YA && (G == 32 || G == 64)) {
+    // The direct build for aligned dY rows where dY fits in the last-level cache
+    // (measured: config 1, 104 -> 101 us; config 3, 802 -> 611 us).  With a dY
+    // of 686 MB (config 2) it was slower than the ring build (305 -> 361 us),
+    // which keeps the waves of a workgroup in step on each group's dY and W^T.
+    // For YA rows it took as long as the ring build (138 us at config 1), whose
+    // default it is not.
+    if constexpr (G == 32 || G == 64) {
         const int build = bwdf_build();
-        if (build == 2 || (build == 0 && B * lddy * 2 <= kMallBytes)) {
+        if (build == 2 || (build == 0 && !YA && B * lddy * 2 <= kMallBytes)) {
             if (p.BT == 64) return launch_ring<T, G, 4, YA, 1, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
             return launch_ring<T, G, 8, YA, 2, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
         }

@@ -128,8 +128,8 @@ int haste_ffi_bwd_features_config(int64_t B, int64_t D, int64_t F, int64_t O, in
 /*
  * Selects the main kernel of later haste_ffi_bwd_features[_sr] calls in this
  * process (host-only): 0 (the default) chooses by shape; 1 always the LDS-ring
- * build; 2 the direct build wherever it exists (16-byte aligned dY rows,
- * G = 32 or 64), else the ring build.  Both builds give the same results up to
+ * build; 2 the direct build wherever it exists (G = 32 or 64), else the ring
+ * build.  Both builds give the same results up to
  * the order of fp32 additions.  Returns the previous setting, or
  * HASTE_ERR_INVALID_ARG for another value.  For tests and tuning; no
  * counterpart in the reference.

@@ -94,7 +94,7 @@ def test_backward_features(dev, B, D, O, G, F, mode):
 
 
 # every (G, BT, RT) case under the LDS-ring build (1) and, where it exists
-# (G = 32, 64 with 16-byte aligned dY rows), the direct build (2)
+# (G = 32, 64), the direct build (2)
 BUILD_CASES = [c + (1,) for c in RING_CASES] + [c + (2,) for c in RING_CASES if c[3] in (32, 64)]
 
 
@@ -262,6 +262,7 @@ def test_backward_weights_streaming_dY(dev):
         torch.testing.assert_close(db[l0:l1].cpu(), oracle.bias_grad(dy), **TOL32)
 
 
+@pytest.mark.parametrize("build", [1, 2])  # bwd-features main kernel: LDS ring, direct where built
 @pytest.mark.parametrize("B,D,O,G,F,pad,col0", [
     (37, 300, 2003, 64, 64, 0, 0),    # [B, O] contiguous, O odd
     (64, 768, 4133, 32, 32, 4, 0),    # odd row stride past O
@@ -272,12 +273,20 @@ def test_backward_weights_streaming_dY(dev):
     (130, 300, 5000, 64, 64, 3, 5),   # the view starts 5 columns into a row of 5008
     (70, 300, 3001, 32, 32, 0, 1001), # the tail columns of a head/tail concat
 ])
-def test_backward_reads_rows_at_any_stride(dev, oracle_mod, B, D, O, G, F, pad, col0):
+def test_backward_reads_rows_at_any_stride(dev, oracle_mod, B, D, O, G, F, pad, col0, build):
     """The backward kernels read grad-of-logits rows in place whatever their
     alignment (rows start on 2-byte boundaries) and read nothing past label O
     of the last row: the tensor here ends there, with NaN in the rest of each
     row.  Results are bit-identical to the same data in 16-byte aligned rows,
-    and match the oracle."""
+    and match the oracle, under each bwd-features main-kernel build."""
+    prev = _lib.lib().haste_ffi_bwd_features_set_build(build)
+    try:
+        _any_stride_case(dev, B, D, O, G, F, pad, col0)
+    finally:
+        _lib.lib().haste_ffi_bwd_features_set_build(prev)
+
+
+def _any_stride_case(dev, B, D, O, G, F, pad, col0):
     x, W, bias, idx, dY = make_case(B, D, O, G, F, idx_mode="random", seed=13)
     lddy = col0 + O + pad
     buf = torch.full(((B - 1) * lddy + col0 + O,), float("nan"), dtype=torch.bfloat16, device=dev)
