@@ -579,32 +579,57 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     auto tail_shift = [&](int64_t g, int mt, int ks) __attribute__((always_inline)) -> int {
         return g == Gc - 1 ? sh_last[mt][ks] : 0;
     };
-    // a: the fragment (YA: the aligned chunk holding its start); YA b: the next chunk
-    auto load_y = [&](int64_t g, u32x4 (&a)[MT][KS], u32x4 (&b)[MT][KS]) __attribute__((always_inline)) {
+    // a: the fragment (YA: the aligned chunk holding its start).  YA: the chunk
+    // after it is the aligned chunk that lane + 16 (the same row's next 8
+    // labels) loaded -- for the lanes of k-chunk 3 that of lane - 48 at the next
+    // k-step -- so it is taken across lanes (ds_bpermute) instead of loaded
+    // again; only k-chunk 3's last k-step loads its next chunk itself (e, one
+    // per M tile; the other lanes' e loads are out of range).
+    auto load_y = [&](int64_t g, u32x4 (&a)[MT][KS], u32x4 (&e)[MT][1]) __attribute__((always_inline)) {
         const uint32_t go = (uint32_t)g * (uint32_t)(G * 2);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const uint32_t o = yoff2[mt] + go + ks * 64;
-                if constexpr (YA) {
+                if constexpr (YA)
                     a[mt][ks] = buf_load16(yr, last_row[mt] ? o - 2 * tail_shift(g, mt, ks) : o - mb[mt]);
-                    b[mt][ks] = buf_load16(yr, last_row[mt] ? kOOB : o - mb[mt] + 16);
-                } else {
+                else
                     a[mt][ks] = buf_load16(yr, o);
-                }
+            }
+            if constexpr (YA) {
+                const uint32_t o = yoff2[mt] + go + (KS - 1) * 64;
+                e[mt][0] = buf_load16(yr, kq == 3 && !last_row[mt] ? o - mb[mt] + 16 : kOOB);
             }
         }
     };
+    const int nb_addr = ((lane + 16) & 63) * 4;  // ds_bpermute source: lane + 16
+    auto next_chunk = [&](const u32x4& v) __attribute__((always_inline)) -> u32x4 {
+        u32x4 r;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = (uint32_t)__builtin_amdgcn_ds_bpermute(nb_addr, (int)v[q]);
+        return r;
+    };
     // the fragments as the MFMA takes them: YA chunks joined; labels >= O zeroed
     // (only the last group has any: a uniform branch)
-    auto prep_y = [&](int64_t g, u32x4 (&a)[MT][KS], const u32x4 (&b)[MT][KS]) __attribute__((always_inline)) {
+    auto prep_y = [&](int64_t g, u32x4 (&a)[MT][KS], const u32x4 (&e)[MT][1]) __attribute__((always_inline)) {
         if constexpr (YA) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+            for (int mt = 0; mt < MT; ++mt) {
+                u32x4 nxt[KS];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    // what this lane offers to lane - 16: its own chunk, or for
+                    // k-chunk 0 (read by k-chunk 3 of the previous k-step) the
+                    // next k-step's chunk
+                    const u32x4 offer = (kq == 0 && ks + 1 < KS) ? a[mt][ks + 1] : a[mt][ks];
+                    nxt[ks] = next_chunk(offer);
+                    if (ks == KS - 1 && kq == 3) nxt[ks] = e[mt][0];
+                }
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
-                    a[mt][ks] = shift_pair16(a[mt][ks], b[mt][ks], last_row[mt] ? 0u : mb[mt]);
+                    a[mt][ks] = shift_pair16(a[mt][ks], nxt[ks], last_row[mt] ? 0u : mb[mt]);
+            }
         }
         const int64_t rem = O - g * G;
         if (rem >= G) return;
@@ -757,7 +782,7 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     static_assert(kGroupUnroll % NS == 0, "unroll");
     Frag fq[NS];
     u32x4 ya[NS][MT][KS];
-    u32x4 yb[YA ? NS : 1][MT][KS];  // YA: the second chunk of each fragment
+    u32x4 yb[YA ? NS : 1][MT][1];  // YA: k-chunk 3's chunk past the group
     u32x2 mraw[NS];
     u32x2 mq[DEPTH];  // uniform meta of groups i .. i+DEPTH-1
     {
@@ -858,15 +883,13 @@ int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint1
              int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t F,
              int64_t O, hipStream_t st) {
     (void)F;
-    // The direct build for aligned dY rows where dY fits in the last-level cache
-    // (measured: config 1, 104 -> 101 us; config 3, 802 -> 611 us).  With a dY
-    // of 686 MB (config 2) it was slower than the ring build (305 -> 361 us),
+    // The direct build where dY fits in the last-level cache (measured: config
+    // 1, 104 -> 101 us, YA rows 137 -> 122 us; config 3, 802 -> 611 us).  With a
+    // dY of 686 MB (config 2) it was slower than the ring build (305 -> 361 us),
     // which keeps the waves of a workgroup in step on each group's dY and W^T.
-    // For YA rows it took as long as the ring build (138 us at config 1), whose
-    // default it is not.
     if constexpr (G == 32 || G == 64) {
         const int build = bwdf_build();
-        if (build == 2 || (build == 0 && !YA && B * lddy * 2 <= kMallBytes)) {
+        if (build == 2 || (build == 0 && B * lddy * 2 <= kMallBytes)) {
             if (p.BT == 64) return launch_ring<T, G, 4, YA, 1, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
             return launch_ring<T, G, 8, YA, 2, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
         }
