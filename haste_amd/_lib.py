@@ -70,6 +70,8 @@ SIGNATURES = {
     "haste_sr_round_bf16": (ctypes.c_int, [_P, _P, _I64, _U64, _U64, _P]),
     "haste_sgd_sr_step": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _F32, _F32, _F32, _I32, _I32,
                                          _U64, _U64, _P]),
+    "haste_sgd_sr_step_f16": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _F32, _F32, _F32, _I32, _I32,
+                                         _U64, _U64, _P]),
     "haste_sgd_sr_step_multi": (ctypes.c_int, [ctypes.POINTER(SgdTensor), _I32, _I32, _F32, _F32,
                                                _F32, _I32, _I32, _U64, _P]),
     "haste_transpose_features": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I64, _P]),

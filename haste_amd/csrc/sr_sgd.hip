@@ -67,7 +67,18 @@ struct SgdBatch {
     int32_t count;
 };
 
-template <int GD, bool USE_MOM, bool DO_SR>
+// WF16: fp16 weights (an fp16 w_ptr in _sgd_m_wd_sr): read as fp16, and the
+// bf16 result of the update stored as fp16 (round to nearest even).
+template <bool WF16>
+__device__ __forceinline__ float w_to_f32(uint32_t h) {
+    return WF16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+}
+template <bool WF16>
+__device__ __forceinline__ uint32_t w_store_bits(uint32_t bf) {
+    return WF16 ? f32_to_f16_rne(bf16_bits_to_f32(bf)) : bf;
+}
+
+template <int GD, bool USE_MOM, bool DO_SR, bool WF16>
 __global__ __launch_bounds__(kSgdThreads) void sgd_sr_kernel(const SgdBatch b, float lr, float wd,
                                                              float mu, uint64_t seed) {
     const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
@@ -97,8 +108,8 @@ __global__ __launch_bounds__(kSgdThreads) void sgd_sr_kernel(const SgdBatch b, f
 #pragma unroll
         for (int e = 0; e < kVec; ++e) {
             uint32_t wb = (e & 1) ? (wv[e >> 1] >> 16) : (wv[e >> 1] & 0xFFFFu);
-            outb[e] = sgd_one(bf16_bits_to_f32(wb), gf[e], &mv[e], USE_MOM, lr, wd, mu, DO_SR,
-                              offset0 + (uint64_t)(i + e), k0, k1);
+            outb[e] = w_store_bits<WF16>(sgd_one(w_to_f32<WF16>(wb), gf[e], &mv[e], USE_MOM, lr,
+                                                 wd, mu, DO_SR, offset0 + (uint64_t)(i + e), k0, k1));
         }
         u32x4 ov;
 #pragma unroll
@@ -116,8 +127,9 @@ __global__ __launch_bounds__(kSgdThreads) void sgd_sr_kernel(const SgdBatch b, f
             const int64_t j = i + e;
             if (j >= n) break;
             float mv = USE_MOM ? m[j] : 0.f;
-            w[j] = (uint16_t)sgd_one(bf16_bits_to_f32(w[j]), load_grad1<GD>(g, j), &mv, USE_MOM,
-                                     lr, wd, mu, DO_SR, offset0 + (uint64_t)j, k0, k1);
+            w[j] = (uint16_t)w_store_bits<WF16>(sgd_one(w_to_f32<WF16>(w[j]), load_grad1<GD>(g, j),
+                                                        &mv, USE_MOM, lr, wd, mu, DO_SR,
+                                                        offset0 + (uint64_t)j, k0, k1));
             if (USE_MOM) m[j] = mv;
         }
     }
@@ -131,7 +143,7 @@ struct SgdTensor {
     uint64_t offset0;
 };
 
-template <int GD>
+template <int GD, bool WF16>
 int launch_sgd(const SgdTensor* ts, int count, float lr, float wd, float mu, int use_mom,
                int do_sr, uint64_t seed, hipStream_t st) {
     for (int base = 0; base < count; base += kMaxSegs) {
@@ -154,8 +166,8 @@ int launch_sgd(const SgdTensor* ts, int count, float lr, float wd, float mu, int
         if (c == 0) continue;
         HASTE_CHECK_ARG(blocks < (int64_t)1 << 31, "haste_sgd_sr_step: tensors too large");
 #define HASTE_SGD_LAUNCH(UM, SR)                                                               \
-    sgd_sr_kernel<GD, UM, SR><<<dim3((unsigned)blocks), dim3(kSgdThreads), 0, st>>>(b, lr, wd, \
-                                                                                   mu, seed)
+    sgd_sr_kernel<GD, UM, SR, WF16><<<dim3((unsigned)blocks), dim3(kSgdThreads), 0, st>>>(   \
+        b, lr, wd, mu, seed)
         if (use_mom && do_sr) HASTE_SGD_LAUNCH(true, true);
         else if (use_mom) HASTE_SGD_LAUNCH(true, false);
         else if (do_sr) HASTE_SGD_LAUNCH(false, true);
@@ -221,16 +233,17 @@ extern "C" int haste_sr_round_bf16(const float* x, uint16_t* out, int64_t n, uin
 }
 
 namespace {
+template <bool WF16 = false>
 int sgd_dispatch(const haste::SgdTensor* ts, int count, int32_t g_dtype, float lr, float wd,
                  float mu, int32_t use_mom, int32_t do_sr, uint64_t seed, hipStream_t st,
                  const char* fn) {
     switch (g_dtype) {
     case HASTE_DTYPE_BF16:
-        return haste::launch_sgd<HASTE_DTYPE_BF16>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
+        return haste::launch_sgd<HASTE_DTYPE_BF16, WF16>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
     case HASTE_DTYPE_F16:
-        return haste::launch_sgd<HASTE_DTYPE_F16>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
+        return haste::launch_sgd<HASTE_DTYPE_F16, WF16>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
     case HASTE_DTYPE_F32:
-        return haste::launch_sgd<HASTE_DTYPE_F32>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
+        return haste::launch_sgd<HASTE_DTYPE_F32, WF16>(ts, count, lr, wd, mu, use_mom, do_sr, seed, st);
     default:
         haste::set_error("%s: unsupported gradient dtype code %d", fn, (int)g_dtype);
         return HASTE_ERR_UNSUPPORTED;
@@ -248,6 +261,18 @@ extern "C" int haste_sgd_sr_step(uint16_t* w, const void* g, int32_t g_dtype, fl
     const haste::SgdTensor t{w, g, m, n, offset0};
     return sgd_dispatch(&t, 1, g_dtype, lr, wd, mu, use_mom, do_sr, seed,
                         static_cast<hipStream_t>(stream), "haste_sgd_sr_step");
+}
+
+extern "C" int haste_sgd_sr_step_f16(uint16_t* w, const void* g, int32_t g_dtype, float* m,
+                                     int64_t n, float lr, float wd, float mu, int32_t use_mom,
+                                     int32_t do_sr, uint64_t seed, uint64_t offset0, void* stream) {
+    HASTE_CHECK_ARG(n >= 0, "haste_sgd_sr_step_f16: n must be >= 0 (got %lld)", (long long)n);
+    if (n == 0) return HASTE_OK;
+    HASTE_CHECK_ARG(w != nullptr && g != nullptr, "haste_sgd_sr_step_f16: null pointer");
+    HASTE_CHECK_ARG(!use_mom || m != nullptr, "haste_sgd_sr_step_f16: momentum buffer is NULL");
+    const haste::SgdTensor t{w, g, m, n, offset0};
+    return sgd_dispatch<true>(&t, 1, g_dtype, lr, wd, mu, use_mom, do_sr, seed,
+                              static_cast<hipStream_t>(stream), "haste_sgd_sr_step_f16");
 }
 
 extern "C" int haste_sgd_sr_step_multi(const haste_sgd_tensor* tensors, int32_t count,

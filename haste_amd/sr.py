@@ -47,13 +47,16 @@ def sgd_update(weights: torch.Tensor, gradient: torch.Tensor, momentum_buf: torc
     else:
         assert weights.shape == gradient.shape
         assert not use_mom_flag, "momentum_buf is required when momentum is used"
-    if weights.dtype != torch.bfloat16:
-        raise NotImplementedError(f"sgd_update: weights must be bfloat16 (got {weights.dtype})")
+    if weights.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(f"sgd_update: weights must be bfloat16 or float16 "
+                                  f"(got {weights.dtype})")
     require_device(weights, "weights")
     require_device(gradient, "gradient")
     if use_mom_flag:
         assert momentum_buf.dtype == torch.float32
-    _lib.call("haste_sgd_sr_step", weights.data_ptr(), gradient.data_ptr(),
+    # fp16 weights: the bf16 result is stored as fp16, as the reference's store does
+    fn = "haste_sgd_sr_step" if weights.dtype == torch.bfloat16 else "haste_sgd_sr_step_f16"
+    _lib.call(fn, weights.data_ptr(), gradient.data_ptr(),
               dtype_code(gradient.dtype),
               momentum_buf.data_ptr() if use_mom_flag else None, weights.numel(),
               float(learning_rate), float(weight_decay), float(momentum), use_mom_flag,
@@ -70,6 +73,23 @@ def sgd_update_multi(weights, gradients, momentum_bufs, learning_rate: float, we
     assert len(gradients) == n and (momentum_bufs is None or len(momentum_bufs) == n)
     if n == 0:
         return
+    if any(w.dtype == torch.float16 for w in weights):
+        # fp16 weights go one tensor at a time (same seed, offsets from 0); the
+        # bf16 ones share the launch below
+        keep = []
+        for i, w in enumerate(weights):
+            m = None if momentum_bufs is None else momentum_bufs[i]
+            if w.dtype == torch.float16:
+                sgd_update(w, gradients[i], m, learning_rate, weight_decay, momentum,
+                           use_momentum, stochastic_rounding, seed)
+            else:
+                keep.append(i)
+        if not keep:
+            return
+        weights = [weights[i] for i in keep]
+        gradients = [gradients[i] for i in keep]
+        momentum_bufs = None if momentum_bufs is None else [momentum_bufs[i] for i in keep]
+        n = len(weights)
     use_mom_flag = 1 if (use_momentum and momentum != 0.0) else 0
     gdt = gradients[0].dtype
     arr = (_lib.SgdTensor * n)()

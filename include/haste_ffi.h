@@ -247,6 +247,17 @@ int haste_sgd_sr_step(uint16_t* w, const void* g, int32_t g_dtype, float* m, int
                       uint64_t seed, uint64_t offset0, void* stream);
 
 /*
+ * haste_sgd_sr_step on fp16 weights: w is read as fp16, the update computed and
+ * rounded to bf16 (SR or RNE) exactly as above, and that bf16 value stored as
+ * fp16 (round to nearest even) -- what _sgd_m_wd_sr does with an fp16 w_ptr,
+ * whose bf16 result the store converts (shared_ffi/sr_triton.py:111, 159-166;
+ * fp16 parameters reach it through SRSgd.step, shared_ffi/optim_sr.py:86-109).
+ */
+int haste_sgd_sr_step_f16(uint16_t* w, const void* g, int32_t g_dtype, float* m, int64_t n,
+                          float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
+                          uint64_t seed, uint64_t offset0, void* stream);
+
+/*
  * The same step over several tensors in one launch (one kernel per 8
  * tensors): tensor i uses offsets offset0_i + j.  SRSgd.step calls
  * sgd_update once per parameter (shared_ffi/optim_sr.py:64-112, all

@@ -67,6 +67,9 @@ def lib() -> ctypes.CDLL:
         L.ho_f32_to_bf16_rne.restype = ctypes.c_uint16
         L.ho_sr_round_bf16.argtypes = [P, P, i64, u64, u64]
         L.ho_sgd_sr_step.argtypes = [P, P, c_int, P, i64, f32, f32, f32, c_int, c_int, u64, u64]
+        L.ho_sgd_sr_step_f16w.argtypes = [P, P, c_int, P, i64, f32, f32, f32, c_int, c_int, u64,
+                                          u64]
+        L.ho_f32_to_f16_rne_arr.argtypes = [P, P, i64]
         L.ho_rewire_scores.argtypes = [P, P, i64, i64, i64]
         L.ho_rewire.argtypes = [P, P, i64, i64, i64, i64, c_int, f32, i64, c_int, c_int, f32, u64, P, P]
         L.ho_rewire.restype = i64
@@ -145,6 +148,35 @@ def sgd_sr_step(w_bits: np.ndarray, g: np.ndarray, m: np.ndarray | None, lr: flo
                          np.float32(lr), np.float32(wd), np.float32(mu), int(bool(use_mom)),
                          int(bool(do_sr)), seed, offset0)
     return w, mm
+
+
+def sgd_sr_step_f16w(w: np.ndarray, g: np.ndarray, m: np.ndarray | None, lr: float, wd: float,
+                     mu: float, use_mom: bool, do_sr: bool, seed: int, offset0: int = 0):
+    """_sgd_m_wd_sr on fp16 weights (shared_ffi/sr_triton.py:109-168 with an fp16
+    w_ptr: the bf16 result of the update is stored as fp16).  ``w`` is float16;
+    ``g`` as for sgd_sr_step.  Returns (new float16 weights, new momentum or None)."""
+    wb = np.array(np.asarray(w, dtype=np.float16).view(np.uint16), copy=True, order="C")
+    if g.dtype == np.uint16:
+        g_dtype = BF16
+    elif g.dtype == np.float16:
+        g_dtype = F16
+    else:
+        g_dtype = F32
+        g = g.astype(np.float32)
+    g = np.ascontiguousarray(g)
+    mm = None if m is None else np.array(m, dtype=np.float32, copy=True, order="C")
+    lib().ho_sgd_sr_step_f16w(_ptr(wb), _ptr(g), g_dtype, None if mm is None else _ptr(mm),
+                              wb.size, np.float32(lr), np.float32(wd), np.float32(mu),
+                              int(bool(use_mom)), int(bool(do_sr)), seed, offset0)
+    return wb.view(np.float16), mm
+
+
+def f32_to_f16_rne(x: np.ndarray) -> np.ndarray:
+    """The oracle's fp32 -> fp16 conversion (round to nearest even), as uint16 bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().ho_f32_to_f16_rne_arr(_ptr(x), _ptr(out), x.size)
+    return out
 
 
 def rewire_scores(w_bits: np.ndarray, G: int) -> np.ndarray:

@@ -120,6 +120,32 @@ float ho_f16_to_f32(uint16_t h) {
     return u2f(s | ((e + 112u) << 23) | (m << 13));
 }
 
+/* fp32 -> IEEE binary16, round to nearest even (overflow to infinity, NaN to a
+ * quiet NaN with the sign kept).  Pinned against numpy's float16 conversion. */
+uint16_t ho_f32_to_f16_rne(float f) {
+    uint32_t u = f2u(f);
+    uint32_t s = (u >> 16) & 0x8000u;
+    uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t)(s | 0x7E00u | ((a >> 13) & 0x3FFu));
+    if (a >= 0x47800000u) {  /* >= 65536: infinity, or the largest values round up to it */
+        return (uint16_t)(s | 0x7C00u);
+    }
+    if (a < 0x38800000u) {  /* below 2^-14: a subnormal (or zero) result */
+        /* value = a_float; result = round(value / 2^-24) as an integer mantissa */
+        float v = u2f(a);
+        double q = ldexp((double)v, 24);  /* exact: v has 24 significant bits */
+        double r = nearbyint(q);          /* round to nearest even (default mode) */
+        return (uint16_t)(s | (uint32_t)r);
+    }
+    /* normal range: keep 10 mantissa bits, round the dropped 13 to nearest even */
+    uint32_t e = (a >> 23) - 112u;
+    uint32_t m = a & 0x7FFFFFu;
+    uint32_t h = (e << 10) | (m >> 13);
+    uint32_t rest = m & 0x1FFFu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h += 1u;  /* may carry into e */
+    return (uint16_t)(s | h);
+}
+
 enum { HO_BF16 = 0, HO_F16 = 1, HO_F32 = 2 };
 
 static inline float load_any(const void* p, int dtype, int64_t i) {
@@ -157,6 +183,34 @@ void ho_sgd_sr_step(uint16_t* w, const void* g, int g_dtype, float* m, int64_t n
         w[i] = do_sr ? ho_sr_bf16(nw, ho_randint(seed, offset0 + (uint64_t)i))
                      : ho_f32_to_bf16_rne(nw);
     }
+}
+
+/* The same step on fp16 weights (an fp16 w_ptr in _sgd_m_wd_sr): w is read as
+ * fp16, the update rounded to bf16 as above (SR or RNE), and the bf16 value
+ * stored as fp16 (round to nearest even, the store's conversion). */
+void ho_sgd_sr_step_f16w(uint16_t* w, const void* g, int g_dtype, float* m, int64_t n,
+                         float lr, float wd, float mu, int use_mom, int do_sr,
+                         uint64_t seed, uint64_t offset0) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float wf = ho_f16_to_f32(w[i]);
+        float gf = load_any(g, g_dtype, i);
+        gf = fmaf(wd, wf, gf);
+        float upd = gf;
+        if (use_mom) {
+            float mv = fmaf(mu, m[i], gf);
+            m[i] = mv;
+            upd = mv;
+        }
+        float nw = fmaf(-lr, upd, wf);
+        uint16_t b = do_sr ? ho_sr_bf16(nw, ho_randint(seed, offset0 + (uint64_t)i))
+                           : ho_f32_to_bf16_rne(nw);
+        w[i] = ho_f32_to_f16_rne(ho_bf16_to_f32(b));
+    }
+}
+
+void ho_f32_to_f16_rne_arr(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ho_f32_to_f16_rne(x[i]);
 }
 
 int ho_num_threads(void) {

@@ -96,6 +96,51 @@ def test_sgd_update_api(dev):
     assert np.array_equal(bits(wd_), ref_w)
 
 
+@pytest.mark.parametrize("gdt", GRAD_DTYPES)
+@pytest.mark.parametrize("use_mom,do_sr", [(False, True), (True, True), (True, False)])
+@pytest.mark.parametrize("n", [8 * 1000 + 5, 16])
+def test_sgd_step_f16_weights(dev, gdt, use_mom, do_sr, n):
+    """fp16 weights (haste_sgd_sr_step_f16): bit-identical to the oracle's step
+    on fp16 weights, which is pinned on the CPU to the bf16-weight step followed
+    by numpy's fp16 conversion."""
+    g = torch.Generator().manual_seed(n + 1)
+    w = ((torch.rand(n, generator=g) - 0.5) * 4).to(torch.float16)
+    grad = (torch.randn(n, generator=g) * 0.05).to(gdt)
+    m = torch.randn(n, generator=g) * 0.01
+    wd_, gd_, md_ = w.to(dev), grad.to(dev), m.to(dev)
+    _lib.call("haste_sgd_sr_step_f16", wd_.data_ptr(), gd_.data_ptr(), _C.dtype_code(gdt),
+              md_.data_ptr() if use_mom else None, n, 0.05, 1e-4, 0.9, int(use_mom), int(do_sr),
+              2**33 + 43, 0, _C.stream_of(wd_))
+    g_np = bits(grad) if gdt == torch.bfloat16 else grad.numpy()
+    ref_w, ref_m = oracle.sgd_sr_step_f16w(w.numpy(), g_np, m.numpy() if use_mom else None, 0.05,
+                                           1e-4, 0.9, use_mom, do_sr, 2**33 + 43)
+    assert np.array_equal(wd_.cpu().numpy().view(np.uint16), ref_w.view(np.uint16))
+    if use_mom:
+        assert np.array_equal(md_.cpu().numpy().view(np.uint32), ref_m.view(np.uint32))
+
+
+def test_srsgd_f16_and_bf16_params(dev):
+    """SRSgd over an fp16 and a bf16 parameter (the reference sends both to
+    sgd_update): each matches the oracle with the step's seed, offsets from 0."""
+    from haste_amd.optim_sr import SRSgd
+    g = torch.Generator().manual_seed(3)
+    p16 = torch.nn.Parameter((torch.rand(1000, generator=g) - 0.5).to(torch.float16).to(dev))
+    pbf = torch.nn.Parameter((torch.rand(777, generator=g) - 0.5).to(torch.bfloat16).to(dev))
+    w16, wbf = p16.detach().cpu().clone(), pbf.detach().cpu().clone()
+    g16 = (torch.randn(1000, generator=g) * 0.05).to(torch.float16)
+    gbf = (torch.randn(777, generator=g) * 0.05).to(torch.bfloat16)
+    p16.grad, pbf.grad = g16.to(dev), gbf.to(dev)
+    opt = SRSgd([p16, pbf], lr=0.05, weight_decay=1e-4, momentum=0.9, seed=19)
+    opt.step()
+    m16 = np.zeros(1000, np.float32)
+    mbf = np.zeros(777, np.float32)
+    ref16, _ = oracle.sgd_sr_step_f16w(w16.numpy(), g16.numpy(), m16, 0.05, 1e-4, 0.9, True,
+                                       True, 19)
+    refbf, _ = oracle.sgd_sr_step(bits(wbf), bits(gbf), mbf, 0.05, 1e-4, 0.9, True, True, 19)
+    assert np.array_equal(p16.detach().cpu().numpy().view(np.uint16), ref16.view(np.uint16))
+    assert np.array_equal(bits(pbf.detach()), refbf)
+
+
 @pytest.mark.parametrize("use_mom", [False, True])
 def test_sgd_multi_matches_per_tensor_oracle(dev, use_mom):
     """One launch over tensors of mixed sizes (tails, an unaligned view, an empty one)

@@ -169,3 +169,54 @@ def test_sgd_closed_forms(oracle_mod):
     # momentum scales the old buffer, not the new gradient: m = 1, g = 1, mu = 0.25
     # -> m' = 1.25, w' = 0 - 1 * 1.25
     assert one(0.0, 1.0, 1.0, 1.0, 0.0, 0.25, True) == (-1.25, 1.25)
+
+
+def test_f32_to_f16_matches_numpy():
+    """The oracle's fp32 -> fp16 conversion (used for fp16 weights) is numpy's
+    round-to-nearest-even conversion: on every bf16 value (the inputs it gets),
+    on random fp32 values, and around the subnormal, overflow and halfway cases."""
+    import oracle
+    bf = np.arange(65536, dtype=np.uint32)
+    xs = [(bf << 16).view(np.float32)]
+    rng = np.random.default_rng(5)
+    xs.append(rng.standard_normal(100000).astype(np.float32) * np.float32(2.0) ** rng.integers(-30, 18, 100000).astype(np.float32))
+    edges = np.array([65504, 65519.99, 65520, 65536, 2.0 ** -14, 2.0 ** -24, 2.0 ** -25,
+                      1.5 * 2.0 ** -25, 3 * 2.0 ** -26, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11],
+                     dtype=np.float32)
+    xs.append(np.concatenate([edges, -edges]))
+    for x in xs:
+        finite = ~np.isnan(x)
+        got = oracle.f32_to_f16_rne(x[finite])
+        with np.errstate(over="ignore"):
+            ref = x[finite].astype(np.float16).view(np.uint16)
+        assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("gdt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("use_mom,do_sr", [(False, True), (True, True), (False, False)])
+def test_sgd_f16_weights_is_bf16_step_then_fp16_store(gdt, use_mom, do_sr):
+    """On fp16 weights the step is the bf16-weight step on the same fp32 values
+    (fp16 -> fp32 is exact), followed by the store's fp16 conversion (numpy's):
+    checked where the weights are bf16-representable, so both oracles take the
+    same inputs; with lr = 0 and no SR the weights are fp16(RNE_bf16(w))."""
+    import oracle
+    rng = np.random.default_rng(11)
+    n = 4099
+    w16 = (rng.random(n, dtype=np.float32) - 0.5).astype(np.float16)
+    wbf = f32_to_bf16_bits(w16.astype(np.float32))      # bf16 of the fp16 value
+    w16 = bf16_bits_to_f32(wbf).astype(np.float16)       # fp16 values that are bf16 exact
+    g32 = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    g = {"f32": g32, "bf16": f32_to_bf16_bits(g32), "f16": g32.astype(np.float16)}[gdt]
+    m = (rng.standard_normal(n) * 0.01).astype(np.float32)
+    got_w, got_m = oracle.sgd_sr_step_f16w(w16, g, m if use_mom else None, 0.05, 1e-4, 0.9,
+                                           use_mom, do_sr, 2**33 + 7)
+    ref_b, ref_m = oracle.sgd_sr_step(wbf, g, m if use_mom else None, 0.05, 1e-4, 0.9, use_mom,
+                                      do_sr, 2**33 + 7)
+    assert np.array_equal(got_w.view(np.uint16), bf16_bits_to_f32(ref_b).astype(np.float16).view(np.uint16))
+    if use_mom:
+        assert np.array_equal(got_m.view(np.uint32), ref_m.view(np.uint32))
+    # lr = 0, no SR: fp16 of the bf16 rounding of an arbitrary fp16 weight
+    w_any = (rng.standard_normal(n) * 3).astype(np.float16)
+    out, _ = oracle.sgd_sr_step_f16w(w_any, g, None, 0.0, 0.0, 0.0, False, False, 1)
+    expect = bf16_bits_to_f32(f32_to_bf16_bits(w_any.astype(np.float32))).astype(np.float16)
+    assert np.array_equal(out.view(np.uint16), expect.view(np.uint16))
