@@ -504,16 +504,17 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
     }
 }
 
-// Direct build: no LDS ring and no barrier per group.  Each wave loads the MFMA operand fragments of a group's W^T tiles
-// straight from the workspace -- one contiguous 1 KB block per tile and k-step
-// in the chunk-major twt layout -- with the positions' partial-row offsets and
-// its dY fragments, two groups ahead, and adds its products into its own
-// columns of the partial (the same update as the ring build: a round of up to
-// RT tiles, layer-1 tiles added with their layer-0 pairs, further rounds of
-// large ranges done at once).  The waves share nothing until the partial is
-// written out.  Every wave reads the tiles itself: four times the ring's W^T
-// reads, from L2.  YA: dY rows off 16-byte boundaries, loaded as in the ring
-// build (two aligned chunks per fragment, joined by a funnel shift).
+// Direct build: no LDS ring and no barrier per group.  Each wave loads the
+// MFMA operand fragments of a group's W^T tiles straight from the workspace
+// (one contiguous 1 KB block per tile and k-step in the chunk-major twt
+// layout), the positions' partial-row offsets and its dY fragments, two or
+// five groups ahead, and adds its products into its own columns of the partial
+// (the same update as the ring build: a round of up to RT tiles, layer-1 tiles
+// added with their layer-0 pairs, further rounds of large ranges done at
+// once).  The waves share nothing until the partial is written out.  Every
+// wave reads the tiles itself: four times the ring's W^T reads, from L2.  YA:
+// dY rows off 16-byte boundaries; a lane loads the aligned chunk holding its
+// fragment's start and takes the next one from a neighbouring lane.
 template <typename T, int G, int WAVES, int RT_, int MT_, bool YA>
 __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
