@@ -1,7 +1,8 @@
 // The main kernel of the backward to features (a workgroup per group slice x
-// feature range x batch tile, partial sums in LDS) and its launch templates.
-// Instantiated by ffi_bwd_features.hip for dY rows that start on 16-byte
-// boundaries and by ffi_bwd_features_ya.hip (YA) for any other rows.
+// feature range x batch tile, partial sums in LDS) in two builds -- the LDS-ring
+// build and the direct build -- and their launch templates.  Instantiated by
+// ffi_bwd_features.hip for dY rows that start on 16-byte boundaries and by
+// ffi_bwd_features_ya.hip (YA) for any other rows.
 #pragma once
 
 #include <type_traits>
