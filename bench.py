@@ -57,14 +57,17 @@ CONFIGS = {
 
 def phase_bytes(B, D, O, G, F):
     """Algorithmic HBM bytes per phase (bf16 tensors, momentum 0): every tensor
-    read or written once.  bwd_weights_sgd keeps the fp32 gradients on chip:
-    dY, X, idx read, W and bias read and written.  The unfused phases
-    (bwd_weights writing fp32 dW/dbias, sgd reading them) are listed too."""
+    read or written once.  The step's bwd_features reads dY, W and idx and leaves
+    dX (its per-slice partials) to bwd_weights_sgd, whose launch writes it; that
+    phase keeps the fp32 gradients on chip: dY, X, idx read, W and bias read and
+    written, dX written.  The unfused phases (bwd_weights writing fp32
+    dW/dbias, sgd reading them) are listed too."""
     Gc = (O + G - 1) // G
     return {
         "fwd": 2 * B * O + 2 * O * F + 4 * Gc * F + 2 * B * D + 2 * O,
-        "bwd_features": 2 * B * O + 2 * O * F + 4 * Gc * F + 2 * B * D,
-        "bwd_weights_sgd": 2 * B * O + 2 * B * D + 4 * Gc * F + (2 + 2) * O * F + (2 + 2) * O,
+        "bwd_features": 2 * B * O + 2 * O * F + 4 * Gc * F,
+        "bwd_weights_sgd": (2 * B * O + 2 * B * D + 4 * Gc * F + (2 + 2) * O * F + (2 + 2) * O
+                            + 2 * B * D),
         "bwd_weights": 2 * B * O + 2 * B * D + 4 * Gc * F + 4 * O * F + 4 * O,
         "sgd": (2 + 4 + 2) * O * F + (2 + 4 + 2) * O,
     }
@@ -191,7 +194,7 @@ def setup_step(cfg, dev):
 
 
 def step_fns(st, x, dY):
-    return [lambda: st.forward(x), lambda: st.backward_features(dY, st.ldo),
+    return [lambda: st.forward(x), lambda: st.backward_features(dY, st.ldo, defer_dx=True),
             lambda: st.backward_weights_sgd(dY, st.ldo)]
 
 
@@ -441,7 +444,7 @@ def main():
     # are not written): what a training loop runs per batch
     fl_names = ["fwd_bce", "bwd_features", "bwd_weights_sgd"]
     fl_ms, fl_per, _ = timed([lambda: st.forward_bce(x, labels),
-                              lambda: st.backward_features(st.dY_buf, ldy),
+                              lambda: st.backward_features(st.dY_buf, ldy, defer_dx=True),
                               lambda: st.backward_weights_sgd(st.dY_buf, ldy)],
                              max(5, args.steps // 2), 2, stream)
 

@@ -108,15 +108,69 @@ __host__ __device__ constexpr int twt_chunk_of(int it, int G) {
     return twt_chunk_major(G) ? (it / 16) % (G / 8) : it % (G / 8);
 }
 
-// The main-kernel build selected by haste_ffi_bwd_features_set_build (0 by
-// shape, 1 LDS ring, 2 direct where built).
-int bwdf_build();
-
 struct BwdFPlan {
     int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;
     int64_t RT, DCMAX;  // ring tiles of the main kernel; its partial's trash rows start at DCMAX
     int64_t tfeat_off, tsrc_off, perm_off, meta_off, twt_off, prep_bytes, ws_bytes;
 };
+
+// Sum of the S per-slice partials of dX^T (fp32 [S, D, Bp]) at feature d,
+// batch columns b4 .. b4+3.
+__device__ __forceinline__ f32x4 sum_slices(const float* __restrict__ ws, int64_t D, int Bp,
+                                            int S, int64_t d, int b4) {
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float* p = ws + d * Bp + b4;
+    const int64_t step = D * Bp;
+#pragma unroll 4
+    for (int s = 0; s < S; ++s) v += *reinterpret_cast<const f32x4*>(p + s * step);
+    return v;
+}
+
+// The final pass of backward to features with stochastic rounding, as a job of
+// ntiles tiles of 32 features x 32 batch columns (nx tiles along D): sum the
+// slices, transpose [D, B] -> [B, D] and round to bf16 with
+// tl.randint(seed, b*D + d).
+struct ReduceJob {
+    const float* ws;
+    uint16_t* dX;
+    int B, Bp, D, S, nx, ntiles;
+    uint32_t k0, k1;
+};
+
+inline ReduceJob reduce_job(const BwdFPlan& p, const float* ws, uint16_t* dX, int64_t B,
+                            int64_t D, uint64_t seed) {
+    ReduceJob j{ws, dX, (int)B, (int)p.Bp, (int)D, (int)p.S, (int)ceil_div(D, 32), 0,
+                (uint32_t)seed, (uint32_t)(seed >> 32)};
+    j.ntiles = j.nx * (int)ceil_div(B, 32);
+    return j;
+}
+
+// Tile `tile` of the job, by a workgroup of 256 threads; t: 32 x 33 floats of LDS.
+__device__ __forceinline__ void reduce_sr_tile(const ReduceJob& j, int tile, float (*t)[33]) {
+    const int d0 = (tile % j.nx) * 32, b0 = (tile / j.nx) * 32;
+    {
+        const int r = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (d0 + r < j.D) v = sum_slices(j.ws, j.D, j.Bp, j.S, d0 + r, b0 + c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[r][c4 + e] = v[e];
+    }
+    __syncthreads();
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // ty in 0..7
+    for (int r = ty; r < 32; r += 8) {
+        const int b = b0 + r, d = d0 + tx;
+        if (d < j.D && b < j.B) {
+            const uint64_t off = (uint64_t)b * j.D + d;
+            j.dX[(int64_t)b * j.D + d] = (uint16_t)sr_bf16(
+                t[tx][r], philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, j.k0, j.k1));
+        }
+    }
+}
+
+// The main-kernel build selected by haste_ffi_bwd_features_set_build (0 by
+// shape, 1 LDS ring, 2 direct where built).
+int bwdf_build();
+
 
 inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
     BwdFPlan p;

@@ -52,6 +52,7 @@ struct SgdArgs {
     const int* perm;
     const int* meta;
     int ndr, Tcap;
+    ReduceJob rj;  // ntiles > 0: workgroups Gc .. Gc + ntiles - 1 run this job's tiles
 };
 
 namespace {
@@ -129,7 +130,14 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     // the last group (partial when O % G != 0, the shortest workgroup) is
     // dispatched first: with Gc = 8k + 1 groups, XCD 0 holds one workgroup
     // more than the others, and it is then that one
-    const int64_t g = blockIdx.x == 0 ? (int64_t)gridDim.x - 1 : (int64_t)blockIdx.x - 1;
+    const int64_t Gc = (O + G - 1) / G;
+    if constexpr (SGD) {
+        if (blockIdx.x >= Gc) {
+            reduce_sr_tile(sg.rj, (int)(blockIdx.x - Gc), reinterpret_cast<float (*)[33]>(lds));
+            return;
+        }
+    }
+    const int64_t g = blockIdx.x == 0 ? Gc - 1 : (int64_t)blockIdx.x - 1;
     const int tid = threadIdx.x;
     // the wave index as a scalar: branches on wm / wn / active are then scalar
     // branches that skip their MFMAs (an MFMA under an EXEC mask still runs and
@@ -482,13 +490,13 @@ int launch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* 
            void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B, int64_t D, int64_t F,
            int64_t O, const SgdArgs& sg, hipStream_t st) {
     const int64_t Gc = ceil_div(O, G);
-    if (Gc > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes ||
+    if (Gc + (SGD ? sg.rj.ntiles : 0) > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes ||
         ((int64_t)kKC * lddy + 8) * 2 > kMaxRsrcBytes || (int64_t)G * F * 4 > kMaxRsrcBytes) {
         set_error("haste_ffi_bwd_weights: problem too large (Gc %lld, lddy %lld, D*ldx %lld)",
                   (long long)Gc, (long long)lddy, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
-    ffi_bwd_w_kernel<T, G, FP, SGD, YNT, YS><<<dim3((unsigned)Gc), dim3(kThreads), 0, st>>>(
+    ffi_bwd_w_kernel<T, G, FP, SGD, YNT, YS><<<dim3((unsigned)(Gc + (SGD ? sg.rj.ntiles : 0))), dim3(kThreads), 0, st>>>(
         idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, (int)B, (int)D, (int)F, O, sg);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_weights");
     return HASTE_OK;

@@ -293,16 +293,6 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
 // ------------------------------------------------------------- reduce ------
 // Both reduce kernels read the partials as 16-byte rows of 4 batch columns
 // (Bp is a multiple of 64, so every such read is in bounds and aligned).
-__device__ __forceinline__ f32x4 sum_slices(const float* __restrict__ ws, int64_t D, int Bp,
-                                            int S, int64_t d, int b4) {
-    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-    const float* p = ws + d * Bp + b4;
-    const int64_t step = D * Bp;
-#pragma unroll 4
-    for (int s = 0; s < S; ++s) v += *reinterpret_cast<const f32x4*>(p + s * step);
-    return v;
-}
-
 __global__ __launch_bounds__(256) void bwdf_reduce_kernel(const float* __restrict__ ws,
                                                           float* __restrict__ dXT, int B, int Bp,
                                                           int D, int S) {
@@ -321,29 +311,9 @@ __global__ __launch_bounds__(256) void bwdf_reduce_kernel(const float* __restric
 
 // Sum over slices, transpose [D, B] -> [B, D] and stochastically round to bf16
 // with tl.randint(seed, b*D + d).  Tile: 32 features x 32 batch columns.
-__global__ __launch_bounds__(256) void bwdf_reduce_sr_kernel(const float* __restrict__ ws,
-                                                             uint16_t* __restrict__ dX, int B,
-                                                             int Bp, int D, int S, uint32_t k0,
-                                                             uint32_t k1) {
+__global__ __launch_bounds__(256) void bwdf_reduce_sr_kernel(ReduceJob job) {
     __shared__ float t[32][33];
-    const int d0 = blockIdx.x * 32, b0 = blockIdx.y * 32;
-    {
-        const int r = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
-        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (d0 + r < D) v = sum_slices(ws, D, Bp, S, d0 + r, b0 + c4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[r][c4 + e] = v[e];
-    }
-    __syncthreads();
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // ty in 0..7
-    for (int r = ty; r < 32; r += 8) {
-        const int b = b0 + r, d = d0 + tx;
-        if (d < D && b < B) {
-            const uint64_t off = (uint64_t)b * D + d;
-            dX[(int64_t)b * D + d] =
-                (uint16_t)sr_bf16(t[tx][r], philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, k0, k1));
-        }
-    }
+    reduce_sr_tile(job, blockIdx.x, t);
 }
 
 // Checks the arguments and the workspace size; returns the plan.
@@ -524,12 +494,21 @@ extern "C" int haste_ffi_bwd_features_sr(const int32_t* idx, const void* W, cons
                                  workspace_bytes, B, D, F, O, G, dtype, plan_ready, st, &p);
     if (rc != HASTE_OK) return rc;
     const float* ws = reinterpret_cast<const float*>(static_cast<const char*>(workspace) + p.prep_bytes);
-    dim3 grid((unsigned)haste::ceil_div(D, 32), (unsigned)haste::ceil_div(B, 32));
-    haste::bwdf_reduce_sr_kernel<<<grid, dim3(256), 0, st>>>(ws, dX, (int)B, (int)p.Bp, (int)D,
-                                                            (int)p.S, (uint32_t)seed,
-                                                            (uint32_t)(seed >> 32));
+    const haste::ReduceJob job = haste::reduce_job(p, ws, dX, B, D, seed);
+    haste::bwdf_reduce_sr_kernel<<<dim3((unsigned)job.ntiles), dim3(256), 0, st>>>(job);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features_sr");
     return HASTE_OK;
+}
+
+extern "C" int haste_ffi_bwd_features_partials(const int32_t* idx, const void* W, const void* dY,
+                                               int64_t lddy, void* workspace,
+                                               int64_t workspace_bytes, int64_t B, int64_t D,
+                                               int64_t F, int64_t O, int64_t G, int32_t dtype,
+                                               int32_t plan_ready, void* stream) {
+    haste::BwdFPlan p;
+    return haste::run_partials("haste_ffi_bwd_features_partials", idx, W, dY, lddy, workspace,
+                               workspace_bytes, B, D, F, O, G, dtype, plan_ready,
+                               static_cast<hipStream_t>(stream), &p);
 }
 
 extern "C" int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype, float* m,

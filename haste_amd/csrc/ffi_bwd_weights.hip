@@ -70,36 +70,37 @@ extern "C" int haste_ffi_bwd_weights(const int32_t* idx, const void* xT, int64_t
                                              dbias_dtype, B, D, F, O, G, none, st);
 }
 
-extern "C" int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx,
-                                         const void* dY, int64_t lddy, uint16_t* W,
-                                         uint16_t* bias, float* m_W, float* m_bias, void* dW,
-                                         int32_t dW_dtype, void* dbias, int32_t dbias_dtype,
-                                         float lr, float wd, float mu, int32_t use_mom,
-                                         int32_t do_sr, uint64_t seed, void* bwdf_workspace,
-                                         int64_t bwdf_workspace_bytes, int64_t B, int64_t D,
-                                         int64_t F, int64_t O, int64_t G, int32_t dtype,
-                                         void* stream) {
-    const char* fn = "haste_ffi_bwd_weights_sgd";
-    int rc = haste::check_bwdw(fn, idx, xT, ldx, dY, lddy, dW_dtype, dbias, dbias_dtype, B, D, F,
-                               O, G, dtype);
+namespace haste {
+namespace {
+
+// The fused weight-gradient + SGD step; dX != NULL: also the final pass of
+// backward to features (the partials a haste_ffi_bwd_features_partials call
+// left in bwdf_workspace -> dX), as trailing workgroups of the same launch.
+int bwdw_sgd(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, const void* dY,
+             int64_t lddy, uint16_t* W, uint16_t* bias, float* m_W, float* m_bias, void* dW,
+             int32_t dW_dtype, void* dbias, int32_t dbias_dtype, float lr, float wd, float mu,
+             int32_t use_mom, int32_t do_sr, uint64_t seed, uint16_t* dX, uint64_t dx_seed,
+             void* bwdf_workspace, int64_t bwdf_workspace_bytes, int64_t B, int64_t D, int64_t F,
+             int64_t O, int64_t G, int32_t dtype, void* stream) {
+    int rc = check_bwdw(fn, idx, xT, ldx, dY, lddy, dW_dtype, dbias, dbias_dtype, B, D, F, O, G,
+                        dtype);
     if (rc != HASTE_OK) return rc;
     HASTE_CHECK_ARG(dtype == HASTE_DTYPE_BF16, "%s: the SGD step updates bf16 weights only", fn);
     if (O * F > 0xFFFFFFFFll) {
-        haste::set_error("%s: O*F = %lld exceeds 2^32 - 1 elements", fn, (long long)(O * F));
+        set_error("%s: O*F = %lld exceeds 2^32 - 1 elements", fn, (long long)(O * F));
         return HASTE_ERR_UNSUPPORTED;
     }
-    HASTE_CHECK_ARG(W != nullptr && haste::aligned16(W), "%s: W must be a 16-byte aligned pointer",
-                    fn);
-    HASTE_CHECK_ARG(dW == nullptr || haste::aligned16(dW), "%s: dW must be 16-byte aligned", fn);
-    HASTE_CHECK_ARG(!use_mom || (m_W != nullptr && haste::aligned16(m_W) &&
+    HASTE_CHECK_ARG(W != nullptr && aligned16(W), "%s: W must be a 16-byte aligned pointer", fn);
+    HASTE_CHECK_ARG(dW == nullptr || aligned16(dW), "%s: dW must be 16-byte aligned", fn);
+    HASTE_CHECK_ARG(!use_mom || (m_W != nullptr && aligned16(m_W) &&
                                  (bias == nullptr || m_bias != nullptr)),
                     "%s: momentum buffers missing or misaligned", fn);
-    haste::SgdArgs sg{W, bias, m_W, m_bias, lr, wd, mu, use_mom ? 1 : 0, do_sr ? 1 : 0,
-                      (uint32_t)seed, (uint32_t)(seed >> 32), nullptr, nullptr, nullptr, nullptr,
-                      0, 0};
+    SgdArgs sg{W, bias, m_W, m_bias, lr, wd, mu, use_mom ? 1 : 0, do_sr ? 1 : 0,
+               (uint32_t)seed, (uint32_t)(seed >> 32), nullptr, nullptr, nullptr, nullptr,
+               0, 0, ReduceJob{}};
     if (bwdf_workspace != nullptr) {
-        const haste::BwdFPlan p = haste::make_plan(B, D, F, O, G);
-        HASTE_CHECK_ARG(haste::aligned16(bwdf_workspace) &&
+        const BwdFPlan p = make_plan(B, D, F, O, G);
+        HASTE_CHECK_ARG(aligned16(bwdf_workspace) &&
                             bwdf_workspace_bytes >= p.prep_bytes + p.ws_bytes,
                         "%s: bwd-features workspace too small or misaligned (%lld bytes, need %lld)",
                         fn, (long long)bwdf_workspace_bytes, (long long)(p.prep_bytes + p.ws_bytes));
@@ -110,9 +111,46 @@ extern "C" int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int
         sg.meta = reinterpret_cast<const int*>(base + p.meta_off);
         sg.ndr = (int)p.ndr;
         sg.Tcap = (int)p.Tcap;
+        if (dX != nullptr)
+            sg.rj = reduce_job(p, reinterpret_cast<const float*>(base + p.prep_bytes), dX, B, D,
+                               dx_seed);
     }
-    return haste::dispatch<haste::BF16, true>(idx, static_cast<const uint16_t*>(xT), ldx,
-                                              static_cast<const uint16_t*>(dY), lddy, dW, dW_dtype,
-                                              dbias, dbias_dtype, B, D, F, O, G, sg,
-                                              static_cast<hipStream_t>(stream));
+    return dispatch<BF16, true>(idx, static_cast<const uint16_t*>(xT), ldx,
+                                static_cast<const uint16_t*>(dY), lddy, dW, dW_dtype, dbias,
+                                dbias_dtype, B, D, F, O, G, sg, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+}  // namespace haste
+
+extern "C" int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx,
+                                         const void* dY, int64_t lddy, uint16_t* W,
+                                         uint16_t* bias, float* m_W, float* m_bias, void* dW,
+                                         int32_t dW_dtype, void* dbias, int32_t dbias_dtype,
+                                         float lr, float wd, float mu, int32_t use_mom,
+                                         int32_t do_sr, uint64_t seed, void* bwdf_workspace,
+                                         int64_t bwdf_workspace_bytes, int64_t B, int64_t D,
+                                         int64_t F, int64_t O, int64_t G, int32_t dtype,
+                                         void* stream) {
+    return haste::bwdw_sgd("haste_ffi_bwd_weights_sgd", idx, xT, ldx, dY, lddy, W, bias, m_W,
+                           m_bias, dW, dW_dtype, dbias, dbias_dtype, lr, wd, mu, use_mom, do_sr,
+                           seed, nullptr, 0, bwdf_workspace, bwdf_workspace_bytes, B, D, F, O, G,
+                           dtype, stream);
+}
+
+extern "C" int haste_ffi_bwd_weights_sgd_dx(const int32_t* idx, const void* xT, int64_t ldx,
+                                            const void* dY, int64_t lddy, uint16_t* W,
+                                            uint16_t* bias, float* m_W, float* m_bias, float lr,
+                                            float wd, float mu, int32_t use_mom, int32_t do_sr,
+                                            uint64_t seed, uint16_t* dX, uint64_t dx_seed,
+                                            void* bwdf_workspace, int64_t bwdf_workspace_bytes,
+                                            int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+                                            int32_t dtype, void* stream) {
+    const char* fn = "haste_ffi_bwd_weights_sgd_dx";
+    HASTE_CHECK_ARG(dX != nullptr && bwdf_workspace != nullptr,
+                    "%s: dX and the bwd-features workspace are required", fn);
+    return haste::bwdw_sgd(fn, idx, xT, ldx, dY, lddy, W, bias, m_W, m_bias, nullptr,
+                           HASTE_DTYPE_F32, nullptr, HASTE_DTYPE_F32, lr, wd, mu, use_mom, do_sr,
+                           seed, dX, dx_seed, bwdf_workspace, bwdf_workspace_bytes, B, D, F, O, G,
+                           dtype, stream);
 }

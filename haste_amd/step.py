@@ -55,6 +55,7 @@ class FFITrainStep:
         # (written by backward_features, or by backward_weights_sgd for the weights
         # it updates); None when stale
         self._wt_version = None
+        self._dx_pending = False  # backward_features(defer_dx=True) left dX to the weight update
         self.bce_ws = None   # forward_bce's label bits + loss partials (allocated on first use)
         self.dY_buf = None
         self.loss_buf = None
@@ -154,7 +155,7 @@ class FFITrainStep:
         gradient -> backward to features (dX) -> fused weight/bias gradient +
         SR-SGD.  Returns the loss (0-d fp32 device tensor) of the step's forward."""
         loss = self.forward_bce(x, labels)
-        self.backward_features(self.dY_buf, self.ldo)
+        self.backward_features(self.dY_buf, self.ldo, defer_dx=True)
         self.backward_weights_sgd(self.dY_buf, self.ldo)
         return loss
 
@@ -166,24 +167,37 @@ class FFITrainStep:
                              f"stride lddy >= {self.O} (a multiple of 8 when O < 8; got "
                              f"{dY.dtype}, {dY.numel()} elements, lddy={lddy})")
 
-    def backward_features(self, dY: torch.Tensor, lddy: int) -> None:
-        """dX [B, D] bf16 = SR(feature gradient, seed 123) (bindings.py:44-48)."""
+    def backward_features(self, dY: torch.Tensor, lddy: int, defer_dx: bool = False) -> None:
+        """dX [B, D] bf16 = SR(feature gradient, seed 123) (bindings.py:44-48).
+        ``defer_dx``: leave the per-slice partial sums in the workspace; the next
+        ``backward_weights_sgd`` writes dX from them in its own launch (the final
+        pass then fills the tail of the weight update instead of being a kernel of
+        its own).  dX is not valid in between."""
         self._check_dY(dY, lddy)
         # the index plan depends on idx only: rebuilt when idx changes (rewire);
         # W^T is reused when the last fused weight update wrote it for these weights
         ready = 0
         if self._plan_version == self.idx._version:
             ready = 2 if self._wt_version == self.W._version else 1
-        _lib.call("haste_ffi_bwd_features_sr", self.idx.data_ptr(), self.W.data_ptr(),
-                  dY.data_ptr(), lddy, self.dX.data_ptr(), SR_SEED_GRAD_X, self.ws.data_ptr(),
-                  self.ws.numel(), self.B, self.D, self.F, self.O, self.G, self.code, ready,
-                  _C.stream_of(self.W))
+        if defer_dx:
+            _lib.call("haste_ffi_bwd_features_partials", self.idx.data_ptr(), self.W.data_ptr(),
+                      dY.data_ptr(), lddy, self.ws.data_ptr(), self.ws.numel(), self.B, self.D,
+                      self.F, self.O, self.G, self.code, ready, _C.stream_of(self.W))
+        else:
+            _lib.call("haste_ffi_bwd_features_sr", self.idx.data_ptr(), self.W.data_ptr(),
+                      dY.data_ptr(), lddy, self.dX.data_ptr(), SR_SEED_GRAD_X, self.ws.data_ptr(),
+                      self.ws.numel(), self.B, self.D, self.F, self.O, self.G, self.code, ready,
+                      _C.stream_of(self.W))
+        self._dx_pending = defer_dx
         self._plan_version = self.idx._version
         self._wt_version = self.W._version
 
     def backward_weights(self, dY: torch.Tensor, lddy: int) -> None:
         """dW [O, F] and dbias [O] in grad_dtype."""
         self._check_dY(dY, lddy)
+        if self._dx_pending:
+            raise RuntimeError("FFITrainStep.backward_weights: dX of backward_features("
+                               "defer_dx=True) is finished by backward_weights_sgd only")
         self._grad_buffers()
         _lib.call("haste_ffi_bwd_weights", self.idx.data_ptr(), self.xT_buf.data_ptr(), self.ldx,
                   dY.data_ptr(), lddy, self.dW.data_ptr(), self.gcode,
@@ -210,19 +224,32 @@ class FFITrainStep:
     def backward_weights_sgd(self, dY: torch.Tensor, lddy: int) -> None:
         """Weight and bias gradients (fp32, kept on chip) applied at once by SR-SGD
         (momentum 0) with the current seed, then seed += 1: bit-identical to
-        ``backward_weights`` + ``sgd`` with fp32 gradients, in one kernel."""
+        ``backward_weights`` + ``sgd`` with fp32 gradients, in one kernel.  After
+        ``backward_features(defer_dx=True)`` the same launch also writes dX."""
         self._check_dY(dY, lddy)
         if self.grad_dtype != torch.float32:
             raise ValueError("FFITrainStep.backward_weights_sgd: the fused update uses fp32 "
                              "gradients (grad_dtype=torch.float32)")
         # refresh W^T in the bwd-features workspace when its plan matches idx
         plan_ok = self._plan_version == self.idx._version
-        _lib.call("haste_ffi_bwd_weights_sgd", self.idx.data_ptr(), self.xT_buf.data_ptr(),
-                  self.ldx, dY.data_ptr(), lddy, self.W.data_ptr(),
-                  None if self.bias is None else self.bias.data_ptr(), None, None, None,
-                  _lib.DTYPE_F32, None, _lib.DTYPE_F32, self.lr, self.wd, 0.0, 0, 1, self.seed,
-                  self.ws.data_ptr() if plan_ok else None, self.ws.numel() if plan_ok else 0,
-                  self.B, self.D, self.F, self.O, self.G, self.code, _C.stream_of(self.W))
+        bias = None if self.bias is None else self.bias.data_ptr()
+        if self._dx_pending:
+            if not plan_ok:
+                raise RuntimeError("FFITrainStep.backward_weights_sgd: idx changed after "
+                                   "backward_features(defer_dx=True)")
+            _lib.call("haste_ffi_bwd_weights_sgd_dx", self.idx.data_ptr(), self.xT_buf.data_ptr(),
+                      self.ldx, dY.data_ptr(), lddy, self.W.data_ptr(), bias, None, None, self.lr,
+                      self.wd, 0.0, 0, 1, self.seed, self.dX.data_ptr(), SR_SEED_GRAD_X,
+                      self.ws.data_ptr(), self.ws.numel(), self.B, self.D, self.F, self.O, self.G,
+                      self.code, _C.stream_of(self.W))
+            self._dx_pending = False
+        else:
+            _lib.call("haste_ffi_bwd_weights_sgd", self.idx.data_ptr(), self.xT_buf.data_ptr(),
+                      self.ldx, dY.data_ptr(), lddy, self.W.data_ptr(), bias, None, None, None,
+                      _lib.DTYPE_F32, None, _lib.DTYPE_F32, self.lr, self.wd, 0.0, 0, 1,
+                      self.seed, self.ws.data_ptr() if plan_ok else None,
+                      self.ws.numel() if plan_ok else 0, self.B, self.D, self.F, self.O, self.G,
+                      self.code, _C.stream_of(self.W))
         # the kernel wrote W in place: move torch's version counter, as an in-place
         # torch op would, and record that the workspace holds W^T of this version
         torch.autograd.graph.increment_version(self.W)
@@ -230,7 +257,8 @@ class FFITrainStep:
         self.seed += 1
 
     def step(self, x: torch.Tensor, dY: torch.Tensor, lddy: int) -> None:
-        """forward -> backward to features (dX) -> fused weight/bias gradient + SR-SGD."""
+        """forward -> backward to features (partials) -> fused weight/bias gradient +
+        SR-SGD, whose launch also finishes dX."""
         self.forward(x)
-        self.backward_features(dY, lddy)
+        self.backward_features(dY, lddy, defer_dx=True)
         self.backward_weights_sgd(dY, lddy)

@@ -175,6 +175,20 @@ int haste_ffi_bwd_features_sr(const int32_t* idx, const void* W, const void* dY,
                               int64_t G, int32_t dtype, int32_t plan_ready, void* stream);
 
 /*
+ * The first part of haste_ffi_bwd_features[_sr]: the per-slice fp32 partial
+ * sums of dX^T, left in the workspace (same arguments and plan_ready meaning).
+ * The final pass -- summing the slices into dX -- is then done by
+ * haste_ffi_bwd_weights_sgd_dx, inside its own launch, so that a training step
+ * runs it in the tail of the fused weight update instead of as a kernel of its
+ * own.  No counterpart in the reference (its bwd-features kernel writes dX^T
+ * directly, shared_ffi/ffi_backward_features.cu:417-633).
+ */
+int haste_ffi_bwd_features_partials(const int32_t* idx, const void* W, const void* dY,
+                                    int64_t lddy, void* workspace, int64_t workspace_bytes,
+                                    int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+                                    int32_t dtype, int32_t plan_ready, void* stream);
+
+/*
  * Backward to weights (+ optional bias gradient):
  *   dW[l, j] = sum_b dY[b, l] * xT[idx[l/G, j], b]    stored as dW_dtype (RNE for 16-bit)
  *   dbias[l] = sum_b dY[b, l]                           stored as dbias_dtype (NULL = skip)
@@ -211,6 +225,26 @@ int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx, c
                               int32_t do_sr, uint64_t seed, void* bwdf_workspace,
                               int64_t bwdf_workspace_bytes, int64_t B, int64_t D, int64_t F,
                               int64_t O, int64_t G, int32_t dtype, void* stream);
+
+/*
+ * haste_ffi_bwd_weights_sgd (no dW / dbias outputs; bwdf_workspace required)
+ * that also finishes the backward to features of the same step: dX [B, D] bf16
+ * = SR(sum of the partials that the last haste_ffi_bwd_features_partials call
+ * with this workspace and these sizes left in it, tl.randint(dx_seed, b*D + d)),
+ * bit-identical to haste_ffi_bwd_features_sr.  The bwd-features call must have
+ * been made with the same W as this call reads (before its update) and an
+ * unchanged idx; dX must not overlap the other buffers.  Replaces, for one
+ * FFI layer, the reference's backward to features with its bf16 rounding
+ * (shared_ffi/bindings.py:44-48), backward to weights and the layer's SR-SGD
+ * step, as haste_ffi_bwd_features_partials + this call.
+ */
+int haste_ffi_bwd_weights_sgd_dx(const int32_t* idx, const void* xT, int64_t ldx, const void* dY,
+                                 int64_t lddy, uint16_t* W, uint16_t* bias, float* m_W,
+                                 float* m_bias, float lr, float wd, float mu, int32_t use_mom,
+                                 int32_t do_sr, uint64_t seed, uint16_t* dX, uint64_t dx_seed,
+                                 void* bwdf_workspace, int64_t bwdf_workspace_bytes, int64_t B,
+                                 int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype,
+                                 void* stream);
 
 /*
  * haste_sgd_sr_step on the weights W [O, F] (bf16) of an FFI layer (element

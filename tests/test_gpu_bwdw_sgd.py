@@ -110,8 +110,9 @@ def test_fused_matches_separate_and_oracle(dev, B, D, O, G, F, has_bias, use_mom
 @pytest.mark.parametrize("B,D,O,G,F", [(128, 768, 8193, 64, 128), (72, 500, 3001, 32, 64),
                                        (512, 768, 270001, 64, 128)])  # dY > 256 MB: streamed
 def test_train_step_fused_equals_unfused(dev, B, D, O, G, F):
-    """FFITrainStep.step (fused weight-gradient + SGD, which also hands the next
-    step's bwd-features the transposed updated weights) gives dX, W and bias
+    """FFITrainStep.step (bwd-features partials, then the fused weight-gradient
+    + SGD launch that also writes dX and hands the next step's bwd-features the
+    transposed updated weights) gives dX, W and bias
     bit-identical to backward + sgd (which rebuild W^T every step), step by
     step; idx is drawn with replacement, so duplicated indices (hi/lo W^T rows)
     occur."""
@@ -132,3 +133,77 @@ def test_train_step_fused_equals_unfused(dev, B, D, O, G, F):
         assert np.array_equal(bits(Wa), bits(Wb)), f"W differs at step {step}"
         assert np.array_equal(bits(ba), bits(bb))
     assert sa.seed == sb.seed == 12
+
+
+DX_CASES = [
+    # B, D, O, G, F, bias, momentum, lddy = O (the last dY row ends at label O)
+    (64, 768, 4096, 32, 32, True, False, False),
+    (128, 768, 8193, 64, 128, True, False, True),    # config 1 shape, 1-label last group
+    (100, 300, 1000, 16, 48, True, True, False),     # G = 16, B and D not multiples of 32
+    (96, 512, 2050, 64, 64, False, False, False),    # no bias
+    (130, 768, 3001, 128, 128, True, True, True),    # G = 128, momentum
+    (33, 200, 700, 128, 256, True, False, False),    # F = 256, one batch tile of 33 rows
+    (72, 500, 3001, 32, 64, True, False, True),      # several feature ranges and slices
+]
+
+
+@pytest.mark.parametrize("B,D,O,G,F,has_bias,use_mom,ys", DX_CASES)
+def test_weight_update_finishes_dx(dev, B, D, O, G, F, has_bias, use_mom, ys):
+    """haste_ffi_bwd_features_partials + haste_ffi_bwd_weights_sgd_dx (the
+    final bwd-features pass as trailing workgroups of the weight update) give
+    dX, W, bias and momentum bit-identical to haste_ffi_bwd_features_sr +
+    haste_ffi_bwd_weights_sgd, and leave W^T of the updated weights in the
+    workspace: a following bwd-features call with plan_ready = 2 matches one
+    that rebuilds it."""
+    x, W, bias, idx, dY, lddy, mW, mb = setup(B, D, O, G, F, seed=3 * O + F)
+    if ys:
+        dY, lddy = dY[:, :O].contiguous(), O
+    lr, wd, mu, seed = 0.05, 1e-4, 0.9, 7 + G
+    xT, ldx = _C.padded_transpose(x.to(dev))
+    idx_d, dY_d = idx.to(dev), dY.to(dev)
+    st = _C.stream_of(dY_d)
+    code = _lib.DTYPE_BF16
+    out = {}
+    for mode in ("separate", "merged"):
+        ws = _C.bwd_features_workspace(B, D, F, O, G, torch.bfloat16, dev)
+        Wm, bm, mWm, mbm = W.to(dev), bias.to(dev), mW.to(dev), mb.to(dev)
+        dX = torch.full((B, D), 3.0, dtype=torch.bfloat16, device=dev)
+        bp = bm.data_ptr() if has_bias else None
+        mwp, mbp = (mWm.data_ptr(), mbm.data_ptr()) if use_mom else (None, None)
+        if mode == "separate":
+            _lib.call("haste_ffi_bwd_features_sr", idx_d.data_ptr(), Wm.data_ptr(),
+                      dY_d.data_ptr(), lddy, dX.data_ptr(), 123, ws.data_ptr(), ws.numel(), B, D,
+                      F, O, G, code, 0, st)
+            _lib.call("haste_ffi_bwd_weights_sgd", idx_d.data_ptr(), xT.data_ptr(), ldx,
+                      dY_d.data_ptr(), lddy, Wm.data_ptr(), bp, mwp, mbp, None, _lib.DTYPE_F32,
+                      None, _lib.DTYPE_F32, lr, wd, mu, int(use_mom), 1, seed, ws.data_ptr(),
+                      ws.numel(), B, D, F, O, G, code, st)
+        else:
+            _lib.call("haste_ffi_bwd_features_partials", idx_d.data_ptr(), Wm.data_ptr(),
+                      dY_d.data_ptr(), lddy, ws.data_ptr(), ws.numel(), B, D, F, O, G, code, 0,
+                      st)
+            _lib.call("haste_ffi_bwd_weights_sgd_dx", idx_d.data_ptr(), xT.data_ptr(), ldx,
+                      dY_d.data_ptr(), lddy, Wm.data_ptr(), bp, mwp, mbp, lr, wd, mu,
+                      int(use_mom), 1, seed, dX.data_ptr(), 123, ws.data_ptr(), ws.numel(), B, D,
+                      F, O, G, code, st)
+        # the next step's bwd-features on the workspace's W^T of the updated weights
+        dX_next = torch.empty(B, D, dtype=torch.bfloat16, device=dev)
+        _lib.call("haste_ffi_bwd_features_sr", idx_d.data_ptr(), Wm.data_ptr(), dY_d.data_ptr(),
+                  lddy, dX_next.data_ptr(), 124, ws.data_ptr(), ws.numel(), B, D, F, O, G, code,
+                  2, st)
+        torch.cuda.synchronize()
+        out[mode] = (bits(dX), bits(Wm), bits(bm), mWm.cpu(), mbm.cpu(), bits(dX_next))
+    a, b = out["separate"], out["merged"]
+    assert np.array_equal(b[0], a[0]), "dX of the merged launch differs"
+    assert np.array_equal(b[1], a[1]) and np.array_equal(b[2], a[2]), "W / bias differ"
+    assert torch.equal(b[3], a[3]) and torch.equal(b[4], a[4]), "momentum differs"
+    assert np.array_equal(b[5], a[5]), "W^T refreshed by the merged launch differs"
+    assert not np.array_equal(a[0], bits(torch.full((B, D), 3.0, dtype=torch.bfloat16)))
+    # and the refreshed W^T is that of the updated weights: a rebuild agrees
+    ws = _C.bwd_features_workspace(B, D, F, O, G, torch.bfloat16, dev)
+    Wu = torch.from_numpy(a[1].view(np.int16)).view(torch.bfloat16).to(dev)
+    dX_rb = torch.empty(B, D, dtype=torch.bfloat16, device=dev)
+    _lib.call("haste_ffi_bwd_features_sr", idx_d.data_ptr(), Wu.data_ptr(), dY_d.data_ptr(), lddy,
+              dX_rb.data_ptr(), 124, ws.data_ptr(), ws.numel(), B, D, F, O, G, code, 0, st)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(dX_rb), b[5])
