@@ -1,10 +1,16 @@
 """FFI fwd + bwd + SR-SGD step throughput on one MI355X (BASELINE.json metric).
 
 One step = forward logits (incl. the X -> X^T copy), backward to features
-(deterministic, fused SR to bf16 with seed 123), and backward to weights and
-bias (fp32, kept on chip) fused with the SR-SGD update of weights and bias
-(lr 0.05, wd 1e-4, momentum 0, seed 42 + step; bit-identical to separate
-gradient and SGD kernels, whose step time is reported as "unfused").  Inputs are
+(deterministic, SR to bf16 with seed 123), and backward to weights and bias
+(fp32, kept on chip) fused with the SR-SGD update of weights and bias (lr 0.05,
+wd 1e-4, momentum 0, seed 42 + step; bit-identical to separate gradient and SGD
+kernels, whose step time is reported as "unfused"); the launch of the update
+also runs the final pass of backward to features (the sum of its per-slice
+partials into dX).
+
+Warm-up: W steps, continued until the GPU has run the step for WARM_MS
+(the MI355X reaches its steady clock after about 25 ms of sustained load; the
+step time then stays flat for seconds), then exactly K timed steps.  Inputs are
 synthetic and resident in HBM before timing; the grad of the logits
 dY = bf16(sigmoid(z) - Y) is computed once from the initial logits (BASELINE
 configs: Y binary, ~5 positives per row (10 at config 4), Zipf(1.1) over
@@ -141,6 +147,26 @@ def make_dY(logits, pos, lddy, dev):
     return dY
 
 
+WARM_MS = 50.0
+
+
+def warm_up(fn_list, warmup):
+    """Run at least ``warmup`` steps, and more until WARM_MS of wall time (the host
+    syncs every 10 steps past ``warmup``, so that is GPU time); returns the count."""
+    import torch
+
+    w0 = time.perf_counter()
+    n = 0
+    while n < warmup or (time.perf_counter() - w0) * 1e3 < WARM_MS:
+        for fn in fn_list:
+            fn()
+        n += 1
+        if n >= warmup and n % 10 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
 def timed(fn_list, steps, warmup, stream):
     """(ms per step, per-phase ms, wall s).  The step time comes from K steps with
     nothing but the two bracketing events (on the stream every kernel runs on);
@@ -149,10 +175,7 @@ def timed(fn_list, steps, warmup, stream):
     the step time)."""
     import torch
 
-    for _ in range(warmup):
-        for fn in fn_list:
-            fn()
-    torch.cuda.synchronize()
+    warm_up(fn_list, warmup)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
@@ -459,6 +482,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_ms": WARM_MS,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
