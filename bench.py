@@ -516,7 +516,9 @@ def main():
         src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            # an elementwise kernel (torch's own copy_ is a runtime blit, whose
+            # writes WRITE_SIZE has not always counted)
+            torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
     del st, x, dY_buf, labels
