@@ -93,6 +93,14 @@ def padded_transpose(features: torch.Tensor) -> Tuple[torch.Tensor, int]:
     return buf[:, :B], ld
 
 
+def f16_compute(t: torch.Tensor) -> torch.Tensor:
+    """An fp32 operand as the reference's fp32 kernels use it: rounded to fp16 to
+    nearest (__float2half_rn as they load it, e.g. ffi_forward_kernels.cu:350-356,
+    ffi_backward_features.cu:288-303, ffi_backward_weights.cu:352-368); 16-bit
+    tensors pass through."""
+    return t.to(torch.float16) if t.dtype == torch.float32 else t
+
+
 def _check_locations(locations: torch.Tensor, L: int, FANIN: int, gsize: int) -> torch.Tensor:
     require_device(locations, "locations")
     Gc = (L + gsize - 1) // gsize
@@ -133,16 +141,55 @@ def ffi_forward_cuda(locations: torch.Tensor, features: torch.Tensor, weights: t
         if bias.dtype != features.dtype:
             raise RuntimeError("bias dtype must match features dtype")
         bias = bias.contiguous()
-    xT, ldx = rows_aligned(features)
-    W = weights.contiguous()
+    xT, ldx = rows_aligned(f16_compute(features))
+    W = f16_compute(weights).contiguous()
     # rows padded to 128-byte lines (the reference pads to 8 labels): a group's
     # logit row segment is then one line, written whole
     L_pad = round64(L)
     out = torch.empty(B, L_pad, dtype=features.dtype, device=features.device)
-    _lib.call("haste_ffi_forward", locations.data_ptr(), xT.data_ptr(), ldx, W.data_ptr(),
-              None if bias is None else bias.data_ptr(), out.data_ptr(), L_pad, B, H, FANIN, L,
-              gsize, dtype_code(features.dtype), stream_of(features))
+    forward_into(locations, xT, ldx, W, bias, out, L_pad, B, H, FANIN, L, gsize,
+                 features.dtype, stream_of(features))
     return out if L_pad == L else out.narrow(1, 0, L)
+
+
+def ffi_forward_f32(locations: torch.Tensor, xT16: torch.Tensor, ldx: int,
+                    weights: torch.Tensor, bias: Optional[torch.Tensor], B: int, H: int,
+                    FANIN: int, L: int, gsize: int) -> torch.Tensor:
+    """ffi_forward_cuda of an fp32 layer whose transposed features are already the
+    fp16 copy ``xT16`` ([H, B] rows at stride ldx % 8 == 0, 16-byte aligned):
+    fp32 logits [B, L] (a view of a [B, ceil64(L)] buffer)."""
+    require_device(weights, "weights")
+    if tuple(weights.shape) != (L, FANIN):
+        raise RuntimeError(f"weights must be [L={L}, FANIN={FANIN}] (got {list(weights.shape)})")
+    if weights.dtype != torch.float32 or xT16.dtype != torch.float16:
+        raise RuntimeError("ffi_forward_f32: fp32 weights and fp16 transposed features")
+    locations = _check_locations(locations, L, FANIN, gsize)
+    if bias is not None:
+        if not (bias.dim() == 1 and bias.size(0) == L):
+            raise RuntimeError("bias must be [L]")
+        if bias.dtype != torch.float32:
+            raise RuntimeError("bias dtype must match features dtype")
+        bias = bias.contiguous()
+    L_pad = round64(L)
+    out = torch.empty(B, L_pad, dtype=torch.float32, device=weights.device)
+    forward_into(locations, xT16, ldx, f16_compute(weights).contiguous(), bias, out, L_pad, B, H,
+                 FANIN, L, gsize, torch.float32, stream_of(weights))
+    return out if L_pad == L else out.narrow(1, 0, L)
+
+
+def forward_into(locations: torch.Tensor, xT: torch.Tensor, ldx: int, W: torch.Tensor,
+                 bias: Optional[torch.Tensor], out: torch.Tensor, ldo: int, B: int, D: int,
+                 F: int, O: int, G: int, dtype: torch.dtype, stream: int) -> None:
+    """The forward kernel on prepared operands: ``dtype`` bf16/fp16 (xT, W, bias and
+    out in it) or fp32 (xT and W already rounded to fp16 by f16_compute; bias
+    and out fp32, out[:, :O] of a [B, ldo] buffer)."""
+    b = None if bias is None else bias.data_ptr()
+    if dtype == torch.float32:
+        _lib.call("haste_ffi_forward_f16_f32out", locations.data_ptr(), xT.data_ptr(), ldx,
+                  W.data_ptr(), b, out.data_ptr(), ldo, B, D, F, O, G, stream)
+    else:
+        _lib.call("haste_ffi_forward", locations.data_ptr(), xT.data_ptr(), ldx, W.data_ptr(), b,
+                  out.data_ptr(), ldo, B, D, F, O, G, dtype_code(dtype), stream)
 
 
 def bwd_features_workspace(B: int, H: int, FANIN: int, L: int, gsize: int, dtype: torch.dtype,
@@ -168,13 +215,13 @@ def ffi_backward_features_cuda(features: torch.Tensor, weights: torch.Tensor,
         raise RuntimeError(f"grad_outputs must be [B={B}, L={L}] (got {list(grad_outputs.shape)})")
     if grad_outputs.dtype != weights.dtype:
         raise RuntimeError("grad_outputs dtype must match weights dtype")
-    dY, lddy = grad_rows(grad_outputs)
-    W = weights.contiguous()
-    ws = bwd_features_workspace(B, H, FANIN, L, gsize, weights.dtype, weights.device)
+    dY, lddy = grad_rows(f16_compute(grad_outputs))
+    W = f16_compute(weights).contiguous()
+    ws = bwd_features_workspace(B, H, FANIN, L, gsize, W.dtype, weights.device)
     out = torch.empty(H, B, dtype=torch.float32, device=weights.device)
     _lib.call("haste_ffi_bwd_features", locations.data_ptr(), W.data_ptr(), dY.data_ptr(), lddy,
               out.data_ptr(), ws.data_ptr(), ws.numel(), B, H, FANIN, L, gsize,
-              dtype_code(weights.dtype), 0, stream_of(weights))
+              dtype_code(W.dtype), 0, stream_of(weights))
     return out
 
 
@@ -184,17 +231,18 @@ def ffi_backward_features_cuda(features: torch.Tensor, weights: torch.Tensor,
 def ffi_backward_weights_cuda(features: torch.Tensor, weights: torch.Tensor,
                               locations: torch.Tensor, grad_outputs: torch.Tensor, B: int, H: int,
                               FANIN: int, L: int, gsize: int) -> torch.Tensor:
-    """Returns dW [L, FANIN] in the features dtype (RNE of the fp32 sum)."""
+    """Returns dW [L, FANIN] in the features dtype (RNE of the fp32 sum; for fp32
+    features the fp32 sum of the fp16-rounded operands, as the reference)."""
     require_device(features, "features")
     require_device(grad_outputs, "grad_outputs")
     _check_sizes(features, weights, B, H, FANIN, L)
     locations = _check_locations(locations, L, FANIN, gsize)
     if tuple(grad_outputs.shape) != (B, L):
         raise RuntimeError(f"grad_outputs must be [B={B}, L={L}] (got {list(grad_outputs.shape)})")
-    xT, ldx = rows_aligned(features)
-    dY, lddy = grad_rows(grad_outputs)
+    xT, ldx = rows_aligned(f16_compute(features))
+    dY, lddy = grad_rows(f16_compute(grad_outputs).to(xT.dtype))
     dW = torch.empty(L, FANIN, dtype=features.dtype, device=features.device)
     _lib.call("haste_ffi_bwd_weights", locations.data_ptr(), xT.data_ptr(), ldx, dY.data_ptr(),
               lddy, dW.data_ptr(), dtype_code(features.dtype), None, 0, B, H, FANIN, L, gsize,
-              dtype_code(features.dtype), stream_of(features))
+              dtype_code(xT.dtype), stream_of(features))
     return dW

@@ -45,6 +45,8 @@ SIGNATURES = {
     "haste_abi_version": (ctypes.c_int, []),
     "haste_ffi_forward": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                          _I64, _I32, _P]),
+    "haste_ffi_forward_f16_f32out": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _I64, _I64, _I64,
+                                                    _I64, _I64, _I64, _P]),
     "haste_ffi_forward_bce_workspace_size": (_I64, [_I64, _I64, _I64]),
     "haste_ffi_forward_bce": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P, _P,
                                              _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P]),

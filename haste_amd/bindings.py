@@ -123,15 +123,18 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
     dev = weights.device
     if grad_output.dtype != dtype:
         grad_output = grad_output.to(dtype)
-    dY, lddy = _C.grad_rows(grad_output)
+    # an fp32 layer computes with fp16 copies of W, X and grad_output, as the
+    # reference's fp32 kernels round them when they load them
+    f32 = dtype == torch.float32
+    dY, lddy = _C.grad_rows(_C.f16_compute(grad_output))
     locs = group_locations.contiguous()
-    W = weights.contiguous()
+    W = _C.f16_compute(weights).contiguous()
     stream = _C.stream_of(W)
-    code = _C.dtype_code(dtype)
+    code = _C.dtype_code(W.dtype)
 
     grad_x = None
     if need_x:
-        ent = _bwdf_workspace(locs, B, D, F, O, gsize, dtype, stream)
+        ent = _bwdf_workspace(locs, B, D, F, O, gsize, W.dtype, stream)
         ws = ent.ws
         # 1: the plan is current; 2: the transposed weights too (written by the
         # SRSgd step that last updated these weights, haste_sgd_sr_step_wt, and
@@ -155,19 +158,24 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
             _WT_TARGETS[W.data_ptr()] = ent
 
     grad_w = grad_b = None
+    if f32 and need_b:
+        # the reference's torch.sum(grad_output, dim=0) in fp32 (bindings.py:40),
+        # not the kernel's sum of the fp16 copy
+        grad_b = grad_output.sum(0).to(bias_dtype)
+        need_b = False
     if need_w or need_b:
-        ldx = xT.stride(0)
+        xT, ldx = _C.rows_aligned(_C.f16_compute(xT))
         grad_w = torch.empty(O, F, dtype=w_grad_dtype, device=dev) if need_w else None
-        grad_b = torch.empty(O, dtype=bias_dtype, device=dev) if need_b else None
+        if need_b:
+            grad_b = torch.empty(O, dtype=bias_dtype, device=dev)
         if need_w:
             dw_ptr, dw_code = grad_w.data_ptr(), _C.dtype_code(w_grad_dtype)
         else:  # bias only: the kernel still needs a dW target
-            scratch = torch.empty(O, F, dtype=dtype, device=dev)
+            scratch = torch.empty(O, F, dtype=W.dtype, device=dev)
             dw_ptr, dw_code = scratch.data_ptr(), code
         _lib.call("haste_ffi_bwd_weights", locs.data_ptr(), xT.data_ptr(), ldx, dY.data_ptr(),
-                  lddy, dw_ptr, dw_code, None if grad_b is None else grad_b.data_ptr(),
-                  0 if grad_b is None else _C.dtype_code(bias_dtype), B, D, F, O, gsize,
-                  code, stream)
+                  lddy, dw_ptr, dw_code, grad_b.data_ptr() if need_b else None,
+                  _C.dtype_code(bias_dtype) if need_b else 0, B, D, F, O, gsize, code, stream)
     return grad_x, grad_w, grad_b
 
 
@@ -182,8 +190,13 @@ class GroupFFIMulFunction(torch.autograd.Function):
             raise RuntimeError(f"features must be 2-D [B, D] (got {list(features.shape)})")
         B, D = features.shape
         O, F = weights.shape
-        xT, ldx = _C.padded_transpose(features)          # bindings.py:19, rows padded to 8
-        out = _C.ffi_forward_cuda(group_locations, xT, weights, bias, B, D, F, O, gsize)
+        # bindings.py:19, rows padded to 8; an fp32 layer keeps the fp16 copy its
+        # kernels compute with (the reference's fp32 kernels round X as they load it)
+        xT, ldx = _C.padded_transpose(_C.f16_compute(features))
+        if features.dtype == torch.float32:
+            out = _C.ffi_forward_f32(group_locations, xT, ldx, weights, bias, B, D, F, O, gsize)
+        else:
+            out = _C.ffi_forward_cuda(group_locations, xT, weights, bias, B, D, F, O, gsize)
         ctx.save_for_backward(xT, weights, group_locations)
         ctx.gsize = int(gsize)
         ctx.use_bias = bias is not None
@@ -230,15 +243,14 @@ class HeadTailFFIFunction(torch.autograd.Function):
         buf = torch.empty(B, ld, dtype=dt, device=x_tail.device)
         out = buf[:, s0: s0 + H + O]
         out[:, :H].copy_(head)
-        xT, ldx = _C.padded_transpose(x_tail)
+        xT, ldx = _C.padded_transpose(_C.f16_compute(x_tail))
         locs = _C._check_locations(group_locations, O, F, gsize)
         if weights.dtype != dt or (bias is not None and bias.dtype != dt):
             raise RuntimeError("weights and bias dtype must match x_tail's")
-        W = weights.contiguous()
+        W = _C.f16_compute(weights).contiguous()
         b = None if bias is None else bias.contiguous()
-        _lib.call("haste_ffi_forward", locs.data_ptr(), xT.data_ptr(), ldx, W.data_ptr(),
-                  None if b is None else b.data_ptr(), buf[:, s0 + H:].data_ptr(), ld, B, D, F, O,
-                  gsize, _C.dtype_code(dt), _C.stream_of(x_tail))
+        _C.forward_into(locs, xT, ldx, W, b, buf[:, s0 + H:], ld, B, D, F, O, gsize, dt,
+                        _C.stream_of(x_tail))
         ctx.save_for_backward(x_head, head_weight, xT, weights, group_locations)
         ctx.H, ctx.gsize = H, int(gsize)
         ctx.head_has_bias = head_bias is not None

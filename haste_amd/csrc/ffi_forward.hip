@@ -38,7 +38,9 @@ constexpr int kStoreNT = 2;    // buffer-store cache policy: nt (non-temporal) o
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kMaxTilesPerWG = 8;
 
-template <int G, int FP>
+// ESZ: bytes per output element (2: logits in the inputs' 16-bit type, 4: fp32
+// logits of the fp32 layer).
+template <int G, int FP, int ESZ = 2>
 struct FwdCfg {
     static constexpr int KS = FP / 32;     // MFMA k-steps
     static constexpr int MTILES = G / 16;  // label tiles in the group
@@ -57,7 +59,7 @@ struct FwdCfg {
     static constexpr int RB = kBT * 2 + 16;       // LDS bytes per gathered row
     static constexpr int PIECES = FP * (kBT / 8); // 16-byte pieces per tile
     static constexpr int PPT = PIECES / kThreads; // >= 1 (FP >= 32)
-    static constexpr int SRB = MT * 32 + 16;      // LDS bytes per staged output row
+    static constexpr int SRB = MT * 16 * ESZ + 16;  // LDS bytes per staged output row
     static constexpr int STG = NT * 16 * SRB;     // staged output bytes per wave
     static_assert(MTILES % WM == 0 && PPT >= 1, "tile shape");
 };
@@ -94,7 +96,9 @@ __device__ __forceinline__ float bce_dy_pos(float x) {
 
 // LAST: the workgroup's group is the last one and holds fewer than G labels;
 // its stores are per element so that no column >= O is written.
-template <typename T, int G, int FP, bool LAST, bool BCE>
+// O32: fp32 bias and fp32 logits (the fp32 layer, whose features and weights the
+// caller has rounded to fp16); otherwise bias and logits are T.
+template <typename T, int G, int FP, bool LAST, bool BCE, bool O32>
 __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                                           const uint16_t* __restrict__ xT, int64_t ldx,
                                           const uint16_t* __restrict__ W,
@@ -102,9 +106,12 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                                           uint16_t* __restrict__ out, int64_t ldo, int B, int D,
                                           int F, int64_t O, int64_t g, int b_chunk0, int ntiles,
                                           char (*Xg)[FP * FwdCfg<G, FP>::RB],
-                                          char (*stg)[FwdCfg<G, FP>::STG], const BceArgs& bce,
+                                          char (*stg)[FwdCfg<G, FP, O32 ? 4 : 2>::STG],
+                                          const BceArgs& bce,
                                           float* s_red) {
-    using C = FwdCfg<G, FP>;
+    static_assert(!(BCE && O32), "the BCE epilogue writes 16-bit dY");
+    constexpr int ESZ = O32 ? 4 : 2;
+    using C = FwdCfg<G, FP, ESZ>;
     constexpr int KS = C::KS, MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SRB = C::SRB;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -134,7 +141,9 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
     // W fragments (A operand) and bias of this wave's label tiles; rows >= O and
     // slots >= F are outside the resources and read as zero.
     const rsrc_t wr = make_rsrc(W + l0 * F, (int64_t)nl * F * 2);
-    const rsrc_t br = bias != nullptr ? make_rsrc(bias + l0, (int64_t)nl * 2) : make_rsrc(W, 0);
+    const rsrc_t br = bias != nullptr
+        ? make_rsrc(reinterpret_cast<const char*>(bias) + l0 * ESZ, (int64_t)nl * ESZ)
+        : make_rsrc(W, 0);
     u32x4 wf[MT][KS];
     float bv[MT][4];
 #pragma unroll
@@ -148,7 +157,8 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
         const int lb = (wm * MT + mt) * 16 + kq * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            bv[mt][i] = bits_to_f32<T>(__builtin_amdgcn_raw_buffer_load_b16(br, (lb + i) * 2, 0, 0));
+            bv[mt][i] = O32 ? __builtin_bit_cast(float, buf_load4(br, (uint32_t)(lb + i) * 4))
+                            : bits_to_f32<T>(__builtin_amdgcn_raw_buffer_load_b16(br, (lb + i) * 2, 0, 0));
     }
 
     // chunks starting at or past B read as zero, columns >= B of a partial chunk
@@ -238,13 +248,14 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
             if (t + 2 < ntiles) fetch(b_base + 2 * kBT, xv);
         }
 
-        // ---- epilogue: + bias (fp32), RNE.  A lane holds 4 consecutive labels of
-        // one batch row; they are staged in LDS and written as row segments.
+        // ---- epilogue: + bias (fp32), RNE (O32: kept in fp32).  A lane holds 4
+        // consecutive labels of one batch row; they are staged in LDS and written
+        // as row segments.
         // Rows >= B fall outside the tile's resource.  The last (partial) group
         // stores per element instead, so no column >= O is written. ----
         float dprod = 1.0f;  // BCE: the tile's d factors of this lane
-        const rsrc_t orr = make_rsrc(out + (int64_t)b_base * ldo + l0,
-                                     (int64_t)(std::min(kBT, B - b_base) - 1) * ldo * 2 + nl * 2);
+        const rsrc_t orr = make_rsrc(reinterpret_cast<char*>(out) + ((int64_t)b_base * ldo + l0) * ESZ,
+                                     ((int64_t)(std::min(kBT, B - b_base) - 1) * ldo + nl) * ESZ);
         // BCE with logits wanted: the rounded logits go out directly, 8 bytes per
         // lane (rows past B and labels past O outside the resource)
         const rsrc_t lgr = BCE && bce.logits != nullptr
@@ -258,6 +269,20 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
             for (int mt = 0; mt < MT; ++mt) {
                 const int ll = (wm * MT + mt) * 16 + kq * 4;  // label within the group
                 const f32x4 v = acc[mt][nt];
+                if constexpr (O32) {
+                    const u32x4 h4 = __builtin_bit_cast(
+                        u32x4, (f32x4{v[0] + bv[mt][0], v[1] + bv[mt][1], v[2] + bv[mt][2],
+                                      v[3] + bv[mt][3]}));
+                    const uint32_t off4 = (uint32_t)((int64_t)rb * ldo + ll) * 4;
+                    if constexpr (!LAST) {
+                        *reinterpret_cast<u32x4*>(&stg[wave][(nt * 16 + col) * SRB + (mt * 16 + kq * 4) * 4]) = h4;
+                    } else {
+                        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // as the 16-bit LAST stores below
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) buf_store4(h4[i], orr, ll + i < nl ? off4 + 4 * i : kOOB);
+                    }
+                    continue;
+                }
                 u32x2 h = u32x2{pack2_rne<T>(v[0] + bv[mt][0], v[1] + bv[mt][1]),
                                 pack2_rne<T>(v[2] + bv[mt][2], v[3] + bv[mt][3])};
                 if constexpr (BCE) {
@@ -322,7 +347,7 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
         // instruction (full 128-byte lines at MT = 4); the wave reads back only
         // what it wrote, and a wave's LDS accesses complete in order
         auto flush = [&](const rsrc_t& dst) {
-            constexpr int LPR = MT * 2;     // lanes per staged row (MT*32 bytes)
+            constexpr int LPR = MT * ESZ;   // lanes per staged row (MT*16*ESZ bytes)
             constexpr int RPI = 64 / LPR;   // rows per instruction
 #pragma unroll
             for (int r0 = 0; r0 < NT * 16; r0 += RPI) {
@@ -337,7 +362,7 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                 // stream of them does not evict the gathered rows and weights;
                 // dY (BCE) is read back by the backward kernels and stays cached
                 __builtin_amdgcn_raw_buffer_store_b128(
-                    v, dst, own ? (uint32_t)((int64_t)rb * ldo * 2 + (wm * MT * 16) * 2 + cb) : kOOB, 0,
+                    v, dst, own ? (uint32_t)(((int64_t)rb * ldo + wm * MT * 16) * ESZ + cb) : kOOB, 0,
                     BCE ? 0 : kStoreNT);
             }
         };
@@ -358,16 +383,16 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
 // Register bound: four waves per SIMD at G = 64, FP = 128 (the split labels
 // above), three there for the BCE epilogue, whose extra registers would
 // otherwise cost a wave; two elsewhere.
-template <int G, int FP, bool BCE>
-constexpr int fwd_waves_per_simd() { return G == 64 && FP == 128 ? (BCE ? 3 : 4) : 2; }
+template <int G, int FP, bool BCE, bool O32>
+constexpr int fwd_waves_per_simd() { return G == 64 && FP == 128 && !O32 ? (BCE ? 3 : 4) : 2; }
 
-template <typename T, int G, int FP, bool BCE>
-__global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE>())) void ffi_fwd_kernel(
+template <typename T, int G, int FP, bool BCE, bool O32>
+__global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE, O32>())) void ffi_fwd_kernel(
     const int32_t* __restrict__ idx, const uint16_t* __restrict__ xT, int64_t ldx,
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
     int64_t ldo, int B, int D, int F, int64_t O, int64_t Gc, int nchunks, int tiles_per_chunk,
     BceArgs bce) {
-    using C = FwdCfg<G, FP>;
+    using C = FwdCfg<G, FP, O32 ? 4 : 2>;
     __shared__ __attribute__((aligned(16))) char Xg[C::NB][FP * C::RB];
     __shared__ __attribute__((aligned(16))) char stg[4][C::STG];
     __shared__ float s_red[4];
@@ -384,11 +409,11 @@ __global__ __launch_bounds__(kThreads, (fwd_waves_per_simd<G, FP, BCE>())) void 
     const int ntiles = min(tiles_per_chunk, (B - b_chunk0 + kBT - 1) / kBT);
     if constexpr (BCE) bce.part += work;
     if ((g + 1) * G > O)
-        fwd_group<T, G, FP, true, BCE>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
-                                       ntiles, Xg, stg, bce, s_red);
+        fwd_group<T, G, FP, true, BCE, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g,
+                                            b_chunk0, ntiles, Xg, stg, bce, s_red);
     else
-        fwd_group<T, G, FP, false, BCE>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g, b_chunk0,
-                                        ntiles, Xg, stg, bce, s_red);
+        fwd_group<T, G, FP, false, BCE, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, g,
+                                             b_chunk0, ntiles, Xg, stg, bce, s_red);
 }
 
 // Batch chunks per group: the whole batch per workgroup (up to kMaxTilesPerWG
@@ -405,11 +430,12 @@ int64_t fwd_chunks(int64_t B, int64_t Gc, int64_t* tpc) {
 // The host-side limits of launch_fwd: the grid and the 32-bit buffer offsets.
 // haste_ffi_forward_bce checks them before it marks any label bits, so a call
 // that fails here leaves the workspace zero.
-int check_fwd_size(int64_t B, int64_t D, int64_t ldx, int64_t ldo, int64_t O, int64_t G) {
+int check_fwd_size(int64_t B, int64_t D, int64_t ldx, int64_t ldo, int64_t O, int64_t G,
+                   int64_t out_esz = 2) {
     const int64_t Gc = ceil_div(O, G);
     int64_t tpc = 1;
     const int64_t grid = 8 * ceil_div(Gc * fwd_chunks(B, Gc, &tpc), 8);
-    if (grid > 0x7FFFFFFF || (int64_t)kBT * ldo * 2 > kMaxRsrcBytes ||
+    if (grid > 0x7FFFFFFF || (int64_t)kBT * ldo * out_esz > kMaxRsrcBytes ||
         D * ldx * 2 > kMaxRsrcBytes) {
         set_error("haste_ffi_forward: problem too large (grid %lld, ldo %lld, D*ldx %lld)",
                   (long long)grid, (long long)ldo, (long long)(D * ldx));
@@ -418,47 +444,52 @@ int check_fwd_size(int64_t B, int64_t D, int64_t ldx, int64_t ldo, int64_t O, in
     return HASTE_OK;
 }
 
-template <typename T, int G, int FP>
+// O32 (fp16 inputs, fp32 bias and logits) is launched without the BCE epilogue.
+template <typename T, int G, int FP, bool O32>
 int launch_fwd(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
                const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
                int64_t O, const BceArgs* bce, hipStream_t st) {
-    const int rc = check_fwd_size(B, D, ldx, ldo, O, G);
+    const int rc = check_fwd_size(B, D, ldx, ldo, O, G, O32 ? 4 : 2);
     if (rc != HASTE_OK) return rc;
     const int64_t Gc = ceil_div(O, G);
     int64_t tpc = 1;
     const int64_t nchunks = fwd_chunks(B, Gc, &tpc);
     const int64_t grid = 8 * ceil_div(Gc * nchunks, 8);
-    if (bce != nullptr)
-        ffi_fwd_kernel<T, G, FP, true><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
-            idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks,
-            (int)tpc, *bce);
-    else
-        ffi_fwd_kernel<T, G, FP, false><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
-            idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks,
-            (int)tpc, BceArgs{nullptr, 0, nullptr, nullptr});
+    if constexpr (!O32) {
+        if (bce != nullptr) {
+            ffi_fwd_kernel<T, G, FP, true, false><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
+                idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks,
+                (int)tpc, *bce);
+            HASTE_CHECK_LAUNCH("haste_ffi_forward");
+            return HASTE_OK;
+        }
+    }
+    ffi_fwd_kernel<T, G, FP, false, O32><<<dim3((unsigned)grid), dim3(kThreads), 0, st>>>(
+        idx, xT, ldx, W, bias, out, ldo, (int)B, (int)D, (int)F, O, Gc, (int)nchunks, (int)tpc,
+        BceArgs{nullptr, 0, nullptr, nullptr});
     HASTE_CHECK_LAUNCH("haste_ffi_forward");
     return HASTE_OK;
 }
 
-template <typename T, int G>
+template <typename T, int G, bool O32>
 int dispatch_fp(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
                 const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
                 int64_t O, const BceArgs* bce, hipStream_t st) {
-    if (F <= 32) return launch_fwd<T, G, 32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
-    if (F <= 64) return launch_fwd<T, G, 64>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
-    if (F <= 128) return launch_fwd<T, G, 128>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
-    return launch_fwd<T, G, 256>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    if (F <= 32) return launch_fwd<T, G, 32, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    if (F <= 64) return launch_fwd<T, G, 64, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    if (F <= 128) return launch_fwd<T, G, 128, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    return launch_fwd<T, G, 256, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
 }
 
-template <typename T>
+template <typename T, bool O32 = false>
 int dispatch_g(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* W,
                const uint16_t* bias, uint16_t* out, int64_t ldo, int64_t B, int64_t D, int64_t F,
                int64_t O, int64_t G, const BceArgs* bce, hipStream_t st) {
     switch (G) {
-    case 16: return dispatch_fp<T, 16>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
-    case 32: return dispatch_fp<T, 32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
-    case 64: return dispatch_fp<T, 64>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
-    case 128: return dispatch_fp<T, 128>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    case 16: return dispatch_fp<T, 16, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    case 32: return dispatch_fp<T, 32, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    case 64: return dispatch_fp<T, 64, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
+    case 128: return dispatch_fp<T, 128, O32>(idx, xT, ldx, W, bias, out, ldo, B, D, F, O, bce, st);
     default: break;
     }
     set_error("Unsupported group size for FFI kernel. choose from 16,32,64,128 (got %lld)",
@@ -586,6 +617,28 @@ extern "C" int haste_ffi_forward(const int32_t* idx, const void* xT, int64_t ldx
     if (dtype == HASTE_DTYPE_BF16)
         return haste::dispatch_g<haste::BF16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, nullptr, st);
     return haste::dispatch_g<haste::F16>(idx, x, ldx, w, bb, o, ldo, B, D, F, O, G, nullptr, st);
+}
+
+extern "C" int haste_ffi_forward_f16_f32out(const int32_t* idx, const void* xT, int64_t ldx,
+                                            const void* W, const float* bias, float* out,
+                                            int64_t ldo, int64_t B, int64_t D, int64_t F,
+                                            int64_t O, int64_t G, void* stream) {
+    int rc = haste::check_ffi_shape("haste_ffi_forward_f16_f32out", B, D, F, O, G, HASTE_DTYPE_F16);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(idx && xT && W && out, "haste_ffi_forward_f16_f32out: null pointer");
+    HASTE_CHECK_ARG(ldx >= B && ldx % 8 == 0,
+                    "haste_ffi_forward_f16_f32out: ldx must be >= B and a multiple of 8 (ldx=%lld B=%lld)",
+                    (long long)ldx, (long long)B);
+    HASTE_CHECK_ARG(ldo >= O && ldo % 8 == 0,
+                    "haste_ffi_forward_f16_f32out: ldo must be >= O and a multiple of 8 (ldo=%lld O=%lld)",
+                    (long long)ldo, (long long)O);
+    HASTE_CHECK_ARG(haste::aligned16(xT) && haste::aligned16(W) && haste::aligned16(out) &&
+                        (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 4 == 0),
+                    "haste_ffi_forward_f16_f32out: xT, W and out must be 16-byte aligned, bias 4-byte");
+    return haste::dispatch_g<haste::F16, true>(
+        idx, static_cast<const uint16_t*>(xT), ldx, static_cast<const uint16_t*>(W),
+        reinterpret_cast<const uint16_t*>(bias), reinterpret_cast<uint16_t*>(out), ldo, B, D, F, O,
+        G, nullptr, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t haste_ffi_forward_bce_workspace_size(int64_t B, int64_t O, int64_t G) {

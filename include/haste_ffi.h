@@ -64,6 +64,20 @@ int haste_ffi_forward(const int32_t* idx, const void* xT, int64_t ldx, const voi
                       int64_t O, int64_t G, int32_t dtype, void* stream);
 
 /*
+ * The forward of an fp32 layer:
+ *   out[b, l] = sum_j xT[idx[l/G, j], b] * W[l, j]  (+ bias[l]),  fp32 accumulation,
+ * with xT and W in fp16, bias (may be NULL) and out in fp32 (out 16-byte
+ * aligned, ldo % 8 == 0).  Replaces the fp32 instantiation of ffi_forward_cuda
+ * (group_shared_fanin_v1_fp32, shared_ffi/ffi_forward_kernels.cu:289-485,
+ * dispatched at :549-557), which rounds the fp32 features and weights to fp16
+ * (to nearest) as it loads them, accumulates in fp32 and adds the fp32 bias;
+ * here the caller passes the fp16 copies.
+ */
+int haste_ffi_forward_f16_f32out(const int32_t* idx, const void* xT, int64_t ldx, const void* W,
+                                 const float* bias, float* out, int64_t ldo, int64_t B, int64_t D,
+                                 int64_t F, int64_t O, int64_t G, void* stream);
+
+/*
  * Grouped FFI forward fused with the sparse BCE loss of the application's
  * training loop (src/runner.py:469-478, labels in the COO [nnz, 2] int32
  * (row, label) form of src/data.py:26-46):

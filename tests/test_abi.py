@@ -59,6 +59,22 @@ def test_forward_rejects_bad_strides_and_dtype():
     assert _fwd(xT=18) == _lib.HASTE_ERR_INVALID_ARG  # misaligned
 
 
+def test_forward_f32out_rejects_bad_arguments():
+    def call(**kw):
+        args = dict(idx=8, xT=16, ldx=64, W=32, bias=None, out=48, ldo=4096, B=64, D=768, F=32,
+                    O=4096, G=32, stream=None)
+        args.update(kw)
+        return _lib.lib().haste_ffi_forward_f16_f32out(*args.values())
+
+    assert call(G=48) == _lib.HASTE_ERR_UNSUPPORTED
+    assert call(F=24) == _lib.HASTE_ERR_INVALID_ARG
+    assert call(ldo=4092) == _lib.HASTE_ERR_INVALID_ARG
+    assert call(out=52) == _lib.HASTE_ERR_INVALID_ARG   # fp32 logits need 16-byte alignment
+    assert call(bias=50) == _lib.HASTE_ERR_INVALID_ARG  # fp32 bias, 4-byte alignment
+    assert call(idx=None) == _lib.HASTE_ERR_INVALID_ARG
+    assert "haste_ffi_forward_f16_f32out" in _lib.last_error()
+
+
 def test_bwd_features_workspace_size():
     L = _lib.lib()
     n = L.haste_ffi_bwd_features_workspace_size(512, 768, 128, 131073, 64, _lib.DTYPE_BF16)
