@@ -251,7 +251,8 @@ def time_rewire(st, x, dY, cfg, stream, reps=5):
     n_pruned = torch.zeros(1, dtype=torch.int32, device=st.W.device)
 
     def rewire(seed):
-        _lib.call("haste_rewire", st.W.data_ptr(), st.idx.data_ptr(), None, n_pruned.data_ptr(),
+        _lib.call("haste_rewire", st.W.data_ptr(), st.code, st.idx.data_ptr(), None,
+                  n_pruned.data_ptr(),
                   O, F, G, D, _lib.PRUNE_FRACTION, 0.0, k, _lib.REGROW_UNUSED, _lib.INIT_ZERO,
                   1.0 / math.sqrt(F), seed, _C.stream_of(st.W))
         torch.autograd.graph.increment_version(st.W)

@@ -82,11 +82,12 @@ SIGNATURES = {
     "haste_sgd_sr_step_multi": (ctypes.c_int, [ctypes.POINTER(SgdTensor), _I32, _I32, _F32, _F32,
                                                _F32, _I32, _I32, _U64, _P]),
     "haste_transpose_features": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _I64, _P]),
-    "haste_rewire": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _F32, _I64,
-                                    _I32, _I32, _F32, _U64, _P]),
-    "haste_rewire_scores": (ctypes.c_int, [_P, _P, _I32, _I32, _P, _I64, _I64, _I64, _P]),
-    "haste_rewire_ex": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I64, _I64,
-                                       _I64, _I32, _F32, _I64, _I32, _I32, _F32, _U64, _P]),
+    "haste_rewire": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I32, _F32,
+                                    _I64, _I32, _I32, _F32, _U64, _P]),
+    "haste_rewire_scores": (ctypes.c_int, [_P, _I32, _P, _I32, _I32, _P, _I64, _I64, _I64, _P]),
+    "haste_rewire_ex": (ctypes.c_int, [_P, _I32, _P, _P, _I32, _I32, _P, _P, _P, _P, _I64, _I64,
+                                       _I64, _I64, _I32, _F32, _I64, _I32, _I32, _F32, _U64,
+                                       _P]),
 }
 
 _lib = None

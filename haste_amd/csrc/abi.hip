@@ -21,4 +21,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char* haste_last_error(void) { return haste::g_last_error; }
 
-extern "C" int haste_abi_version(void) { return 1; }
+extern "C" int haste_abi_version(void) { return 2; }

@@ -115,8 +115,7 @@ class GroupFixedFanIn(torch.nn.Module):
         if self.out_features == 0:
             return
         _C.require_device(W, "weights")
-        if W.dtype != torch.bfloat16:
-            raise NotImplementedError(f"rewire: weights must be bfloat16 (got {W.dtype})")
+        wcode = _C.dtype_code(W.dtype)   # bf16, fp16 or fp32: rewired in their own dtype
         if not W.is_contiguous() or not self.group_locations.is_contiguous():
             raise RuntimeError("rewire: weights and group_locations must be contiguous")
         F = self.fan_in
@@ -131,7 +130,7 @@ class GroupFixedFanIn(torch.nn.Module):
             seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
         if self._pruned_total is None or self._pruned_total.device != W.device:
             self._pruned_total = torch.zeros(1, dtype=torch.int32, device=W.device)
-        _lib.call("haste_rewire", W.data_ptr(), self.group_locations.data_ptr(), None,
+        _lib.call("haste_rewire", W.data_ptr(), wcode, self.group_locations.data_ptr(), None,
                   self._pruned_total.data_ptr(), self.out_features, F, self.group_size,
                   self.in_features, mode, thr, k,
                   _lib.REGROW_UNUSED if self.regrow_mode == "unused" else _lib.REGROW_RANDOM,
@@ -178,8 +177,7 @@ class GroupFixedFanInReal(GroupFixedFanIn):
         if self.out_features == 0:
             return
         _C.require_device(W, "weights")
-        if W.dtype != torch.bfloat16:
-            raise NotImplementedError(f"rewire: weights must be bfloat16 (got {W.dtype})")
+        wcode = _C.dtype_code(W.dtype)   # bf16, fp16 or fp32: rewired in their own dtype
         if not W.is_contiguous() or not self.group_locations.is_contiguous():
             raise RuntimeError("rewire: weights and group_locations must be contiguous")
         O, F, G = self.out_features, self.fan_in, self.group_size
@@ -188,11 +186,10 @@ class GroupFixedFanInReal(GroupFixedFanIn):
         if self.use_grad and grad is None:
             raise RuntimeError("rewire: use_grad is set but weights.grad is None")
         if grad is not None:
-            if grad.dtype not in (torch.bfloat16, torch.float32):
-                raise NotImplementedError("rewire: grad must be bf16 or fp32")
             grad = grad.contiguous()
         gptr = None if grad is None else grad.data_ptr()
-        gcode = _lib.DTYPE_F32 if (grad is not None and grad.dtype == torch.float32) else _lib.DTYPE_BF16
+        # saliency |W * grad| in torch's promoted dtype of the two (the kernel's rule)
+        gcode = _lib.DTYPE_BF16 if grad is None else _C.dtype_code(grad.dtype)
         smode = _lib.SCORE_MAX if self.score_mode == "max" else _lib.SCORE_MEAN
         st = _C.stream_of(W)
         scores = key_thr = None
@@ -204,8 +201,8 @@ class GroupFixedFanInReal(GroupFixedFanIn):
                 return
             mode, thr = _lib.PRUNE_GLOBAL_FRACTION, 0.0
             scores = torch.empty(Gc, F, dtype=torch.float32, device=W.device)
-            _lib.call("haste_rewire_scores", W.data_ptr(), gptr, gcode, smode, scores.data_ptr(),
-                      O, F, G, st)
+            _lib.call("haste_rewire_scores", W.data_ptr(), wcode, gptr, gcode, smode,
+                      scores.data_ptr(), O, F, G, st)
             # unique keys (scores are >= 0, so their bits order them): the k-th
             # smallest is the last pruned slot; ties go to the lower slot
             keys = (scores.view(-1).view(torch.int32).to(torch.int64) << 32) | torch.arange(
@@ -215,7 +212,8 @@ class GroupFixedFanInReal(GroupFixedFanIn):
             seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
         if self._pruned_total is None or self._pruned_total.device != W.device:
             self._pruned_total = torch.zeros(1, dtype=torch.int32, device=W.device)
-        _lib.call("haste_rewire_ex", W.data_ptr(), self.group_locations.data_ptr(), gptr, gcode,
+        _lib.call("haste_rewire_ex", W.data_ptr(), wcode, self.group_locations.data_ptr(), gptr,
+                  gcode,
                   smode, None if scores is None else scores.data_ptr(),
                   None if key_thr is None else key_thr.data_ptr(), None,
                   self._pruned_total.data_ptr(), O, F, G, self.in_features, mode, thr, k,

@@ -19,7 +19,9 @@
  *                         need only hold O elements (a [B, O] tensor, or a column
  *                         block of a wider one); they are read at some extra cost
  * Element types are HASTE_DTYPE_* codes; other 16-bit tensors must be 16-byte aligned.
- * Supported: dtype bf16 or f16; G in {16, 32, 64, 128}; F % 16 == 0, 16 <= F <= 256.
+ * Supported: dtype bf16 or f16 (fp32 layers: haste_ffi_forward_f16_f32out, and the
+ * fp16 entry points on fp16 copies, as the reference's fp32 kernels compute);
+ * G in {16, 32, 64, 128}; F % 16 == 0, 16 <= F <= 256.
  * The reference envelope is G in {16,32,64}, F <= 128 (F <= 256 for G = 16);
  * this library accepts the wider set.
  */
@@ -333,21 +335,23 @@ int haste_transpose_features(const uint16_t* x, int64_t ldx, uint16_t* xT, int64
                              int64_t D, void* stream);
 
 /*
- * On-device rewire of a bf16 FFI layer (prune + regrow), in place on W and idx.
- * Replaces GroupFixedFanIn.rewire (shared_ffi/rewire.py:143-239) with a
- * deterministic contract:
+ * On-device rewire of an FFI layer (prune + regrow), in place on W and idx.
+ * W is bf16, fp16 or fp32 (w_dtype, as the reference's rewire works in the
+ * weights' own dtype).  Replaces GroupFixedFanIn.rewire
+ * (shared_ffi/rewire.py:143-239) with a deterministic contract:
  *   score[g, j] = (sequential fp32 sum over the group's rows of |W[l, j]|) / rows
  *   prune: THRESHOLD -> score < threshold; FRACTION -> the k smallest (score, j)
  *   regrow index: RANDOM -> floor(philox(seed; g*F+j, 1, 0).w0 * D / 2^32);
  *                 UNUSED -> attempts t = 0.. with counter (g*F+j, 1, t), first
  *                 candidate not present in the group (64 attempts, then the last)
  *   new weights of every row at a pruned slot: ZERO -> 0;
- *     RANDOM -> RNE(fma(u01, 2*bound, -bound)), u01 = (philox(seed; l*F+j, 2, 0).w0 >> 8) * 2^-24
+ *     RANDOM -> fma(u01, 2*bound, -bound), u01 = (philox(seed; l*F+j, 2, 0).w0 >> 8) * 2^-24,
+ *     stored in W's dtype (RNE to bf16 / fp16)
  * scores_out [Gc, F] fp32 and n_pruned (one int32, incremented) may be NULL.
  */
-int haste_rewire(uint16_t* W, int32_t* idx, float* scores_out, int32_t* n_pruned, int64_t O,
-                 int64_t F, int64_t G, int64_t D, int32_t prune_mode, float threshold, int64_t k,
-                 int32_t regrow_mode, int32_t init_mode, float bound, uint64_t seed,
+int haste_rewire(void* W, int32_t w_dtype, int32_t* idx, float* scores_out, int32_t* n_pruned,
+                 int64_t O, int64_t F, int64_t G, int64_t D, int32_t prune_mode, float threshold,
+                 int64_t k, int32_t regrow_mode, int32_t init_mode, float bound, uint64_t seed,
                  void* stream);
 
 /*
@@ -355,8 +359,9 @@ int haste_rewire(uint16_t* W, int32_t* idx, float* scores_out, int32_t* n_pruned
  * (src/group_fanin_real.py:150-286).  haste_rewire_scores writes the fp32
  * scores [ceil(O/G), F]: per slot, the mean (HASTE_SCORE_MEAN, fp32 sum over the
  * group's rows in ascending order / rows) or the max (HASTE_SCORE_MAX) of |W|,
- * or, with grad (bf16 or fp32, [O, F]) not NULL, of the saliency |W * grad| (the
- * product rounded to bf16 for a bf16 grad, as the reference's tensor product).
+ * or, with grad ([O, F], bf16, fp16 or fp32) not NULL, of the saliency |W * grad|
+ * (the product in torch's promoted dtype of W and grad, as the reference's tensor
+ * product: rounded to bf16 / fp16 when both are that format, else fp32).
  * haste_rewire_ex is haste_rewire with those score modes and one more prune
  * mode, HASTE_PRUNE_GLOBAL_FRACTION: prune the slots whose key
  * (bits(score) << 32 | g*F + j) is <= *key_thr, the k-th smallest key of the
@@ -364,10 +369,10 @@ int haste_rewire(uint16_t* W, int32_t* idx, float* scores_out, int32_t* n_pruned
  * selected by the caller on the device from scores_in (the scores of
  * haste_rewire_scores with the same modes).  Regrow and init as haste_rewire.
  */
-int haste_rewire_scores(const uint16_t* W, const void* grad, int32_t grad_dtype,
+int haste_rewire_scores(const void* W, int32_t w_dtype, const void* grad, int32_t grad_dtype,
                         int32_t score_mode, float* scores, int64_t O, int64_t F, int64_t G,
                         void* stream);
-int haste_rewire_ex(uint16_t* W, int32_t* idx, const void* grad, int32_t grad_dtype,
+int haste_rewire_ex(void* W, int32_t w_dtype, int32_t* idx, const void* grad, int32_t grad_dtype,
                     int32_t score_mode, const float* scores_in, const int64_t* key_thr,
                     float* scores_out, int32_t* n_pruned, int64_t O, int64_t F, int64_t G,
                     int64_t D, int32_t prune_mode, float threshold, int64_t k,

@@ -70,12 +70,13 @@ def lib() -> ctypes.CDLL:
         L.ho_sgd_sr_step_f16w.argtypes = [P, P, c_int, P, i64, f32, f32, f32, c_int, c_int, u64,
                                           u64]
         L.ho_f32_to_f16_rne_arr.argtypes = [P, P, i64]
-        L.ho_rewire_scores.argtypes = [P, P, i64, i64, i64]
-        L.ho_rewire.argtypes = [P, P, i64, i64, i64, i64, c_int, f32, i64, c_int, c_int, f32, u64, P, P]
+        L.ho_rewire_scores.argtypes = [P, c_int, P, i64, i64, i64]
+        L.ho_rewire.argtypes = [P, c_int, P, i64, i64, i64, i64, c_int, f32, i64, c_int, c_int,
+                                f32, u64, P, P]
         L.ho_rewire.restype = i64
-        L.ho_rewire_scores_ex.argtypes = [P, P, c_int, c_int, P, i64, i64, i64]
-        L.ho_rewire_ex.argtypes = [P, P, P, c_int, c_int, i64, i64, i64, i64, c_int, f32, i64,
-                                   c_int, c_int, f32, u64, P, P]
+        L.ho_rewire_scores_ex.argtypes = [P, c_int, P, c_int, c_int, P, i64, i64, i64]
+        L.ho_rewire_ex.argtypes = [P, c_int, P, P, c_int, c_int, i64, i64, i64, i64, c_int, f32,
+                                   i64, c_int, c_int, f32, u64, P, P]
         L.ho_rewire_ex.restype = i64
         L.ho_num_threads.restype = c_int
         L.ho_set_num_threads.argtypes = [c_int]
@@ -179,27 +180,41 @@ def f32_to_f16_rne(x: np.ndarray) -> np.ndarray:
     return out
 
 
-def rewire_scores(w_bits: np.ndarray, G: int) -> np.ndarray:
+# element types of the rewire functions' weights and gradients (haste_oracle.c HO_*)
+BF16, F16, F32 = 0, 1, 2
+
+
+def _weights(w: np.ndarray, w_dtype: int, copy: bool):
+    """(C-contiguous weights, dtype code): fp32 arrays are F32; uint16 arrays hold
+    the bit patterns of w_dtype (BF16 or F16)."""
+    if w.dtype == np.float32:
+        return np.array(w, dtype=np.float32, copy=copy, order="C"), F32
+    assert w_dtype in (BF16, F16), "uint16 weights are bf16 or fp16 bit patterns"
+    return np.array(w, dtype=np.uint16, copy=copy, order="C"), w_dtype
+
+
+def rewire_scores(w_bits: np.ndarray, G: int, w_dtype: int = BF16) -> np.ndarray:
     O, F = w_bits.shape
     Gc = (O + G - 1) // G
-    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    w, wd = _weights(w_bits, w_dtype, copy=False)
     s = np.empty((Gc, F), dtype=np.float32)
-    lib().ho_rewire_scores(_ptr(w_bits), _ptr(s), O, F, G)
+    lib().ho_rewire_scores(_ptr(w), wd, _ptr(s), O, F, G)
     return s
 
 
 def rewire(w_bits: np.ndarray, idx: np.ndarray, G: int, D: int, *, prune_mode: int,
            threshold: float = 0.0, k: int = 0, regrow_mode: int = REGROW_RANDOM,
-           init_mode: int = INIT_ZERO, bound: float = 0.0, seed: int = 0):
+           init_mode: int = INIT_ZERO, bound: float = 0.0, seed: int = 0, w_dtype: int = BF16):
     """Rewire contract of haste_oracle.c (restating shared_ffi/rewire.py:143-239).
-    Returns (new weight bits, new idx, n_pruned, scores, mask)."""
-    w = np.array(w_bits, dtype=np.uint16, copy=True, order="C")
+    w_bits: bf16 / fp16 bit patterns (uint16, w_dtype) or fp32 weights.
+    Returns (new weights in the same form, new idx, n_pruned, scores, mask)."""
+    w, wd = _weights(w_bits, w_dtype, copy=True)
     ix = np.array(idx, dtype=np.int32, copy=True, order="C")
     O, F = w.shape
     Gc = ix.shape[0]
     scores = np.empty((Gc, F), dtype=np.float32)
     mask = np.empty((Gc, F), dtype=np.uint8)
-    n = lib().ho_rewire(_ptr(w), _ptr(ix), O, F, G, D, prune_mode, np.float32(threshold), k,
+    n = lib().ho_rewire(_ptr(w), wd, _ptr(ix), O, F, G, D, prune_mode, np.float32(threshold), k,
                         regrow_mode, init_mode, np.float32(bound), seed, _ptr(scores), _ptr(mask))
     return w, ix, int(n), scores, mask.astype(bool)
 
@@ -208,25 +223,34 @@ PRUNE_GLOBAL_FRACTION = 2
 SCORE_MEAN, SCORE_MAX = 0, 1
 
 
-def _grad_f32(grad):
-    """grad as an fp32 array and whether it was bf16 (uint16 bit patterns)."""
+def _grad_f32(grad, grad_dtype: int, wd: int):
+    """(grad as an fp32 array, the dtype of the product W * grad): grad is None,
+    bit patterns (uint16) of grad_dtype (BF16 or F16) or fp32.  The product's
+    dtype is torch's promotion of the two: one 16-bit format for both, else fp32."""
     if grad is None:
-        return None, 0
+        return None, F32
     if grad.dtype == np.uint16:
-        return np.ascontiguousarray(bf16_bits_to_f32(grad), dtype=np.float32), 1
-    return np.ascontiguousarray(grad, dtype=np.float32), 0
+        assert grad_dtype in (BF16, F16), "uint16 gradients are bf16 or fp16 bit patterns"
+        gf = (bf16_bits_to_f32(grad) if grad_dtype == BF16 else
+              np.asarray(grad, dtype=np.uint16).view(np.float16).astype(np.float32))
+        gd = grad_dtype
+    else:
+        gf, gd = grad, F32
+    return np.ascontiguousarray(gf, dtype=np.float32), (gd if gd == wd else F32)
 
 
 def rewire_scores_ex(w_bits: np.ndarray, G: int, score_mode: int = SCORE_MEAN,
-                     grad: np.ndarray | None = None) -> np.ndarray:
+                     grad: np.ndarray | None = None, w_dtype: int = BF16,
+                     grad_dtype: int = BF16) -> np.ndarray:
     """Scores of the application's rewire variant (haste_oracle.c:ho_rewire_scores_ex);
-    grad is None, bf16 bit patterns (uint16) or fp32."""
+    weights and grad are None (grad only), bit patterns (uint16) of w_dtype /
+    grad_dtype, or fp32."""
     O, F = w_bits.shape
     Gc = (O + G - 1) // G
-    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
-    gf, gb = _grad_f32(grad)
+    w, wd = _weights(w_bits, w_dtype, copy=False)
+    gf, pd = _grad_f32(grad, grad_dtype, wd)
     s = np.empty((Gc, F), dtype=np.float32)
-    lib().ho_rewire_scores_ex(_ptr(w_bits), None if gf is None else _ptr(gf), gb, score_mode,
+    lib().ho_rewire_scores_ex(_ptr(w), wd, None if gf is None else _ptr(gf), pd, score_mode,
                               _ptr(s), O, F, G)
     return s
 
@@ -234,19 +258,21 @@ def rewire_scores_ex(w_bits: np.ndarray, G: int, score_mode: int = SCORE_MEAN,
 def rewire_ex(w_bits: np.ndarray, idx: np.ndarray, G: int, D: int, *, prune_mode: int,
               score_mode: int = SCORE_MEAN, grad: np.ndarray | None = None,
               threshold: float = 0.0, k: int = 0, regrow_mode: int = REGROW_RANDOM,
-              init_mode: int = INIT_ZERO, bound: float = 0.0, seed: int = 0):
+              init_mode: int = INIT_ZERO, bound: float = 0.0, seed: int = 0,
+              w_dtype: int = BF16, grad_dtype: int = BF16):
     """The application's rewire variant (GroupFixedFanInReal.rewire,
     src/group_fanin_real.py:150-286) under the contract of haste_oracle.c;
     k is per group for PRUNE_FRACTION and for the whole layer for
-    PRUNE_GLOBAL_FRACTION.  Returns (weight bits, idx, n_pruned, scores, mask)."""
-    w = np.array(w_bits, dtype=np.uint16, copy=True, order="C")
+    PRUNE_GLOBAL_FRACTION.  Weights and grad as rewire_scores_ex.
+    Returns (weights in the same form, idx, n_pruned, scores, mask)."""
+    w, wd = _weights(w_bits, w_dtype, copy=True)
     ix = np.array(idx, dtype=np.int32, copy=True, order="C")
     O, F = w.shape
     Gc = ix.shape[0]
-    gf, gb = _grad_f32(grad)
+    gf, pd = _grad_f32(grad, grad_dtype, wd)
     scores = np.empty((Gc, F), dtype=np.float32)
     mask = np.empty((Gc, F), dtype=np.uint8)
-    n = lib().ho_rewire_ex(_ptr(w), _ptr(ix), None if gf is None else _ptr(gf), gb, score_mode,
+    n = lib().ho_rewire_ex(_ptr(w), wd, _ptr(ix), None if gf is None else _ptr(gf), pd, score_mode,
                            O, F, G, D, prune_mode, np.float32(threshold), k, regrow_mode,
                            init_mode, np.float32(bound), seed, _ptr(scores), _ptr(mask))
     return w, ix, int(n), scores, mask.astype(bool)

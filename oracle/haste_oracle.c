@@ -250,7 +250,9 @@ void ho_set_num_threads(int n) {
  *  4. weights of every row of the group at a pruned slot:
  *       ZERO: 0.   RANDOM: u = philox(key = seed, ctr = (l*F + j, 2, 0, 0)).w0,
  *       v = fma((float)(u >> 8) * 2^-24, 2*bound, -bound), bound = 1/sqrt(F)
- *       (fp32, passed in), stored RNE to bf16.           (rewire.py:219-239)
+ *       (fp32, passed in), stored in W's dtype: RNE to bf16 / fp16, or as is
+       for fp32 weights (uniform_ in the weights' dtype, rewire.py:226-237).
+ * W: bf16 or fp16 bit patterns, or fp32 values (w_dtype HO_BF16 / HO_F16 / HO_F32).
  * Returns the number of pruned slots.  Scores and mask are optional outputs.
  * Pinned: invariants and brute-force selection in tests/test_oracle_rewire.py.
  * --------------------------------------------------------------------------- */
@@ -268,14 +270,36 @@ static uint32_t philox_w0(uint64_t seed, uint32_t c0, uint32_t c1, uint32_t c2) 
     return out[0];
 }
 
-void ho_rewire_scores(const uint16_t* W, float* scores, int64_t O, int64_t F, int64_t G) {
+/* W of dtype w_dtype (HO_BF16 / HO_F16 bit patterns, or HO_F32 values): element i
+ * as fp32 (exact), and stored from fp32 (RNE to the 16-bit formats) -- the
+ * reference's rewire works in the weights' own dtype (rewire.py:155,224-237). */
+static float w_get(const void* W, int w_dtype, int64_t i) {
+    if (w_dtype == HO_F32) return ((const float*)W)[i];
+    uint16_t h = ((const uint16_t*)W)[i];
+    return w_dtype == HO_F16 ? ho_f16_to_f32(h) : ho_bf16_to_f32(h);
+}
+static void w_set(void* W, int w_dtype, int64_t i, float v) {
+    if (w_dtype == HO_F32)
+        ((float*)W)[i] = v;
+    else
+        ((uint16_t*)W)[i] = w_dtype == HO_F16 ? ho_f32_to_f16_rne(v) : ho_f32_to_bf16_rne(v);
+}
+/* v rounded to dtype dt (RNE) and back: the value of a tensor product in dt */
+static float round_as(float v, int dt) {
+    if (dt == HO_BF16) return ho_bf16_to_f32(ho_f32_to_bf16_rne(v));
+    if (dt == HO_F16) return ho_f16_to_f32(ho_f32_to_f16_rne(v));
+    return v;
+}
+
+void ho_rewire_scores(const void* W, int w_dtype, float* scores, int64_t O, int64_t F,
+                      int64_t G) {
     int64_t Gc = (O + G - 1) / G;
     for (int64_t g = 0; g < Gc; ++g) {
         int64_t l0 = g * G, l1 = l0 + G < O ? l0 + G : O;
         float cnt = (float)(l1 - l0);
         for (int64_t j = 0; j < F; ++j) {
             float s = 0.0f;
-            for (int64_t l = l0; l < l1; ++l) s += fabsf(ho_bf16_to_f32(W[l * F + j]));
+            for (int64_t l = l0; l < l1; ++l) s += fabsf(w_get(W, w_dtype, l * F + j));
             scores[g * F + j] = s / cnt;
         }
     }
@@ -285,9 +309,10 @@ void ho_rewire_scores(const uint16_t* W, float* scores, int64_t O, int64_t F, in
  * The application's variant, GroupFixedFanInReal.rewire
  * (src/group_fanin_real.py:150-286):
  *  value v[l][j] = |W| or, with grad, the saliency |W * grad|
- *          (group_fanin_real.py:199-204); with grad_bf16 the product (exact in
- *          fp32 for two bf16 values) is rounded to bf16, as the reference's bf16
- *          tensor product; with an fp32 grad it is the fp32 product.
+ *          (group_fanin_real.py:199-204): the product in prod_dtype, torch's
+ *          promoted dtype of (W, grad) -- for two 16-bit values of one format
+ *          the (exact) fp32 product rounded to that format, else the fp32
+ *          product; grad is passed as its fp32 values.
  *  score  MEAN: fp32 sum over the group's rows in ascending order / rows
  *         (group_fanin_real.py:206-212,226-228); MAX: max over the rows
  *         (group_fanin_real.py:213-220).
@@ -298,23 +323,16 @@ void ho_rewire_scores(const uint16_t* W, float* scores, int64_t O, int64_t F, in
 enum { HO_PRUNE_GLOBAL_FRACTION = 2 };
 enum { HO_SCORE_MEAN = 0, HO_SCORE_MAX = 1 };
 
-void ho_rewire_scores_ex(const uint16_t* W, const float* grad, int grad_bf16, int score_mode,
-                         float* scores, int64_t O, int64_t F, int64_t G) {
+void ho_rewire_scores_ex(const void* W, int w_dtype, const float* grad, int prod_dtype,
+                         int score_mode, float* scores, int64_t O, int64_t F, int64_t G) {
     int64_t Gc = (O + G - 1) / G;
     for (int64_t g = 0; g < Gc; ++g) {
         int64_t l0 = g * G, l1 = l0 + G < O ? l0 + G : O;
         for (int64_t j = 0; j < F; ++j) {
             float acc = score_mode == HO_SCORE_MAX ? -INFINITY : 0.0f;
             for (int64_t l = l0; l < l1; ++l) {
-                float w = ho_bf16_to_f32(W[l * F + j]);
-                float v;
-                if (!grad) {
-                    v = fabsf(w);
-                } else if (grad_bf16) {
-                    v = fabsf(ho_bf16_to_f32(ho_f32_to_bf16_rne(w * grad[l * F + j])));
-                } else {
-                    v = fabsf(w * grad[l * F + j]);
-                }
+                float w = w_get(W, w_dtype, l * F + j);
+                float v = grad ? fabsf(round_as(w * grad[l * F + j], prod_dtype)) : fabsf(w);
                 acc = score_mode == HO_SCORE_MAX ? (v > acc ? v : acc) : acc + v;
             }
             scores[g * F + j] = score_mode == HO_SCORE_MAX ? acc : acc / (float)(l1 - l0);
@@ -327,19 +345,19 @@ static int cmp_u64(const void* a, const void* b) {
     return x < y ? -1 : (x > y ? 1 : 0);
 }
 
-static int64_t rewire_apply(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G,
-                            int64_t D, int prune_mode, float thr, int64_t k, int regrow_mode,
-                            int init_mode, float bound, uint64_t seed, const float* scores,
-                            uint8_t* mask);
+static int64_t rewire_apply(void* W, int w_dtype, int32_t* idx, int64_t O, int64_t F,
+                            int64_t G, int64_t D, int prune_mode, float thr, int64_t k,
+                            int regrow_mode, int init_mode, float bound, uint64_t seed,
+                            const float* scores, uint8_t* mask);
 
-int64_t ho_rewire_ex(uint16_t* W, int32_t* idx, const float* grad, int grad_bf16,
+int64_t ho_rewire_ex(void* W, int w_dtype, int32_t* idx, const float* grad, int prod_dtype,
                      int score_mode, int64_t O, int64_t F, int64_t G, int64_t D,
                      int prune_mode, float thr, int64_t k, int regrow_mode, int init_mode,
                      float bound, uint64_t seed, float* scores_out, uint8_t* mask_out) {
     int64_t Gc = (O + G - 1) / G, n = Gc * F;
     float* scores = (float*)malloc(sizeof(float) * (size_t)n);
     uint8_t* mask = (uint8_t*)calloc((size_t)n, 1);
-    ho_rewire_scores_ex(W, grad, grad_bf16, score_mode, scores, O, F, G);
+    ho_rewire_scores_ex(W, w_dtype, grad, prod_dtype, score_mode, scores, O, F, G);
     if (prune_mode == HO_PRUNE_GLOBAL_FRACTION) {
         /* keys (bits(score) << 32 | slot) order the scores (>= 0) with ties to the lower slot */
         uint64_t* keys = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)n);
@@ -352,8 +370,8 @@ int64_t ho_rewire_ex(uint16_t* W, int32_t* idx, const float* grad, int grad_bf16
         for (int64_t r = 0; r < k && r < n; ++r) mask[keys[r] & 0xFFFFFFFFu] = 1;
         free(keys);
     }
-    int64_t total = rewire_apply(W, idx, O, F, G, D, prune_mode, thr, k, regrow_mode, init_mode,
-                                 bound, seed, scores, mask);
+    int64_t total = rewire_apply(W, w_dtype, idx, O, F, G, D, prune_mode, thr, k, regrow_mode,
+                                 init_mode, bound, seed, scores, mask);
     if (scores_out) memcpy(scores_out, scores, sizeof(float) * (size_t)n);
     if (mask_out) memcpy(mask_out, mask, (size_t)n);
     free(scores);
@@ -361,19 +379,20 @@ int64_t ho_rewire_ex(uint16_t* W, int32_t* idx, const float* grad, int grad_bf16
     return total;
 }
 
-int64_t ho_rewire(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G, int64_t D,
-                  int prune_mode, float thr, int64_t k, int regrow_mode, int init_mode,
-                  float bound, uint64_t seed, float* scores_out, uint8_t* mask_out) {
-    return ho_rewire_ex(W, idx, NULL, 0, HO_SCORE_MEAN, O, F, G, D, prune_mode, thr, k,
-                        regrow_mode, init_mode, bound, seed, scores_out, mask_out);
+int64_t ho_rewire(void* W, int w_dtype, int32_t* idx, int64_t O, int64_t F, int64_t G,
+                  int64_t D, int prune_mode, float thr, int64_t k, int regrow_mode,
+                  int init_mode, float bound, uint64_t seed, float* scores_out,
+                  uint8_t* mask_out) {
+    return ho_rewire_ex(W, w_dtype, idx, NULL, HO_F32, HO_SCORE_MEAN, O, F, G, D, prune_mode,
+                        thr, k, regrow_mode, init_mode, bound, seed, scores_out, mask_out);
 }
 
 /* prune (threshold / per-group fraction into mask; global fraction: mask given),
  * regrow and re-initialise; returns the number of pruned slots */
-static int64_t rewire_apply(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int64_t G,
-                            int64_t D, int prune_mode, float thr, int64_t k, int regrow_mode,
-                            int init_mode, float bound, uint64_t seed, const float* scores,
-                            uint8_t* mask) {
+static int64_t rewire_apply(void* W, int w_dtype, int32_t* idx, int64_t O, int64_t F,
+                            int64_t G, int64_t D, int prune_mode, float thr, int64_t k,
+                            int regrow_mode, int init_mode, float bound, uint64_t seed,
+                            const float* scores, uint8_t* mask) {
     int64_t Gc = (O + G - 1) / G;
     int64_t total = 0;
     for (int64_t g = 0; g < Gc; ++g) {
@@ -416,11 +435,11 @@ static int64_t rewire_apply(uint16_t* W, int32_t* idx, int64_t O, int64_t F, int
             for (int64_t j = 0; j < F; ++j) {
                 if (!mk[j]) continue;
                 if (init_mode == HO_INIT_ZERO) {
-                    W[l * F + j] = 0;
+                    w_set(W, w_dtype, l * F + j, 0.0f);
                 } else {
                     uint32_t u = philox_w0(seed, (uint32_t)(l * F + j), 2u, 0u);
                     float u01 = (float)(u >> 8) * 0x1p-24f;
-                    W[l * F + j] = ho_f32_to_bf16_rne(fmaf(u01, 2.0f * bound, -bound));
+                    w_set(W, w_dtype, l * F + j, fmaf(u01, 2.0f * bound, -bound));
                 }
             }
         }

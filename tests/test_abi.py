@@ -29,7 +29,7 @@ def test_library_exports_every_symbol():
 
 
 def test_version_and_error_string():
-    assert _lib.lib().haste_abi_version() == 1
+    assert _lib.lib().haste_abi_version() == 2
     assert isinstance(_lib.last_error(), str)
 
 
@@ -101,9 +101,16 @@ def test_sgd_rejects_bad_dtype_and_missing_momentum():
 
 def test_rewire_rejects_bad_modes():
     L = _lib.lib()
-    assert L.haste_rewire(16, 32, None, None, 100, 8, 16, 50, 5, 0.0, 0, 0, 0, 0.1, 1, None) == \
-        _lib.HASTE_ERR_INVALID_ARG
-    assert L.haste_rewire(16, 32, None, None, 100, 8, 16, 50, 1, 0.0, 9, 0, 0, 0.1, 1, None) == \
+    bf16 = _lib.DTYPE_BF16
+    assert L.haste_rewire(16, bf16, 32, None, None, 100, 8, 16, 50, 5, 0.0, 0, 0, 0, 0.1, 1,
+                          None) == _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_rewire(16, bf16, 32, None, None, 100, 8, 16, 50, 1, 0.0, 9, 0, 0, 0.1, 1,
+                          None) == _lib.HASTE_ERR_INVALID_ARG
+    # weights must be bf16, fp16 or fp32
+    assert L.haste_rewire(16, 7, 32, None, None, 100, 8, 16, 50, 1, 0.0, 2, 0, 0, 0.1, 1,
+                          None) == _lib.HASTE_ERR_INVALID_ARG
+    assert "bf16, fp16 or fp32" in _lib.last_error()
+    assert L.haste_rewire_scores(16, 7, None, 0, 0, 32, 100, 8, 16, None) == \
         _lib.HASTE_ERR_INVALID_ARG
 
 

@@ -129,3 +129,71 @@ def test_f32_head_tail_logits(dev):
     torch.testing.assert_close(W.grad.cpu(), oracle.ffi_backward_weights(idxc, h(xT), h(gt), G),
                                **TOL32)
     assert torch.equal(bias.grad, g_out[:, H:].sum(0))
+
+
+# ---- rewire of fp16 / fp32 layers (the reference rewires in the weights' dtype,
+# shared_ffi/rewire.py:155,224-237): bit-exact against the oracle ----
+def _w_np(t):
+    t = t.detach().cpu()
+    return t.numpy().copy() if t.dtype == torch.float32 else t.view(torch.int16).numpy().view(np.uint16).copy()
+
+
+_WCODE = {torch.float16: oracle.F16, torch.float32: oracle.F32, torch.bfloat16: oracle.BF16}
+
+
+@pytest.mark.parametrize("wdt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("init", ["zero", "random"])
+def test_rewire_f16_f32_layers_match_oracle(dev, wdt, init):
+    O, F, G, D = 1000, 64, 32, 300
+    torch.manual_seed(7)
+    layer = GroupFixedFanIn(D, O, F, group_size=G, prune_mode="fraction", rewire_fraction=0.15,
+                            init_mode=init, dtype=wdt)
+    w, idx = _w_np(layer.weights), layer.group_locations.numpy().copy()
+    seed = 0x5EED + O
+    ref_w, ref_idx, ref_n, _, _ = oracle.rewire(
+        w, idx, G, D, prune_mode=oracle.PRUNE_FRACTION, k=int(F * 0.15),
+        init_mode=oracle.INIT_RANDOM if init == "random" else oracle.INIT_ZERO,
+        bound=1.0 / F ** 0.5, seed=seed, w_dtype=_WCODE[wdt])
+    layer = layer.to(dev)
+    layer.rewire(seed=seed)
+    torch.cuda.synchronize()
+    assert layer.weights.dtype == wdt
+    assert layer.pruned_total == ref_n
+    assert np.array_equal(layer.group_locations.cpu().numpy(), ref_idx)
+    assert np.array_equal(_w_np(layer.weights), ref_w)
+
+
+@pytest.mark.parametrize("wdt,gdt,score", [(torch.float16, torch.float16, "mean"),
+                                           (torch.float16, torch.float32, "max"),
+                                           (torch.float32, torch.float32, "mean"),
+                                           (torch.float32, None, "max")])
+def test_app_rewire_f16_f32_layers_match_oracle(dev, wdt, gdt, score):
+    from haste_amd.rewire import GroupFixedFanInReal
+    O, F, G, D = 777, 128, 64, 768
+    torch.manual_seed(8)
+    layer = GroupFixedFanInReal(D, O, F, group_size=G, prune_mode="fraction",
+                                rewire_fraction=0.15, init_mode="random", score_mode=score,
+                                regrow_mode="unused", dtype=wdt,
+                                fp32_grads=gdt == torch.float32 and wdt != torch.float32)
+    w, idx = _w_np(layer.weights), layer.group_locations.numpy().copy()
+    g_np = None
+    if gdt is not None:
+        gt = (torch.randn(O, F, generator=torch.Generator().manual_seed(9)) * 1e-2).to(gdt)
+        g_np = _w_np(gt)
+    Gc = (O + G - 1) // G
+    k = int(Gc * F * 0.15)
+    seed = 0xFACE + O
+    ref_w, ref_idx, ref_n, _, _ = oracle.rewire_ex(
+        w, idx, G, D, prune_mode=oracle.PRUNE_GLOBAL_FRACTION,
+        score_mode=oracle.SCORE_MAX if score == "max" else oracle.SCORE_MEAN, grad=g_np, k=k,
+        regrow_mode=oracle.REGROW_UNUSED, init_mode=oracle.INIT_RANDOM, bound=1.0 / F ** 0.5,
+        seed=seed, w_dtype=_WCODE[wdt], grad_dtype=_WCODE[gdt] if gdt is not None else oracle.BF16)
+    layer = layer.to(dev)
+    if gdt is not None:
+        layer.use_grad = True
+        layer.weights.grad = gt.to(dev)
+    layer.rewire(seed=seed)
+    torch.cuda.synchronize()
+    assert layer.pruned_total == ref_n == k
+    assert np.array_equal(layer.group_locations.cpu().numpy(), ref_idx)
+    assert np.array_equal(_w_np(layer.weights), ref_w)

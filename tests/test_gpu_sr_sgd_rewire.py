@@ -212,8 +212,8 @@ def test_rewire(dev, O, F, G, D, prune, kt, regrow, init):
     idxd = torch.from_numpy(idx).to(dev)
     scores = torch.empty(Gc, F, device=dev)
     cnt = torch.zeros(1, dtype=torch.int32, device=dev)
-    _lib.call("haste_rewire", Wd.data_ptr(), idxd.data_ptr(), scores.data_ptr(), cnt.data_ptr(), O, F,
-              G, D, pm, thr, k, rm, im, bound, seed, _C.stream_of(Wd))
+    _lib.call("haste_rewire", Wd.data_ptr(), _lib.DTYPE_BF16, idxd.data_ptr(), scores.data_ptr(),
+              cnt.data_ptr(), O, F, G, D, pm, thr, k, rm, im, bound, seed, _C.stream_of(Wd))
     assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
     assert np.array_equal(idxd.cpu().numpy(), ref_idx)
     assert np.array_equal(bits(Wd), ref_w)

@@ -187,3 +187,72 @@ def test_app_rewire_invariants():
     rows_mask = np.repeat(mask, 16, axis=0)[:200]
     assert np.all(w2[rows_mask] == 0) and np.array_equal(w2[~rows_mask], wb[~rows_mask])
     assert np.array_equal(ix2[~mask], idx[~mask]) and ix2.min() >= 0 and ix2.max() < D
+
+
+# ---- fp16 and fp32 weights (the reference's rewire works in the weights' dtype,
+# shared_ffi/rewire.py:155,169-185,224-237; group_fanin_real.py:199-204) ----
+def _np_of(t):
+    """A tensor as the oracle takes it: uint16 bit patterns (bf16 / fp16) or fp32."""
+    if t.dtype == torch.float32:
+        return t.numpy()
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+_CODE = {torch.bfloat16: oracle.BF16, torch.float16: oracle.F16, torch.float32: oracle.F32}
+
+
+@pytest.mark.parametrize("mode", ["mean", "max"])
+@pytest.mark.parametrize("wdt,gdt", [(torch.float16, None), (torch.float16, torch.float16),
+                                     (torch.float16, torch.float32),
+                                     (torch.float16, torch.bfloat16),
+                                     (torch.float32, None), (torch.float32, torch.float32),
+                                     (torch.float32, torch.bfloat16)])
+def test_app_scores_other_weight_dtypes_match_reference_steps(mode, wdt, gdt):
+    """Scores of fp16 / fp32 weights, with or without a gradient of any dtype,
+    equal the reference's torch steps on the same tensors (the product W * grad in
+    torch's promoted dtype: fp16 for two fp16 tensors, else fp32)."""
+    Wb, gb = _app_case(seed=12)
+    W = (Wb.float() * 1.7).to(wdt)
+    grad = None if gdt is None else (gb.float() * 0.9).to(gdt)
+    sm = oracle.SCORE_MEAN if mode == "mean" else oracle.SCORE_MAX
+    got = torch.from_numpy(oracle.rewire_scores_ex(
+        _np_of(W), 16, sm, None if grad is None else _np_of(grad), w_dtype=_CODE[wdt],
+        grad_dtype=_CODE[gdt] if gdt is not None else oracle.BF16))
+    ref = _ref_scores(W, grad, 16, mode)
+    if mode == "max":
+        assert torch.equal(got, ref)
+    else:
+        torch.testing.assert_close(got, ref, rtol=2e-6, atol=0)
+    if grad is None and mode == "mean":
+        assert np.array_equal(got.numpy(), oracle.rewire_scores(_np_of(W), 16, w_dtype=_CODE[wdt]))
+
+
+@pytest.mark.parametrize("init_mode", ["zero", "random"])
+def test_rewire_weight_dtypes_agree(init_mode):
+    """Weights that bf16, fp16 and fp32 all hold exactly give the same scores, mask
+    and indices in every format; the re-initialised weights are the fp32 draws
+    stored in each format (RNE to bf16 / fp16, as is for fp32), every other
+    weight unchanged."""
+    O, F, G, D = 96, 16, 32, 60
+    w, idx = _layer(O, F, G, D, seed=4)
+    wf = bf16_bits_to_f32(w)                   # |w| <= 1/4: exact in fp16 too
+    b = 1 / math.sqrt(F)
+    im = oracle.INIT_ZERO if init_mode == "zero" else oracle.INIT_RANDOM
+    kw = dict(prune_mode=oracle.PRUNE_FRACTION, k=5, regrow_mode=oracle.REGROW_UNUSED,
+              init_mode=im, bound=b, seed=21)
+    wh = wf.astype(np.float16).view(np.uint16)
+    r_bf = oracle.rewire(w, idx, G, D, **kw)
+    r_h = oracle.rewire(wh, idx, G, D, w_dtype=oracle.F16, **kw)
+    r_f = oracle.rewire(wf.copy(), idx, G, D, **kw)
+    for r in (r_h, r_f):
+        assert np.array_equal(r[1], r_bf[1]) and r[2] == r_bf[2]
+        assert np.array_equal(r[3], r_bf[3]) and np.array_equal(r[4], r_bf[4])
+    rows = r_bf[4][np.arange(O) // G]
+    assert np.array_equal(r_f[0][~rows], wf[~rows]) and np.array_equal(r_h[0][~rows], wh[~rows])
+    assert np.array_equal(f32_to_bf16_bits(r_f[0]), r_bf[0])
+    assert np.array_equal(r_f[0].astype(np.float16).view(np.uint16), r_h[0])
+    if init_mode == "zero":
+        assert np.all(r_f[0][rows] == 0)
+    else:
+        v = r_f[0][rows]
+        assert np.all(np.abs(v) <= b) and np.unique(v).size == v.size  # fp32 draws, unrounded
