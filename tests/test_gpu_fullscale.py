@@ -1,4 +1,4 @@
-"""Value checks at the full sizes of BASELINE configs 1 and 4 (GPU).
+"""Value checks at the full sizes of BASELINE configs 1 to 4 (GPU).
 
 Config 1 (B=512, D=768, O=131073, G=64, F=128) is checked whole against the
 CPU oracle: forward, backward to features (fp32 and the SR'd bf16 dX),
@@ -12,7 +12,8 @@ groups -- the first, the one holding label 2^31 / B, and the last (64
 labels) -- with dY zero outside them, so the oracle's result on those groups
 alone is exact for dX.  Logits, dX, dW, dbias and the fused SR-SGD bits of
 their rows are compared; rows outside them get dW = 0 and the decay-only
-update.
+update.  Configs 2 and 3 are checked the same way on three groups each,
+through the training step's own backward (partials + fused update with dX).
 
 Tolerances as in test_gpu_ffi.py: rtol 1e-2 / atol 1e-3 for bf16 outputs,
 rtol 1e-4 / atol 1e-5 for fp32 ones, bit-exact for SR and SR-SGD.
@@ -148,4 +149,68 @@ def test_config4_full_size_spot_groups(dev):
         assert np.array_equal(bits(W[a:b]).reshape(-1), ref), (a, b)
         ref_b, _ = oracle.sgd_sr_step(bits(b0[a:b]), db[a:b].cpu().numpy(), None, LR, WD, 0.0,
                                       False, True, 7, offset0=a)
+        assert np.array_equal(bits(bias[a:b]), ref_b), (a, b)
+
+
+@pytest.mark.parametrize("cfg", [
+    # config 2: 670K labels, F = 64; dY (686 MB) beyond the last-level cache, so
+    # bwd-features runs its LDS-ring build
+    dict(B=512, D=768, O=670_091, G=64, F=64, relu=False, seed=41),
+    # config 3: D = 4096 (many feature ranges, 64-column batch tiles), F = 256,
+    # post-ReLU features (about half zeros)
+    dict(B=256, D=4096, O=500_000, G=32, F=256, relu=True, seed=51),
+])
+def test_configs_2_3_full_size_spot_groups(dev, cfg):
+    """BASELINE configs 2 and 3 at full size: the training step (forward, bwd-features
+    partials finished by the fused update's launch, fused SR-SGD) checked on the
+    first, a middle and the last group against the oracle, with dY zero outside
+    them (so dX of those groups alone is exact); other rows get dW = 0 and the
+    decay-only update."""
+    B, D, O, G, F = cfg["B"], cfg["D"], cfg["O"], cfg["G"], cfg["F"]
+    Gc = (O + G - 1) // G
+    x, W, bias, idx = make(B, D, O, G, F, dev, seed=cfg["seed"])
+    if cfg["relu"]:
+        x = x.clamp_min(0)
+    groups = [0, Gc // 2, Gc - 1]
+    spans = [(g * G, min(O, (g + 1) * G)) for g in groups]
+    w0, b0 = W.clone(), bias.clone()
+    st = FFITrainStep(W, bias, idx, B, D, G, LR, WD, seed=9)
+    xT = x.cpu().t().contiguous()
+    idx_s = idx.cpu()[groups]
+    W_s = torch.cat([w0[a:b].cpu() for a, b in spans])
+    b_s = torch.cat([b0[a:b].cpu() for a, b in spans])
+
+    gy = torch.Generator(device=dev).manual_seed(cfg["seed"] + 1)
+    dY = torch.zeros(B, st.ldo, dtype=torch.bfloat16, device=dev)
+    for a, b in spans:
+        dY[:, a:b] = (torch.randn(B, b - a, generator=gy, device=dev) * 0.1).to(torch.bfloat16)
+    dY_s = torch.cat([dY[:, a:b].cpu() for a, b in spans], dim=1)
+    # the reference values of dW / dbias and the fp32 feature gradient, before the step
+    st.forward(x)
+    logits = st.logits
+    got = torch.cat([logits[:, a:b].cpu() for a, b in spans], dim=1)
+    torch.testing.assert_close(got.float(), oracle.ffi_forward(idx_s, xT, W_s, b_s, G), **TOL16)
+    dW, db = bwd_weights_fp32(idx, st.xT_buf, st.ldx, dY, st.ldo, B, D, F, O, G)
+    ref_w = oracle.ffi_backward_weights(idx_s, xT, dY_s, G)
+    torch.testing.assert_close(torch.cat([dW[a:b].cpu() for a, b in spans]), ref_w, **TOL32)
+    torch.testing.assert_close(torch.cat([db[a:b].cpu() for a, b in spans]), oracle.bias_grad(dY_s),
+                               **TOL32)
+    dxt = bwd_features_fp32(idx, W, dY, st.ldo, B, D, F, O, G)
+    torch.testing.assert_close(dxt.cpu(), oracle.ffi_backward_features(idx_s, W_s, dY_s, G, D),
+                               **TOL32)
+
+    # the training step's backward: partials, then the fused update writes dX too
+    st.backward_features(dY, st.ldo, defer_dx=True)
+    st.backward_weights_sgd(dY, st.ldo)
+    torch.cuda.synchronize()
+    exp = oracle.sr_round_bf16(dxt.t().contiguous().cpu().numpy(), 123)
+    assert np.array_equal(bits(st.dX), exp)
+    others = [G + 1, Gc // 3 * G + 5, O - G - 1]  # rows outside the groups
+    assert all(not dW[r].any() and float(db[r]) == 0.0 for r in others)
+    for (a, b) in spans + [(r, r + 1) for r in others]:
+        ref, _ = oracle.sgd_sr_step(bits(w0[a:b]).reshape(-1), dW[a:b].cpu().numpy().reshape(-1),
+                                    None, LR, WD, 0.0, False, True, 9, offset0=a * F)
+        assert np.array_equal(bits(W[a:b]).reshape(-1), ref), (a, b)
+        ref_b, _ = oracle.sgd_sr_step(bits(b0[a:b]), db[a:b].cpu().numpy(), None, LR, WD, 0.0,
+                                      False, True, 9, offset0=a)
         assert np.array_equal(bits(bias[a:b]), ref_b), (a, b)
