@@ -3,8 +3,10 @@
 ``FFITrainStep`` runs forward -> backward to features -> backward to weights
 and bias fused with the SR-SGD update of weights and bias, calling
 libhaste_ffi.so directly with buffers allocated once, so a step launches only
-HIP kernels (no allocator traffic, no host sync) and can be captured in a HIP
-graph.  It computes the same quantities as GroupFFIMulFunction + SRSgd with
+HIP kernels (no allocator traffic, no host sync).  The SR-SGD seed is a launch
+argument, so a step captured in a HIP graph replays with the seed it was
+captured with (capture each step's seed, or run the steps eagerly, to keep the
+seed += 1 schedule).  It computes the same quantities as GroupFFIMulFunction + SRSgd with
 two deliberate choices: the weight and bias gradients are fp32 (``grad_dtype``)
 and, in ``step``, never leave the chip (the SGD update is applied in the
 epilogue of the weight-gradient kernel; the result is bit-identical to
