@@ -14,7 +14,9 @@ step time then stays flat for seconds), then exactly K timed steps.  Inputs are
 synthetic and resident in HBM before timing; the grad of the logits
 dY = bf16(sigmoid(z) - Y) is computed once from the initial logits (BASELINE
 configs: Y binary, ~5 positives per row (10 at config 4), Zipf(1.1) over
-labels).  "fused_loss" times the step a training loop runs instead: the
+labels).  "hip_graph" is the same step captured once in a HIP graph and
+replayed (the SR-SGD seed is read and advanced on the device).  "fused_loss"
+times the step a training loop runs instead: the
 forward computes dY = sigma(z) - Y and the BCE loss from the COO labels in its
 epilogue (no logits written), then the same backward and update.
 
@@ -472,6 +474,19 @@ def main():
                               lambda: st.backward_weights_sgd(st.dY_buf, ldy)],
                              max(5, args.steps // 2), 2, stream)
 
+    # the same fused step captured once in a HIP graph and replayed (the SR-SGD seed
+    # read and advanced on the device), on a copy of the parameters
+    from haste_amd.step import FFITrainStep
+    gst = FFITrainStep(st.W.clone(), None if st.bias is None else st.bias.clone(), st.idx, B, D,
+                       G, lr=LR, weight_decay=WD, seed=SEED, device_seed=True)
+    gst.step(x, dY_buf, ldy)   # builds the index plan outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gst.step(x, dY_buf, ldy)
+    gr_ms, _, _ = timed([graph.replay], max(5, args.steps // 2), 2, stream)
+    del graph, gst
+
     pb = phase_bytes(B, D, O, G, F)
     phase_gbs = {n: pb[n] / (phase_ms[n] * 1e-3) / 1e9 for n in NAMES}
     dom = max(NAMES, key=lambda n: phase_ms[n])
@@ -507,6 +522,9 @@ def main():
                        "workload": "forward + sparse BCE gradient from COO labels (loss summed "
                                    "on the device, logits not written) + bwd_features + "
                                    "bwd_weights + SR-SGD"},
+        "hip_graph": {"ms_per_step": gr_ms, "samples_per_s": B / (gr_ms * 1e-3),
+                      "workload": "the same step captured once in a HIP graph "
+                                  "(FFITrainStep(device_seed=True)) and replayed"},
         "wall_s": wall,
     }
     tr = measured_traffic(args.config, dom)

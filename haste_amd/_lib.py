@@ -72,6 +72,10 @@ SIGNATURES = {
     "haste_ffi_bwd_weights_sgd_dx": (ctypes.c_int, [_P, _P, _I64, _P, _I64, _P, _P, _P, _P, _F32,
                                                     _F32, _F32, _I32, _I32, _U64, _P, _U64, _P,
                                                     _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
+    "haste_ffi_bwd_weights_sgd_dx_dev_seed": (ctypes.c_int, [_P, _P, _I64, _P, _I64, _P, _P, _P,
+                                                             _P, _F32, _F32, _F32, _I32, _I32,
+                                                             _P, _P, _U64, _P, _I64, _I64, _I64,
+                                                             _I64, _I64, _I64, _I32, _P]),
     "haste_sgd_sr_step_wt": (ctypes.c_int, [_P, _P, _I32, _P, _F32, _F32, _F32, _I32, _I32, _U64,
                                             _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
     "haste_sr_round_bf16": (ctypes.c_int, [_P, _P, _I64, _U64, _U64, _P]),

@@ -53,6 +53,7 @@ struct SgdArgs {
     const int* meta;
     int ndr, Tcap;
     ReduceJob rj;  // ntiles > 0: workgroups Gc .. Gc + ntiles - 1 run this job's tiles
+    const uint64_t* seed_dev;  // not NULL: the Philox seed is read here (k0, k1 unused)
 };
 
 namespace {
@@ -139,6 +140,15 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     }
     const int64_t g = blockIdx.x == 0 ? Gc - 1 : (int64_t)blockIdx.x - 1;
     const int tid = threadIdx.x;
+    // the SGD step's Philox key: the launch's seed, or the device-side seed
+    uint32_t sk0 = sg.k0, sk1 = sg.k1;
+    if constexpr (SGD) {
+        if (sg.seed_dev != nullptr) {
+            const uint64_t s = *sg.seed_dev;
+            sk0 = (uint32_t)s;
+            sk1 = (uint32_t)(s >> 32);
+        }
+    }
     // the wave index as a scalar: branches on wm / wn / active are then scalar
     // branches that skip their MFMAs (an MFMA under an EXEC mask still runs and
     // writes every lane)
@@ -392,8 +402,8 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                 const int64_t l = l0 + tid;
                 float mv = sg.use_mom ? sg.mb[l] : 0.f;
                 sg.bias[l] = (uint16_t)sgd_one(bf16_bits_to_f32(bpre), s_bg[tid], &mv, sg.use_mom,
-                                               sg.lr, sg.wd, sg.mu, sg.do_sr, (uint64_t)l, sg.k0,
-                                               sg.k1);
+                                               sg.lr, sg.wd, sg.mu, sg.do_sr, (uint64_t)l, sk0,
+                                               sk1);
                 if (sg.use_mom) sg.mb[l] = mv;
             }
         }
@@ -436,7 +446,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const uint32_t wb = (k & 1) ? (wv[k >> 1] >> 16) : (wv[k >> 1] & 0xFFFFu);
-                    const uint32_t r = sg.do_sr ? philox_w0_32(off + k, sg.k0, sg.k1) : 0u;
+                    const uint32_t r = sg.do_sr ? philox_w0_32(off + k, sk0, sk1) : 0u;
                     ob[k] = sgd_one_r(bf16_bits_to_f32(wb), gv[k], &mv[k], sg.use_mom, sg.lr,
                                       sg.wd, sg.mu, sg.do_sr, r);
                 }

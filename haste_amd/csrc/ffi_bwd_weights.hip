@@ -81,7 +81,8 @@ int bwdw_sgd(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, co
              int32_t dW_dtype, void* dbias, int32_t dbias_dtype, float lr, float wd, float mu,
              int32_t use_mom, int32_t do_sr, uint64_t seed, uint16_t* dX, uint64_t dx_seed,
              void* bwdf_workspace, int64_t bwdf_workspace_bytes, int64_t B, int64_t D, int64_t F,
-             int64_t O, int64_t G, int32_t dtype, void* stream) {
+             int64_t O, int64_t G, int32_t dtype, void* stream,
+             const uint64_t* seed_dev = nullptr) {
     int rc = check_bwdw(fn, idx, xT, ldx, dY, lddy, dW_dtype, dbias, dbias_dtype, B, D, F, O, G,
                         dtype);
     if (rc != HASTE_OK) return rc;
@@ -97,7 +98,7 @@ int bwdw_sgd(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, co
                     "%s: momentum buffers missing or misaligned", fn);
     SgdArgs sg{W, bias, m_W, m_bias, lr, wd, mu, use_mom ? 1 : 0, do_sr ? 1 : 0,
                (uint32_t)seed, (uint32_t)(seed >> 32), nullptr, nullptr, nullptr, nullptr,
-               0, 0, ReduceJob{}};
+               0, 0, ReduceJob{}, seed_dev};
     if (bwdf_workspace != nullptr) {
         const BwdFPlan p = make_plan(B, D, F, O, G);
         HASTE_CHECK_ARG(aligned16(bwdf_workspace) &&
@@ -122,6 +123,37 @@ int bwdw_sgd(const char* fn, const int32_t* idx, const void* xT, int64_t ldx, co
 
 }  // namespace
 }  // namespace haste
+
+namespace haste {
+namespace {
+// seed += 1 on the device (one lane; a vector store, its address from a VGPR)
+__global__ void seed_advance_kernel(uint64_t* __restrict__ seed) {
+    const int t = (int)threadIdx.x;
+    if (t == 0) seed[t] += 1u;
+}
+}  // namespace
+}  // namespace haste
+
+extern "C" int haste_ffi_bwd_weights_sgd_dx_dev_seed(
+    const int32_t* idx, const void* xT, int64_t ldx, const void* dY, int64_t lddy, uint16_t* W,
+    uint16_t* bias, float* m_W, float* m_bias, float lr, float wd, float mu, int32_t use_mom,
+    int32_t do_sr, uint64_t* seed_dev, uint16_t* dX, uint64_t dx_seed, void* bwdf_workspace,
+    int64_t bwdf_workspace_bytes, int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+    int32_t dtype, void* stream) {
+    const char* fn = "haste_ffi_bwd_weights_sgd_dx_dev_seed";
+    HASTE_CHECK_ARG(dX != nullptr && bwdf_workspace != nullptr,
+                    "%s: dX and the bwd-features workspace are required", fn);
+    HASTE_CHECK_ARG(seed_dev != nullptr && reinterpret_cast<uintptr_t>(seed_dev) % 8 == 0,
+                    "%s: seed_dev must be an 8-byte aligned device pointer", fn);
+    int rc = haste::bwdw_sgd(fn, idx, xT, ldx, dY, lddy, W, bias, m_W, m_bias, nullptr,
+                             HASTE_DTYPE_F32, nullptr, HASTE_DTYPE_F32, lr, wd, mu, use_mom,
+                             do_sr, 0, dX, dx_seed, bwdf_workspace, bwdf_workspace_bytes, B, D, F,
+                             O, G, dtype, stream, seed_dev);
+    if (rc != HASTE_OK) return rc;
+    haste::seed_advance_kernel<<<dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream)>>>(seed_dev);
+    HASTE_CHECK_LAUNCH(fn);
+    return HASTE_OK;
+}
 
 extern "C" int haste_ffi_bwd_weights_sgd(const int32_t* idx, const void* xT, int64_t ldx,
                                          const void* dY, int64_t lddy, uint16_t* W,

@@ -3,10 +3,12 @@
 ``FFITrainStep`` runs forward -> backward to features -> backward to weights
 and bias fused with the SR-SGD update of weights and bias, calling
 libhaste_ffi.so directly with buffers allocated once, so a step launches only
-HIP kernels (no allocator traffic, no host sync).  The SR-SGD seed is a launch
-argument, so a step captured in a HIP graph replays with the seed it was
-captured with (capture each step's seed, or run the steps eagerly, to keep the
-seed += 1 schedule).  It computes the same quantities as GroupFFIMulFunction + SRSgd with
+HIP kernels (no allocator traffic, no host sync).  With ``device_seed=True`` the
+SR-SGD seed lives in device memory and the fused update advances it there, so
+``step`` (and ``step_bce``) can be captured once in a HIP graph
+(torch.cuda.graph) and replayed step after step with the seed += 1 schedule;
+otherwise the seed is a launch argument, and a captured step would replay the
+seed it was captured with.  It computes the same quantities as GroupFFIMulFunction + SRSgd with
 two deliberate choices: the weight and bias gradients are fp32 (``grad_dtype``)
 and, in ``step``, never leave the chip (the SGD update is applied in the
 epilogue of the weight-gradient kernel; the result is bit-identical to
@@ -29,7 +31,8 @@ from .bindings import SR_SEED_GRAD_X
 class FFITrainStep:
     def __init__(self, weights: torch.Tensor, bias, group_locations: torch.Tensor, batch: int,
                  in_features: int, group_size: int, lr: float, weight_decay: float,
-                 seed: int = 42, grad_dtype: torch.dtype = torch.float32):
+                 seed: int = 42, grad_dtype: torch.dtype = torch.float32,
+                 device_seed: bool = False):
         _C.require_device(weights, "weights")
         if weights.dtype != torch.bfloat16:
             raise NotImplementedError("FFITrainStep: bf16 weights only")
@@ -64,14 +67,24 @@ class FFITrainStep:
         self.code = _lib.DTYPE_BF16
         self.gcode = _C.dtype_code(grad_dtype)
         self._sgd_args = None
+        # device_seed: the fused update's seed, read and advanced on the device
+        self._seed_dev = (torch.tensor([self.seed], dtype=torch.int64, device=dev)
+                          if device_seed else None)
 
     def state_dict(self) -> dict:
         """The step's own state (the parameters W, bias and idx belong to the caller):
-        the SR seed the next update will use."""
-        return {"seed": int(self.seed)}
+        the SR seed the next update will use (device_seed: read from the device,
+        a sync)."""
+        return {"seed": self.current_seed()}
 
     def load_state_dict(self, state: dict) -> None:
         self.seed = int(state["seed"])
+        if self._seed_dev is not None:
+            self._seed_dev.fill_(self.seed)
+
+    def current_seed(self) -> int:
+        """The seed the next SGD update uses (device_seed: a device sync)."""
+        return int(self._seed_dev.item()) if self._seed_dev is not None else int(self.seed)
 
     @property
     def dW(self) -> torch.Tensor:
@@ -216,12 +229,16 @@ class FFITrainStep:
         (optim_sr.py:59-62: one seed per step, offsets from 0 per tensor); one launch.
         Applies the gradients of the last ``backward_weights`` call."""
         self._grad_buffers()
+        if self._seed_dev is not None:
+            self.seed = self.current_seed()
         self._sgd_args[-2] = self.seed
         self._sgd_args[-1] = _C.stream_of(self.W)
         _lib.call("haste_sgd_sr_step_multi", *self._sgd_args)
         torch.autograd.graph.increment_version(self.W)
         self._wt_version = None  # W changed, W^T not refreshed
         self.seed += 1
+        if self._seed_dev is not None:
+            self._seed_dev.add_(1)
 
     def backward_weights_sgd(self, dY: torch.Tensor, lddy: int) -> None:
         """Weight and bias gradients (fp32, kept on chip) applied at once by SR-SGD
@@ -235,7 +252,20 @@ class FFITrainStep:
         # refresh W^T in the bwd-features workspace when its plan matches idx
         plan_ok = self._plan_version == self.idx._version
         bias = None if self.bias is None else self.bias.data_ptr()
-        if self._dx_pending:
+        if self._seed_dev is not None and not self._dx_pending:
+            raise ValueError("FFITrainStep(device_seed=True).backward_weights_sgd follows "
+                             "backward_features(defer_dx=True) (as step and step_bce do)")
+        if self._dx_pending and self._seed_dev is not None:
+            if not plan_ok:
+                raise RuntimeError("FFITrainStep.backward_weights_sgd: idx changed after "
+                                   "backward_features(defer_dx=True)")
+            _lib.call("haste_ffi_bwd_weights_sgd_dx_dev_seed", self.idx.data_ptr(),
+                      self.xT_buf.data_ptr(), self.ldx, dY.data_ptr(), lddy, self.W.data_ptr(),
+                      bias, None, None, self.lr, self.wd, 0.0, 0, 1, self._seed_dev.data_ptr(),
+                      self.dX.data_ptr(), SR_SEED_GRAD_X, self.ws.data_ptr(), self.ws.numel(),
+                      self.B, self.D, self.F, self.O, self.G, self.code, _C.stream_of(self.W))
+            self._dx_pending = False
+        elif self._dx_pending:
             if not plan_ok:
                 raise RuntimeError("FFITrainStep.backward_weights_sgd: idx changed after "
                                    "backward_features(defer_dx=True)")
@@ -256,7 +286,8 @@ class FFITrainStep:
         # torch op would, and record that the workspace holds W^T of this version
         torch.autograd.graph.increment_version(self.W)
         self._wt_version = self.W._version if plan_ok else None
-        self.seed += 1
+        if self._seed_dev is None:
+            self.seed += 1
 
     def step(self, x: torch.Tensor, dY: torch.Tensor, lddy: int) -> None:
         """forward -> backward to features (partials) -> fused weight/bias gradient +

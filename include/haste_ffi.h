@@ -263,6 +263,25 @@ int haste_ffi_bwd_weights_sgd_dx(const int32_t* idx, const void* xT, int64_t ldx
                                  void* stream);
 
 /*
+ * haste_ffi_bwd_weights_sgd_dx with the SGD step's Philox seed in device memory:
+ * the launch reads *seed_dev (a uint64) as its seed and then adds 1 to it on the
+ * device (one more small kernel on the stream), the per-step seed schedule of
+ * SRSgd (shared_ffi/optim_sr.py:59-62) without a host value.  A training step
+ * made of calls that take no host-side state that changes per step can then be
+ * captured once in a HIP graph and replayed step after step.  No counterpart in
+ * the reference; results are bit-identical to haste_ffi_bwd_weights_sgd_dx with
+ * seed = the value *seed_dev held.
+ */
+int haste_ffi_bwd_weights_sgd_dx_dev_seed(const int32_t* idx, const void* xT, int64_t ldx,
+                                          const void* dY, int64_t lddy, uint16_t* W,
+                                          uint16_t* bias, float* m_W, float* m_bias, float lr,
+                                          float wd, float mu, int32_t use_mom, int32_t do_sr,
+                                          uint64_t* seed_dev, uint16_t* dX, uint64_t dx_seed,
+                                          void* bwdf_workspace, int64_t bwdf_workspace_bytes,
+                                          int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+                                          int32_t dtype, void* stream);
+
+/*
  * haste_sgd_sr_step on the weights W [O, F] (bf16) of an FFI layer (element
  * offsets l*F + j from 0; bit-identical), which also writes the transposed
  * weights of the UPDATED W into a haste_ffi_bwd_features workspace holding the
