@@ -366,31 +366,35 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
                     BCE ? 0 : kStoreNT);
             }
         };
-        // Two waves along the labels whose staged rows are half a 128-byte line
-        // each (G = 64 at F >= 128: MT = 2, 16-bit output): after a barrier the
-        // pair's rows go out as whole lines, wave (wm, wn) writing rows
-        // [wm*NT*8, (wm+1)*NT*8) of the pair's NT*16 with both halves (its own
-        // and its partner's staged labels), so no line is written in two halves
-        // by two waves at different times.
-        constexpr bool kPairFlush = C::WM == 2 && MT * 16 * ESZ == 64;
-        auto flush_pair = [&](const rsrc_t& dst) {
-            constexpr int ROWS = NT * 8;  // rows of the pair's block this wave writes
-            static_assert(ROWS % 8 == 0, "8 rows of 128 bytes per instruction");
+        // Several waves along the labels whose staged rows are less than a
+        // 128-byte line each (G = 64 at F >= 128: two waves of 64 bytes; G = 128
+        // at F >= 128: four of 64): after a barrier the group's rows go out as
+        // whole lines, wave (wm, wn) writing rows [wm, wm+1) * NT*16/WM of the
+        // NT*16 rows its wn block staged, with every wave's labels, so no line is
+        // written in parts by different waves at different times.
+        constexpr int SEG = MT * 16 * ESZ;  // bytes of a row that one wave staged
+        constexpr bool kGroupFlush = C::WM > 1 && SEG < 128;
+        auto flush_group = [&](const rsrc_t& dst) {
+            constexpr int LPRG = C::WM * SEG / 16;  // lanes per whole group row
+            constexpr int RPIG = 64 / LPRG;         // rows per instruction
+            constexpr int ROWS = NT * 16 / C::WM;   // rows this wave writes
+            static_assert(!kGroupFlush || (LPRG <= 64 && ROWS % RPIG == 0),
+                          "whole rows per instruction");
 #pragma unroll
-            for (int r0 = 0; r0 < ROWS; r0 += 8) {
-                const int rs = wm * ROWS + r0 + lane / 8;  // staged row of the pair
-                const int cb = (lane % 8) * 16;            // byte within the 128-byte row
-                const int src = cb / 64 + C::WM * wn;      // the wave that staged this half
-                const u32x4 v = *reinterpret_cast<const u32x4*>(&stg[src][rs * SRB + cb % 64]);
+            for (int r0 = 0; r0 < ROWS; r0 += RPIG) {
+                const int rs = wm * ROWS + r0 + lane / LPRG;  // staged row of the block
+                const int cb = (lane % LPRG) * 16;            // byte within the group row
+                const int src = cb / SEG + C::WM * wn;        // the wave that staged it
+                const u32x4 v = *reinterpret_cast<const u32x4*>(&stg[src][rs * SRB + cb % SEG]);
                 const int rb = wn * NT * 16 + rs;
                 __builtin_amdgcn_raw_buffer_store_b128(
                     v, dst, (uint32_t)((int64_t)rb * ldo * ESZ + cb), 0, BCE ? 0 : kStoreNT);
             }
         };
         if constexpr (!LAST) {
-            if constexpr (kPairFlush) {
-                __syncthreads();  // the partner's half is staged
-                flush_pair(orr);
+            if constexpr (kGroupFlush) {
+                __syncthreads();  // every wave's labels are staged
+                flush_group(orr);
             } else {
                 flush(orr);
             }
