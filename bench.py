@@ -21,18 +21,18 @@ forward computes dY = sigma(z) - Y and the BCE loss from the COO labels in its
 epilogue (no logits written), then the same backward and update.
 
 The headline (``value``) is config 1 (--config).  The same line carries:
-  * "configs": the step at BASELINE configs 2 and 4 (O = 670K / 3M), each with
-    per-phase times and %HBM, and the rewire of those configs (prune 15 % per
-    group by mean |W|, regrow unused indices, zero init; every 1000 steps in
-    the reference's runs) timed alone and with the index re-plan it costs the
-    next step, raw and amortised over 1000 steps;
+  * "configs": the step at BASELINE configs 2, 3 and 4 (O = 670K / 500K / 3M),
+    each with per-phase times and %HBM; at configs 2 and 4 also their rewire
+    (prune 15 % per group by mean |W|, regrow unused indices, zero init; every
+    1000 steps in the reference's runs) timed alone and with the index re-plan
+    it costs the next step, raw and amortised over 1000 steps;
   * "dropin_api": the reference's own API path at config 1 (GroupFixedFanIn
     forward, autograd backward with dX, SRSgd.step), bf16 and fp32 gradients;
   * "cpu_baseline": the CPU oracle's step (PyTorch-CPU gather + bmm, C/OpenMP
     SR-SGD) on all the host cores in this process's affinity.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1]
-                       [--extra-configs 2,4] [--no-dropin] [--no-cpu-baseline]
+                       [--extra-configs 2,3,4] [--no-dropin] [--no-cpu-baseline]
                        [--copy-calibration]
 Prints one JSON line.
 """
@@ -53,6 +53,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 LR, WD, SEED = 0.05, 1e-4, 42
 REWIRE_FRACTION, REWIRE_INTERVAL = 0.15, 1000
+REWIRE_CONFIGS = (2, 4)  # the BASELINE configs that include a rewire step
 
 CONFIGS = {
     0: dict(B=64, D=768, O=4096, G=32, F=32, pos=5),
@@ -301,7 +302,8 @@ def run_extra_config(c, steps, warmup, dev):
     ms, per, _ = timed(step_fns(st, x, dY), steps, warmup, stream)
     rep = {"B": cfg["B"], "D": cfg["D"], "O": cfg["O"], "G": cfg["G"], "fan_in": cfg["F"]}
     rep.update(phase_report(cfg, ms, per))
-    rep["rewire"] = time_rewire(st, x, dY, cfg, stream)
+    if c in REWIRE_CONFIGS:
+        rep["rewire"] = time_rewire(st, x, dY, cfg, stream)
     del st, x, dY
     torch.cuda.empty_cache()
     return rep
@@ -435,8 +437,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
-    ap.add_argument("--extra-configs", default="2,4",
-                    help="comma-separated BASELINE configs also timed (with rewire); '' for none")
+    ap.add_argument("--extra-configs", default="2,3,4",
+                    help="comma-separated BASELINE configs also timed (configs 2 and 4 with "
+                         "their rewire); '' for none")
     ap.add_argument("--no-dropin", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",

@@ -70,6 +70,7 @@ def lib() -> ctypes.CDLL:
         L.ho_sgd_sr_step_f16w.argtypes = [P, P, c_int, P, i64, f32, f32, f32, c_int, c_int, u64,
                                           u64]
         L.ho_f32_to_f16_rne_arr.argtypes = [P, P, i64]
+        L.ho_f32_to_bf16_rne_arr.argtypes = [P, P, i64]
         L.ho_rewire_scores.argtypes = [P, c_int, P, i64, i64, i64]
         L.ho_rewire.argtypes = [P, c_int, P, i64, i64, i64, i64, c_int, f32, i64, c_int, c_int,
                                 f32, u64, P, P]
@@ -177,6 +178,16 @@ def f32_to_f16_rne(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty(x.shape, dtype=np.uint16)
     lib().ho_f32_to_f16_rne_arr(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def f32_to_bf16_rne(x: np.ndarray) -> np.ndarray:
+    """The C oracle's fp32 -> bf16 conversion (ho_f32_to_bf16_rne: round to nearest
+    even, NaN kept quiet with its sign), as uint16 bits.  It rounds the SGD result
+    when stochastic rounding is off and the rewire's new weights."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().ho_f32_to_bf16_rne_arr(_ptr(x), _ptr(out), x.size)
     return out
 
 

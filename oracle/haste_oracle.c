@@ -213,6 +213,10 @@ void ho_f32_to_f16_rne_arr(const float* x, uint16_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = ho_f32_to_f16_rne(x[i]);
 }
 
+void ho_f32_to_bf16_rne_arr(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ho_f32_to_bf16_rne(x[i]);
+}
+
 int ho_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -214,3 +214,35 @@ def test_configs_2_3_full_size_spot_groups(dev, cfg):
         ref_b, _ = oracle.sgd_sr_step(bits(b0[a:b]), db[a:b].cpu().numpy(), None, LR, WD, 0.0,
                                       False, True, 9, offset0=a)
         assert np.array_equal(bits(bias[a:b]), ref_b), (a, b)
+
+
+@pytest.mark.parametrize("cfg", [2, 4])
+def test_rewire_full_size(dev, cfg):
+    """Rewire at the full sizes that configs 2 and 4 run it every 1000 steps
+    (shared_ffi/rewire.py:143-239 with the build's contract): prune the
+    int(F * 0.15) smallest mean-|W| slots of every group (k = 9 at config 2,
+    19 at config 4), regrow indices unused in the group, zero init.  Scores,
+    indices, weights and the pruned count bit-exact against the oracle."""
+    O, F, G = {2: (670091, 64, 64), 4: (3_000_000, 128, 128)}[cfg]
+    D, k = 768, int(F * 0.15)
+    Gc = (O + G - 1) // G
+    g = torch.Generator(device=dev).manual_seed(100 + cfg)
+    Wd = ((torch.rand(O, F, generator=g, device=dev) * 2 - 1) / F ** 0.5).to(torch.bfloat16)
+    idxd = torch.randint(0, D, (Gc, F), generator=g, device=dev, dtype=torch.int32)
+    w, idx = bits(Wd), idxd.cpu().numpy()
+    seed = 0x5EED0000 + cfg
+    ref_w, ref_idx, ref_n, ref_s, _ = oracle.rewire(
+        w, idx, G, D, prune_mode=oracle.PRUNE_FRACTION, k=k, regrow_mode=oracle.REGROW_UNUSED,
+        init_mode=oracle.INIT_ZERO, bound=1.0 / F ** 0.5, seed=seed)
+    scores = torch.empty(Gc, F, device=dev)
+    cnt = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("haste_rewire", Wd.data_ptr(), _lib.DTYPE_BF16, idxd.data_ptr(), scores.data_ptr(),
+              cnt.data_ptr(), O, F, G, D, _lib.PRUNE_FRACTION, 0.0, k, _lib.REGROW_UNUSED,
+              _lib.INIT_ZERO, 1.0 / F ** 0.5, seed, _C.stream_of(Wd))
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == ref_n
+    assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+    assert np.array_equal(idxd.cpu().numpy(), ref_idx)
+    assert np.array_equal(bits(Wd), ref_w)
+    # every group pruned exactly k slots
+    assert ref_n == Gc * k

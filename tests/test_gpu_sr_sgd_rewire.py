@@ -190,6 +190,7 @@ REWIRE_CASES = [
     (3000, 64, 16, 100, "threshold", 0.05, "random", "random"),
     (2000, 256, 128, 4096, "fraction", 38, "unused", "random"),
     (777, 16, 32, 40, "fraction", 8, "unused", "random"),
+    (20000, 128, 128, 768, "fraction", 19, "unused", "zero"),   # config 4's rewire shape
 ]
 
 
