@@ -52,6 +52,14 @@ __host__ __device__ constexpr int max_dc(int bt, int G, int rt) {
     return (kLdsBytes - kLdsMisc - ring_bytes(G, rt)) / 4 / acc_stride(bt) - kTrashRows;
 }
 
+// The staged build (bwdf_staged.hpp): eight waves, each owning one W^T tile
+// of a group's range, and a double-buffered LDS copy of each group's dY tile
+// of bt rows x G labels beside the partial.
+constexpr int kStagedWaves = 8;
+__host__ __device__ constexpr int staged_max_dc(int bt, int G) {
+    return (kLdsBytes - kLdsMisc - 2 * bt * 2 * G) / 4 / acc_stride(bt) - kTrashRows;
+}
+
 // Probability that a range holds more than rt layer-0 tiles when its share of
 // a group's F indices is Binomial(F, q) -- an upper bound for indices drawn
 // uniformly without replacement, whose share is hypergeometric.
@@ -90,27 +98,22 @@ inline int64_t pick_ring(int64_t BT, int64_t D, int64_t F, int64_t G) {
     return ring;
 }
 
-// W^T for G <= 64 (the sizes with a direct bwd-features build) is stored in
-// tiles of 16 rows, chunk-major: the 16-byte chunk k (labels 8k .. 8k+7) of row
-// p of a tile is chunk k*16 + p of the tile, so the 16 rows' chunk k -- what 16
-// lanes of an MFMA operand fragment read -- are one contiguous 256-byte block.
-// For G = 128 it is row-major.  Element offset of the chunk of labels lc ..
-// lc+7 of tile row `row` (a group's rows start at a multiple of 16), and the
-// (row, chunk) of a group's it-th chunk in storage order.
-__host__ __device__ constexpr bool twt_chunk_major(int G) { return G <= 64; }
+// W^T is stored in tiles of 16 rows, chunk-major: the 16-byte chunk k (labels
+// 8k .. 8k+7) of row p of a tile is chunk k*16 + p of the tile, so the 16 rows'
+// chunk k -- what 16 lanes of an MFMA operand fragment read -- are one
+// contiguous 256-byte block.  Element offset of the chunk of labels lc .. lc+7
+// of tile row `row` (a group's rows start at a multiple of 16), and the (row,
+// chunk) of a group's it-th chunk in storage order.
 __host__ __device__ constexpr int64_t twt_elem(int64_t row, int lc, int G) {
-    return twt_chunk_major(G) ? (row / 16) * 16 * G + ((lc / 8) * 16 + row % 16) * 8 : row * G + lc;
+    return (row / 16) * 16 * G + ((lc / 8) * 16 + row % 16) * 8;
 }
-__host__ __device__ constexpr int twt_row_of(int it, int G) {
-    return twt_chunk_major(G) ? (it / (2 * G)) * 16 + it % 16 : it / (G / 8);
-}
-__host__ __device__ constexpr int twt_chunk_of(int it, int G) {
-    return twt_chunk_major(G) ? (it / 16) % (G / 8) : it % (G / 8);
-}
+__host__ __device__ constexpr int twt_row_of(int it, int G) { return (it / (2 * G)) * 16 + it % 16; }
+__host__ __device__ constexpr int twt_chunk_of(int it, int G) { return (it / 16) % (G / 8); }
 
 struct BwdFPlan {
     int64_t Gc, BT, nbt, Bp, ndr, Dc, S, gps, Tcap;
     int64_t RT, DCMAX;  // ring tiles of the main kernel; its partial's trash rows start at DCMAX
+    int64_t staged;     // the plan is for the staged main kernel (RT unused)
     int64_t tfeat_off, tsrc_off, perm_off, meta_off, twt_off, prep_bytes, ws_bytes;
 };
 
@@ -172,21 +175,57 @@ __device__ __forceinline__ void reduce_sr_tile(const ReduceJob& j, int tile, flo
 int bwdf_build();
 
 
-inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
+// Batch columns per workgroup of the staged build, 32 or 64, by a model of
+// the clocks a CU spends per (group, range, batch tile): LDS -- staging the dY
+// tile (about 13 clocks per KB written), reading its operands (4.4 per KB) and
+// the partial read-modify-writes (17.8 per KB) for each of the range's tiles
+// -- against the vector-memory address path (about 45 bytes per clock: the dY
+// tile plus every wave's W^T fragment loads, issued whether or not the wave has
+// a tile), plus about 150 clocks of per-group overhead; times the number of
+// (group, range, batch tile) units.  Measured rates on the pool's MI355X.
+inline int64_t pick_staged_bt(int64_t B, int64_t D, int64_t F, int64_t G) {
+    int64_t best_bt = 32;
+    double best = -1.0;
+    for (int64_t bt = 32; bt <= 64; bt *= 2) {
+        if (bt > 32 && B <= 32) break;
+        const int64_t ndr = ceil_div(D, (int64_t)staged_max_dc((int)bt, (int)G));
+        const double tiles = std::ceil((double)F / (double)ndr / 16.0) + 0.5;
+        const double stg = (double)(bt * 2 * G) / 1024.0;  // KB
+        const double lds = stg * 13.0 + tiles * (stg * 4.4 + 16.0 * bt * 4 / 1024.0 * 17.8);
+        const double ta = (stg * 1024.0 + (kStagedWaves + 2) * (G / 32) * 1024.0 +
+                           kStagedWaves * 256.0) / 45.0;
+        const double cost = (double)(ndr * ceil_div(B, bt)) * (std::max(lds, ta) + 150.0);
+        if (best < 0.0 || cost < best) {
+            best = cost;
+            best_bt = bt;
+        }
+    }
+    return best_bt;
+}
+
+// The plan for the staged build (staged = true) or the ring / direct builds.
+inline BwdFPlan make_plan_for(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G, bool staged) {
     BwdFPlan p;
     p.Gc = ceil_div(O, G);
-    // 128 batch columns per workgroup, or 64 when the batch is that small or
-    // when a 128-column partial would split D into 8 or more feature ranges
-    // (every range re-reads dY; with 64 columns a range holds twice the
-    // features: config 3, D = 4096, 15 -> 8 ranges, bwd-features 868 -> 804 us;
-    // at 3-4 ranges the 128-column build is faster: config 1 103 vs 149 us)
-    p.BT = 128;
-    if (B <= 64 || ceil_div(D, (int64_t)max_dc(128, (int)G, (int)pick_ring(128, D, F, G))) >= 8)
-        p.BT = 64;
+    p.staged = staged;
+    if (p.staged) {
+        p.BT = pick_staged_bt(B, D, F, G);
+        p.RT = 0;
+        p.DCMAX = staged_max_dc((int)p.BT, (int)G);
+    } else {
+        // 128 batch columns per workgroup, or 64 when the batch is that small or
+        // when a 128-column partial would split D into 8 or more feature ranges
+        // (every range re-reads dY; with 64 columns a range holds twice the
+        // features: config 3, D = 4096, 15 -> 8 ranges, bwd-features 868 -> 804 us;
+        // at 3-4 ranges the 128-column build is faster: config 1 103 vs 149 us)
+        p.BT = 128;
+        if (B <= 64 || ceil_div(D, (int64_t)max_dc(128, (int)G, (int)pick_ring(128, D, F, G))) >= 8)
+            p.BT = 64;
+        p.RT = pick_ring(p.BT, D, F, G);
+        p.DCMAX = max_dc((int)p.BT, (int)G, (int)p.RT);
+    }
     p.nbt = ceil_div(B, p.BT);
     p.Bp = p.nbt * p.BT;
-    p.RT = pick_ring(p.BT, D, F, G);
-    p.DCMAX = max_dc((int)p.BT, (int)G, (int)p.RT);
     p.ndr = ceil_div(D, p.DCMAX);
     p.Dc = ceil_div(D, p.ndr);
     int64_t S = std::max<int64_t>(1, kTargetCTAs / (p.nbt * p.ndr));
@@ -208,6 +247,23 @@ inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G)
     p.prep_bytes = p.twt_off + r256(p.Gc * p.Tcap * 16 * G * 2);
     p.ws_bytes = p.S * D * p.Bp * 4;
     return p;
+}
+
+// The plan of the build that haste_ffi_bwd_features_set_build selects (1 ring,
+// 2 direct, 3 staged; 0: by shape).  By shape, G >= 32 takes the staged build
+// where a group's range holds seven or more tiles of 16 positions, so that
+// nearly all of its eight waves have a tile (measured, config 1: 86 -> 82 us;
+// config 4: 3452 -> 2402 us; with four tiles, configs 2 and 3, it was slower
+// than the ring and direct builds: 295 -> 336 and 606 -> 805 us), and where
+// the slice's W^T tiles span at most kMaxRsrcBytes (its 32-bit tile offsets).
+inline BwdFPlan make_plan(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G) {
+    const int build = bwdf_build();
+    if (G >= 32 && (build == 0 || build == 3)) {
+        const BwdFPlan p = make_plan_for(B, D, F, O, G, true);
+        const bool fits = (p.gps + 8) * p.Tcap * 16 * G * 2 <= kMaxRsrcBytes;
+        if (fits && (build == 3 || F >= 7 * 16 * p.ndr)) return p;
+    }
+    return make_plan_for(B, D, F, O, G, false);
 }
 
 // One 16-byte chunk (labels lc .. lc+7 of the group) of the W^T row described by

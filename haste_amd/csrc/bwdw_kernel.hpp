@@ -369,8 +369,8 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     // Chunk it = tid + k*256 (k < kWtPre) has its tsrc entry loaded here, long
     // before the pass needs it.
     constexpr int CHP = PR / 8;
-    auto wt_row = [](int it) { return twt_chunk_major(G) ? (it / (16 * CHP)) * 16 + it % 16 : it / CHP; };
-    auto wt_chk = [](int it) { return twt_chunk_major(G) ? (it / 16) % CHP : it % CHP; };
+    auto wt_row = [](int it) { return (it / (16 * CHP)) * 16 + it % 16; };
+    auto wt_chk = [](int it) { return (it / 16) % CHP; };
     constexpr int kWtPre = 8;
     int wsrc[SGD ? kWtPre : 1];
     int wt_rows = 0;

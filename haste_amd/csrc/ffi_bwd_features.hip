@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "bwdf_main.hpp"
+#include "bwdf_staged.hpp"
 
 
 namespace haste {
@@ -382,16 +383,18 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
                     w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, GatherSgd{}); \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
-            rc = ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)   \
-                    : run_main<BF16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st); \
+            rc = p.staged ? bwdf_run_staged(dtype, G, ya, tfeat, meta, twt, y, lddy, ws, p, B, D, O, st) \
+                 : ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)  \
+                      : run_main<BF16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st); \
         } else {                                                                                \
             if (gather) {                                                                       \
                 bwdf_gather_kernel<F16, GG, false><<<pgrid, dim3(256), 0, st>>>(                \
                     w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, GatherSgd{}); \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
-            rc = ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)   \
-                    : run_main<F16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);  \
+            rc = p.staged ? bwdf_run_staged(dtype, G, ya, tfeat, meta, twt, y, lddy, ws, p, B, D, O, st) \
+                 : ya ? bwdf_run_main_ya(dtype, G, tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st)  \
+                      : run_main<F16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st);  \
         }                                                                                       \
         break;
         HASTE_BWDF_G(16)
@@ -437,8 +440,8 @@ int bwdf_build() { return g_bwdf_build.load(std::memory_order_relaxed); }
 }  // namespace haste
 
 extern "C" int haste_ffi_bwd_features_set_build(int32_t build) {
-    HASTE_CHECK_ARG(build >= 0 && build <= 2,
-                    "haste_ffi_bwd_features_set_build: build must be 0, 1 or 2 (got %d)", (int)build);
+    HASTE_CHECK_ARG(build >= 0 && build <= 3,
+                    "haste_ffi_bwd_features_set_build: build must be 0, 1, 2 or 3 (got %d)", (int)build);
     return haste::g_bwdf_build.exchange(build);
 }
 

@@ -135,20 +135,24 @@ int64_t haste_ffi_bwd_features_workspace_size(int64_t B, int64_t D, int64_t F, i
 /*
  * How haste_ffi_bwd_features splits the work for these sizes (host-only, no
  * GPU call): cfg[0] = batch columns per workgroup, cfg[1] = W^T tiles of 16
- * positions per LDS ring round, cfg[2] = feature ranges, cfg[3] = group
- * slices.  For tuning and tests; no counterpart in the reference.
+ * positions per LDS ring round (0 for the staged build, whose waves own one
+ * tile each), cfg[2] = feature ranges, cfg[3] = group slices.  The split
+ * depends on the build selected by haste_ffi_bwd_features_set_build.  For
+ * tuning and tests; no counterpart in the reference.
  */
 int haste_ffi_bwd_features_config(int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
                                   int32_t dtype, int64_t* cfg);
 
 /*
- * Selects the main kernel of later haste_ffi_bwd_features[_sr] calls in this
- * process (host-only): 0 (the default) chooses by shape; 1 always the LDS-ring
- * build; 2 the direct build wherever it exists (G = 32 or 64), else the ring
- * build.  Both builds give the same results up to
- * the order of fp32 additions.  Returns the previous setting, or
- * HASTE_ERR_INVALID_ARG for another value.  For tests and tuning; no
- * counterpart in the reference.
+ * Selects the main kernel of later bwd-features calls in this process
+ * (host-only): 0 (the default) and 3 the staged build for G >= 32, else the
+ * LDS-ring build; 1 always the LDS-ring build; 2 the direct build wherever it
+ * exists (G = 32 or 64), else the ring build.  The builds give the same
+ * results up to the order of fp32 additions.  The workspace layout (plan)
+ * differs between the staged build and the others, so a plan made under one
+ * setting must be remade (plan_ready = 0) after a change.  Returns the
+ * previous setting, or HASTE_ERR_INVALID_ARG for another value.  For tests and
+ * tuning; no counterpart in the reference.
  */
 int haste_ffi_bwd_features_set_build(int32_t build);
 

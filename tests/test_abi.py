@@ -173,11 +173,36 @@ def test_ring_cases_reach_every_bwd_features_build():
     from bwdf_cases import RING_CASES, all_variants, kernel_config
 
     seen = set()
-    for B, D, O, G, F, _ in RING_CASES:
-        BT, RT, ndr, _S = kernel_config(_lib.lib(), B, D, O, G, F)
-        assert ndr >= 2, (B, D, O, G, F)
-        seen.add((G, BT, RT))
+    prev = _lib.lib().haste_ffi_bwd_features_set_build(1)
+    try:
+        for B, D, O, G, F, _ in RING_CASES:
+            BT, RT, ndr, _S = kernel_config(_lib.lib(), B, D, O, G, F)
+            assert ndr >= 2, (B, D, O, G, F)
+            seen.add((G, BT, RT))
+    finally:
+        _lib.lib().haste_ffi_bwd_features_set_build(prev)
     assert seen == all_variants()
+
+
+def test_staged_cases_reach_every_staged_build():
+    """tests/bwdf_cases.STAGED_CASES maps onto every (G, BT) build of the staged
+    main kernel, with one and with several feature ranges; the default build
+    (0) is the staged one for G >= 32 and the ring build for G = 16."""
+    from bwdf_cases import STAGED_CASES, kernel_config, staged_variants
+
+    L = _lib.lib()
+    seen = set()
+    prev = L.haste_ffi_bwd_features_set_build(3)
+    try:
+        for B, D, O, G, F, _ in STAGED_CASES:
+            BT, RT, ndr, _S = kernel_config(L, B, D, O, G, F)
+            assert RT == 0, (B, D, O, G, F)
+            seen.add((G, BT, ndr >= 2))
+    finally:
+        L.haste_ffi_bwd_features_set_build(prev)
+    assert seen == staged_variants()
+    assert kernel_config(L, 512, 768, 131073, 64, 128)[1] == 0   # default: staged
+    assert kernel_config(L, 100, 300, 1000, 16, 16)[1] > 0        # G = 16: ring
 
 
 def test_forward_bce_noalloc_rejects_shapes_beyond_its_scratch():
@@ -197,9 +222,10 @@ def test_forward_bce_noalloc_rejects_shapes_beyond_its_scratch():
 
 def test_bwd_features_set_build():
     L = _lib.lib()
-    assert L.haste_ffi_bwd_features_set_build(3) == _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_ffi_bwd_features_set_build(4) == _lib.HASTE_ERR_INVALID_ARG
     assert L.haste_ffi_bwd_features_set_build(-1) == _lib.HASTE_ERR_INVALID_ARG
     prev = L.haste_ffi_bwd_features_set_build(1)
     assert prev == 0
     assert L.haste_ffi_bwd_features_set_build(2) == 1
-    assert L.haste_ffi_bwd_features_set_build(prev) == 2
+    assert L.haste_ffi_bwd_features_set_build(3) == 2
+    assert L.haste_ffi_bwd_features_set_build(prev) == 3

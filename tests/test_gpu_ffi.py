@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from bwdf_cases import RING_CASES, kernel_config
+from bwdf_cases import RING_CASES, STAGED_CASES, kernel_config
 from haste_amd import _C, _lib
 
 pytestmark = pytest.mark.gpu
@@ -94,8 +94,10 @@ def test_backward_features(dev, B, D, O, G, F, mode):
 
 
 # every (G, BT, RT) case under the LDS-ring build (1) and, where it exists
-# (G = 32, 64), the direct build (2)
-BUILD_CASES = [c + (1,) for c in RING_CASES] + [c + (2,) for c in RING_CASES if c[3] in (32, 64)]
+# (G = 32, 64), the direct build (2); every staged (G, BT) case and the ring
+# cases with G >= 32 under the staged build (3)
+BUILD_CASES = ([c + (1,) for c in RING_CASES] + [c + (2,) for c in RING_CASES if c[3] in (32, 64)]
+               + [c + (3,) for c in STAGED_CASES] + [c + (3,) for c in RING_CASES if c[3] >= 32])
 
 
 @pytest.mark.parametrize("B,D,O,G,F,mode,build", BUILD_CASES)
@@ -103,10 +105,10 @@ def test_backward_features_every_build(dev, B, D, O, G, F, mode, build):
     """One shape per (G, batch tile, ring tiles) build of the main kernel (the
     coverage of RING_CASES is checked on the CPU in test_abi.py), under each
     main-kernel build."""
-    BT, RT, _, _ = kernel_config(_lib.lib(), B, D, O, G, F)
     x, W, bias, idx, dY = make_case(B, D, O, G, F, idx_mode=mode, seed=11)
     prev = _lib.lib().haste_ffi_bwd_features_set_build(build)
     try:
+        BT, RT, _, _ = kernel_config(_lib.lib(), B, D, O, G, F)
         dXT = _C.ffi_backward_features_cuda(x.t().contiguous().to(dev), W.to(dev), idx.to(dev),
                                             dY.to(dev), B, D, F, O, G)
         torch.cuda.synchronize()
@@ -262,7 +264,7 @@ def test_backward_weights_streaming_dY(dev):
         torch.testing.assert_close(db[l0:l1].cpu(), oracle.bias_grad(dy), **TOL32)
 
 
-@pytest.mark.parametrize("build", [1, 2])  # bwd-features main kernel: LDS ring, direct where built
+@pytest.mark.parametrize("build", [1, 2, 3])  # bwd-features main kernel: ring, direct, staged
 @pytest.mark.parametrize("B,D,O,G,F,pad,col0", [
     (37, 300, 2003, 64, 64, 0, 0),    # [B, O] contiguous, O odd
     (64, 768, 4133, 32, 32, 4, 0),    # odd row stride past O
