@@ -170,30 +170,30 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
                                     delta);
     // (32 bits: the tile's resource spans at most kMaxRsrcBytes)
     const uint32_t yrow = delta + (uint32_t)((int64_t)prow * lddy * 2) + (uint32_t)pbyte;
-    // YA: elements by which group g's piece is loaded early (0 unless it
+    // groups are indexed from the slice's first (i = g - g_lo); the last group
+    // of dY is i == last_i
+    const int last_i = (int)(Gc - 1 - g_lo);
+    // YA: elements by which the last group's piece is loaded early (0 unless it
     // straddles O in dY's last row)
-    auto piece_sh = [&](int64_t g) __attribute__((always_inline)) -> int {
-        if constexpr (!YA) {
-            return 0;
-        } else {
-            const int64_t over = g * G + plab + PB / 2 - O;
-            return p_last_row && over > 0 && over < PB / 2 ? (int)over : 0;
-        }
+    int sh_last = 0;
+    if constexpr (YA) {
+        const int64_t over = (Gc - 1) * G + plab + PB / 2 - O;
+        sh_last = p_last_row && over > 0 && over < PB / 2 ? (int)over : 0;
+    }
+    auto load_y = [&](int i) __attribute__((always_inline)) -> Piece {
+        const uint32_t sh = YA && i == last_i ? (uint32_t)sh_last : 0u;
+        return load_piece<PW>(yr, yrow + (uint32_t)(g_lo + i) * (uint32_t)(G * 2) - 2u * sh);
     };
-    auto load_y = [&](int64_t g) __attribute__((always_inline)) -> Piece {
-        return load_piece<PW>(yr, yrow + (uint32_t)g * (uint32_t)(G * 2) - 2u * (uint32_t)piece_sh(g));
-    };
-    // group g's piece into staging buffer buf (labels >= O zeroed)
+    // group i's piece into staging buffer buf (labels >= O zeroed)
     const int soff = stg_off<G>(prow, pbyte / 16) + (PB < 16 ? pbyte % 16 : 0);
-    auto stage = [&](int64_t g, const Piece& pc, int buf) __attribute__((always_inline)) {
+    auto stage = [&](int i, const Piece& pc, int buf) __attribute__((always_inline)) {
         uint32_t w[PW];
         unpack_piece<PW>(pc, w);
-        if (g >= Gc - 1) {  // uniform: the last group (or one past the end)
+        if (i >= last_i) {  // uniform: the last group (or past the end)
             if constexpr (YA) {
-                const int sh = piece_sh(g);
-                if (sh) piece_shift_down<PW>(w, sh);
+                if (i == last_i && sh_last) piece_shift_down<PW>(w, sh_last);
             }
-            const int64_t nv = O - (g * G + plab);  // labels of the piece below O
+            const int64_t nv = O - ((g_lo + i) * G + plab);  // labels of the piece below O
 #pragma unroll
             for (int k = 0; k < PW; ++k)
                 w[k] &= (2 * k + 1 < nv) ? 0xFFFFFFFFu : (2 * k < nv ? 0xFFFFu : 0u);
@@ -334,17 +334,17 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
             u32x2 m0[DEPTH + 1];
 #pragma unroll
             for (int k = 0; k <= DEPTH; ++k) m0[k] = load_meta(k);
-            const Piece y0 = load_y(g_lo);
+            const Piece y0 = load_y(0);
             for (int k = tid * 4; k < dn * AS; k += NTH * 4)
                 *reinterpret_cast<f32x4*>(&acc[k]) = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k <= DEPTH; ++k) mu[k] = uniform_meta(m0[k]);
-            stage(g_lo, y0, 0);
+            stage(0, y0, 0);
 #pragma unroll
             for (int k = 0; k < DEPTH; ++k) {
                 __builtin_amdgcn_sched_barrier(0);
                 load_frag(k, mu[k], fq[k % NS]);
-                yq[k % NS] = load_y(g_lo + k + 1);
+                yq[k % NS] = load_y(k + 1);
                 mraw[k % NS] = load_meta(k + DEPTH + 1);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -357,30 +357,31 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
             constexpr int P = K % 2;                // staging buffer of group i
             constexpr int QN = (Q + DEPTH) % NS;    // slot of step i + DEPTH
             load_frag(i + DEPTH, mu[DEPTH], fq[QN]);
-            yq[QN] = load_y(g_lo + i + DEPTH + 1);
+            yq[QN] = load_y(i + DEPTH + 1);
             mraw[QN] = load_meta(i + 2 * DEPTH + 1);
             const u32x2 m = mu[0];
             const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
             const bool mine = wave < tm - tb;  // uniform: the wave has a layer-0 tile
+            // The previous group's partial rows are read, and this group's
+            // products computed, whether or not the wave has a tile (fod is always
+            // a valid row offset; a wave without a tile multiplies some other
+            // tile, and neither result is written): branches here would only add
+            // register initialisations.
             f32x4 old[MT];
-            if (has_d) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    old[mt] = *reinterpret_cast<const f32x4*>(accb + fod + mt * 64 + colb);
-            }
-            stage(g_lo + i + 1, yq[Q], 1 - P);
+            for (int mt = 0; mt < MT; ++mt)
+                old[mt] = *reinterpret_cast<const f32x4*>(accb + fod + mt * 64 + colb);
+            stage(i + 1, yq[Q], 1 - P);
             f32x4 pc[MT];
-            if (mine) {
-                u32x4 a[MT][KS];
-                read_a(P, a);
-                mma(a, fq[Q].b0, pc);
-                if constexpr (L1) {
-                    if (wave < te - tm) {
-                        f32x4 c1[MT];
-                        mma(a, fq[Q].b1, c1);
+            u32x4 a[MT][KS];
+            read_a(P, a);
+            mma(a, fq[Q].b0, pc);
+            if constexpr (L1) {
+                if (wave < te - tm) {
+                    f32x4 c1[MT];
+                    mma(a, fq[Q].b1, c1);
 #pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) pc[mt] += c1[mt];
-                    }
+                    for (int mt = 0; mt < MT; ++mt) pc[mt] += c1[mt];
                 }
             }
             if (has_d) {
