@@ -52,10 +52,11 @@ __host__ __device__ constexpr int max_dc(int bt, int G, int rt) {
     return (kLdsBytes - kLdsMisc - ring_bytes(G, rt)) / 4 / acc_stride(bt) - kTrashRows;
 }
 
-// The staged build (bwdf_staged.hpp): eight waves, each owning one W^T tile
-// of a group's range, and a double-buffered LDS copy of each group's dY tile
-// of bt rows x G labels beside the partial.
-constexpr int kStagedWaves = 8;
+// The staged build (bwdf_staged.hpp): kStagedTiles W^T tiles of a group's
+// range in its pipeline, dealt over its waves, and a double-buffered LDS copy
+// of each group's dY tile of bt rows x G labels beside the partial.
+constexpr int kStagedTiles = 8;
+constexpr int kStagedWaves = 8;  // the model's wave count (pick_staged_bt)
 __host__ __device__ constexpr int staged_max_dc(int bt, int G) {
     return (kLdsBytes - kLdsMisc - 2 * bt * 2 * G) / 4 / acc_stride(bt) - kTrashRows;
 }

@@ -37,9 +37,10 @@
 namespace haste {
 namespace {
 
-template <int G, int BT>
+template <int G, int BT, int W>
 struct StagedCfg {
-    static constexpr int WAVES = kStagedWaves;
+    static constexpr int WAVES = W;
+    static constexpr int TPW = kStagedTiles / W;  // pipeline tiles per wave
     static constexpr int NTH = 64 * WAVES;
     static constexpr int KS = G / 32;        // MFMA k-steps over the group's labels
     static constexpr int MT = BT / 16;       // 16-row blocks of the batch tile
@@ -54,6 +55,7 @@ struct StagedCfg {
     static constexpr int NS = DEPTH + 1;     // register slots of the pipeline
     static constexpr int L1W = 2;            // waves that load layer-1 tiles in the pipeline
     static_assert(G >= 32, "staged build: G >= 32");
+    static_assert(TPW * W == kStagedTiles, "tiles per wave");
     static_assert(PB == 4 || PB == 8 || PB == 16 || PB == 32, "dY piece");
     static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0, "unroll");
     static_assert(DCMAX > 0, "LDS budget");
@@ -122,14 +124,15 @@ __device__ __forceinline__ void piece_shift_down(uint32_t (&w)[PW], int sh) {
     for (int k = 0; k < PW; ++k) w[k] = o[k];
 }
 
-template <typename T, int G, int BT, bool YA>
-__global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
+template <typename T, int G, int BT, int W, bool YA>
+__global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
     const int* __restrict__ tfeat, const int* __restrict__ meta, const uint16_t* __restrict__ twt,
     const uint16_t* __restrict__ dY, int64_t lddy, float* __restrict__ ws, int B, int Bp, int D,
     int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
-    using C = StagedCfg<G, BT>;
+    using C = StagedCfg<G, BT, W>;
     constexpr int KS = C::KS, MT = C::MT, STG = C::STG, PB = C::PB, PW = C::PW, AS = C::AS;
     constexpr int NTH = C::NTH, DEPTH = C::DEPTH, NS = C::NS, WAVES = C::WAVES, L1W = C::L1W;
+    constexpr int TPW = C::TPW;
     using Piece = typename PieceT<PW>::type;
     __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
     __shared__ __attribute__((aligned(16))) char stg[2][STG];
@@ -255,9 +258,9 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
     auto run = [&](auto l1c) __attribute__((always_inline)) {
         constexpr bool L1 = decltype(l1c)::value;
         struct Frag {
-            u32x4 b0[KS];            // layer-0 tile `wave`
+            u32x4 b0[TPW][KS];       // layer-0 tiles wave + WAVES*k
             u32x4 b1[L1 ? KS : 1];   // layer-1 tile `wave`
-            int fo;                  // partial-row byte offset of the lane's position
+            int fo[TPW];             // partial-row byte offsets of the lane's positions
         };
         auto load_frag = [&](int i, u32x2 m, Frag& fr) __attribute__((always_inline)) {
             const uint32_t tb = m[0] & 0xFFFFu, tm = m[0] >> 16;
@@ -266,14 +269,18 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
             const uint32_t t1 = (uint32_t)i * (uint32_t)Tcap + tm + (uint32_t)wave;
             const uint32_t fl = (uint32_t)lane * 16u;  // the lane's 16 bytes of a k-step's 1 KB
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                fr.b0[ks] = buf_load16(wr_s, t0 * (16u * G * 2u) + fl + ks * 1024u);
+            for (int k = 0; k < TPW; ++k)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    fr.b0[k][ks] = buf_load16(wr_s, (t0 + k * WAVES) * (16u * G * 2u) + fl + ks * 1024u);
             if constexpr (L1) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
                     fr.b1[ks] = buf_load16(wr_s, t1 * (16u * G * 2u) + fl + ks * 1024u);
             }
-            fr.fo = (int)buf_load4(fr_s, (t0 * 16u + (uint32_t)col) * 4u);
+#pragma unroll
+            for (int k = 0; k < TPW; ++k)
+                fr.fo[k] = (int)buf_load4(fr_s, ((t0 + k * WAVES) * 16u + (uint32_t)col) * 4u);
         };
         auto mma = [&](const u32x4 (&a)[MT][KS], const u32x4 (&b)[KS], f32x4 (&c)[MT])
             __attribute__((always_inline)) {
@@ -285,10 +292,11 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
                 c[mt] = v;
             }
         };
-        // Tiles of group g_lo + i beyond the pipeline's (layer-0 tiles >= WAVES,
-        // layer-1 tiles >= L1W), loaded and added at once: wave w takes layer-0
-        // tiles w + WAVES*k (k >= 1) with their layer-1 pairs, and layer-1 tile w
-        // when w >= L1W (its layer-0 pair is the wave's pipeline tile, added one
+        // Tiles of group g_lo + i beyond the pipeline's (layer-0 tiles >=
+        // kStagedTiles, layer-1 tiles >= L1W), loaded and added at once by the
+        // wave that owns the layer-0 tile of the same index (t % WAVES): layer-0
+        // tiles past the pipeline's with their layer-1 pairs, and the layer-1
+        // tiles whose layer-0 pair is one of the wave's pipeline tiles (added one
         // group later by the same wave).
         auto extra = [&](int i, u32x2 m, int buf) __attribute__((always_inline)) {
             const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
@@ -316,8 +324,9 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
                     *p = *p + (c0[mt] + c1[mt]);
                 }
             };
-            for (int t = wave + WAVES; t < n0; t += WAVES) one(t, true, t < n1);
-            if (wave >= L1W && wave < n1) one(wave, false, true);
+            for (int t = wave + kStagedTiles; t < n0; t += WAVES) one(t, true, t < n1);
+            for (int t = wave; t < kStagedTiles && t < n1; t += WAVES)
+                if (t >= L1W) one(t, false, true);
             // every load of this pass has been used; say so, so that later code
             // need not wait for them
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -327,9 +336,11 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
         Piece yq[NS];
         u32x2 mraw[NS];
         u32x2 mu[DEPTH + 1];  // uniform metadata of groups i .. i+DEPTH
-        f32x4 pd[MT];         // products of the previous group
-        int fod = 0;
-        bool has_d = false;
+        f32x4 pd[TPW][MT];    // products of the previous group
+        int fod[TPW];
+        int n0d = 0;          // uniform: layer-0 tiles of the previous group
+#pragma unroll
+        for (int k = 0; k < TPW; ++k) fod[k] = 0;
         {
             u32x2 m0[DEPTH + 1];
 #pragma unroll
@@ -361,44 +372,52 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
             mraw[QN] = load_meta(i + 2 * DEPTH + 1);
             const u32x2 m = mu[0];
             const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
-            const bool mine = wave < tm - tb;  // uniform: the wave has a layer-0 tile
             // The previous group's partial rows are read, and this group's
-            // products computed, whether or not the wave has a tile (fod is always
-            // a valid row offset; a wave without a tile multiplies some other
-            // tile, and neither result is written): branches here would only add
-            // register initialisations.
-            f32x4 old[MT];
+            // products computed, whether or not the wave has the tile (fod is
+            // always a valid row offset; a wave without the tile multiplies some
+            // other tile, and neither result is written): branches here would
+            // only add register initialisations.
+            f32x4 old[TPW][MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                old[mt] = *reinterpret_cast<const f32x4*>(accb + fod + mt * 64 + colb);
+            for (int k = 0; k < TPW; ++k)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    old[k][mt] = *reinterpret_cast<const f32x4*>(accb + fod[k] + mt * 64 + colb);
             stage(i + 1, yq[Q], 1 - P);
-            f32x4 pc[MT];
+            f32x4 pc[TPW][MT];
             u32x4 a[MT][KS];
             read_a(P, a);
-            mma(a, fq[Q].b0, pc);
+#pragma unroll
+            for (int k = 0; k < TPW; ++k) mma(a, fq[Q].b0[k], pc[k]);
             if constexpr (L1) {
                 if (wave < te - tm) {
                     f32x4 c1[MT];
                     mma(a, fq[Q].b1, c1);
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) pc[mt] += c1[mt];
+                    for (int mt = 0; mt < MT; ++mt) pc[0][mt] += c1[mt];
                 }
             }
-            if (has_d) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    *reinterpret_cast<f32x4*>(accb + fod + mt * 64 + colb) = old[mt] + pd[mt];
+            for (int k = 0; k < TPW; ++k) {
+                if (wave + k * WAVES < n0d) {  // uniform: the wave had tile k
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        *reinterpret_cast<f32x4*>(accb + fod[k] + mt * 64 + colb) = old[k][mt] + pd[k][mt];
+                }
             }
-            has_d = mine;
+            n0d = tm - tb;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) pd[mt] = pc[mt];
-            fod = fq[Q].fo;
+            for (int k = 0; k < TPW; ++k) {
+                fod[k] = fq[Q].fo[k];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) pd[k][mt] = pc[k][mt];
+            }
 #pragma unroll
             for (int k = 0; k < DEPTH; ++k) mu[k] = mu[k + 1];
             mu[DEPTH] = uniform_meta(mraw[Q]);
             __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
             __builtin_amdgcn_s_barrier();
-            if (tm - tb > WAVES || te - tm > L1W) {  // uniform, rare
+            if (tm - tb > kStagedTiles || te - tm > L1W) {  // uniform, rare
                 extra(i, m, P);
                 __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
                 __builtin_amdgcn_s_barrier();
@@ -412,11 +431,14 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
             body(i + 4, std::integral_constant<int, 4>{});
             body(i + 5, std::integral_constant<int, 5>{});
         }
-        if (has_d) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                f32x4* p = reinterpret_cast<f32x4*>(accb + fod + mt * 64 + colb);
-                *p = *p + pd[mt];
+        for (int k = 0; k < TPW; ++k) {
+            if (wave + k * WAVES < n0d) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f32x4* p = reinterpret_cast<f32x4*>(accb + fod[k] + mt * 64 + colb);
+                    *p = *p + pd[k][mt];
+                }
             }
         }
         // every load has been used (the last iterations' look-ahead loads are
@@ -437,7 +459,7 @@ __global__ __launch_bounds__(64 * kStagedWaves, 1) void bwdf_staged_kernel(
     }
 }
 
-template <typename T, int G, int BT, bool YA>
+template <typename T, int G, int BT, int W, bool YA>
 int launch_staged(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
                   int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
                   hipStream_t st) {
@@ -447,7 +469,7 @@ int launch_staged(const int* tfeat, const int* meta, const uint16_t* twt, const 
         set_error("haste_ffi_bwd_features: lddy = %lld too large", (long long)lddy);
         return HASTE_ERR_UNSUPPORTED;
     }
-    bwdf_staged_kernel<T, G, BT, YA><<<dim3((unsigned)grid), dim3(64 * kStagedWaves), 0, st>>>(
+    bwdf_staged_kernel<T, G, BT, W, YA><<<dim3((unsigned)grid), dim3(64 * W), 0, st>>>(
         tfeat, meta, twt, dY, lddy, ws, (int)B, (int)p.Bp, (int)D, O, p.Gc, (int)p.nbt, (int)p.ndr,
         (int)p.Dc, (int)p.gps, (int)p.S, (int)p.Tcap);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_features");

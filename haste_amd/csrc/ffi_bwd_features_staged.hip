@@ -1,6 +1,8 @@
 // The staged backward-to-features main kernel (bwdf_staged.hpp) for every
 // group size it is built for (G = 32, 64, 128), batch tile (32, 64 columns),
-// element type and dY row alignment.
+// element type and dY row alignment, with eight waves of one pipeline tile each
+// (measured at config 1: four waves of two tiles each, half the operand reads
+// from LDS, took 78 against 72 us, and 3109 against 2643 us at config 4).
 #include "bwdf_staged.hpp"
 
 namespace haste {
@@ -10,8 +12,8 @@ template <typename T, int G, bool YA>
 int staged_bt(const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
               int64_t lddy, float* ws, const BwdFPlan& p, int64_t B, int64_t D, int64_t O,
               hipStream_t st) {
-    if (p.BT == 64) return launch_staged<T, G, 64, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
-    return launch_staged<T, G, 32, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    if (p.BT == 64) return launch_staged<T, G, 64, 8, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
+    return launch_staged<T, G, 32, 8, YA>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
 }
 template <typename T, int G>
 int staged_ya(bool ya, const int* tfeat, const int* meta, const uint16_t* twt, const uint16_t* dY,
