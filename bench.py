@@ -28,6 +28,10 @@ The headline (``value``) is config 1 (--config).  The same line carries:
     it costs the next step, raw and amortised over 1000 steps;
   * "dropin_api": the reference's own API path at config 1 (GroupFixedFanIn
     forward, autograd backward with dX, SRSgd.step), bf16 and fp32 gradients;
+  * "sr_floor": the phases that round stochastically (the fused update, and the
+    unfused SGD) against both of their floors: HBM (algorithmic bytes at the
+    peak) and the Philox arithmetic of one tl.randint word per element, timed
+    live with haste_sr_words_fold (the words alone);
   * "cpu_baseline": the CPU oracle's step (PyTorch-CPU gather + bmm, C/OpenMP
     SR-SGD) on all the host cores in this process's affinity.
 
@@ -224,6 +228,56 @@ def step_fns(st, x, dY):
             lambda: st.backward_weights_sgd(dY, st.ldo)]
 
 
+def sr_word_rate(dev, n=1 << 26, reps=5):
+    """tl.randint words per second of haste_sr_words_fold, the Philox4x32-10
+    arithmetic of the SR and SR-SGD kernels alone (one word per weight, fixed
+    by bit-exact parity with tl.randint), timed with events on the stream it
+    runs on."""
+    import torch
+
+    from haste_amd import _C, _lib
+
+    fold = torch.empty((n + 63) // 64, dtype=torch.int32, device=dev)
+    st = _C.stream_of(fold)
+    for _ in range(2):
+        _lib.call("haste_sr_words_fold", fold.data_ptr(), n, SEED, st)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        _lib.call("haste_sr_words_fold", fold.data_ptr(), n, SEED, st)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return n * reps / (e0.elapsed_time(e1) * 1e-3)
+
+
+def sr_words(B, D, O, F):
+    """Random words per launch of the phases that round stochastically: the fused
+    update draws one per weight and bias element and one per dX element (its
+    trailing workgroups round dX); the unfused SGD one per weight and bias."""
+    return {"bwd_weights_sgd": O * F + O + B * D, "sgd": O * F + O}
+
+
+def sr_floor_report(cfg, phases_ms, word_rate):
+    """For each SR phase: the HBM floor (its algorithmic bytes at the peak), the
+    Philox floor (its words at the measured word rate), and the phase time as a
+    fraction of the larger one."""
+    B, D, O, F, G = cfg["B"], cfg["D"], cfg["O"], cfg["F"], cfg["G"]
+    pb, words = phase_bytes(B, D, O, G, F), sr_words(B, D, O, F)
+    out = {}
+    for name, ms in phases_ms.items():
+        if name not in words:
+            continue
+        hbm_us = pb[name] / (HBM_PEAK_GBS * 1e9) * 1e6
+        valu_us = words[name] / word_rate * 1e6
+        floor = max(hbm_us, valu_us)
+        out[name] = {"words": words[name], "hbm_floor_us": round(hbm_us, 2),
+                     "valu_floor_us": round(valu_us, 2),
+                     "bound": "valu" if valu_us > hbm_us else "hbm",
+                     "measured_us": round(ms * 1e3, 2), "frac_of_floor": round(floor / (ms * 1e3), 4)}
+    return out
+
+
 def phase_report(cfg, ms_per_step, per):
     B, D, O, G, F = cfg["B"], cfg["D"], cfg["O"], cfg["G"], cfg["F"]
     pb = phase_bytes(B, D, O, G, F)
@@ -293,7 +347,7 @@ def time_rewire(st, x, dY, cfg, stream, reps=5):
             "mode": f"fraction {REWIRE_FRACTION} per group (k={k}), regrow unused, init zero"}
 
 
-def run_extra_config(c, steps, warmup, dev):
+def run_extra_config(c, steps, warmup, dev, word_rate):
     import torch
 
     cfg = CONFIGS[c]
@@ -302,6 +356,7 @@ def run_extra_config(c, steps, warmup, dev):
     ms, per, _ = timed(step_fns(st, x, dY), steps, warmup, stream)
     rep = {"B": cfg["B"], "D": cfg["D"], "O": cfg["O"], "G": cfg["G"], "fan_in": cfg["F"]}
     rep.update(phase_report(cfg, ms, per))
+    rep["sr_floor"] = sr_floor_report(cfg, dict(zip(NAMES, per)), word_rate)
     if c in REWIRE_CONFIGS:
         rep["rewire"] = time_rewire(st, x, dY, cfg, stream)
     del st, x, dY
@@ -490,6 +545,7 @@ def main():
     gr_ms, _, _ = timed([graph.replay], max(5, args.steps // 2), 2, stream)
     del graph, gst
 
+    word_rate = sr_word_rate(dev)
     pb = phase_bytes(B, D, O, G, F)
     phase_gbs = {n: pb[n] / (phase_ms[n] * 1e-3) / 1e9 for n in NAMES}
     dom = max(NAMES, key=lambda n: phase_ms[n])
@@ -518,6 +574,9 @@ def main():
                           "mfma_frac": rep["step_mfma_frac"]},
         "phases_us": rep["phases_us"],
         "phases_hbm_frac": rep["phases_hbm_frac"],
+        "sr_floor": {"words_per_s": word_rate,
+                     "probe": "haste_sr_words_fold: 2^26 tl.randint words, XOR-folded 64 to 1",
+                     "phases": sr_floor_report(cfg, dict(phase_ms, sgd=un_per[3]), word_rate)},
         "unfused": {"ms_per_step": un_ms, "samples_per_s": B / (un_ms * 1e-3),
                     "phases_us": {n: round(v * 1e3, 2) for n, v in zip(un_names, un_per)}},
         "fused_loss": {"ms_per_step": fl_ms, "samples_per_s": B / (fl_ms * 1e-3),
@@ -553,7 +612,8 @@ def main():
                                     "autograd backward of a [B, O] grad + SRSgd.step (momentum 0)")
     extras = [int(c) for c in args.extra_configs.split(",") if c.strip()]
     if extras:
-        result["configs"] = {str(c): run_extra_config(c, max(10, args.steps // 2), 3, dev)
+        result["configs"] = {str(c): run_extra_config(c, max(10, args.steps // 2), 3, dev,
+                                                      word_rate)
                              for c in extras if c != args.config}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg)

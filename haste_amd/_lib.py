@@ -79,6 +79,7 @@ SIGNATURES = {
     "haste_sgd_sr_step_wt": (ctypes.c_int, [_P, _P, _I32, _P, _F32, _F32, _F32, _I32, _I32, _U64,
                                             _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
     "haste_sr_round_bf16": (ctypes.c_int, [_P, _P, _I64, _U64, _U64, _P]),
+    "haste_sr_words_fold": (ctypes.c_int, [_P, _I64, _U64, _P]),
     "haste_sgd_sr_step": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _F32, _F32, _F32, _I32, _I32,
                                          _U64, _U64, _P]),
     "haste_sgd_sr_step_f16": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _F32, _F32, _F32, _I32, _I32,

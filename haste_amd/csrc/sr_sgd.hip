@@ -209,6 +209,29 @@ __global__ __launch_bounds__(256) void sr_round_kernel(const float* __restrict__
     }
 }
 
+// The tl.randint words of the SR and SR-SGD kernels alone: thread t draws the
+// words of offsets 64t .. 64t+63 (those below n) and writes their XOR, so the
+// kernel is bound by the Philox arithmetic (4 bytes written per 64 words).
+constexpr int kFoldWords = 64;
+__global__ __launch_bounds__(256) void sr_words_fold_kernel(uint32_t* __restrict__ fold, int64_t n,
+                                                            uint32_t k0, uint32_t k1) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i0 = t * kFoldWords;
+    if (i0 >= n) return;
+    uint32_t acc = 0u;
+    if (i0 + kFoldWords <= n) {
+#pragma unroll 4
+        for (int e = 0; e < kFoldWords; ++e) {
+            const uint64_t off = (uint64_t)(i0 + e);
+            acc ^= philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, k0, k1);
+        }
+    } else {
+        for (int64_t i = i0; i < n; ++i)
+            acc ^= philox_w0((uint32_t)i, (uint32_t)((uint64_t)i >> 32), 0u, k0, k1);
+    }
+    fold[t] = acc;
+}
+
 }  // namespace
 
 int sr_round_bf16(const float* x, uint16_t* out, int64_t n, uint64_t seed, uint64_t offset0,
@@ -223,6 +246,20 @@ int sr_round_bf16(const float* x, uint16_t* out, int64_t n, uint64_t seed, uint6
 }
 
 }  // namespace haste
+
+extern "C" int haste_sr_words_fold(uint32_t* fold, int64_t n, uint64_t seed, void* stream) {
+    HASTE_CHECK_ARG(n >= 0, "haste_sr_words_fold: n must be >= 0 (got %lld)", (long long)n);
+    if (n == 0) return HASTE_OK;
+    HASTE_CHECK_ARG(fold != nullptr, "haste_sr_words_fold: null pointer");
+    const int64_t threads = haste::ceil_div(n, (int64_t)haste::kFoldWords);
+    const int64_t blocks = haste::ceil_div(threads, (int64_t)256);
+    HASTE_CHECK_ARG(blocks < (int64_t)1 << 31, "haste_sr_words_fold: n too large");
+    haste::sr_words_fold_kernel<<<dim3((unsigned)blocks), dim3(256), 0,
+                                  static_cast<hipStream_t>(stream)>>>(fold, n, (uint32_t)seed,
+                                                                      (uint32_t)(seed >> 32));
+    HASTE_CHECK_LAUNCH("haste_sr_words_fold");
+    return HASTE_OK;
+}
 
 extern "C" int haste_sr_round_bf16(const float* x, uint16_t* out, int64_t n, uint64_t seed,
                                    uint64_t offset0, void* stream) {

@@ -302,6 +302,16 @@ int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype, float* m, 
                          int64_t O, int64_t G, int32_t dtype, void* stream);
 
 /*
+ * The random words of the stochastic rounding alone: draws tl.randint(seed, i)
+ * for i < n, as the SR and SR-SGD kernels do, and writes the XOR of each 64
+ * consecutive words: fold[t] = XOR of words 64t .. min(64t + 63, n - 1),
+ * t < ceil(n / 64).  No counterpart in the reference: it times the arithmetic
+ * floor of the SR-SGD step (Philox4x32-10 per weight, which bit-exact
+ * tl.randint fixes), the bound beside HBM for those kernels.
+ */
+int haste_sr_words_fold(uint32_t* fold, int64_t n, uint64_t seed, void* stream);
+
+/*
  * Stochastic rounding fp32 -> bf16: out[i] = SR(x[i], tl.randint(seed, offset0 + i)).
  * Replaces stochastic_rounding (shared_ffi/sr_triton.py:51-59).
  */

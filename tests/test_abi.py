@@ -205,6 +205,13 @@ def test_staged_cases_reach_every_staged_build():
     assert kernel_config(L, 100, 300, 1000, 16, 16)[1] > 0        # G = 16: ring
 
 
+def test_sr_words_fold_rejects_bad_arguments():
+    L = _lib.lib()
+    assert L.haste_sr_words_fold(None, -1, 0, None) == _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_sr_words_fold(None, 10, 0, None) == _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_sr_words_fold(None, 0, 0, None) == 0
+
+
 def test_forward_bce_noalloc_rejects_shapes_beyond_its_scratch():
     """The no-allocation forward+loss refuses, before any HIP call, a shape whose
     workspace exceeds the library's fixed per-GPU scratch (64 MiB): BASELINE

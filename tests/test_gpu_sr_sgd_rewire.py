@@ -273,3 +273,16 @@ def test_app_rewire(dev, O, F, G, D, score, gk, prune, regrow, init):
     assert np.array_equal(bits(layer.weights), ref_w)
     if prune == "fraction":
         assert ref_n == k
+
+
+@pytest.mark.parametrize("n,seed", [(1, 42), (64, 42), (1000, 2**32 + 7), (262144 + 13, 123)])
+def test_sr_words_fold(dev, n, seed):
+    """haste_sr_words_fold draws exactly the tl.randint words of the SR kernels:
+    the XOR of each 64 consecutive words, bit-exact against the oracle's randint."""
+    nf = (n + 63) // 64
+    fold = torch.zeros(nf, dtype=torch.int32, device=dev)
+    _lib.call("haste_sr_words_fold", fold.data_ptr(), n, seed, _C.stream_of(fold))
+    w = np.zeros(nf * 64, dtype=np.uint32)
+    w[:n] = oracle.randint(seed, 0, n)
+    exp = np.bitwise_xor.reduce(w.reshape(nf, 64), axis=1)
+    assert np.array_equal(fold.cpu().numpy().view(np.uint32), exp)
