@@ -87,7 +87,12 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     return (u & 0x7FFFFFFFu) > 0x7F800000u ? qnan : v;
 }
 
+// fp32 -> fp16 round-to-nearest-even of the fp32 value f itself: the empty asm
+// keeps the compiler from folding the conversion into the operation that made
+// f (an fma followed by it would become v_fma_mixlo_f16, which rounds the exact
+// result to fp16 once instead of rounding it to fp32 first).
 __device__ __forceinline__ uint32_t f32_to_f16_rne(float f) {
+    asm volatile("" : "+v"(f));
     _Float16 h = (_Float16)f;
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }

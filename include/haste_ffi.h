@@ -381,6 +381,8 @@ int haste_transpose_features(const uint16_t* x, int64_t ldx, uint16_t* xT, int64
  *     RANDOM -> fma(u01, 2*bound, -bound), u01 = (philox(seed; l*F+j, 2, 0).w0 >> 8) * 2^-24,
  *     stored in W's dtype (RNE to bf16 / fp16)
  * scores_out [Gc, F] fp32 and n_pruned (one int32, incremented) may be NULL.
+ * idx entries are indices in [0, D).  UNUSED regrow is a second launch on the
+ * stream: between the two, the pruned slots of idx hold -1.
  */
 int haste_rewire(void* W, int32_t w_dtype, int32_t* idx, float* scores_out, int32_t* n_pruned,
                  int64_t O, int64_t F, int64_t G, int64_t D, int32_t prune_mode, float threshold,

@@ -143,8 +143,9 @@ _WCODE = {torch.float16: oracle.F16, torch.float32: oracle.F32, torch.bfloat16: 
 
 @pytest.mark.parametrize("wdt", [torch.float16, torch.float32])
 @pytest.mark.parametrize("init", ["zero", "random"])
-def test_rewire_f16_f32_layers_match_oracle(dev, wdt, init):
-    O, F, G, D = 1000, 64, 32, 300
+@pytest.mark.parametrize("O,F,G,D", [(1000, 64, 32, 300), (1001, 13, 16, 50), (130, 256, 128, 900),
+                                     (100000, 64, 32, 300)])
+def test_rewire_f16_f32_layers_match_oracle(dev, wdt, init, O, F, G, D):
     torch.manual_seed(7)
     layer = GroupFixedFanIn(D, O, F, group_size=G, prune_mode="fraction", rewire_fraction=0.15,
                             init_mode=init, dtype=wdt)

@@ -191,11 +191,23 @@ REWIRE_CASES = [
     (2000, 256, 128, 4096, "fraction", 38, "unused", "random"),
     (777, 16, 32, 40, "fraction", 8, "unused", "random"),
     (20000, 128, 128, 768, "fraction", 19, "unused", "zero"),   # config 4's rewire shape
+    # rows of 26 bytes: groups start off 16-byte boundaries and W ends mid-piece
+    (1001, 13, 7, 50, "fraction", 3, "unused", "random"),
+    (257, 1, 4, 9, "fraction", 1, "unused", "zero"),
+    (300, 200, 300, 1000, "fraction", 30, "unused", "zero"),    # one group in 5 row chunks
+    # more groups than resident workgroups: each workgroup takes several in turn
+    (120000, 32, 16, 300, "threshold", 0.03, "random", "random"),
+    (150000, 64, 32, 768, "fraction", 9, "unused", "random"),
 ]
 
 
 @pytest.mark.parametrize("O,F,G,D,prune,kt,regrow,init", REWIRE_CASES)
-def test_rewire(dev, O, F, G, D, prune, kt, regrow, init):
+@pytest.mark.parametrize("woff", [0, 1], ids=["aligned", "offset"])
+def test_rewire(dev, O, F, G, D, prune, kt, regrow, init, woff):
+    """woff=1: W starts one element into its allocation (2 bytes off a 16-byte
+    boundary), so no group is written back as whole 16-byte pieces."""
+    if woff and O > 2000:
+        pytest.skip("the offset variant runs on the small shapes")
     rng = np.random.default_rng(O)
     bound = 1.0 / math.sqrt(F)
     w = oracle.f32_to_bf16_bits(rng.uniform(-bound, bound, (O, F)).astype(np.float32))
@@ -209,7 +221,10 @@ def test_rewire(dev, O, F, G, D, prune, kt, regrow, init):
     seed = 0x1234ABCD5678 + O
     ref_w, ref_idx, ref_n, ref_s, _ = oracle.rewire(w, idx, G, D, prune_mode=pm, threshold=thr, k=k,
                                                     regrow_mode=rm, init_mode=im, bound=bound, seed=seed)
-    Wd = torch.from_numpy(w.view(np.int16)).to(dev).view(torch.bfloat16)
+    buf = torch.full((O * F + 2 * woff,), 7, dtype=torch.int16)
+    buf[woff:woff + O * F] = torch.from_numpy(w.view(np.int16).reshape(-1))
+    bufd = buf.to(dev)
+    Wd = bufd[woff:woff + O * F].view(torch.bfloat16).view(O, F)
     idxd = torch.from_numpy(idx).to(dev)
     scores = torch.empty(Gc, F, device=dev)
     cnt = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -218,6 +233,8 @@ def test_rewire(dev, O, F, G, D, prune, kt, regrow, init):
     assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
     assert np.array_equal(idxd.cpu().numpy(), ref_idx)
     assert np.array_equal(bits(Wd), ref_w)
+    b = bufd.cpu()   # the elements either side of W are untouched
+    assert torch.all(b[:woff] == 7) and torch.all(b[woff + O * F:] == 7)
     assert int(cnt.item()) == ref_n
 
 
