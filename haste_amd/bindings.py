@@ -37,11 +37,13 @@ def _grad_dtype(p: torch.Tensor) -> torch.dtype:
     return gd if gd is not None else p.dtype
 
 
-# Feature-gradient workspaces reused across backward calls.  The index plan in a
-# workspace depends on group_locations only, so a call with the same index
-# tensor (same object, unchanged version counter: a rewire bumps it) skips
-# rebuilding it.  Keyed by shape, dtype, device and stream too: a workspace's
-# partial sums are written and read in stream order.
+# Feature-gradient workspaces reused across backward calls, one per layer: the
+# index plan in a workspace depends on group_locations only, so a call with the
+# same index tensor (same object, unchanged version counter: a rewire bumps it)
+# skips rebuilding it.  Keyed by the index tensor's address (a layer) and by
+# shape, dtype, device and stream (a workspace's partial sums are written and
+# read in stream order); the _WS_CACHE_SIZE most recently used are kept, so a
+# model with up to that many FFI layers never rebuilds a plan it had.
 class _Workspace:
     __slots__ = ("ws", "dims", "stream", "locs", "locs_version", "locs_ptr", "wt_ptr",
                  "wt_version", "__weakref__")
@@ -63,7 +65,7 @@ class _Workspace:
 
 
 _WS_CACHE: "collections.OrderedDict[tuple, _Workspace]" = collections.OrderedDict()
-_WS_CACHE_SIZE = 2
+_WS_CACHE_SIZE = 4
 # weights data_ptr -> the workspace whose plan was last used with them, so that
 # SRSgd can refresh its transposed weights while it updates them (the next
 # backward then skips the gather)
@@ -72,7 +74,7 @@ _WT_TARGETS: "weakref.WeakValueDictionary[int, _Workspace]" = weakref.WeakValueD
 
 def _bwdf_workspace(locs: torch.Tensor, B: int, D: int, F: int, O: int, gsize: int,
                     dtype: torch.dtype, stream: int) -> _Workspace:
-    key = (locs.device, B, D, F, O, gsize, dtype, stream)
+    key = (locs.data_ptr(), locs.device, B, D, F, O, gsize, dtype, stream)
     ent = _WS_CACHE.get(key)
     if ent is None:
         ent = _Workspace(_C.bwd_features_workspace(B, D, F, O, gsize, dtype, locs.device),
@@ -89,10 +91,12 @@ def mark_wt_refreshed(ent: _Workspace, weights: torch.Tensor) -> None:
     ent.wt_ptr, ent.wt_version = weights.data_ptr(), weights._version
 
 
-def clear_wt_refreshed() -> None:
-    """Forget every refreshed transposed-weight copy (the next backward gathers)."""
+def clear_wt_refreshed(weights: Optional[torch.Tensor] = None) -> None:
+    """Forget the refreshed transposed-weight copy of ``weights`` (of every
+    layer when None): the next backward gathers W^T from the weights again."""
     for ent in _WS_CACHE.values():
-        ent.wt_ptr, ent.wt_version = 0, -1
+        if weights is None or ent.wt_ptr == weights.data_ptr():
+            ent.wt_ptr, ent.wt_version = 0, -1
 
 
 def wt_target(weights: torch.Tensor):

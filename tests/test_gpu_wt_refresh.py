@@ -100,3 +100,61 @@ def test_training_loop_with_refresh_matches_without(dev):
         assert torch.equal(u.view(torch.int16), v.view(torch.int16))
     for (ka, va), (kb, vb) in zip(a.state_dict().items(), b.state_dict().items()):
         assert torch.equal(va, vb), ka
+
+
+@pytest.mark.parametrize("clear", [True, False])
+def test_edit_through_data_needs_clear_wt_refreshed(dev, clear):
+    """An edit through ``W.data`` does not move the weights' version counter, so
+    the refreshed W^T would be reused: ``bindings.clear_wt_refreshed(W)``, called
+    as documented, makes the next backward gather again (input gradients then
+    equal the plain path's bit for bit); without it they differ."""
+    B, D, O, G, F = 64, 300, 3001, 64, 64
+
+    def run(refresh, clear_after_edit):
+        bindings._WS_CACHE.clear()
+        torch.manual_seed(0)
+        layer = GroupFixedFanIn(D, O, F, group_size=G, rewire_threshold=0.0,
+                                dtype=torch.bfloat16).to(dev)
+        opt = SRSgd(layer.parameters(), lr=0.05, weight_decay=1e-4, momentum=0.9, seed=42,
+                    refresh_transposed=refresh)
+        gen = torch.Generator(device=dev).manual_seed(1)
+        gx = []
+        for step in range(3):
+            x = torch.randn(B, D, generator=gen, device=dev).to(torch.bfloat16).requires_grad_(True)
+            dY = (torch.randn(B, O, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+            opt.zero_grad()
+            layer(x).backward(dY)
+            gx.append(x.grad.clone())
+            opt.step()
+            if step == 1:
+                layer.weights.data.mul_(0.75)
+                if clear_after_edit:
+                    bindings.clear_wt_refreshed(layer.weights)
+        torch.cuda.synchronize()
+        return gx
+
+    a = run(True, clear)
+    b = run(False, False)
+    assert torch.equal(a[1].view(torch.int16), b[1].view(torch.int16))
+    same = torch.equal(a[2].view(torch.int16), b[2].view(torch.int16))
+    assert same == clear
+
+
+def test_same_shape_layers_keep_their_own_plans(dev):
+    """Two FFI layers of one shape each keep their own workspace: after
+    alternating backwards both index plans are still valid (none is rebuilt)."""
+    B, D, O, G, F = 32, 256, 2000, 32, 32
+    bindings._WS_CACHE.clear()
+    torch.manual_seed(3)
+    layers = [GroupFixedFanIn(D, O, F, group_size=G, rewire_threshold=0.0,
+                              dtype=torch.bfloat16).to(dev) for _ in range(2)]
+    gen = torch.Generator(device=dev).manual_seed(4)
+    for _ in range(2):
+        for layer in layers:
+            x = torch.randn(B, D, generator=gen, device=dev).to(torch.bfloat16).requires_grad_(True)
+            layer(x).backward(torch.ones(B, O, device=dev, dtype=torch.bfloat16))
+    torch.cuda.synchronize()
+    assert len(bindings._WS_CACHE) == 2
+    for layer in layers:
+        locs = layer.group_locations
+        assert sum(ent.plan_valid(locs) for ent in bindings._WS_CACHE.values()) == 1
