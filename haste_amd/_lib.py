@@ -21,6 +21,7 @@ HASTE_ERR_WORKSPACE = -3
 HASTE_ERR_HIP = -4
 
 DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
+DTYPE_F8E4M3, DTYPE_F8E5M2 = 3, 4  # SR outputs and SGD weights only
 PRUNE_THRESHOLD, PRUNE_FRACTION, PRUNE_GLOBAL_FRACTION = 0, 1, 2
 SCORE_MEAN, SCORE_MAX = 0, 1
 REGROW_RANDOM, REGROW_UNUSED = 0, 1
@@ -79,6 +80,9 @@ SIGNATURES = {
     "haste_sgd_sr_step_wt": (ctypes.c_int, [_P, _P, _I32, _P, _F32, _F32, _F32, _I32, _I32, _U64,
                                             _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
     "haste_sr_round_bf16": (ctypes.c_int, [_P, _P, _I64, _U64, _U64, _P]),
+    "haste_sr_round": (ctypes.c_int, [_P, _P, _I32, _I64, _U64, _U64, _P]),
+    "haste_sgd_sr_step_f8": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _I64, _F32, _F32, _F32,
+                                            _I32, _I32, _U64, _U64, _P]),
     "haste_sr_words_fold": (ctypes.c_int, [_P, _I64, _U64, _P]),
     "haste_sgd_sr_step": (ctypes.c_int, [_P, _P, _I32, _P, _I64, _F32, _F32, _F32, _I32, _I32,
                                          _U64, _U64, _P]),

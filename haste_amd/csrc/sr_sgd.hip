@@ -209,6 +209,150 @@ __global__ __launch_bounds__(256) void sr_round_kernel(const float* __restrict__
     }
 }
 
+// ---- fp16 and fp8 outputs, fp8 weights (sr_triton.py:18-25,43-46,146,167-168)
+// OCP fp8: E4M3 "fn" (bias 7, no infinities, S.1111.111 NaN, largest finite
+// 448 = 0x7E) and E5M2 (bias 15, IEEE infinities / NaNs, largest finite
+// 57344 = 0x7B).
+template <int FMT>
+struct F8Fmt {
+    static constexpr int M = FMT == HASTE_DTYPE_F8E4M3 ? 3 : 2;
+    static constexpr int bias = FMT == HASTE_DTYPE_F8E4M3 ? 7 : 15;
+    static constexpr uint32_t maxcode = FMT == HASTE_DTYPE_F8E4M3 ? 0x7Eu : 0x7Bu;
+    // 2^(M - emin): the smallest subnormal is 1 / sub_scale
+    static constexpr float sub_scale = FMT == HASTE_DTYPE_F8E4M3 ? 512.0f : 65536.0f;
+};
+
+// fp8 code -> fp32, exact.
+template <int FMT>
+__device__ __forceinline__ float f8_to_f32(uint32_t c) {
+    using F = F8Fmt<FMT>;
+    const uint32_t s = (c & 0x80u) << 24;
+    const uint32_t e = (c & 0x7Fu) >> F::M, m = c & ((1u << F::M) - 1u);
+    const uint32_t normal = s | ((e + 127u - F::bias) << 23) | (m << (23 - F::M));
+    const float sub = (float)m * (1.0f / F::sub_scale);
+    float v = e == 0 ? __uint_as_float(s | __float_as_uint(sub)) : __uint_as_float(normal);
+    if constexpr (FMT == HASTE_DTYPE_F8E4M3)
+        v = (c & 0x7Fu) == 0x7Fu ? __uint_as_float(s | 0x7FC00000u) : v;
+    else
+        v = e == 31u ? __uint_as_float(s | 0x7F800000u | (m ? 0x400000u : 0u)) : v;
+    return v;
+}
+
+// fp32 -> fp8, round to nearest even, saturating: finite overflow and
+// infinities give the largest finite value with the sign kept; NaN gives
+// sign | 0x7F.  Below the smallest normal the code is the value in units of the
+// smallest subnormal, rounded to nearest even (2^M being the smallest normal).
+template <int FMT>
+__device__ __forceinline__ uint32_t f32_to_f8(float f) {
+    using F = F8Fmt<FMT>;
+    constexpr int rb = 23 - F::M;
+    const uint32_t u = __float_as_uint(f), s = (u >> 24) & 0x80u, a = u & 0x7FFFFFFFu;
+    const uint32_t sub = (uint32_t)__builtin_rintf(__uint_as_float(a) * F::sub_scale);
+    const uint32_t nrm = ((a + ((1u << (rb - 1)) - 1u) + ((a >> rb) & 1u)) >> rb) -
+                         ((uint32_t)(127 - F::bias) << F::M);
+    uint32_t code = a < (uint32_t)(128 - F::bias) << 23 ? sub : min(nrm, F::maxcode);
+    code = a >= 0x7F800000u ? (a == 0x7F800000u ? F::maxcode : 0x7Fu) : code;
+    return s | code;
+}
+
+// The output code of stochastic_rounding for output dtype OUT.
+template <int OUT>
+__device__ __forceinline__ uint32_t sr_code(float x, uint32_t r) {
+    if constexpr (OUT == HASTE_DTYPE_F8E4M3) {
+        const uint32_t u = __float_as_uint(x);
+        const uint32_t nan = ((u >> 24) & 0x80u) | 0x7Fu;
+        const uint32_t c = f32_to_f8<HASTE_DTYPE_F8E4M3>(__uint_as_float((u + (r & 0xFFFFFu)) & 0xFFF00000u));
+        return (u & 0x7FFFFFFFu) > 0x7F800000u ? nan : c;
+    } else {
+        const uint32_t b = sr_bf16(x, r);
+        if constexpr (OUT == HASTE_DTYPE_F16) return f32_to_f16_rne(bf16_bits_to_f32(b));
+        else if constexpr (OUT == HASTE_DTYPE_F8E5M2) return f32_to_f8<OUT>(bf16_bits_to_f32(b));
+        else return b;
+    }
+}
+
+// SR of one tensor to output dtype OUT (2- or 1-byte codes), 8 elements per thread.
+template <int OUT>
+__global__ __launch_bounds__(256) void sr_round_any_kernel(const float* __restrict__ x,
+                                                           void* __restrict__ out, int64_t n,
+                                                           int32_t vec, uint32_t k0, uint32_t k1,
+                                                           uint64_t offset0) {
+    constexpr bool B1 = OUT == HASTE_DTYPE_F8E4M3 || OUT == HASTE_DTYPE_F8E5M2;
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kVec;
+    if (vec && i + kVec <= n) {
+        const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + i));
+        const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + i) + 1);
+        const float xf[kVec] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        uint32_t c[kVec];
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) {
+            const uint64_t off = offset0 + (uint64_t)(i + e);
+            c[e] = sr_code<OUT>(xf[e], philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, k0, k1));
+        }
+        if constexpr (B1) {
+            *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(out) + i) =
+                u32x2{c[0] | c[1] << 8 | c[2] << 16 | c[3] << 24,
+                      c[4] | c[5] << 8 | c[6] << 16 | c[7] << 24};
+        } else {
+            *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + i) =
+                u32x4{c[0] | c[1] << 16, c[2] | c[3] << 16, c[4] | c[5] << 16, c[6] | c[7] << 16};
+        }
+    } else {
+        for (int e = 0; e < kVec; ++e) {
+            const int64_t j = i + e;
+            if (j >= n) break;
+            const uint64_t off = offset0 + (uint64_t)j;
+            const uint32_t c =
+                sr_code<OUT>(x[j], philox_w0((uint32_t)off, (uint32_t)(off >> 32), 0u, k0, k1));
+            if constexpr (B1) static_cast<uint8_t*>(out)[j] = (uint8_t)c;
+            else static_cast<uint16_t*>(out)[j] = (uint16_t)c;
+        }
+    }
+}
+
+// The SGD step of sgd_sr_kernel on one tensor of fp8 weights: loaded exactly,
+// the bf16 result stored as fp8 (f32_to_f8).
+template <int GD, bool USE_MOM, bool DO_SR, int FMT>
+__global__ __launch_bounds__(kSgdThreads) void sgd_sr_f8_kernel(
+    uint8_t* __restrict__ w, const void* __restrict__ g, float* __restrict__ m, int64_t n,
+    int32_t vec, float lr, float wd, float mu, uint64_t seed, uint64_t offset0) {
+    const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+    const int64_t i = ((int64_t)blockIdx.x * kSgdThreads + threadIdx.x) * kVec;
+    auto one = [&](uint32_t wc, float gf, float* mv, int64_t j) __attribute__((always_inline)) {
+        return f32_to_f8<FMT>(bf16_bits_to_f32(sgd_one(f8_to_f32<FMT>(wc), gf, mv, USE_MOM, lr, wd,
+                                                      mu, DO_SR, offset0 + (uint64_t)j, k0, k1)));
+    };
+    if (vec && i + kVec <= n) {
+        const u32x2 wv = *reinterpret_cast<const u32x2*>(w + i);
+        float gf[kVec];
+        load_grad8<GD>(g, i, gf);
+        float mv[kVec];
+        if constexpr (USE_MOM) {
+            const f32x4 a = reinterpret_cast<const f32x4*>(m + i)[0];
+            const f32x4 c = reinterpret_cast<const f32x4*>(m + i)[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { mv[e] = a[e]; mv[4 + e] = c[e]; }
+        }
+        uint32_t oc[kVec];
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) oc[e] = one((wv[e >> 2] >> (8 * (e & 3))) & 0xFFu, gf[e], &mv[e], i + e);
+        *reinterpret_cast<u32x2*>(w + i) = u32x2{oc[0] | oc[1] << 8 | oc[2] << 16 | oc[3] << 24,
+                                                 oc[4] | oc[5] << 8 | oc[6] << 16 | oc[7] << 24};
+        if constexpr (USE_MOM) {
+            reinterpret_cast<f32x4*>(m + i)[0] = f32x4{mv[0], mv[1], mv[2], mv[3]};
+            reinterpret_cast<f32x4*>(m + i)[1] = f32x4{mv[4], mv[5], mv[6], mv[7]};
+        }
+    } else {
+        for (int e = 0; e < kVec; ++e) {
+            const int64_t j = i + e;
+            if (j >= n) break;
+            float mv = USE_MOM ? m[j] : 0.f;
+            w[j] = (uint8_t)one(w[j], load_grad1<GD>(g, j), &mv, j);
+            if (USE_MOM) m[j] = mv;
+        }
+    }
+}
+
 // The tl.randint words of the SR and SR-SGD kernels alone: thread t draws the
 // words of offsets 64t .. 64t+63 (those below n) and writes their XOR, so the
 // kernel is bound by the Philox arithmetic (4 bytes written per 64 words).
@@ -267,6 +411,97 @@ extern "C" int haste_sr_round_bf16(const float* x, uint16_t* out, int64_t n, uin
     if (n == 0) return HASTE_OK;
     HASTE_CHECK_ARG(x != nullptr && out != nullptr, "haste_sr_round_bf16: null pointer");
     return haste::sr_round_bf16(x, out, n, seed, offset0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int haste_sr_round(const float* x, void* out, int32_t out_dtype, int64_t n,
+                              uint64_t seed, uint64_t offset0, void* stream) {
+    HASTE_CHECK_ARG(n >= 0, "haste_sr_round: n must be >= 0 (got %lld)", (long long)n);
+    HASTE_CHECK_ARG(out_dtype == HASTE_DTYPE_BF16 || out_dtype == HASTE_DTYPE_F16 ||
+                        out_dtype == HASTE_DTYPE_F8E4M3 || out_dtype == HASTE_DTYPE_F8E5M2,
+                    "haste_sr_round: output dtype must be bf16, fp16, fp8 e4m3 or fp8 e5m2 "
+                    "(dtype code %d)", (int)out_dtype);
+    if (n == 0) return HASTE_OK;
+    HASTE_CHECK_ARG(x != nullptr && out != nullptr, "haste_sr_round: null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (out_dtype == HASTE_DTYPE_BF16)
+        return haste::sr_round_bf16(x, static_cast<uint16_t*>(out), n, seed, offset0, st);
+    const int64_t blocks = haste::ceil_div(n, (int64_t)256 * haste::kVec);
+    HASTE_CHECK_ARG(blocks < (int64_t)1 << 31, "haste_sr_round: tensor too large");
+    const bool b1 = out_dtype != HASTE_DTYPE_F16;
+    const int32_t vec = haste::aligned16(x) &&
+                        (reinterpret_cast<uintptr_t>(out) & (b1 ? 7u : 15u)) == 0;
+    const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#define HASTE_SR_LAUNCH(OUT)                                                             \
+    haste::sr_round_any_kernel<OUT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(x, out, n, \
+                                                                              vec, k0, k1, \
+                                                                              offset0)
+    if (out_dtype == HASTE_DTYPE_F16) HASTE_SR_LAUNCH(HASTE_DTYPE_F16);
+    else if (out_dtype == HASTE_DTYPE_F8E4M3) HASTE_SR_LAUNCH(HASTE_DTYPE_F8E4M3);
+    else HASTE_SR_LAUNCH(HASTE_DTYPE_F8E5M2);
+#undef HASTE_SR_LAUNCH
+    HASTE_CHECK_LAUNCH("haste_sr_round");
+    return HASTE_OK;
+}
+
+namespace {
+template <int FMT, int GD>
+void launch_sgd_f8(uint8_t* w, const void* g, float* m, int64_t n, int64_t blocks, int32_t vec,
+                   float lr, float wd, float mu, int32_t use_mom, int32_t do_sr, uint64_t seed,
+                   uint64_t offset0, hipStream_t st) {
+#define HASTE_SGD8_LAUNCH(UM, SR)                                                           \
+    haste::sgd_sr_f8_kernel<GD, UM, SR, FMT><<<dim3((unsigned)blocks),                    \
+                                               dim3(haste::kSgdThreads), 0, st>>>(         \
+        w, g, m, n, vec, lr, wd, mu, seed, offset0)
+    if (use_mom && do_sr) HASTE_SGD8_LAUNCH(true, true);
+    else if (use_mom) HASTE_SGD8_LAUNCH(true, false);
+    else if (do_sr) HASTE_SGD8_LAUNCH(false, true);
+    else HASTE_SGD8_LAUNCH(false, false);
+#undef HASTE_SGD8_LAUNCH
+}
+template <int FMT>
+int sgd_f8_dispatch(uint8_t* w, const void* g, int32_t g_dtype, float* m, int64_t n,
+                    int64_t blocks, int32_t vec, float lr, float wd, float mu, int32_t use_mom,
+                    int32_t do_sr, uint64_t seed, uint64_t offset0, hipStream_t st) {
+    switch (g_dtype) {
+    case HASTE_DTYPE_BF16:
+        launch_sgd_f8<FMT, HASTE_DTYPE_BF16>(w, g, m, n, blocks, vec, lr, wd, mu, use_mom, do_sr, seed, offset0, st);
+        break;
+    case HASTE_DTYPE_F16:
+        launch_sgd_f8<FMT, HASTE_DTYPE_F16>(w, g, m, n, blocks, vec, lr, wd, mu, use_mom, do_sr, seed, offset0, st);
+        break;
+    case HASTE_DTYPE_F32:
+        launch_sgd_f8<FMT, HASTE_DTYPE_F32>(w, g, m, n, blocks, vec, lr, wd, mu, use_mom, do_sr, seed, offset0, st);
+        break;
+    default:
+        haste::set_error("haste_sgd_sr_step_f8: unsupported gradient dtype code %d", (int)g_dtype);
+        return HASTE_ERR_UNSUPPORTED;
+    }
+    HASTE_CHECK_LAUNCH("haste_sgd_sr_step_f8");
+    return HASTE_OK;
+}
+}  // namespace
+
+extern "C" int haste_sgd_sr_step_f8(uint8_t* w, int32_t w_dtype, const void* g, int32_t g_dtype,
+                                    float* m, int64_t n, float lr, float wd, float mu,
+                                    int32_t use_mom, int32_t do_sr, uint64_t seed,
+                                    uint64_t offset0, void* stream) {
+    HASTE_CHECK_ARG(n >= 0, "haste_sgd_sr_step_f8: n must be >= 0 (got %lld)", (long long)n);
+    HASTE_CHECK_ARG(w_dtype == HASTE_DTYPE_F8E4M3 || w_dtype == HASTE_DTYPE_F8E5M2,
+                    "haste_sgd_sr_step_f8: weights must be fp8 e4m3 or e5m2 (dtype code %d)",
+                    (int)w_dtype);
+    if (n == 0) return HASTE_OK;
+    HASTE_CHECK_ARG(w != nullptr && g != nullptr, "haste_sgd_sr_step_f8: null pointer");
+    HASTE_CHECK_ARG(!use_mom || m != nullptr, "haste_sgd_sr_step_f8: momentum buffer is NULL");
+    const int64_t blocks = haste::ceil_div(n, haste::kSegBlockElems);
+    HASTE_CHECK_ARG(blocks < (int64_t)1 << 31, "haste_sgd_sr_step_f8: tensor too large");
+    const int32_t vec = (reinterpret_cast<uintptr_t>(w) & 7u) == 0 && haste::aligned16(g) &&
+                        (!use_mom || haste::aligned16(m));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return w_dtype == HASTE_DTYPE_F8E4M3
+               ? sgd_f8_dispatch<HASTE_DTYPE_F8E4M3>(w, g, g_dtype, m, n, blocks, vec, lr, wd,
+                                                     mu, use_mom, do_sr, seed, offset0, st)
+               : sgd_f8_dispatch<HASTE_DTYPE_F8E5M2>(w, g, g_dtype, m, n, blocks, vec, lr, wd,
+                                                     mu, use_mom, do_sr, seed, offset0, st);
 }
 
 namespace {

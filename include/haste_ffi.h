@@ -43,6 +43,9 @@ enum {
 };
 
 enum { HASTE_DTYPE_BF16 = 0, HASTE_DTYPE_F16 = 1, HASTE_DTYPE_F32 = 2 };
+/* OCP float8 formats (torch.float8_e4m3fn, torch.float8_e5m2), for the outputs
+ * of haste_sr_round and the weights of haste_sgd_sr_step_f8 only. */
+enum { HASTE_DTYPE_F8E4M3 = 3, HASTE_DTYPE_F8E5M2 = 4 };
 
 enum { HASTE_PRUNE_THRESHOLD = 0, HASTE_PRUNE_FRACTION = 1, HASTE_PRUNE_GLOBAL_FRACTION = 2 };
 enum { HASTE_SCORE_MEAN = 0, HASTE_SCORE_MAX = 1 };
@@ -319,6 +322,21 @@ int haste_sr_round_bf16(const float* x, uint16_t* out, int64_t n, uint64_t seed,
                         uint64_t offset0, void* stream);
 
 /*
+ * stochastic_rounding (shared_ffi/sr_triton.py:43-59) for the other output
+ * dtypes the reference dispatches on (out_dtype): HASTE_DTYPE_F8E4M3 takes
+ * stochastic_rounding_to_fp8 (sr_triton.py:18-25: the low 20 bits of
+ * tl.randint(seed, offset0 + i) added to the fp32 pattern, the low 20 bits
+ * cleared, then converted); HASTE_DTYPE_BF16, HASTE_DTYPE_F16 and
+ * HASTE_DTYPE_F8E5M2 take the bf16 rounding of haste_sr_round_bf16, stored in
+ * the output dtype (as the reference's store converts it).  Conversions round to
+ * nearest even; fp8 ones saturate (finite overflow and infinities become the
+ * largest finite value with the sign kept, NaN becomes sign | 0x7F).  out holds
+ * n elements of 2 (bf16, fp16) or 1 (fp8) bytes.
+ */
+int haste_sr_round(const float* x, void* out, int32_t out_dtype, int64_t n, uint64_t seed,
+                   uint64_t offset0, void* stream);
+
+/*
  * Fused SGD step on bf16 weights, in place (one pass):
  *   g' = fma(wd, w, g);  [m' = fma(mu, m, g'); m = m';]  w' = fma(-lr, m' or g', w)
  *   w  = do_sr ? SR(w', tl.randint(seed, offset0 + i)) : RNE(w')
@@ -339,6 +357,16 @@ int haste_sgd_sr_step(uint16_t* w, const void* g, int32_t g_dtype, float* m, int
 int haste_sgd_sr_step_f16(uint16_t* w, const void* g, int32_t g_dtype, float* m, int64_t n,
                           float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
                           uint64_t seed, uint64_t offset0, void* stream);
+
+/*
+ * haste_sgd_sr_step on fp8 weights (w_dtype HASTE_DTYPE_F8E4M3 or
+ * HASTE_DTYPE_F8E5M2, n one-byte codes): _sgd_m_wd_sr (sr_triton.py:109-168)
+ * with an fp8 w_ptr.  Weights load exactly; the bf16 result (SR or RNE) is
+ * stored as fp8, rounded to nearest even and saturating as in haste_sr_round.
+ */
+int haste_sgd_sr_step_f8(uint8_t* w, int32_t w_dtype, const void* g, int32_t g_dtype, float* m,
+                         int64_t n, float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
+                         uint64_t seed, uint64_t offset0, void* stream);
 
 /*
  * The same step over several tensors in one launch (one kernel per 8

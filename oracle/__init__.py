@@ -38,6 +38,7 @@ _LIB_PATH = os.path.join(_HERE, "libhaste_oracle.so")
 _lib = None
 
 BF16, F16, F32 = 0, 1, 2
+F8E4M3, F8E5M2 = 3, 4   # OCP float8 e4m3fn / e5m2 (torch.float8_e4m3fn / float8_e5m2)
 PRUNE_THRESHOLD, PRUNE_FRACTION = 0, 1
 REGROW_RANDOM, REGROW_UNUSED = 0, 1
 INIT_ZERO, INIT_RANDOM = 0, 1
@@ -70,6 +71,12 @@ def lib() -> ctypes.CDLL:
         L.ho_sgd_sr_step_f16w.argtypes = [P, P, c_int, P, i64, f32, f32, f32, c_int, c_int, u64,
                                           u64]
         L.ho_f32_to_f16_rne_arr.argtypes = [P, P, i64]
+        L.ho_sr_round.argtypes = [P, P, c_int, i64, u64, u64]
+        L.ho_sgd_sr_step_f8w.argtypes = [P, c_int, P, c_int, P, i64, f32, f32, f32, c_int, c_int,
+                                         u64, u64]
+        L.ho_f8_to_f32_arr.argtypes = [P, c_int, P, i64]
+        L.ho_f32_to_f8_arr.argtypes = [P, c_int, P, i64]
+        L.ho_sr_e4m3_words.argtypes = [f32, P, P, i64]
         L.ho_f32_to_bf16_rne_arr.argtypes = [P, P, i64]
         L.ho_rewire_scores.argtypes = [P, c_int, P, i64, i64, i64]
         L.ho_rewire.argtypes = [P, c_int, P, i64, i64, i64, i64, c_int, f32, i64, c_int, c_int,
@@ -295,3 +302,57 @@ def set_num_threads(n: int) -> None:
 
 def num_threads() -> int:
     return int(lib().ho_num_threads())
+
+
+def f8_to_f32(codes: np.ndarray, fmt: int) -> np.ndarray:
+    """fp8 codes (uint8) of format fmt (F8E4M3 / F8E5M2) -> fp32, exact
+    (ho_f8_to_f32)."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.empty(c.shape, dtype=np.float32)
+    lib().ho_f8_to_f32_arr(_ptr(c), fmt, _ptr(out), c.size)
+    return out
+
+
+def f32_to_f8(x: np.ndarray, fmt: int) -> np.ndarray:
+    """fp32 -> fp8 codes, round to nearest even, saturating (ho_f32_to_f8)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib().ho_f32_to_f8_arr(_ptr(x), fmt, _ptr(out), x.size)
+    return out
+
+
+def sr_e4m3_words(x: float, words: np.ndarray) -> np.ndarray:
+    """stochastic_rounding_to_fp8 of one value under each random word (uint32)."""
+    w = np.ascontiguousarray(words, dtype=np.uint32)
+    out = np.empty(w.shape, dtype=np.uint8)
+    lib().ho_sr_e4m3_words(float(x), _ptr(w), _ptr(out), w.size)
+    return out
+
+
+def sr_round(x: np.ndarray, out_dtype: int, seed: int, offset0: int = 0) -> np.ndarray:
+    """stochastic_rounding(x, output, seed) (sr_triton.py:27-59) for an output of
+    dtype out_dtype (BF16 / F16: uint16 bit patterns; F8E4M3 / F8E5M2: uint8 codes)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8 if out_dtype in (F8E4M3, F8E5M2) else np.uint16)
+    lib().ho_sr_round(_ptr(x), _ptr(out), out_dtype, x.size, seed, offset0)
+    return out
+
+
+def sgd_sr_step_f8w(w: np.ndarray, fmt: int, g: np.ndarray, m: np.ndarray | None, lr: float,
+                    wd: float, mu: float, use_mom: bool, do_sr: bool, seed: int,
+                    offset0: int = 0):
+    """_sgd_m_wd_sr (sr_triton.py:109-168) on fp8 weights (uint8 codes of fmt):
+    the bf16 result of the update stored as fp8.  ``g`` is float32, or uint16
+    bf16 bit patterns, or float16.  Returns (new codes, new momentum or None)."""
+    wc = np.ascontiguousarray(w, dtype=np.uint8).copy()
+    if g.dtype == np.float32:
+        g_dtype = F32
+    elif g.dtype == np.uint16:
+        g_dtype = BF16
+    else:
+        g_dtype = F16
+    g = np.ascontiguousarray(g)
+    mm = None if m is None else np.ascontiguousarray(m, dtype=np.float32).copy()
+    lib().ho_sgd_sr_step_f8w(_ptr(wc), fmt, _ptr(g), g_dtype, None if mm is None else _ptr(mm),
+                             wc.size, lr, wd, mu, int(use_mom), int(do_sr), seed, offset0)
+    return wc, mm

@@ -209,6 +209,126 @@ void ho_sgd_sr_step_f16w(uint16_t* w, const void* g, int g_dtype, float* m, int6
     }
 }
 
+/* ---- fp16 and fp8 outputs (sr_triton.py:18-25,43-46,146,167-168) ----
+ * The reference's stochastic_rounding writes float8_e4m3fn outputs through
+ * stochastic_rounding_to_fp8 (20 random bits, the fp32 pattern cut to 12 bits,
+ * then converted), and every other output dtype through the bf16 rounding
+ * followed by the store's conversion to the output dtype; _sgd_m_wd_sr stores
+ * its bf16 result into fp16 / fp8 weights the same way.  The conversions:
+ *   fp16: round to nearest even (ho_f32_to_f16_rne);
+ *   fp8:  round to nearest even, saturating: finite values beyond the largest
+ *         finite one and infinities become the largest finite value with the
+ *         input's sign (Triton's conversion for float8 stores on NVIDIA GPUs is
+ *         cvt.rn.satfinite); NaN becomes sign | 0x7F.
+ * Pinned: every fp8 code decodes as torch's float8 types do; in-range
+ * encodings equal torch's conversions (which round to nearest even); the
+ * saturation and the 20-bit rounding by closed forms (exact unbiasedness over
+ * all 2^20 random words) in tests/test_oracle_fp8.py.  The NaN and overflow
+ * results of the reference are not pinned (Triton is not runnable here). */
+enum { HO_F8E4M3 = 3, HO_F8E5M2 = 4 };
+
+static int f8_mant(int fmt) { return fmt == HO_F8E4M3 ? 3 : 2; }
+static int f8_bias(int fmt) { return fmt == HO_F8E4M3 ? 7 : 15; }
+static uint32_t f8_maxcode(int fmt) { return fmt == HO_F8E4M3 ? 0x7Eu : 0x7Bu; }
+
+/* OCP E4M3 ("fn": bias 7, no infinities, S.1111.111 NaN) or E5M2 (bias 15,
+ * IEEE infinities and NaNs) -> fp32, exact. */
+float ho_f8_to_f32(uint8_t c, int fmt) {
+    const int M = f8_mant(fmt), bias = f8_bias(fmt);
+    const uint32_t s = (uint32_t)(c & 0x80u) << 24;
+    const uint32_t e = (c & 0x7Fu) >> M, m = c & ((1u << M) - 1u);
+    if (fmt == HO_F8E4M3 && (c & 0x7Fu) == 0x7Fu) return u2f(s | 0x7FC00000u);
+    if (fmt == HO_F8E5M2 && e == 31u) return u2f(s | 0x7F800000u | (m ? 0x400000u : 0u));
+    float v = e == 0 ? ldexpf((float)m, 1 - bias - M) : ldexpf((float)((1u << M) | m), (int)e - bias - M);
+    return s ? -v : v;
+}
+
+uint8_t ho_f32_to_f8(float f, int fmt) {
+    const int M = f8_mant(fmt), bias = f8_bias(fmt), emin = 1 - bias;
+    const uint32_t maxcode = f8_maxcode(fmt);
+    const uint32_t u = f2u(f), s = (u >> 24) & 0x80u, a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint8_t)(s | 0x7Fu);
+    if (a == 0x7F800000u) return (uint8_t)(s | maxcode);
+    if (a < (uint32_t)(emin + 127) << 23) {
+        /* below the smallest normal: an integer count of the smallest subnormal,
+         * rounded to nearest even (2^M is the smallest normal's code) */
+        const float q = rintf(ldexpf(u2f(a), M - emin));
+        return (uint8_t)(s | (uint32_t)q);
+    }
+    const int rb = 23 - M;
+    uint32_t code = ((a + ((1u << (rb - 1)) - 1u) + ((a >> rb) & 1u)) >> rb) -
+                    ((uint32_t)(127 - bias) << M);
+    if (code > maxcode) code = maxcode;
+    return (uint8_t)(s | code);
+}
+
+/* stochastic_rounding_to_fp8 (sr_triton.py:18-25): add the low 20 random bits
+ * to the fp32 pattern (32-bit wrap), clear the low 20 bits, convert.  NaN
+ * inputs give NaN (not pinned, as for bf16). */
+uint8_t ho_sr_e4m3(float x, uint32_t r) {
+    uint32_t u = f2u(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint8_t)(((u >> 24) & 0x80u) | 0x7Fu);
+    u = (u + (r & 0xFFFFFu)) & 0xFFF00000u;
+    return ho_f32_to_f8(u2f(u), HO_F8E4M3);
+}
+
+/* stochastic_rounding(x, output, seed) for an output of dtype out_dtype
+ * (HO_BF16, HO_F16, HO_F8E4M3, HO_F8E5M2): 2-byte or 1-byte codes. */
+void ho_sr_round(const float* x, void* out, int out_dtype, int64_t n, uint64_t seed,
+                 uint64_t offset0) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const uint32_t r = ho_randint(seed, offset0 + (uint64_t)i);
+        if (out_dtype == HO_F8E4M3) {
+            ((uint8_t*)out)[i] = ho_sr_e4m3(x[i], r);
+            continue;
+        }
+        const uint16_t b = ho_sr_bf16(x[i], r);
+        if (out_dtype == HO_F8E5M2)
+            ((uint8_t*)out)[i] = ho_f32_to_f8(ho_bf16_to_f32(b), HO_F8E5M2);
+        else if (out_dtype == HO_F16)
+            ((uint16_t*)out)[i] = ho_f32_to_f16_rne(ho_bf16_to_f32(b));
+        else
+            ((uint16_t*)out)[i] = b;
+    }
+}
+
+/* _sgd_m_wd_sr on fp8 weights (w_fmt HO_F8E4M3 / HO_F8E5M2): loaded exactly,
+ * updated as ho_sgd_sr_step, the bf16 result stored as fp8. */
+void ho_sgd_sr_step_f8w(uint8_t* w, int w_fmt, const void* g, int g_dtype, float* m, int64_t n,
+                        float lr, float wd, float mu, int use_mom, int do_sr, uint64_t seed,
+                        uint64_t offset0) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float wf = ho_f8_to_f32(w[i], w_fmt);
+        float gf = load_any(g, g_dtype, i);
+        gf = fmaf(wd, wf, gf);
+        float upd = gf;
+        if (use_mom) {
+            float mv = fmaf(mu, m[i], gf);
+            m[i] = mv;
+            upd = mv;
+        }
+        float nw = fmaf(-lr, upd, wf);
+        uint16_t b = do_sr ? ho_sr_bf16(nw, ho_randint(seed, offset0 + (uint64_t)i))
+                           : ho_f32_to_bf16_rne(nw);
+        w[i] = ho_f32_to_f8(ho_bf16_to_f32(b), w_fmt);
+    }
+}
+
+void ho_f8_to_f32_arr(const uint8_t* c, int fmt, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ho_f8_to_f32(c[i], fmt);
+}
+
+void ho_f32_to_f8_arr(const float* x, int fmt, uint8_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ho_f32_to_f8(x[i], fmt);
+}
+
+/* SR to e4m3 of one value under each of n random words (for closed-form checks). */
+void ho_sr_e4m3_words(float x, const uint32_t* r, uint8_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ho_sr_e4m3(x, r[i]);
+}
+
 void ho_f32_to_f16_rne_arr(const float* x, uint16_t* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) out[i] = ho_f32_to_f16_rne(x[i]);
 }

@@ -236,3 +236,18 @@ def test_bwd_features_set_build():
     assert L.haste_ffi_bwd_features_set_build(2) == 1
     assert L.haste_ffi_bwd_features_set_build(3) == 2
     assert L.haste_ffi_bwd_features_set_build(prev) == 3
+
+
+def test_sr_round_and_f8_sgd_reject_bad_arguments():
+    """Checked before any HIP call: output / weight dtypes outside the supported
+    ones, negative sizes, null pointers."""
+    L = _lib.lib()
+    E = _lib.HASTE_ERR_INVALID_ARG
+    assert L.haste_sr_round(None, None, _lib.DTYPE_F32, 10, 1, 0, None) == E
+    assert L.haste_sr_round(None, None, _lib.DTYPE_F16, -1, 1, 0, None) == E
+    assert L.haste_sr_round(None, None, _lib.DTYPE_F8E4M3, 10, 1, 0, None) == E
+    assert L.haste_sr_round(None, None, _lib.DTYPE_F8E5M2, 0, 1, 0, None) == 0
+    args = (0.1, 0.0, 0.0, 0, 1, 5, 0, None)
+    assert L.haste_sgd_sr_step_f8(None, _lib.DTYPE_BF16, None, _lib.DTYPE_F32, None, 10, *args) == E
+    assert L.haste_sgd_sr_step_f8(None, _lib.DTYPE_F8E4M3, None, _lib.DTYPE_F32, None, 10, *args) == E
+    assert L.haste_sgd_sr_step_f8(None, _lib.DTYPE_F8E5M2, None, _lib.DTYPE_F32, None, 0, *args) == 0
