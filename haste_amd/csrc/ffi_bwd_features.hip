@@ -291,6 +291,111 @@ __global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __rest
     }
 }
 
+// haste_sgd_sr_step_wt: the SGD step of GatherSgd on W, then W^T of the updated
+// weights as bwdf_gather_kernel writes it.  A workgroup takes kWtLabels labels
+// (W rows) of one group: it updates those rows, stages them in LDS and writes
+// their two 16-byte chunks of every W^T row of the group's tiles (the tiles are
+// chunk-major, so a label block's chunks are contiguous runs of 512 bytes).
+// Small workgroups keep the tail of the grid short and the occupancy high; the
+// work is the Philox arithmetic of the SR words.  Rows >= O read as zeros
+// through the buffer resources and are never written.
+constexpr int kWtLabels = 16;
+constexpr int kWtBatch = 2;  // chunks of 8 weights per thread (F <= 256)
+
+template <int G, int GD>
+__global__ __launch_bounds__(256) void sgd_wt_kernel(uint16_t* __restrict__ W,
+                                                     const int* __restrict__ tsrc,
+                                                     const int* __restrict__ perm,
+                                                     uint16_t* __restrict__ twt, int F, int64_t O,
+                                                     int Tcap, const int* __restrict__ meta,
+                                                     int ndr, GatherSgd sg) {
+    constexpr int NB = G / kWtLabels;  // workgroups per group
+    constexpr int GB = GD == HASTE_DTYPE_F32 ? 4 : 2;  // gradient bytes per element
+    __shared__ uint32_t s_w[kWtLabels * 129];  // kWtLabels rows of (F + 2) halves
+    __shared__ int s_perm[256];
+    const int64_t g = blockIdx.x / NB;
+    const int h = (int)(blockIdx.x % NB);
+    const int tid = threadIdx.x;
+    const int ldw = F / 2 + 1;
+    const int cpr = F / 8;  // chunks per row
+    const int64_t l0 = g * G + h * kWtLabels;
+    const int rows = (int)max<int64_t>(0, min<int64_t>(kWtLabels, O - l0));
+    const int nch = rows * cpr;
+    const int64_t e0 = l0 * F;
+    const rsrc_t rw = make_rsrc_u32(W + e0, (uint32_t)(rows * F * 2));
+    const rsrc_t rg = make_rsrc_u32(static_cast<const char*>(sg.g) + e0 * GB, (uint32_t)(rows * F * GB));
+    const rsrc_t rm = make_rsrc_u32(sg.use_mom ? sg.m + e0 : sg.m, sg.use_mom ? (uint32_t)(rows * F * 4) : 0u);
+    if (tid < F) s_perm[tid] = perm[g * F + tid];
+    u32x4 wv[kWtBatch], gv0[kWtBatch], gv1[kWtBatch];
+    f32x4 mv0[kWtBatch], mv1[kWtBatch];
+#pragma unroll
+    for (int b = 0; b < kWtBatch; ++b) {
+        const int it = b * 256 + tid;
+        const uint32_t c = (uint32_t)it;
+        wv[b] = buf_load16(rw, it < nch ? c * 16u : kOOB);
+        gv0[b] = buf_load16(rg, it < nch ? c * (8u * GB) : kOOB);
+        if constexpr (GB == 4) gv1[b] = buf_load16(rg, it < nch ? c * 32u + 16u : kOOB);
+        mv0[b] = __builtin_bit_cast(f32x4, buf_load16(rm, it < nch ? c * 32u : kOOB));
+        mv1[b] = __builtin_bit_cast(f32x4, buf_load16(rm, it < nch ? c * 32u + 16u : kOOB));
+    }
+#pragma unroll
+    for (int b = 0; b < kWtBatch; ++b) {
+        const int it = b * 256 + tid;
+        if (b * 256 >= kWtLabels * cpr) break;  // uniform: F <= 128 fills one pass
+        const int l = it / cpr, j0 = (it % cpr) * 8;
+        float gf[8];
+        if constexpr (GB == 4) {
+            const f32x4 a = __builtin_bit_cast(f32x4, gv0[b]), c = __builtin_bit_cast(f32x4, gv1[b]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { gf[k] = a[k]; gf[4 + k] = c[k]; }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t lo = gv0[b][q] & 0xFFFFu, hi = gv0[b][q] >> 16;
+                gf[2 * q] = GD == HASTE_DTYPE_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                gf[2 * q + 1] = GD == HASTE_DTYPE_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+            }
+        }
+        float mv[8] = {mv0[b][0], mv0[b][1], mv0[b][2], mv0[b][3],
+                       mv1[b][0], mv1[b][1], mv1[b][2], mv1[b][3]};
+        const int64_t e = e0 + (int64_t)it * 8;
+        uint32_t ob[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t w16 = (k & 1) ? (wv[b][k >> 1] >> 16) : (wv[b][k >> 1] & 0xFFFFu);
+            ob[k] = sgd_one(bf16_bits_to_f32(w16), gf[k], &mv[k], sg.use_mom, sg.lr, sg.wd, sg.mu,
+                            sg.do_sr, (uint64_t)(e + k), sg.k0, sg.k1);
+        }
+        const u32x4 v = u32x4{ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16), ob[4] | (ob[5] << 16),
+                              ob[6] | (ob[7] << 16)};
+        buf_store16(v, rw, it < nch ? (uint32_t)it * 16u : kOOB);
+        if (sg.use_mom) {
+            buf_store16(__builtin_bit_cast(u32x4, f32x4{mv[0], mv[1], mv[2], mv[3]}), rm,
+                        it < nch ? (uint32_t)it * 32u : kOOB);
+            buf_store16(__builtin_bit_cast(u32x4, f32x4{mv[4], mv[5], mv[6], mv[7]}), rm,
+                        it < nch ? (uint32_t)it * 32u + 16u : kOOB);
+        }
+        if (l < kWtLabels) {  // rows >= O stage zeros
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s_w[l * ldw + j0 / 2 + q] = it < nch ? v[q] : 0u;
+        }
+    }
+    const int nrows = meta[(g * ndr + ndr - 1) * kMetaStride + 1] * 16;
+    __syncthreads();
+    const int lb = h * kWtLabels;
+    auto wvf = [&](int l, int slot) -> uint32_t {
+        const uint32_t w2 = s_w[(l - lb) * ldw + (slot >> 1)];
+        return (slot & 1) ? (w2 >> 16) : (w2 & 0xFFFFu);
+    };
+    // per tile of 16 rows: chunk 2h of its rows, then chunk 2h + 1 (32 chunks, 512 bytes)
+    for (int it = tid; it < nrows * 2; it += 256) {
+        const int row = (it >> 5) * 16 + (it & 15);
+        const int lc = lb + ((it >> 4) & 1) * 8;
+        const u32x4 v = wt_chunk<BF16>(tsrc[(g * Tcap) * 16 + row], s_perm, wvf, lc);
+        *reinterpret_cast<u32x4*>(twt + twt_elem((g * Tcap) * 16 + row, lc, G)) = v;
+    }
+}
+
 // ------------------------------------------------------------- reduce ------
 // Both reduce kernels read the partials as 16-byte rows of 4 batch columns
 // (Bp is a multiple of 64, so every such read is in bounds and aligned).
@@ -539,18 +644,23 @@ extern "C" int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype,
     const int* meta = reinterpret_cast<const int*>(base + p.meta_off);
     uint16_t* twt = reinterpret_cast<uint16_t*>(base + p.twt_off);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)p.Gc);
-    switch (G) {
-#define HASTE_SGD_WT(GG)                                                                            \
-    case GG:                                                                                        \
-        haste::bwdf_gather_kernel<haste::BF16, GG, true><<<grid, dim3(256), 0, st>>>(               \
-            W, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, sg);                      \
-        break;
-        HASTE_SGD_WT(16)
-        HASTE_SGD_WT(32)
-        HASTE_SGD_WT(64)
-        HASTE_SGD_WT(128)
+    auto launch = [&](auto gc) {
+        constexpr int GG = decltype(gc)::value;
+        const dim3 grid((unsigned)(p.Gc * (GG / haste::kWtLabels)));
+#define HASTE_SGD_WT(GD)                                                                    \
+    haste::sgd_wt_kernel<GG, GD><<<grid, dim3(256), 0, st>>>(W, tsrc, perm, twt, (int)F, O, \
+                                                             (int)p.Tcap, meta, (int)p.ndr, \
+                                                             sg)
+        if (g_dtype == HASTE_DTYPE_F32) HASTE_SGD_WT(HASTE_DTYPE_F32);
+        else if (g_dtype == HASTE_DTYPE_BF16) HASTE_SGD_WT(HASTE_DTYPE_BF16);
+        else HASTE_SGD_WT(HASTE_DTYPE_F16);
 #undef HASTE_SGD_WT
+    };
+    switch (G) {
+    case 16: launch(std::integral_constant<int, 16>{}); break;
+    case 32: launch(std::integral_constant<int, 32>{}); break;
+    case 64: launch(std::integral_constant<int, 64>{}); break;
+    case 128: launch(std::integral_constant<int, 128>{}); break;
     default:
         haste::set_error("%s: unsupported group size %lld", fn, (long long)G);
         return HASTE_ERR_UNSUPPORTED;
