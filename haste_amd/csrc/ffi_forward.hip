@@ -52,7 +52,11 @@ struct FwdCfg {
     // G = 64, FP = 128 two waves share the labels (32 W registers each, twice
     // the LDS reads of the gathered rows), so that four workgroups fit a CU:
     // the 2049 groups of a 131K-label layer then run in two rounds, not three.
-    static constexpr int WM = (G == 64 && FP == 128) ? 2 : MTILES * KS <= 16 ? 1 : (MTILES * KS <= 32 ? 2 : 4);
+    // At G = 32, FP = 256 two label waves halve the W fragment loads (every
+    // wave of a label row loads all of its fragments): those loads were a third
+    // of the kernel's vector-memory instructions, whose address path bounds it.
+    static constexpr int WM = ((G == 64 && FP == 128) || (G == 32 && FP == 256)) ? 2
+                              : MTILES * KS <= 16 ? 1 : (MTILES * KS <= 32 ? 2 : 4);
     static constexpr int WN = 4 / WM;             // waves along the batch
     static constexpr int MT = MTILES / WM;        // label tiles per wave
     static constexpr int NT = (kBT / 16) / WN;    // 16-column batch tiles per wave
