@@ -40,7 +40,10 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The raw handle of torch's current stream on t's device (what
+    torch.cuda.current_stream(t.device).cuda_stream returns, without building a
+    Stream object: this runs several times per layer and step)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def require_device(t: torch.Tensor, name: str) -> None:

@@ -66,6 +66,9 @@ SIGNATURES = {
                                                        _I64, _I64, _I64, _I32, _I32, _P]),
     "haste_ffi_bwd_weights": (ctypes.c_int, [_P, _P, _I64, _P, _I64, _P, _I32, _P, _I32, _I64,
                                              _I64, _I64, _I64, _I64, _I32, _P]),
+    "haste_ffi_bwd_weights_dx": (ctypes.c_int, [_P, _P, _I64, _P, _I64, _P, _I32, _P, _I32, _P,
+                                                _U64, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                                _I32, _P]),
     "haste_ffi_bwd_weights_sgd": (ctypes.c_int, [_P, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I32,
                                                  _P, _I32, _F32, _F32, _F32, _I32, _I32, _U64,
                                                  _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32,

@@ -137,6 +137,9 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
     code = _C.dtype_code(W.dtype)
 
     grad_x = None
+    # bf16 layer with weight or bias gradients too: dX is finished by the
+    # weight-gradient launch (haste_ffi_bwd_weights_dx) instead of a reduce kernel
+    dx_in_w = need_x and dtype == torch.bfloat16 and (need_w or need_b)
     if need_x:
         ent = _bwdf_workspace(locs, B, D, F, O, gsize, W.dtype, stream)
         ws = ent.ws
@@ -146,7 +149,12 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
         ready = 0
         if ent.plan_valid(locs):
             ready = 2 if ent.wt_valid(W) else 1
-        if dtype == torch.bfloat16:
+        if dx_in_w:
+            grad_x = torch.empty(B, D, dtype=dtype, device=dev)
+            _lib.call("haste_ffi_bwd_features_partials", locs.data_ptr(), W.data_ptr(),
+                      dY.data_ptr(), lddy, ws.data_ptr(), ws.numel(), B, D, F, O, gsize, code,
+                      ready, stream)
+        elif dtype == torch.bfloat16:
             grad_x = torch.empty(B, D, dtype=dtype, device=dev)
             _lib.call("haste_ffi_bwd_features_sr", locs.data_ptr(), W.data_ptr(),
                       dY.data_ptr(), lddy, grad_x.data_ptr(), SR_SEED_GRAD_X, ws.data_ptr(),
@@ -177,9 +185,17 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
         else:  # bias only: the kernel still needs a dW target
             scratch = torch.empty(O, F, dtype=W.dtype, device=dev)
             dw_ptr, dw_code = scratch.data_ptr(), code
-        _lib.call("haste_ffi_bwd_weights", locs.data_ptr(), xT.data_ptr(), ldx, dY.data_ptr(),
-                  lddy, dw_ptr, dw_code, grad_b.data_ptr() if need_b else None,
-                  _C.dtype_code(bias_dtype) if need_b else 0, B, D, F, O, gsize, code, stream)
+        if dx_in_w:
+            _lib.call("haste_ffi_bwd_weights_dx", locs.data_ptr(), xT.data_ptr(), ldx,
+                      dY.data_ptr(), lddy, dw_ptr, dw_code, grad_b.data_ptr() if need_b else None,
+                      _C.dtype_code(bias_dtype) if need_b else 0, grad_x.data_ptr(),
+                      SR_SEED_GRAD_X, ws.data_ptr(), ws.numel(), B, D, F, O, gsize, code,
+                      stream)
+        else:
+            _lib.call("haste_ffi_bwd_weights", locs.data_ptr(), xT.data_ptr(), ldx,
+                      dY.data_ptr(), lddy, dw_ptr, dw_code, grad_b.data_ptr() if need_b else None,
+                      _C.dtype_code(bias_dtype) if need_b else 0, B, D, F, O, gsize, code,
+                      stream)
     return grad_x, grad_w, grad_b
 
 

@@ -10,8 +10,13 @@
 //
 // One workgroup per label group; the contraction runs over the whole batch.
 // MFMA orientation: M = fan-in slots, N = labels, K = batch.
-//  - A (slots x batch) comes straight from L2: for slot j a fragment is 8
-//    consecutive batch entries of row xT[idx[g, j]] (one 16-byte load).
+//  - A (slots x batch): the gathered rows xT[idx[g, j], chunk] are copied
+//    row-major into LDS (one 128-byte line per slot and 64-row chunk, eight
+//    lines per load instruction) and read back as fragments of 8 consecutive
+//    batch entries (ds_read_b128); loaded in MFMA fragment order instead, every
+//    instruction touches 16 lines, each half used.  At G = 128, and at G = 64
+//    with F = 128, a fragment comes straight from L2 (one 16-byte load of row
+//    xT[idx[g, j]]; see BwdWCfg::XS).
 //  - B (batch x labels) is dY[b, g*G:(g+1)*G], copied row-major into LDS in
 //    chunks of 64 batch rows (double-buffered, the chunk after next in flight
 //    in registers) and read back with ds_read_b64_tr_b16, which hands each lane
@@ -36,7 +41,8 @@ namespace haste {
 int check_ffi_shape(const char* fn, int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
                     int32_t dtype);
 
-// Parameters of the fused SGD epilogue (unused when SGD == false).  twt != NULL:
+// Parameters of the fused SGD epilogue (unused when SGD == false; rj is used in
+// either mode).  twt != NULL:
 // also write W^T of the updated weights into the bwd-features workspace
 // (tsrc / perm / meta of its plan, Tcap tile rows per group).
 struct SgdArgs {
@@ -78,11 +84,21 @@ struct BwdWCfg {
     static constexpr int PR0 = kStgBytes / (SP * 4) / 16 * 16;
     static constexpr int PR = PR0 < G ? PR0 : G;              // labels per epilogue pass
     static constexpr int YS_BYTES = 2 * kKC * RB;
+    // X^T staged through LDS: measured 487 -> 467 us at config 3 (G = 32,
+    // F = 256) and 212 -> 209 at config 2 (G = 64, F = 64); unchanged at config 1
+    // (G = 64, F = 128, whose four waves per SIMD leave 128 registers: the
+    // staging there spilled one), and 2132 -> 2164 at config 4 (G = 128).  Those
+    // two keep the fragment loads.
+    static constexpr bool XS = G <= 64 && !(G == 64 && FP == 128);
+    static constexpr int RBX = kKC * 2 + 16;                  // LDS bytes per staged X^T row
+    static constexpr int XS_BYTES = XS ? FP * RBX : 0;        // one chunk of the gathered rows
+    static constexpr int PPTX = FP * (kKC / 8) / kThreads;    // X^T pieces per thread
     static constexpr int STG_BYTES = PR * SP * 4;
-    static constexpr int LDS_BYTES = YS_BYTES > STG_BYTES ? YS_BYTES : STG_BYTES;
+    static constexpr int LDS_BYTES = YS_BYTES + XS_BYTES > STG_BYTES ? YS_BYTES + XS_BYTES : STG_BYTES;
     static constexpr int CPR = FP / 8;                        // 8-slot chunks per staged row
     static constexpr int WPT = (PR * CPR + kThreads - 1) / kThreads;  // chunks per thread, pass 0
     static_assert(PR >= 16 && G % PR == 0, "epilogue pass shape");
+    static_assert(PPTX >= 1 && FP * (kKC / 8) % kThreads == 0, "X^T pieces");
 };
 
 template <typename T>
@@ -122,21 +138,22 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     constexpr bool yshort = YS;
     using C = BwdWCfg<G, FP>;
     constexpr int MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SP = C::SP, PR = C::PR;
+    constexpr bool XS = C::XS;
+    constexpr int RBX = C::RBX, PPTX = XS ? C::PPTX : 1;
     __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
     __shared__ int s_perm[SGD ? FP : 1];
     __shared__ float s_bg[SGD ? G : 1];  // fused step: the bias gradient of the group
     char (*Ys)[kKC * RB] = reinterpret_cast<char (*)[kKC * RB]>(lds);
+    char* Xs = lds + C::YS_BYTES;
     float* stg = reinterpret_cast<float*>(lds);
 
     // the last group (partial when O % G != 0, the shortest workgroup) is
     // dispatched first: with Gc = 8k + 1 groups, XCD 0 holds one workgroup
     // more than the others, and it is then that one
     const int64_t Gc = (O + G - 1) / G;
-    if constexpr (SGD) {
-        if (blockIdx.x >= Gc) {
-            reduce_sr_tile(sg.rj, (int)(blockIdx.x - Gc), reinterpret_cast<float (*)[33]>(lds));
-            return;
-        }
+    if (blockIdx.x >= Gc) {  // the reduce job's tiles (sg.rj.ntiles > 0)
+        reduce_sr_tile(sg.rj, (int)(blockIdx.x - Gc), reinterpret_cast<float (*)[33]>(lds));
+        return;
     }
     const int64_t g = blockIdx.x == 0 ? Gc - 1 : (int64_t)blockIdx.x - 1;
     const int tid = threadIdx.x;
@@ -160,16 +177,29 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     const int nl = (int)std::min<int64_t>(G, O - l0);  // labels of this group
     const int nchunks = (B + kKC - 1) / kKC;
 
-    // A rows: this lane's slots (slots >= F, and inactive waves, read as zero)
+    // Gathered rows (indices outside [0, D) are clamped).  XS: piece tid + q*256
+    // of a chunk is slot tid/8 + 32q, batch entries xbc .. xbc+7 of the chunk;
+    // xrow = byte offset of the slot's row, kOOB for slots >= F.  Otherwise: the
+    // lane's A rows (slots >= F, and inactive waves, read as zero).
     const rsrc_t xr = make_rsrc(xT, (int64_t)D * ldx * 2);
-    int64_t xoff[MT];
-    bool jvalid[MT];
+    const int xbc = (tid % 8) * 8;
+    uint32_t xrow[PPTX];
+    int64_t xoff[XS ? 1 : MT];
+    bool jvalid[XS ? 1 : MT];
+    if constexpr (XS) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int j = (wm * MT + mt) * 16 + col;
-        jvalid[mt] = active && j < F;
-        const int d = jvalid[mt] ? min(max(idx[g * F + j], 0), D - 1) : 0;
-        xoff[mt] = (int64_t)d * ldx;
+        for (int q = 0; q < PPTX; ++q) {
+            const int j = tid / 8 + q * (kThreads / 8);
+            xrow[q] = j < F ? (uint32_t)((int64_t)min(max(idx[g * F + j], 0), D - 1) * ldx * 2) : kOOB;
+        }
+    } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int j = (wm * MT + mt) * 16 + col;
+            jvalid[mt] = active && j < F;
+            const int d = jvalid[mt] ? min(max(idx[g * F + j], 0), D - 1) : 0;
+            xoff[mt] = (int64_t)d * ldx;
+        }
     }
 
     // dY chunk c (rows c*64 ..) -> registers; rows >= B and labels >= O read as
@@ -224,8 +254,22 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
             }
         }
     };
-    // A fragments of chunk c: 8 consecutive batch entries of each slot row
-    // (entries >= B read as zero; a partial 8-entry piece is masked at use)
+    // XS: the X^T pieces of chunk c (entries >= B read as zero, those of a
+    // partial piece are masked when stashed)
+    auto fetch_x = [&](int c, u32x4 (&v)[PPTX]) {
+        const int b0 = c * kKC + xbc;
+#pragma unroll
+        for (int q = 0; q < PPTX; ++q)
+            v[q] = buf_load16(xr, xrow[q] != kOOB && b0 < B ? xrow[q] + (uint32_t)b0 * 2 : kOOB);
+    };
+    auto stash_x = [&](int c, const u32x4 (&v)[PPTX]) {
+        const int nv = B - (c * kKC + xbc);
+#pragma unroll
+        for (int q = 0; q < PPTX; ++q)
+            *reinterpret_cast<u32x4*>(&Xs[(tid / 8 + q * (kThreads / 8)) * RBX + xbc * 2]) = keep_first(v[q], nv);
+    };
+    // Otherwise: the A fragments of chunk c, 8 consecutive batch entries of each
+    // slot row (entries >= B read as zero; a partial 8-entry piece is masked at use)
     auto fetch_a = [&](int c, u32x4 (&a)[2][MT]) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -282,15 +326,22 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
 
     // Ping-pong register sets by chunk parity (the loop body is unrolled twice),
     // so no register copy waits on a load: dY pieces are fetched two chunks
-    // ahead, A fragments one chunk ahead.  Chunks past the end load nothing
-    // (every offset is out of range), so each body issues the same loads.
+    // ahead, A fragments one chunk ahead (XS: X^T pieces one chunk ahead, into
+    // the one LDS buffer once every wave has read it).  Chunks past the end load
+    // nothing (every offset is out of range), so each body issues the same loads.
     u32x4 yr[2][PPT];
-    u32x4 ar[2][2][MT];
+    u32x4 ar[XS ? 1 : 2][2][MT];
+    u32x4 xv[PPTX];
     fetch(0, yr[0]);
     fetch(1, yr[1]);
-    fetch_a(0, ar[0]);
+    if constexpr (XS) fetch_x(0, xv);
+    else fetch_a(0, ar[0]);
     stash(0, 0, yr[0]);
     fetch(2, yr[0]);
+    if constexpr (XS) {
+        stash_x(0, xv);
+        fetch_x(1, xv);
+    }
     __syncthreads();
 
     // lane's tr-read address inside a staged chunk: row 8*kq + 4*half + col/4,
@@ -298,14 +349,22 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     const int tr_off = (kq * 8 + col / 4) * RB + (col % 4) * 8;
     auto body = [&](int c, auto parity) {
         constexpr int P = decltype(parity)::value;
-        fetch_a(c + 1, ar[1 - P]);
+        if constexpr (!XS) fetch_a(c + 1, ar[1 - P]);
         if (active && c < nchunks) {
             const char* ys = Ys[P];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const int nv = B - (c * kKC + ks * 32 + kq * 8);
+                u32x4 af[MT];
+                if constexpr (XS) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) ar[P][ks][mt] = keep_first(ar[P][ks][mt], nv);
+                    for (int mt = 0; mt < MT; ++mt)
+                        af[mt] = *reinterpret_cast<const u32x4*>(
+                            &Xs[((wm * MT + mt) * 16 + col) * RBX + (ks * 32 + kq * 8) * 2]);
+                } else {
+                    const int nv = B - (c * kKC + ks * 32 + kq * 8);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) af[mt] = keep_first(ar[XS ? 0 : P][ks][mt], nv);
+                }
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     const char* p = ys + tr_off + ks * 32 * RB + (wn * NT + nt) * 32;
@@ -314,10 +373,15 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                     const u32x4 bf = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
-                        acc[mt][nt] = mfma16x16x32<T>(ar[P][ks][mt], bf, acc[mt][nt]);
+                        acc[mt][nt] = mfma16x16x32<T>(af[mt], bf, acc[mt][nt]);
                     if (do_bias && nt % C::WM == wm) accb[nt / C::WM] = mfma16x16x32<T>(ones, bf, accb[nt / C::WM]);
                 }
             }
+        }
+        if constexpr (XS) {
+            __syncthreads();  // every wave has read the X^T buffer
+            stash_x(c + 1, xv);
+            fetch_x(c + 2, xv);
         }
         stash(c + 1, 1 - P, yr[1 - P]);  // chunk c + 1 (zeros past the end)
         fetch(c + 3, yr[1 - P]);
@@ -500,13 +564,13 @@ int launch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* 
            void* dW, int dW_dtype, void* dbias, int dbias_dtype, int64_t B, int64_t D, int64_t F,
            int64_t O, const SgdArgs& sg, hipStream_t st) {
     const int64_t Gc = ceil_div(O, G);
-    if (Gc + (SGD ? sg.rj.ntiles : 0) > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes ||
+    if (Gc + sg.rj.ntiles > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes ||
         ((int64_t)kKC * lddy + 8) * 2 > kMaxRsrcBytes || (int64_t)G * F * 4 > kMaxRsrcBytes) {
         set_error("haste_ffi_bwd_weights: problem too large (Gc %lld, lddy %lld, D*ldx %lld)",
                   (long long)Gc, (long long)lddy, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
     }
-    ffi_bwd_w_kernel<T, G, FP, SGD, YNT, YS><<<dim3((unsigned)(Gc + (SGD ? sg.rj.ntiles : 0))), dim3(kThreads), 0, st>>>(
+    ffi_bwd_w_kernel<T, G, FP, SGD, YNT, YS><<<dim3((unsigned)(Gc + sg.rj.ntiles)), dim3(kThreads), 0, st>>>(
         idx, xT, ldx, dY, lddy, dW, dW_dtype, dbias, dbias_dtype, (int)B, (int)D, (int)F, O, sg);
     HASTE_CHECK_LAUNCH("haste_ffi_bwd_weights");
     return HASTE_OK;

@@ -70,6 +70,36 @@ extern "C" int haste_ffi_bwd_weights(const int32_t* idx, const void* xT, int64_t
                                              dbias_dtype, B, D, F, O, G, none, st);
 }
 
+extern "C" int haste_ffi_bwd_weights_dx(const int32_t* idx, const void* xT, int64_t ldx,
+                                        const void* dY, int64_t lddy, void* dW, int32_t dW_dtype,
+                                        void* dbias, int32_t dbias_dtype, uint16_t* dX,
+                                        uint64_t dx_seed, void* bwdf_workspace,
+                                        int64_t bwdf_workspace_bytes, int64_t B, int64_t D,
+                                        int64_t F, int64_t O, int64_t G, int32_t dtype,
+                                        void* stream) {
+    const char* fn = "haste_ffi_bwd_weights_dx";
+    int rc = haste::check_bwdw(fn, idx, xT, ldx, dY, lddy, dW_dtype, dbias, dbias_dtype, B, D, F,
+                               O, G, dtype);
+    if (rc != HASTE_OK) return rc;
+    HASTE_CHECK_ARG(dtype == HASTE_DTYPE_BF16, "%s: dX is bf16: the layer must be bf16", fn);
+    HASTE_CHECK_ARG(dW != nullptr && haste::aligned16(dW), "%s: dW must be a 16-byte aligned pointer", fn);
+    HASTE_CHECK_ARG(dX != nullptr && bwdf_workspace != nullptr,
+                    "%s: dX and the bwd-features workspace are required", fn);
+    const haste::BwdFPlan p = haste::make_plan(B, D, F, O, G);
+    HASTE_CHECK_ARG(haste::aligned16(bwdf_workspace) &&
+                        bwdf_workspace_bytes >= p.prep_bytes + p.ws_bytes,
+                    "%s: bwd-features workspace too small or misaligned (%lld bytes, need %lld)",
+                    fn, (long long)bwdf_workspace_bytes, (long long)(p.prep_bytes + p.ws_bytes));
+    haste::SgdArgs sg{};
+    sg.rj = haste::reduce_job(
+        p, reinterpret_cast<const float*>(static_cast<const char*>(bwdf_workspace) + p.prep_bytes),
+        dX, B, D, dx_seed);
+    return haste::dispatch<haste::BF16, false>(idx, static_cast<const uint16_t*>(xT), ldx,
+                                              static_cast<const uint16_t*>(dY), lddy, dW,
+                                              dW_dtype, dbias, dbias_dtype, B, D, F, O, G, sg,
+                                              static_cast<hipStream_t>(stream));
+}
+
 namespace haste {
 namespace {
 

@@ -158,11 +158,17 @@ __device__ __forceinline__ void fwd_group(const int32_t* __restrict__ idx,
             const int k = ks * 32 + kq * 8;
             wf[mt][ks] = buf_load16(wr, k < F ? (uint32_t)(lr * F + k) * 2 : kOOB);
         }
+        // labels past the group get the out-of-range offset rather than being
+        // left to the range check: loads at consecutive offsets may be merged
+        // into one wider load, which a label past the end would zero as a whole
         const int lb = (wm * MT + mt) * 16 + kq * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            bv[mt][i] = O32 ? __builtin_bit_cast(float, buf_load4(br, (uint32_t)(lb + i) * 4))
-                            : bits_to_f32<T>(__builtin_amdgcn_raw_buffer_load_b16(br, (lb + i) * 2, 0, 0));
+        for (int i = 0; i < 4; ++i) {
+            const bool in = lb + i < nl;
+            bv[mt][i] = O32 ? __builtin_bit_cast(float, buf_load4(br, in ? (uint32_t)(lb + i) * 4 : kOOB))
+                            : bits_to_f32<T>(__builtin_amdgcn_raw_buffer_load_b16(
+                                  br, in ? (lb + i) * 2 : (int)kOOB, 0, 0));
+        }
     }
 
     // chunks starting at or past B read as zero, columns >= B of a partial chunk

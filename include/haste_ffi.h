@@ -225,6 +225,25 @@ int haste_ffi_bwd_weights(const int32_t* idx, const void* xT, int64_t ldx, const
                           int64_t G, int32_t dtype, void* stream);
 
 /*
+ * haste_ffi_bwd_weights (bf16 layer) that also finishes the backward to
+ * features of the same grad_output: dX [B, D] bf16 = SR(sum of the partials
+ * that the last haste_ffi_bwd_features_partials call with this workspace and
+ * these sizes left in it, tl.randint(dx_seed, b*D + d)), bit-identical to
+ * haste_ffi_bwd_features_sr, in trailing workgroups of the same launch instead
+ * of a kernel of its own.  dX must not overlap the other buffers.  Replaces, for
+ * one FFI layer, the reference's backward of GroupFFIMulFunction
+ * (shared_ffi/bindings.py:33-54: ffi_backward_features_cuda + its bf16
+ * rounding, ffi_backward_weights_cuda, torch.sum(grad_output, 0)), as
+ * haste_ffi_bwd_features_partials + this call.
+ */
+int haste_ffi_bwd_weights_dx(const int32_t* idx, const void* xT, int64_t ldx, const void* dY,
+                             int64_t lddy, void* dW, int32_t dW_dtype, void* dbias,
+                             int32_t dbias_dtype, uint16_t* dX, uint64_t dx_seed,
+                             void* bwdf_workspace, int64_t bwdf_workspace_bytes, int64_t B,
+                             int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype,
+                             void* stream);
+
+/*
  * Backward to weights fused with the SR-SGD step on the bf16 weights and bias:
  * computes the fp32 gradients of haste_ffi_bwd_weights and applies to W [O, F]
  * and bias [O] (in place) the update of haste_sgd_sr_step with g = those fp32

@@ -165,6 +165,21 @@ def test_bwd_weights_sgd_dx_requires_dx_and_workspace():
     assert f(*dict(args, dtype=_lib.DTYPE_F16).values()) == _lib.HASTE_ERR_INVALID_ARG
 
 
+def test_bwd_weights_dx_requires_dx_workspace_and_bf16():
+    args = dict(idx=16, xT=16, ldx=64, dY=32, lddy=4096, dW=48, dW_dtype=_lib.DTYPE_F32,
+                dbias=None, dbias_dtype=0, dX=64, dx_seed=123, ws=256, ws_bytes=1 << 30, B=64,
+                D=768, F=32, O=4096, G=32, dtype=_lib.DTYPE_BF16, stream=None)
+    f = _lib.lib().haste_ffi_bwd_weights_dx
+    assert f(*dict(args, dX=None).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert "dX and the bwd-features workspace" in _lib.last_error()
+    assert f(*dict(args, ws=None).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert f(*dict(args, ws_bytes=16).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert "workspace too small" in _lib.last_error()
+    assert f(*dict(args, dW=None).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert f(*dict(args, dtype=_lib.DTYPE_F16).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert "must be bf16" in _lib.last_error()
+
+
 def test_ring_cases_reach_every_bwd_features_build():
     """tests/bwdf_cases.RING_CASES maps onto every (G, BT, RT) build of the
     bwd-features main kernel, each with more than one feature range, so the GPU

@@ -207,3 +207,46 @@ def test_weight_update_finishes_dx(dev, B, D, O, G, F, has_bias, use_mom, ys):
               dX_rb.data_ptr(), 124, ws.data_ptr(), ws.numel(), B, D, F, O, G, code, 0, st)
     torch.cuda.synchronize()
     assert np.array_equal(bits(dX_rb), b[5])
+
+
+@pytest.mark.parametrize("B,D,O,G,F,has_bias,use_mom,ys", DX_CASES)
+def test_weight_gradient_finishes_dx(dev, B, D, O, G, F, has_bias, use_mom, ys):
+    """haste_ffi_bwd_features_partials + haste_ffi_bwd_weights_dx (the drop-in
+    backward: the final bwd-features pass as trailing workgroups of the weight
+    gradient) give dX, dW and dbias bit-identical to haste_ffi_bwd_features_sr +
+    haste_ffi_bwd_weights, for bf16 and fp32 gradient outputs."""
+    x, W, bias, idx, dY, lddy, _, _ = setup(B, D, O, G, F, seed=5 * O + F)
+    if ys:
+        dY, lddy = dY[:, :O].contiguous(), O
+    xT, ldx = _C.padded_transpose(x.to(dev))
+    idx_d, dY_d, W_d = idx.to(dev), dY.to(dev), W.to(dev)
+    st = _C.stream_of(dY_d)
+    code = _lib.DTYPE_BF16
+    for gdt, gcode in ((torch.bfloat16, _lib.DTYPE_BF16), (torch.float32, _lib.DTYPE_F32)):
+        out = {}
+        for mode in ("separate", "merged"):
+            ws = _C.bwd_features_workspace(B, D, F, O, G, torch.bfloat16, dev)
+            dX = torch.full((B, D), 3.0, dtype=torch.bfloat16, device=dev)
+            dW = torch.full((O, F), 5.0, dtype=gdt, device=dev)
+            db = torch.full((O,), 5.0, dtype=gdt, device=dev)
+            dbp = db.data_ptr() if has_bias else None
+            if mode == "separate":
+                _lib.call("haste_ffi_bwd_features_sr", idx_d.data_ptr(), W_d.data_ptr(),
+                          dY_d.data_ptr(), lddy, dX.data_ptr(), 123, ws.data_ptr(), ws.numel(),
+                          B, D, F, O, G, code, 0, st)
+                _lib.call("haste_ffi_bwd_weights", idx_d.data_ptr(), xT.data_ptr(), ldx,
+                          dY_d.data_ptr(), lddy, dW.data_ptr(), gcode, dbp, gcode, B, D, F, O, G,
+                          code, st)
+            else:
+                _lib.call("haste_ffi_bwd_features_partials", idx_d.data_ptr(), W_d.data_ptr(),
+                          dY_d.data_ptr(), lddy, ws.data_ptr(), ws.numel(), B, D, F, O, G, code,
+                          0, st)
+                _lib.call("haste_ffi_bwd_weights_dx", idx_d.data_ptr(), xT.data_ptr(), ldx,
+                          dY_d.data_ptr(), lddy, dW.data_ptr(), gcode, dbp, gcode,
+                          dX.data_ptr(), 123, ws.data_ptr(), ws.numel(), B, D, F, O, G, code, st)
+            torch.cuda.synchronize()
+            out[mode] = (bits(dX), dW.cpu(), db.cpu())
+        a, b = out["separate"], out["merged"]
+        assert np.array_equal(b[0], a[0]), "dX of the merged launch differs"
+        assert torch.equal(b[1], a[1]) and torch.equal(b[2], a[2]), "dW / dbias differ"
+        assert not np.array_equal(a[0], bits(torch.full((B, D), 3.0, dtype=torch.bfloat16)))

@@ -78,6 +78,23 @@ def test_forward(dev, B, D, O, G, F, mode):
     torch.testing.assert_close(out_nb.float().cpu(), oracle.ffi_forward(idx, x.t().contiguous(), W, None, G), **TOL16)
 
 
+@pytest.mark.parametrize("O,G", [(1027, 32), (1034, 32), (4133, 32), (2000, 64)])
+def test_forward_bias_alignment_and_last_group(dev, O, G):
+    """The bias is loaded four labels at a time where it is 8-byte aligned and
+    label by label where it is not, and in the last group (3, 10 and 5 labels at
+    O = 1027, 1034, 4133): every way gives the same logits, bit for bit."""
+    B, D, F = 48, 256, 64
+    x, W, bias, idx, _ = make_case(B, D, O, G, F, idx_mode="random", seed=5)
+    out = gpu_forward(x, W, bias, idx, G, dev)
+    torch.testing.assert_close(out.float().cpu(), oracle.ffi_forward(idx, x.t().contiguous(), W, bias, G),
+                               **TOL16)
+    big = torch.zeros(O + 1, dtype=bias.dtype, device=dev)
+    big[1:] = bias.to(dev)
+    xT = x.t().contiguous().to(dev)
+    out_u = _C.ffi_forward_cuda(idx.to(dev), xT, W.to(dev), big[1:], B, D, F, O, G)
+    assert torch.equal(out_u.cpu(), out.cpu())
+
+
 def test_forward_f16(dev):
     x, W, bias, idx, _ = make_case(64, 768, 4133, 32, 64, dtype=torch.float16)
     out = gpu_forward(x, W, bias, idx, 32, dev)

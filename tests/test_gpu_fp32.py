@@ -23,7 +23,7 @@ TOL32 = dict(rtol=1e-5, atol=1e-5)
 TOL32_DX = dict(rtol=1e-4, atol=1e-5)
 
 CASES = [(64, 768, 4096, 32, 32), (128, 768, 8193, 64, 128), (37, 200, 513, 16, 64),
-         (70, 300, 1000, 128, 128), (20, 512, 777, 16, 256)]
+         (70, 300, 1000, 128, 128), (20, 512, 777, 16, 256), (24, 256, 1034, 32, 64)]
 
 
 def _inputs(B, D, O, G, F, seed):

@@ -83,6 +83,25 @@ def test_momentum_buffers_always_in_state():
         assert "momentum_buf" in loaded["state"][i]
 
 
+def test_zero_grad_matches_torch_optimizer():
+    """SRSgd.zero_grad does what torch.optim.Optimizer.zero_grad does: grads set
+    to None by default, or detached and zeroed in place with set_to_none=False."""
+    for set_to_none in (True, False):
+        ps = [torch.nn.Parameter(torch.randn(3, 4)), torch.nn.Parameter(torch.randn(5))]
+        qs = [torch.nn.Parameter(p.detach().clone()) for p in ps]
+        for a, b in zip(ps, qs):
+            a.grad = torch.randn_like(a)
+            b.grad = a.grad.clone()
+        qs[1].grad = None
+        ps[1].grad = None
+        SRSgd(ps, lr=0.1).zero_grad(set_to_none=set_to_none)
+        torch.optim.SGD(qs, lr=0.1).zero_grad(set_to_none=set_to_none)
+        for a, b in zip(ps, qs):
+            assert (a.grad is None) == (b.grad is None)
+            if a.grad is not None:
+                assert torch.equal(a.grad, b.grad) and not a.grad.requires_grad
+
+
 @pytest.mark.gpu
 def test_resume_is_bit_identical(dev):
     """Train, checkpoint layer + optimizer, keep training; a fresh layer and
