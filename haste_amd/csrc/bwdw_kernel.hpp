@@ -65,11 +65,13 @@ struct SgdArgs {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kKC = 64;               // batch rows per LDS stage
 constexpr int kStgBytes = 34 * 1024;  // LDS for one pass of the staged gradient tile
 
 template <int G, int FP>
 struct BwdWCfg {
+    // batch rows per LDS stage: 32 at G = 32, F = 256, whose smaller stages then
+    // fit four workgroups per CU (LDS and registers), else 64
+    static constexpr int KC = (G == 32 && FP == 256) ? 32 : 64;
     static constexpr int MTILES = FP / 16;                    // slot tiles
     static constexpr int NTILES = G / 16;                     // label tiles
     static constexpr int WM = MTILES < 4 ? MTILES : 4;        // waves along slots
@@ -78,27 +80,27 @@ struct BwdWCfg {
     static constexpr int MT = MTILES / WM;
     static constexpr int NT = NTILES / WN;
     static constexpr int RB = 2 * G + 16;                     // LDS bytes per staged dY row
-    static constexpr int PIECES = kKC * G / 8;                // 16-byte pieces per chunk
+    static constexpr int PIECES = KC * G / 8;                // 16-byte pieces per chunk
     static constexpr int PPT = (PIECES + kThreads - 1) / kThreads;
     static constexpr int SP = FP + 4;                         // staged gradient row (floats)
     static constexpr int PR0 = kStgBytes / (SP * 4) / 16 * 16;
     static constexpr int PR = PR0 < G ? PR0 : G;              // labels per epilogue pass
-    static constexpr int YS_BYTES = 2 * kKC * RB;
+    static constexpr int YS_BYTES = 2 * KC * RB;
     // X^T staged through LDS: measured 487 -> 467 us at config 3 (G = 32,
     // F = 256) and 212 -> 209 at config 2 (G = 64, F = 64); unchanged at config 1
     // (G = 64, F = 128, whose four waves per SIMD leave 128 registers: the
     // staging there spilled one), and 2132 -> 2164 at config 4 (G = 128).  Those
     // two keep the fragment loads.
     static constexpr bool XS = G <= 64 && !(G == 64 && FP == 128);
-    static constexpr int RBX = kKC * 2 + 16;                  // LDS bytes per staged X^T row
+    static constexpr int RBX = KC * 2 + 16;                  // LDS bytes per staged X^T row
     static constexpr int XS_BYTES = XS ? FP * RBX : 0;        // one chunk of the gathered rows
-    static constexpr int PPTX = FP * (kKC / 8) / kThreads;    // X^T pieces per thread
+    static constexpr int PPTX = FP * (KC / 8) / kThreads;    // X^T pieces per thread
     static constexpr int STG_BYTES = PR * SP * 4;
     static constexpr int LDS_BYTES = YS_BYTES + XS_BYTES > STG_BYTES ? YS_BYTES + XS_BYTES : STG_BYTES;
     static constexpr int CPR = FP / 8;                        // 8-slot chunks per staged row
     static constexpr int WPT = (PR * CPR + kThreads - 1) / kThreads;  // chunks per thread, pass 0
     static_assert(PR >= 16 && G % PR == 0, "epilogue pass shape");
-    static_assert(PPTX >= 1 && FP * (kKC / 8) % kThreads == 0, "X^T pieces");
+    static_assert(PPTX >= 1 && FP * (KC / 8) % kThreads == 0, "X^T pieces");
 };
 
 template <typename T>
@@ -123,7 +125,9 @@ __device__ __forceinline__ u32x4 keep_first(u32x4 v, int nv) {
 // the 2049 groups of a 131K-label layer run in two rounds of 1024, not three
 // of 768.
 template <int G, int FP>
-constexpr int bwdw_waves_per_simd() { return G == 64 && FP == 128 ? 4 : G * FP >= 128 * 256 ? 1 : 2; }
+constexpr int bwdw_waves_per_simd() {
+    return (G == 64 && FP == 128) || (G == 32 && FP == 256) ? 4 : G * FP >= 128 * 256 ? 1 : 2;
+}
 
 // dY larger than the last-level cache (kMallBytes): this kernel, its last
 // reader in a training step, streams it with non-temporal loads (YNT), so it
@@ -139,11 +143,11 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     using C = BwdWCfg<G, FP>;
     constexpr int MT = C::MT, NT = C::NT, RB = C::RB, PPT = C::PPT, SP = C::SP, PR = C::PR;
     constexpr bool XS = C::XS;
-    constexpr int RBX = C::RBX, PPTX = XS ? C::PPTX : 1;
+    constexpr int RBX = C::RBX, PPTX = XS ? C::PPTX : 1, KC = C::KC, KSC = KC / 32;
     __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
     __shared__ int s_perm[SGD ? FP : 1];
     __shared__ float s_bg[SGD ? G : 1];  // fused step: the bias gradient of the group
-    char (*Ys)[kKC * RB] = reinterpret_cast<char (*)[kKC * RB]>(lds);
+    char (*Ys)[KC * RB] = reinterpret_cast<char (*)[KC * RB]>(lds);
     char* Xs = lds + C::YS_BYTES;
     float* stg = reinterpret_cast<float*>(lds);
 
@@ -175,21 +179,23 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     const int col = lane & 15, kq = lane >> 4;
     const int64_t l0 = g * G;
     const int nl = (int)std::min<int64_t>(G, O - l0);  // labels of this group
-    const int nchunks = (B + kKC - 1) / kKC;
+    const int nchunks = (B + KC - 1) / KC;
 
-    // Gathered rows (indices outside [0, D) are clamped).  XS: piece tid + q*256
-    // of a chunk is slot tid/8 + 32q, batch entries xbc .. xbc+7 of the chunk;
-    // xrow = byte offset of the slot's row, kOOB for slots >= F.  Otherwise: the
-    // lane's A rows (slots >= F, and inactive waves, read as zero).
+    // Gathered rows (indices outside [0, D) are clamped).  XS: a chunk row is
+    // XPR pieces of 8 batch entries; piece tid + q*256 of a chunk is slot
+    // tid/XPR + q*256/XPR, batch entries xbc .. xbc+7 of the chunk; xrow = byte
+    // offset of the slot's row, kOOB for slots >= F.  Otherwise: the lane's A
+    // rows (slots >= F, and inactive waves, read as zero).
+    constexpr int XPR = KC / 8;
     const rsrc_t xr = make_rsrc(xT, (int64_t)D * ldx * 2);
-    const int xbc = (tid % 8) * 8;
+    const int xbc = (tid % XPR) * 8;
     uint32_t xrow[PPTX];
     int64_t xoff[XS ? 1 : MT];
     bool jvalid[XS ? 1 : MT];
     if constexpr (XS) {
 #pragma unroll
         for (int q = 0; q < PPTX; ++q) {
-            const int j = tid / 8 + q * (kThreads / 8);
+            const int j = tid / XPR + q * (kThreads / XPR);
             xrow[q] = j < F ? (uint32_t)((int64_t)min(max(idx[g * F + j], 0), D - 1) * ldx * 2) : kOOB;
         }
     } else {
@@ -222,16 +228,16 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
 #pragma unroll
     for (int q = 0; q < PPT; ++q) {
         const int over = pcc[q] + 8 - nl;  // > 0 only in the last group
-        sh_last[q] = (yshort && over > 0 && over < 8 && pr[q] == (B - 1) % kKC) ? over : 0;
+        sh_last[q] = (yshort && over > 0 && over < 8 && pr[q] == (B - 1) % KC) ? over : 0;
     }
-    const int c_last = (B - 1) / kKC;
+    const int c_last = (B - 1) / KC;
     auto tail_shift = [&](int c, int q) -> int { return c == c_last ? sh_last[q] : 0; };
     // (the resource starts up to 8 labels before l0, so that an early load of the
     // last group stays inside it: l0 + pcc - sh >= O - 8 >= 0)
     const int pre = yshort ? (int)std::min<int64_t>(l0, 8) : 0;
     auto fetch = [&](int c, u32x4 (&v)[PPT]) {
-        const int b0 = c * kKC;
-        const int rows = std::min(kKC, B - b0);
+        const int b0 = c * KC;
+        const int rows = std::min(KC, B - b0);
         const int lend = pre + ((yshort && b0 + rows == B) ? nl : (nl + 7) / 8 * 8);
         const rsrc_t yr = make_rsrc(dY + (int64_t)b0 * lddy + l0 - pre,
                                     ((int64_t)(rows - 1) * lddy + lend) * 2);
@@ -257,23 +263,24 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     // XS: the X^T pieces of chunk c (entries >= B read as zero, those of a
     // partial piece are masked when stashed)
     auto fetch_x = [&](int c, u32x4 (&v)[PPTX]) {
-        const int b0 = c * kKC + xbc;
+        const int b0 = c * KC + xbc;
 #pragma unroll
         for (int q = 0; q < PPTX; ++q)
             v[q] = buf_load16(xr, xrow[q] != kOOB && b0 < B ? xrow[q] + (uint32_t)b0 * 2 : kOOB);
     };
     auto stash_x = [&](int c, const u32x4 (&v)[PPTX]) {
-        const int nv = B - (c * kKC + xbc);
+        const int nv = B - (c * KC + xbc);
 #pragma unroll
         for (int q = 0; q < PPTX; ++q)
-            *reinterpret_cast<u32x4*>(&Xs[(tid / 8 + q * (kThreads / 8)) * RBX + xbc * 2]) = keep_first(v[q], nv);
+            *reinterpret_cast<u32x4*>(&Xs[(tid / XPR + q * (kThreads / XPR)) * RBX + xbc * 2]) =
+                keep_first(v[q], nv);
     };
     // Otherwise: the A fragments of chunk c, 8 consecutive batch entries of each
     // slot row (entries >= B read as zero; a partial 8-entry piece is masked at use)
-    auto fetch_a = [&](int c, u32x4 (&a)[2][MT]) {
+    auto fetch_a = [&](int c, u32x4 (&a)[KSC][MT]) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int bk = c * kKC + ks * 32 + kq * 8;
+        for (int ks = 0; ks < KSC; ++ks) {
+            const int bk = c * KC + ks * 32 + kq * 8;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
                 a[ks][mt] = buf_load16(xr, jvalid[mt] && bk < B ? (uint32_t)(xoff[mt] + bk) * 2 : kOOB);
@@ -330,7 +337,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
     // the one LDS buffer once every wave has read it).  Chunks past the end load
     // nothing (every offset is out of range), so each body issues the same loads.
     u32x4 yr[2][PPT];
-    u32x4 ar[XS ? 1 : 2][2][MT];
+    u32x4 ar[XS ? 1 : 2][KSC][MT];
     u32x4 xv[PPTX];
     fetch(0, yr[0]);
     fetch(1, yr[1]);
@@ -353,7 +360,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
         if (active && c < nchunks) {
             const char* ys = Ys[P];
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
+            for (int ks = 0; ks < KSC; ++ks) {
                 u32x4 af[MT];
                 if constexpr (XS) {
 #pragma unroll
@@ -361,7 +368,7 @@ __global__ __launch_bounds__(kThreads, (bwdw_waves_per_simd<G, FP>())) void ffi_
                         af[mt] = *reinterpret_cast<const u32x4*>(
                             &Xs[((wm * MT + mt) * 16 + col) * RBX + (ks * 32 + kq * 8) * 2]);
                 } else {
-                    const int nv = B - (c * kKC + ks * 32 + kq * 8);
+                    const int nv = B - (c * KC + ks * 32 + kq * 8);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) af[mt] = keep_first(ar[XS ? 0 : P][ks][mt], nv);
                 }
@@ -565,7 +572,7 @@ int launch(const int32_t* idx, const uint16_t* xT, int64_t ldx, const uint16_t* 
            int64_t O, const SgdArgs& sg, hipStream_t st) {
     const int64_t Gc = ceil_div(O, G);
     if (Gc + sg.rj.ntiles > 0x7FFFFFFF || D * ldx * 2 > kMaxRsrcBytes ||
-        ((int64_t)kKC * lddy + 8) * 2 > kMaxRsrcBytes || (int64_t)G * F * 4 > kMaxRsrcBytes) {
+        ((int64_t)BwdWCfg<G, FP>::KC * lddy + 8) * 2 > kMaxRsrcBytes || (int64_t)G * F * 4 > kMaxRsrcBytes) {
         set_error("haste_ffi_bwd_weights: problem too large (Gc %lld, lddy %lld, D*ldx %lld)",
                   (long long)Gc, (long long)lddy, (long long)(D * ldx));
         return HASTE_ERR_UNSUPPORTED;
