@@ -28,6 +28,7 @@ CASES = [
     (70, 768, 2000, 128, 96, True, True, True),      # G = 128, F < 128 slots, momentum
     (33, 200, 700, 128, 256, True, False, True),     # G = 128, F = 256 (several epilogue passes)
     (64, 4096, 3000, 32, 256, True, True, True),     # wide input, F = 256
+    (37, 512, 999, 32, 240, True, False, True),      # 32-row chunks: a partial chunk, F < 256 slots
 ]
 
 
@@ -144,6 +145,7 @@ DX_CASES = [
     (130, 768, 3001, 128, 128, True, True, True),    # G = 128, momentum
     (33, 200, 700, 128, 256, True, False, False),    # F = 256, one batch tile of 33 rows
     (72, 500, 3001, 32, 64, True, False, True),      # several feature ranges and slices
+    (37, 512, 999, 32, 240, True, False, True),      # 32-row weight-gradient chunks, F < 256
 ]
 
 
