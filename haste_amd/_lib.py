@@ -82,6 +82,9 @@ SIGNATURES = {
                                                              _I64, _I64, _I64, _I32, _P]),
     "haste_sgd_sr_step_wt": (ctypes.c_int, [_P, _P, _I32, _P, _F32, _F32, _F32, _I32, _I32, _U64,
                                             _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
+    "haste_sgd_sr_step_wt_bias": (ctypes.c_int, [_P, _P, _I32, _P, _P, _P, _I32, _P, _F32, _F32,
+                                                 _F32, _I32, _I32, _U64, _P, _I64, _I64, _I64,
+                                                 _I64, _I64, _I64, _I32, _P]),
     "haste_sr_round_bf16": (ctypes.c_int, [_P, _P, _I64, _U64, _U64, _P]),
     "haste_sr_round": (ctypes.c_int, [_P, _P, _I32, _I64, _U64, _U64, _P]),
     "haste_sgd_sr_step_f8": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _I64, _F32, _F32, _F32,

@@ -46,7 +46,7 @@ def _grad_dtype(p: torch.Tensor) -> torch.dtype:
 # model with up to that many FFI layers never rebuilds a plan it had.
 class _Workspace:
     __slots__ = ("ws", "dims", "stream", "locs", "locs_version", "locs_ptr", "wt_ptr",
-                 "wt_version", "__weakref__")
+                 "wt_version", "bias", "__weakref__")
 
     def __init__(self, ws, dims, stream):
         self.ws, self.dims, self.stream = ws, dims, stream
@@ -55,6 +55,7 @@ class _Workspace:
         self.locs_ptr = 0
         self.wt_ptr = 0           # (data_ptr, version) of the weights whose W^T an
         self.wt_version = -1      # optimizer step wrote into the workspace, if any
+        self.bias = None          # weakref to the layer's bias (its last backward), or None
 
     def plan_valid(self, locs) -> bool:
         return (self.locs is not None and self.locs() is locs
@@ -118,7 +119,7 @@ def wt_target(weights: torch.Tensor):
 
 def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.Tensor,
                gsize: int, grad_output: torch.Tensor, need_x: bool, need_w: bool, need_b: bool,
-               w_grad_dtype: torch.dtype, bias_dtype: Optional[torch.dtype]):
+               w_grad_dtype: torch.dtype, bias_dtype: Optional[torch.dtype], bias_ref=None):
     """(grad_x, grad_w, grad_b) of the grouped FFI layer for grad_output [B, O]
     (read in place at any row stride when its columns are contiguous)."""
     D, B = xT.shape
@@ -168,6 +169,7 @@ def _ffi_grads(xT: torch.Tensor, weights: torch.Tensor, group_locations: torch.T
         ent.locs, ent.locs_version, ent.locs_ptr = weakref.ref(locs), locs._version, locs.data_ptr()
         if W is weights and dtype == torch.bfloat16:
             _WT_TARGETS[W.data_ptr()] = ent
+            ent.bias = bias_ref
 
     grad_w = grad_b = None
     if f32 and need_b:
@@ -222,6 +224,8 @@ class GroupFFIMulFunction(torch.autograd.Function):
         ctx.use_bias = bias is not None
         ctx.w_grad_dtype = _grad_dtype(weights)
         ctx.bias_dtype = _grad_dtype(bias) if bias is not None else None
+        # the layer's bias, so that SRSgd can step it in its weights' launch
+        ctx.bias_ref = weakref.ref(bias) if bias is not None else None
         return out
 
     @staticmethod
@@ -231,7 +235,7 @@ class GroupFFIMulFunction(torch.autograd.Function):
         grad_x, grad_w, grad_b = _ffi_grads(
             xT, weights, group_locations, ctx.gsize, grad_output, ctx.needs_input_grad[0],
             ctx.needs_input_grad[1], ctx.use_bias and ctx.needs_input_grad[3], ctx.w_grad_dtype,
-            ctx.bias_dtype)
+            ctx.bias_dtype, ctx.bias_ref)
         return grad_x, grad_w, None, grad_b, None
 
 
@@ -277,6 +281,7 @@ class HeadTailFFIFunction(torch.autograd.Function):
         ctx.use_bias = bias is not None
         ctx.w_grad_dtype = _grad_dtype(weights)
         ctx.bias_dtype = _grad_dtype(bias) if bias is not None else None
+        ctx.bias_ref = weakref.ref(bias) if bias is not None else None
         return out
 
     @staticmethod
@@ -291,5 +296,5 @@ class HeadTailFFIFunction(torch.autograd.Function):
         gb_h = gh.sum(0) if (ctx.head_has_bias and n[2]) else None
         gx_t, gw_t, gb_t = _ffi_grads(xT, weights, group_locations, ctx.gsize,
                                       grad_output[:, H:], n[3], n[4], ctx.use_bias and n[6],
-                                      ctx.w_grad_dtype, ctx.bias_dtype)
+                                      ctx.w_grad_dtype, ctx.bias_dtype, ctx.bias_ref)
         return gx_h, gw_h, gb_h, gx_t, gw_t, None, gb_t, None

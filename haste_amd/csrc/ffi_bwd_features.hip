@@ -201,6 +201,10 @@ struct GatherSgd {
     int g_dtype, use_mom, do_sr;
     float lr, wd, mu;
     uint32_t k0, k1;
+    uint16_t* bias;   // not NULL: also the SGD step on the bias [O] (offsets from 0)
+    const void* gb;   // its gradient [O], gb_dtype
+    float* mb;        // its fp32 momentum [O] (use_mom)
+    int gb_dtype;
 };
 
 template <int GD>
@@ -326,6 +330,19 @@ __global__ __launch_bounds__(256) void sgd_wt_kernel(uint16_t* __restrict__ W,
     const rsrc_t rg = make_rsrc_u32(static_cast<const char*>(sg.g) + e0 * GB, (uint32_t)(rows * F * GB));
     const rsrc_t rm = make_rsrc_u32(sg.use_mom ? sg.m + e0 : sg.m, sg.use_mom ? (uint32_t)(rows * F * 4) : 0u);
     if (tid < F) s_perm[tid] = perm[g * F + tid];
+    // the bias of the workgroup's labels, one per thread, as sgd_sr_kernel steps it
+    if (sg.bias != nullptr && tid < rows) {
+        const int64_t l = l0 + tid;
+        const float gbv = sg.gb_dtype == HASTE_DTYPE_F32
+                              ? static_cast<const float*>(sg.gb)[l]
+                              : (sg.gb_dtype == HASTE_DTYPE_BF16
+                                     ? bf16_bits_to_f32(static_cast<const uint16_t*>(sg.gb)[l])
+                                     : f16_bits_to_f32(static_cast<const uint16_t*>(sg.gb)[l]));
+        float mv = sg.use_mom ? sg.mb[l] : 0.f;
+        sg.bias[l] = (uint16_t)sgd_one(bf16_bits_to_f32(sg.bias[l]), gbv, &mv, sg.use_mom, sg.lr,
+                                       sg.wd, sg.mu, sg.do_sr, (uint64_t)l, sg.k0, sg.k1);
+        if (sg.use_mom) sg.mb[l] = mv;
+    }
     u32x4 wv[kWtBatch], gv0[kWtBatch], gv1[kWtBatch];
     f32x4 mv0[kWtBatch], mv1[kWtBatch];
 #pragma unroll
@@ -619,26 +636,34 @@ extern "C" int haste_ffi_bwd_features_partials(const int32_t* idx, const void* W
                                static_cast<hipStream_t>(stream), &p);
 }
 
-extern "C" int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype, float* m,
-                                    float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
-                                    uint64_t seed, void* workspace, int64_t workspace_bytes,
-                                    int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
-                                    int32_t dtype, void* stream) {
-    const char* fn = "haste_sgd_sr_step_wt";
-    haste::BwdFPlan p;
-    int rc = haste::check_bwdf(fn, B, D, F, O, G, dtype, workspace, workspace_bytes, &p);
+namespace haste {
+namespace {
+int sgd_step_wt(const char* fn, uint16_t* W, const void* g, int32_t g_dtype, float* m,
+                uint16_t* bias, const void* gb, int32_t gb_dtype, float* m_bias, float lr,
+                float wd, float mu, int32_t use_mom, int32_t do_sr, uint64_t seed,
+                void* workspace, int64_t workspace_bytes, int64_t B, int64_t D, int64_t F,
+                int64_t O, int64_t G, int32_t dtype, void* stream) {
+    BwdFPlan p;
+    int rc = check_bwdf(fn, B, D, F, O, G, dtype, workspace, workspace_bytes, &p);
     if (rc != HASTE_OK) return rc;
     HASTE_CHECK_ARG(dtype == HASTE_DTYPE_BF16, "%s: weights must be bf16", fn);
-    HASTE_CHECK_ARG(W && g && haste::aligned16(W) && haste::aligned16(g),
+    HASTE_CHECK_ARG(W && g && aligned16(W) && aligned16(g),
                     "%s: W and g must be 16-byte aligned pointers", fn);
     HASTE_CHECK_ARG(g_dtype == HASTE_DTYPE_BF16 || g_dtype == HASTE_DTYPE_F16 ||
                         g_dtype == HASTE_DTYPE_F32,
                     "%s: bad gradient dtype %d", fn, (int)g_dtype);
-    HASTE_CHECK_ARG(!use_mom || (m != nullptr && haste::aligned16(m)),
+    HASTE_CHECK_ARG(!use_mom || (m != nullptr && aligned16(m)),
                     "%s: momentum buffer must be a 16-byte aligned pointer", fn);
+    if (bias != nullptr) {
+        HASTE_CHECK_ARG(gb != nullptr && (!use_mom || m_bias != nullptr),
+                        "%s: the bias needs its gradient (and momentum buffer)", fn);
+        HASTE_CHECK_ARG(gb_dtype == HASTE_DTYPE_BF16 || gb_dtype == HASTE_DTYPE_F16 ||
+                            gb_dtype == HASTE_DTYPE_F32,
+                        "%s: bad bias gradient dtype %d", fn, (int)gb_dtype);
+    }
     char* base = static_cast<char*>(workspace);
-    const haste::GatherSgd sg{g, m, (int)g_dtype, use_mom ? 1 : 0, do_sr ? 1 : 0, lr, wd, mu,
-                              (uint32_t)seed, (uint32_t)(seed >> 32)};
+    const GatherSgd sg{g, m, (int)g_dtype, use_mom ? 1 : 0, do_sr ? 1 : 0, lr, wd, mu,
+                       (uint32_t)seed, (uint32_t)(seed >> 32), bias, gb, m_bias, (int)gb_dtype};
     const int* tsrc = reinterpret_cast<const int*>(base + p.tsrc_off);
     const int* perm = reinterpret_cast<const int*>(base + p.perm_off);
     const int* meta = reinterpret_cast<const int*>(base + p.meta_off);
@@ -646,11 +671,10 @@ extern "C" int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype,
     hipStream_t st = static_cast<hipStream_t>(stream);
     auto launch = [&](auto gc) {
         constexpr int GG = decltype(gc)::value;
-        const dim3 grid((unsigned)(p.Gc * (GG / haste::kWtLabels)));
+        const dim3 grid((unsigned)(p.Gc * (GG / kWtLabels)));
 #define HASTE_SGD_WT(GD)                                                                    \
-    haste::sgd_wt_kernel<GG, GD><<<grid, dim3(256), 0, st>>>(W, tsrc, perm, twt, (int)F, O, \
-                                                             (int)p.Tcap, meta, (int)p.ndr, \
-                                                             sg)
+    sgd_wt_kernel<GG, GD><<<grid, dim3(256), 0, st>>>(W, tsrc, perm, twt, (int)F, O,        \
+                                                      (int)p.Tcap, meta, (int)p.ndr, sg)
         if (g_dtype == HASTE_DTYPE_F32) HASTE_SGD_WT(HASTE_DTYPE_F32);
         else if (g_dtype == HASTE_DTYPE_BF16) HASTE_SGD_WT(HASTE_DTYPE_BF16);
         else HASTE_SGD_WT(HASTE_DTYPE_F16);
@@ -662,9 +686,35 @@ extern "C" int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype,
     case 64: launch(std::integral_constant<int, 64>{}); break;
     case 128: launch(std::integral_constant<int, 128>{}); break;
     default:
-        haste::set_error("%s: unsupported group size %lld", fn, (long long)G);
+        set_error("%s: unsupported group size %lld", fn, (long long)G);
         return HASTE_ERR_UNSUPPORTED;
     }
     HASTE_CHECK_LAUNCH(fn);
     return HASTE_OK;
+}
+}  // namespace
+}  // namespace haste
+
+extern "C" int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype, float* m,
+                                    float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
+                                    uint64_t seed, void* workspace, int64_t workspace_bytes,
+                                    int64_t B, int64_t D, int64_t F, int64_t O, int64_t G,
+                                    int32_t dtype, void* stream) {
+    return haste::sgd_step_wt("haste_sgd_sr_step_wt", W, g, g_dtype, m, nullptr, nullptr,
+                              HASTE_DTYPE_F32, nullptr, lr, wd, mu, use_mom, do_sr, seed,
+                              workspace, workspace_bytes, B, D, F, O, G, dtype, stream);
+}
+
+extern "C" int haste_sgd_sr_step_wt_bias(uint16_t* W, const void* g, int32_t g_dtype, float* m,
+                                         uint16_t* bias, const void* gb, int32_t gb_dtype,
+                                         float* m_bias, float lr, float wd, float mu,
+                                         int32_t use_mom, int32_t do_sr, uint64_t seed,
+                                         void* workspace, int64_t workspace_bytes, int64_t B,
+                                         int64_t D, int64_t F, int64_t O, int64_t G,
+                                         int32_t dtype, void* stream) {
+    const char* fn = "haste_sgd_sr_step_wt_bias";
+    HASTE_CHECK_ARG(bias != nullptr, "%s: null bias", fn);
+    return haste::sgd_step_wt(fn, W, g, g_dtype, m, bias, gb, gb_dtype, m_bias, lr, wd, mu,
+                              use_mom, do_sr, seed, workspace, workspace_bytes, B, D, F, O, G,
+                              dtype, stream);
 }

@@ -15,7 +15,9 @@ The weights of a grouped FFI layer whose last backward used an index plan
 (``bindings.wt_target``) are updated by haste_sgd_sr_step_wt instead: the same
 update, bit for bit, which also writes the transposed weights that layer's
 next backward reads, so the backward skips gathering them
-(``refresh_transposed=False`` turns this off).  Every updated parameter's
+(``refresh_transposed=False`` turns this off).  When the layer's bias is a
+parameter of the same group with a gradient, haste_sgd_sr_step_wt_bias steps
+it in the same launch (again bit for bit).  Every updated parameter's
 version counter is moved, as an in-place torch op would move it.
   * every parameter that requires a gradient gets its fp32 ``momentum_buf``
     at construction, zero, whether or not momentum is used (optim_sr.py:35-44),
@@ -111,10 +113,30 @@ class SRSgd(Optimizer):
             group["seed"] += 1
             mom_on = self._uses_momentum(group)
 
+            # FFI layers whose last backward used an index plan: their weights
+            # (and their bias, when it is a parameter of this group with a
+            # gradient) are stepped by haste_sgd_sr_step_wt[_bias]
+            targets, fused_bias = {}, {}
+            if self.refresh_transposed:
+                ids = {id(q) for q in group["params"]}
+                for p in group["params"]:
+                    if p.grad is None or p.dtype != torch.bfloat16 or p.dim() != 2:
+                        continue
+                    ent = _bindings.wt_target(p) if p.data.is_contiguous() else None
+                    if ent is None or ent.dims[2:4] != (p.shape[1], p.shape[0]):
+                        continue
+                    targets[id(p)] = ent
+                    b = ent.bias() if ent.bias is not None else None
+                    if (b is not None and id(b) in ids and b.grad is not None
+                            and b.dtype == torch.bfloat16 and b.dim() == 1
+                            and b.shape[0] == p.shape[0] and b.data.is_contiguous()):
+                        fused_bias[id(p)] = b
+            stepped = {id(b) for b in fused_bias.values()}
+
             # bf16 tensors are updated by one fused launch per gradient dtype
             batches = {}
             for p in group["params"]:
-                if p.grad is None:
+                if p.grad is None or id(p) in stepped:
                     continue
                 grad = p.grad
 
@@ -132,18 +154,31 @@ class SRSgd(Optimizer):
 
                 w = p.data
                 g_contig = grad if grad.is_contiguous() else grad.contiguous()
-                ent = (_bindings.wt_target(p) if self.refresh_transposed and w.is_contiguous()
-                       and p.dtype == torch.bfloat16 and p.dim() == 2 else None)
-                if ent is not None and ent.dims[2:4] == (p.shape[1], p.shape[0]):
+                ent = targets.get(id(p))
+                if ent is not None:
                     # an FFI layer's weights: the same update, which also writes the
                     # transposed weights its next backward reads (no gather there)
                     B, D, F, O, G = ent.dims
                     m = self._momentum_buf(p) if mom_on else None
-                    _lib.call("haste_sgd_sr_step_wt", w.data_ptr(), g_contig.data_ptr(),
-                              _C.dtype_code(g_contig.dtype), None if m is None else m.data_ptr(),
-                              float(lr), float(wd), float(mu), int(mom_on), int(bool(sr)),
-                              int(seed), ent.ws.data_ptr(), ent.ws.numel(), B, D, F, O, G,
-                              _lib.DTYPE_BF16, _C.stream_of(w))
+                    mp = None if m is None else m.data_ptr()
+                    b = fused_bias.get(id(p))
+                    if b is None:
+                        _lib.call("haste_sgd_sr_step_wt", w.data_ptr(), g_contig.data_ptr(),
+                                  _C.dtype_code(g_contig.dtype), mp, float(lr), float(wd),
+                                  float(mu), int(mom_on), int(bool(sr)), int(seed),
+                                  ent.ws.data_ptr(), ent.ws.numel(), B, D, F, O, G,
+                                  _lib.DTYPE_BF16, _C.stream_of(w))
+                    else:
+                        gb = b.grad if b.grad.is_contiguous() else b.grad.contiguous()
+                        mb = self._momentum_buf(b) if mom_on else None
+                        _lib.call("haste_sgd_sr_step_wt_bias", w.data_ptr(), g_contig.data_ptr(),
+                                  _C.dtype_code(g_contig.dtype), mp, b.data.data_ptr(),
+                                  gb.data_ptr(), _C.dtype_code(gb.dtype),
+                                  None if mb is None else mb.data_ptr(), float(lr), float(wd),
+                                  float(mu), int(mom_on), int(bool(sr)), int(seed),
+                                  ent.ws.data_ptr(), ent.ws.numel(), B, D, F, O, G,
+                                  _lib.DTYPE_BF16, _C.stream_of(w))
+                        torch.autograd.graph.increment_version(b)
                     torch.autograd.graph.increment_version(p)
                     _bindings.mark_wt_refreshed(ent, p)
                     continue

@@ -324,6 +324,21 @@ int haste_sgd_sr_step_wt(uint16_t* W, const void* g, int32_t g_dtype, float* m, 
                          int64_t O, int64_t G, int32_t dtype, void* stream);
 
 /*
+ * haste_sgd_sr_step_wt that also steps the layer's bias [O] (bf16) with its
+ * gradient gb [O] (bf16, f16 or f32) and fp32 momentum m_bias (read and written
+ * when use_mom), in the same launch: the same update as haste_sgd_sr_step on
+ * the bias with the same seed (offsets l from 0), bit-identical.  Replaces, for
+ * an FFI layer's weights and bias, SRSgd.step's sgd_update calls on both
+ * (shared_ffi/optim_sr.py:99-109, shared_ffi/sr_triton.py:172-213).
+ */
+int haste_sgd_sr_step_wt_bias(uint16_t* W, const void* g, int32_t g_dtype, float* m,
+                              uint16_t* bias, const void* gb, int32_t gb_dtype, float* m_bias,
+                              float lr, float wd, float mu, int32_t use_mom, int32_t do_sr,
+                              uint64_t seed, void* workspace, int64_t workspace_bytes, int64_t B,
+                              int64_t D, int64_t F, int64_t O, int64_t G, int32_t dtype,
+                              void* stream);
+
+/*
  * The random words of the stochastic rounding alone: draws tl.randint(seed, i)
  * for i < n, as the SR and SR-SGD kernels do, and writes the XOR of each 64
  * consecutive words: fold[t] = XOR of words 64t .. min(64t + 63, n - 1),

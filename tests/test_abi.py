@@ -180,6 +180,23 @@ def test_bwd_weights_dx_requires_dx_workspace_and_bf16():
     assert "must be bf16" in _lib.last_error()
 
 
+def test_sgd_wt_bias_rejects_bad_arguments():
+    args = dict(W=16, g=32, g_dtype=_lib.DTYPE_BF16, m=None, bias=48, gb=64,
+                gb_dtype=_lib.DTYPE_F32, mb=None, lr=0.05, wd=1e-4, mu=0.0, use_mom=0, do_sr=1,
+                seed=42, ws=256, ws_bytes=1 << 30, B=64, D=768, F=32, O=4096, G=32,
+                dtype=_lib.DTYPE_BF16, stream=None)
+    f = _lib.lib().haste_sgd_sr_step_wt_bias
+    assert f(*dict(args, bias=None).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert "null bias" in _lib.last_error()
+    assert f(*dict(args, gb=None).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert "bias needs its gradient" in _lib.last_error()
+    assert f(*dict(args, use_mom=1, m=80).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert f(*dict(args, gb_dtype=7).values()) == _lib.HASTE_ERR_INVALID_ARG
+    assert "bad bias gradient dtype" in _lib.last_error()
+    assert f(*dict(args, ws_bytes=16).values()) == _lib.HASTE_ERR_WORKSPACE
+    assert f(*dict(args, dtype=_lib.DTYPE_F16).values()) == _lib.HASTE_ERR_INVALID_ARG
+
+
 def test_ring_cases_reach_every_bwd_features_build():
     """tests/bwdf_cases.RING_CASES maps onto every (G, BT, RT) build of the
     bwd-features main kernel, each with more than one feature range, so the GPU

@@ -65,6 +65,54 @@ def test_sgd_wt_matches_sgd_and_gather(dev, B, D, O, G, F, gdt, use_mom, do_sr):
         idx.cpu(), W2.cpu(), dY.cpu(), G, D), rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("B,D,O,G,F,gdt,bdt,use_mom,do_sr", [
+    (64, 768, 4133, 32, 32, torch.bfloat16, torch.bfloat16, True, True),
+    (100, 300, 2001, 64, 128, torch.float32, torch.float32, False, True),
+    (37, 200, 700, 128, 64, torch.float16, torch.bfloat16, True, False),
+    (96, 512, 1000, 16, 48, torch.bfloat16, torch.float32, True, True),
+])
+def test_sgd_wt_bias_matches_separate_steps(dev, B, D, O, G, F, gdt, bdt, use_mom, do_sr):
+    """haste_sgd_sr_step_wt_bias == haste_sgd_sr_step_wt on the weights plus
+    haste_sgd_sr_step on the bias (same seed, offsets from 0), bit for bit,
+    momentum buffers included."""
+    g = torch.Generator(device=dev).manual_seed(O + 7)
+    Gc = (O + G - 1) // G
+    W = ((torch.rand(O, F, generator=g, device=dev) * 2 - 1) / F ** 0.5).to(torch.bfloat16)
+    grad = (torch.randn(O, F, generator=g, device=dev) * 0.05).to(gdt)
+    m = torch.randn(O, F, generator=g, device=dev) * 0.01
+    bias = (torch.randn(O, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    gb = (torch.randn(O, generator=g, device=dev) * 0.05).to(bdt)
+    mb = torch.randn(O, generator=g, device=dev) * 0.01
+    idx = torch.randint(0, D, (Gc, F), generator=g, device=dev, dtype=torch.int32)
+    lr, wd, mu, seed = 0.05, 1e-4, 0.9, 99
+    st = _C.stream_of(W)
+    ws = _C.bwd_features_workspace(B, D, F, O, G, torch.bfloat16, dev)
+    _lib.call("haste_ffi_bwd_features_plan", idx.data_ptr(), ws.data_ptr(), ws.numel(), B, D, F,
+              O, G, _lib.DTYPE_BF16, st)
+    mp = (lambda t: t.data_ptr() if use_mom else None)
+    W1, m1, b1, mb1 = W.clone(), m.clone(), bias.clone(), mb.clone()
+    _lib.call("haste_sgd_sr_step_wt", W1.data_ptr(), grad.data_ptr(), _C.dtype_code(gdt), mp(m1),
+              lr, wd, mu, int(use_mom), int(do_sr), seed, ws.data_ptr(), ws.numel(), B, D, F, O,
+              G, _lib.DTYPE_BF16, st)
+    _lib.call("haste_sgd_sr_step", b1.data_ptr(), gb.data_ptr(), _C.dtype_code(bdt), mp(mb1), O,
+              lr, wd, mu, int(use_mom), int(do_sr), seed, 0, st)
+    torch.cuda.synchronize()
+    wt1 = ws.clone()
+    W2, m2, b2, mb2 = W.clone(), m.clone(), bias.clone(), mb.clone()
+    _lib.call("haste_sgd_sr_step_wt_bias", W2.data_ptr(), grad.data_ptr(), _C.dtype_code(gdt),
+              mp(m2), b2.data_ptr(), gb.data_ptr(), _C.dtype_code(bdt), mp(mb2), lr, wd, mu,
+              int(use_mom), int(do_sr), seed, ws.data_ptr(), ws.numel(), B, D, F, O, G,
+              _lib.DTYPE_BF16, st)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(W1), bits(W2))
+    assert np.array_equal(bits(b1), bits(b2))
+    assert not np.array_equal(bits(b2), bits(bias))
+    assert torch.equal(wt1, ws)
+    if use_mom:
+        assert torch.equal(m1.view(torch.int32), m2.view(torch.int32))
+        assert torch.equal(mb1.view(torch.int32), mb2.view(torch.int32))
+
+
 def test_training_loop_with_refresh_matches_without(dev):
     """Three SRSgd steps of a drop-in layer: refreshing W^T in the optimizer
     (and skipping the gather in the backward) gives the same weights, bias and
