@@ -6,6 +6,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "bwdf_plan.hpp"
 
@@ -505,6 +506,12 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_main_kernel(
     }
 }
 
+// f(integral_constant<int, K>) for K = 0, 1, ..., in order
+template <int... K, typename F>
+__device__ __forceinline__ void unroll_seq(std::integer_sequence<int, K...>, F&& f) {
+    (f(std::integral_constant<int, K>{}), ...);
+}
+
 // Direct build: no LDS ring and no barrier per group.  Each wave loads the
 // MFMA operand fragments of a group's W^T tiles straight from the workspace
 // (one contiguous 1 KB block per tile and k-step in the chunk-major twt
@@ -614,7 +621,12 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     };
     // the fragments as the MFMA takes them: YA chunks joined; labels >= O zeroed
     // (only the last group has any: a uniform branch)
-    auto prep_y = [&](int64_t g, u32x4 (&a)[MT][KS], const u32x4 (&e)[MT][1]) __attribute__((always_inline)) {
+    // the slice's group holding labels past O (its last, in the last slice), and
+    // the labels it has
+    const int i_tail = (g_hi == Gc && O % G != 0) ? ng - 1 : -1;
+    const int nr_tail = (int)(O - (Gc - 1) * G);
+    auto prep_y = [&](int i, u32x4 (&a)[MT][KS], const u32x4 (&e)[MT][1]) __attribute__((always_inline)) {
+        const int64_t g = g_lo + i;
         if constexpr (YA) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
@@ -633,9 +645,8 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
                     a[mt][ks] = shift_pair16(a[mt][ks], nxt[ks], last_row[mt] ? 0u : mb[mt]);
             }
         }
-        const int64_t rem = O - g * G;
-        if (rem >= G) return;
-        const int nr = (int)max<int64_t>(rem, 0);
+        if (__builtin_expect(i != i_tail, 1)) return;
+        const int nr = nr_tail;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -652,9 +663,9 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     // tile range of group g_lo + i in range r (tb | tm << 16, te), as a buffer
     // load (a scalar load would hold up the wave's LDS waits); past the slice: zero
     const rsrc_t mr = make_rsrc(meta + (g_lo * ndr + r) * kMetaStride,
-                                ((int64_t)(max(ng, 1) - 1) * ndr + 1) * kMetaStride * 4);
+                                ng > 0 ? ((int64_t)(ng - 1) * ndr + 1) * kMetaStride * 4 : 0);
     auto load_meta = [&](int i) __attribute__((always_inline)) -> u32x2 {
-        return buf_load8(mr, i < ng ? (uint32_t)(i * ndr * kMetaStride * 4) : kOOB);
+        return buf_load8(mr, (uint32_t)(i * ndr * kMetaStride * 4));  // i >= ng: past the end
     };
     auto uniform_meta = [](const u32x2& m) __attribute__((always_inline)) -> u32x2 {
         return u32x2{(uint32_t)__builtin_amdgcn_readfirstlane((int)m[0]),
@@ -682,6 +693,27 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
         for (int t = 0; t < RT; ++t) fr.f[t] = (int)buf_load4(frr, (uint32_t)(t * 16 + col) * 4);
     };
 
+    // The same for the first round of a group, through resources over the
+    // slice's tiles: group i's tiles start at row (i*Tcap + tb)*16 of the
+    // slice (the host keeps the slice's bytes under kMaxRsrcBytes); tiles past
+    // the range read the next range's rows, which the round does not use, and
+    // groups past the slice read zero.
+    const int64_t srow0 = g_lo * Tcap * 16;
+    const rsrc_t wsl = make_rsrc(twt + srow0 * G, (int64_t)ng * Tcap * 16 * G * 2);
+    const rsrc_t fsl = make_rsrc(tfeat + srow0, (int64_t)ng * Tcap * 16 * 4);
+    auto load_frag_first = [&](int i, u32x2 m, Frag& fr) __attribute__((always_inline)) {
+        const uint32_t row = ((uint32_t)i * (uint32_t)Tcap + (m[0] & 0xFFFFu)) * 16u;
+        const uint32_t wo = row * (2u * G) + (uint32_t)lane * 16u;
+        const uint32_t fo = row * 4u + (uint32_t)col * 4u;
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                fr.b[t][ks] = buf_load16(wsl, wo + (uint32_t)(t * 16 * G + ks * 512) * 2u);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) fr.f[t] = (int)buf_load4(fsl, fo + (uint32_t)t * 64u);
+    };
+
     auto perm_col = [](int w, int q) { return (q & 1) * (BT / 2) + w * 8 + (q >> 1) * 4; };
     char* acc_b[MT];
 #pragma unroll
@@ -701,44 +733,57 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
             }
         }
     };
-    // First round of a group with N0 layer-0 tiles: layer-1 tile t is the
-    // round's tile N0 + t and adds into its pair's rows.  The partial rows are
-    // read, the MFMAs issued, then the rows written.
-    auto first_n = [&](const u32x4 (&a)[MT][KS], const Frag& fr, auto n0) __attribute__((always_inline)) {
-        constexpr int N0 = decltype(n0)::value;
-        f32x4 old[MT][N0 > 0 ? N0 : 1];
+    // First round of a group with N0 layer-0 and N1 layer-1 tiles (N1 <= N0,
+    // N0 + N1 <= RT): layer-1 tile t is the round's tile N0 + t and adds into
+    // its pair's rows; the round's other fragments are not used.  The partial
+    // rows are read, the MFMAs issued, then the rows written.
+    auto first_n = [&](const u32x4 (&a)[MT][KS], const Frag& fr, auto n0, auto n1) __attribute__((always_inline)) {
+        constexpr int N0 = decltype(n0)::value, N1 = decltype(n1)::value;
+        if constexpr (N0 + N1 <= RT) {
+            f32x4 old[MT][N0];
 #pragma unroll
-        for (int t = 0; t < N0; ++t)
+            for (int t = 0; t < N0; ++t)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) old[mt][t] = *reinterpret_cast<const f32x4*>(acc_b[mt] + fr.f[t]);
-        if constexpr (N0 > 0) {
-            Res rs;
-            mma_round(a, fr, rs);
+                for (int mt = 0; mt < MT; ++mt) old[mt][t] = *reinterpret_cast<const f32x4*>(acc_b[mt] + fr.f[t]);
+            f32x4 c[MT][N0 + N1];
+#pragma unroll
+            for (int t = 0; t < N0 + N1; ++t) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) v = mfma16x16x32<T>(a[mt][ks], fr.b[t][ks], v);
+                    c[mt][t] = v;
+                }
+            }
 #pragma unroll
             for (int t = 0; t < N0; ++t) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    f32x4 v = rs.c[mt][t];
-                    if (N0 + t < RT) v += rs.c[mt][N0 + t];
+                    f32x4 v = c[mt][t];
+                    if (t < N1) v += c[mt][N0 + t];
                     *reinterpret_cast<f32x4*>(acc_b[mt] + fr.f[t]) = old[mt][t] + v;
                 }
             }
         }
     };
-    auto first = [&](const u32x4 (&a)[MT][KS], const Frag& fr, int n0) __attribute__((always_inline)) {
-        static_assert(RT <= 8, "ring tiles");
+    auto first = [&](const u32x4 (&a)[MT][KS], const Frag& fr, int n0, int n1) __attribute__((always_inline)) {
+        static_assert(RT <= 6, "direct build: rounds of at most 6 tiles");
         using std::integral_constant;
-        switch (n0) {
-        case 0: first_n(a, fr, integral_constant<int, 0>{}); break;
-        case 1: first_n(a, fr, integral_constant<int, 1>{}); break;
-        case 2: first_n(a, fr, integral_constant<int, (RT >= 2 ? 2 : 1)>{}); break;
-        case 3: first_n(a, fr, integral_constant<int, (RT >= 3 ? 3 : 1)>{}); break;
-        case 4: first_n(a, fr, integral_constant<int, (RT >= 4 ? 4 : 1)>{}); break;
-        case 5: first_n(a, fr, integral_constant<int, (RT >= 5 ? 5 : 1)>{}); break;
-        case 6: first_n(a, fr, integral_constant<int, (RT >= 6 ? 6 : 1)>{}); break;
-        case 7: first_n(a, fr, integral_constant<int, (RT >= 7 ? 7 : 1)>{}); break;
-        default: first_n(a, fr, integral_constant<int, RT>{}); break;
+#define HASTE_ROUND(A, B)                                                          \
+    case (A) * 8 + (B):                                                             \
+        first_n(a, fr, integral_constant<int, (A)>{}, integral_constant<int, (B)>{}); \
+        break;
+        switch (n0 * 8 + n1) {
+            HASTE_ROUND(1, 0) HASTE_ROUND(1, 1)
+            HASTE_ROUND(2, 0) HASTE_ROUND(2, 1) HASTE_ROUND(2, 2)
+            HASTE_ROUND(3, 0) HASTE_ROUND(3, 1) HASTE_ROUND(3, 2) HASTE_ROUND(3, 3)
+            HASTE_ROUND(4, 0) HASTE_ROUND(4, 1) HASTE_ROUND(4, 2)
+            HASTE_ROUND(5, 0) HASTE_ROUND(5, 1)
+            HASTE_ROUND(6, 0)
+        default: break;  // no layer-0 tile in the range
         }
+#undef HASTE_ROUND
     };
     // Further rounds of a range holding more than RT tiles (rare): loaded and
     // added at once, layer 0 first (layer-1 tiles into trash rows), then layer 1.
@@ -781,7 +826,9 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     // groups of look-ahead where a slot is small (rounds of at most 4
     // fragments: short groups need the deeper pipeline), else two. ----
     constexpr int DEPTH = RT * KS <= 4 ? 5 : 2, NS = DEPTH + 1;
-    static_assert(kGroupUnroll % NS == 0, "unroll");
+    // groups per unrolled iteration, a multiple of NS (groups past the slice
+    // read zero metas and do nothing)
+    constexpr int U = kGroupUnroll % NS == 0 ? kGroupUnroll : NS;
     Frag fq[NS];
     u32x4 ya[NS][MT][KS];
     u32x4 yb[YA ? NS : 1][MT][1];  // YA: k-chunk 3's chunk past the group
@@ -798,7 +845,7 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
 #pragma unroll
         for (int k = 0; k < DEPTH; ++k) {
             __builtin_amdgcn_sched_barrier(0);
-            load_frag(k, mq[k], 0, fq[k % NS]);
+            load_frag_first(k, mq[k], fq[k % NS]);
             load_y(g_lo + k, ya[k % NS], yb[YA ? k % NS : 0]);
             mraw[(k + DEPTH) % NS] = load_meta(k + DEPTH);
         }
@@ -806,29 +853,25 @@ __global__ __launch_bounds__(64 * WAVES / MT_, 1) void bwdf_direct_kernel(
     }
     __syncthreads();  // the partial is clear
     auto body = [&](int i, auto kc) __attribute__((always_inline)) {
-        constexpr int K = decltype(kc)::value;  // i % kGroupUnroll
+        constexpr int K = decltype(kc)::value;  // i % U
         constexpr int Q = K % NS;
         const u32x2 mn = uniform_meta(mraw[(Q + DEPTH) % NS]);  // group i + DEPTH
-        load_frag(i + DEPTH, mn, 0, fq[(Q + DEPTH) % NS]);
+        load_frag_first(i + DEPTH, mn, fq[(Q + DEPTH) % NS]);
         load_y(g_lo + i + DEPTH, ya[(Q + DEPTH) % NS], yb[YA ? (Q + DEPTH) % NS : 0]);
         mraw[(Q + 2 * DEPTH) % NS] = load_meta(i + 2 * DEPTH);
-        prep_y(g_lo + i, ya[Q], yb[YA ? Q : 0]);
+        prep_y(i, ya[Q], yb[YA ? Q : 0]);
         const u32x2 m = mq[0];
         const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
-        first(ya[Q], fq[Q], min(tm - tb, min(RT, te - tb)));
+        const int n0 = min(tm - tb, RT);
+        first(ya[Q], fq[Q], n0, min(te - tb, RT) - n0);
         if (te - tb > RT) extra_rounds(i, m, ya[Q]);  // uniform, rare
 #pragma unroll
         for (int k = 0; k + 1 < DEPTH; ++k) mq[k] = mq[k + 1];
         mq[DEPTH - 1] = mn;
     };
-    for (int i = 0; i < ng; i += kGroupUnroll) {
-        body(i, std::integral_constant<int, 0>{});
-        body(i + 1, std::integral_constant<int, 1>{});
-        body(i + 2, std::integral_constant<int, 2>{});
-        body(i + 3, std::integral_constant<int, 3>{});
-        body(i + 4, std::integral_constant<int, 4>{});
-        body(i + 5, std::integral_constant<int, 5>{});
-    }
+    for (int i = 0; i < ng; i += U)
+        unroll_seq(std::make_integer_sequence<int, U>{},
+                   [&](auto kc) __attribute__((always_inline)) { body(i + decltype(kc)::value, kc); });
     __syncthreads();
 
     // ---- write the partial: ws[s][d_lo + d][bt*BT + b] ----
@@ -889,9 +932,11 @@ int run_main(const int* tfeat, const int* meta, const uint16_t* twt, const uint1
     // 1, 104 -> 101 us, YA rows 137 -> 122 us; config 3, 802 -> 611 us).  With a
     // dY of 686 MB (config 2) it was slower than the ring build (305 -> 361 us),
     // which keeps the waves of a workgroup in step on each group's dY and W^T.
+    // It addresses a slice's W^T tiles with 32-bit offsets.
     if constexpr (G == 32 || G == 64) {
         const int build = bwdf_build();
-        if (build == 2 || (build == 0 && B * lddy * 2 <= kMallBytes)) {
+        const bool fits = (p.gps + 16) * p.Tcap * 16 * G * 2 <= kMaxRsrcBytes;
+        if (fits && (build == 2 || (build == 0 && B * lddy * 2 <= kMallBytes))) {
             if (p.BT == 64) return launch_ring<T, G, 4, YA, 1, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
             return launch_ring<T, G, 8, YA, 2, true>(tfeat, meta, twt, dY, lddy, ws, p, B, D, O, st);
         }

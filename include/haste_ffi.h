@@ -150,7 +150,8 @@ int haste_ffi_bwd_features_config(int64_t B, int64_t D, int64_t F, int64_t O, in
  * Selects the main kernel of later bwd-features calls in this process
  * (host-only): 0 (the default) and 3 the staged build for G >= 32, else the
  * LDS-ring build; 1 always the LDS-ring build; 2 the direct build wherever it
- * exists (G = 32 or 64), else the ring build.  The builds give the same
+ * exists (G = 32 or 64, and a group slice's transposed weights under 2 GB),
+ * else the ring build.  The builds give the same
  * results up to the order of fp32 additions.  The workspace layout (plan)
  * differs between the staged build and the others, so a plan made under one
  * setting must be remade (plan_ready = 0) after a change.  Returns the
