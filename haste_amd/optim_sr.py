@@ -129,8 +129,9 @@ class SRSgd(Optimizer):
                     b = ent.bias() if ent.bias is not None else None
                     if (b is not None and id(b) in ids and b.grad is not None
                             and b.dtype == torch.bfloat16 and b.dim() == 1
-                            and b.shape[0] == p.shape[0] and b.data.is_contiguous()):
-                        fused_bias[id(p)] = b
+                            and b.shape[0] == p.shape[0] and b.data.is_contiguous()
+                            and all(b is not c for c in fused_bias.values())):
+                        fused_bias[id(p)] = b  # (a bias shared by two layers: stepped once)
             stepped = {id(b) for b in fused_bias.values()}
 
             # bf16 tensors are updated by one fused launch per gradient dtype

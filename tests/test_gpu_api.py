@@ -250,7 +250,7 @@ def test_head_tail_logits_match_cat(dev, H):
     # absolute: half an ulp + one ulp + half an ulp of terms below 0.5 < 4e-3
     gx_exp = (g_out[:, :H].float().cpu() @ head.weight.float().cpu()
               + oracle.ffi_backward_features(idxc, Wc, gt, G, D).t())
-    torch.testing.assert_close(gx.float().cpu(), gx_exp, rtol=2e-2, atol=4e-3)
+    torch.testing.assert_close(gx.float().cpu(), gx_exp, rtol=1e-2, atol=4e-3)
     assert (o[:, H:].data_ptr() % 16 == 0) and o.stride(0) % 8 == 0
     assert np.array_equal(bits(o), bits(o_ref))
     assert np.array_equal(bits(gw), bits(gw_ref)) and np.array_equal(bits(gb), bits(gb_ref))
