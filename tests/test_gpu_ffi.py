@@ -64,6 +64,7 @@ CASES = [
     (256, 768, 5000, 64, 64, "dups"),     # 2-tile ring (config 2 family); duplicates overflow it
     (160, 4096, 1000, 32, 256, "random"), # 2-tile ring, 15 ranges (config 3 family), 8 waves
     (1, 64, 64, 64, 64, "random"),
+    (5, 20, 5, 16, 32, "random"),         # O < G (one partial group), D < F (forced duplicates)
 ]
 
 
