@@ -5,7 +5,9 @@
 // Per group g (Gc = ceil(O/G) groups), the distinct indices of idx[g, :] are
 // split by feature range (ndr ranges of Dc features) and laid out in tiles of
 // 16 positions; an index occurring k > 1 times gets a "hi" row in layer 0 and
-// a "lo" row in layer 1.  Workspace regions (byte offsets in BwdFPlan):
+// a "lo" row in layer 1 -- or, in the staged build's plan (in-tile mode), the
+// lo row right after the hi row in the same layer-0 tile, its tfeat entry
+// marked by bit 0, and no layer 1.  Workspace regions (byte offsets in BwdFPlan):
 //   tfeat  int32 [Gc, Tcap*16]  LDS byte offset of the position's feature row
 //   tsrc   int32 [Gc, Tcap*16]  (start << 10) | (count << 1) | lo: the position
 //                               sums W over slots perm[g*F + start .. +count)

@@ -19,12 +19,14 @@
 //    one group never touch the same partial word;
 //  - one barrier per group, after each wave's LDS operations have completed,
 //    orders the groups' partial updates and publishes the next staged tile.
-// A duplicated index's second ("lo") row sits in layer-1 tile t, paired with
-// layer-0 tile t, so its products add into the same rows: waves 0 and 1 also
-// load layer-1 tiles 0 and 1.  A group whose range holds more (more than eight
-// layer-0 tiles or more than two layer-1 tiles) takes the rest in a pass of
-// its own between two more barriers, each wave adding tiles whose features no
-// other wave touches in that pass.
+// A duplicated index's second ("lo") row sits in the same tile as its "hi"
+// row (the plan's in-tile mode: no layer-1 tiles, so no wave carries a second
+// tile in the pipeline), its partial-row offset marked by bit 0: the wave adds
+// the tile's products in two passes, the hi and single rows first, then the lo
+// rows, each pass sending the other lanes to a trash row.  A group whose range
+// holds more than eight tiles takes the rest in a pass of its own between two
+// more barriers, each wave adding tiles whose features no other wave touches
+// in that pass.
 // YA: dY rows at any 2-byte alignment; pieces are loaded from unaligned
 // addresses, and the piece of dY's last row that straddles label O (the end of
 // the tensor) is loaded early and shifted back.
@@ -53,7 +55,6 @@ struct StagedCfg {
     // groups of load look-ahead; G = 128 fragments are four times larger
     static constexpr int DEPTH = G >= 128 ? 2 : 5;
     static constexpr int NS = DEPTH + 1;     // register slots of the pipeline
-    static constexpr int L1W = 2;            // waves that load layer-1 tiles in the pipeline
     static_assert(G >= 32, "staged build: G >= 32");
     static_assert(TPW * W == kStagedTiles, "tiles per wave");
     static_assert(PB == 4 || PB == 8 || PB == 16 || PB == 32, "dY piece");
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
     int64_t O, int64_t Gc, int nbt, int ndr, int Dc, int gps, int S, int Tcap) {
     using C = StagedCfg<G, BT, W>;
     constexpr int KS = C::KS, MT = C::MT, STG = C::STG, PB = C::PB, PW = C::PW, AS = C::AS;
-    constexpr int NTH = C::NTH, DEPTH = C::DEPTH, NS = C::NS, WAVES = C::WAVES, L1W = C::L1W;
+    constexpr int NTH = C::NTH, DEPTH = C::DEPTH, NS = C::NS, WAVES = C::WAVES;
     constexpr int TPW = C::TPW;
     using Piece = typename PieceT<PW>::type;
     __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
@@ -247,37 +248,39 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
     const rsrc_t wr_s = make_rsrc(twt + g_lo * Tcap * 16 * G, (int64_t)ng * Tcap * 16 * G * 2);
     const rsrc_t fr_s = make_rsrc(tfeat + g_lo * Tcap * 16, (int64_t)ng * Tcap * 16 * 4);
 
-    // The pipeline, for waves that load layer-1 tiles (L1) or not.  Step j's
-    // loads -- W^T fragments and partial-row offsets of group j, dY piece of
-    // group j+1, metadata of group j+DEPTH+1 -- are issued in iteration
-    // j-DEPTH into register slot j % NS, in the same order every iteration,
-    // so iteration i waits for exactly the loads of step i.  Iteration i
-    // stages group i+1's dY, multiplies group i and adds group i-1's products
-    // into the partial; kGroupUnroll iterations are unrolled so that every slot
-    // and staging buffer index is a constant.
-    auto run = [&](auto l1c) __attribute__((always_inline)) {
-        constexpr bool L1 = decltype(l1c)::value;
+    // Partial-row byte offsets of a lane's position for the two passes of an
+    // update: pass 1 adds the hi and single rows (lo rows go to a trash row),
+    // pass 2 the lo rows (bit 0 of the plan's offset; the others to a trash row).
+    const int trash_b = (C::DCMAX + (col & (kTrashRows - 1))) * AS * 4;
+    auto pass1 = [&](int fo) __attribute__((always_inline)) { return (fo & 1) ? trash_b : fo; };
+    auto pass2 = [&](int fo) __attribute__((always_inline)) { return (fo & 1) ? fo - 1 : trash_b; };
+    // whether any lane of the wave holds a lo row (uniform)
+    auto any_lo = [](int fo) __attribute__((always_inline)) {
+        return __builtin_amdgcn_ballot_w64((fo & 1) != 0) != 0;
+    };
+
+    // The pipeline.  Step j's loads -- W^T fragments and partial-row offsets
+    // of group j, dY piece of group j+1, metadata of group j+DEPTH+1 -- are
+    // issued in iteration j-DEPTH into register slot j % NS, in the same order
+    // every iteration, so iteration i waits for exactly the loads of step i.
+    // Iteration i stages group i+1's dY, multiplies group i and adds group
+    // i-1's products into the partial; kGroupUnroll iterations are unrolled so
+    // that every slot and staging buffer index is a constant.
+    {
         struct Frag {
-            u32x4 b0[TPW][KS];       // layer-0 tiles wave + WAVES*k
-            u32x4 b1[L1 ? KS : 1];   // layer-1 tile `wave`
-            int fo[TPW];             // partial-row byte offsets of the lane's positions
+            u32x4 b0[TPW][KS];       // tiles wave + WAVES*k
+            int fo[TPW];             // the plan's partial-row offsets of the lane's positions
         };
         auto load_frag = [&](int i, u32x2 m, Frag& fr) __attribute__((always_inline)) {
-            const uint32_t tb = m[0] & 0xFFFFu, tm = m[0] >> 16;
-            // the wave's layer-0 (and layer-1) tile, counted from the slice's first
+            const uint32_t tb = m[0] & 0xFFFFu;
+            // the wave's tile, counted from the slice's first
             const uint32_t t0 = (uint32_t)i * (uint32_t)Tcap + tb + (uint32_t)wave;
-            const uint32_t t1 = (uint32_t)i * (uint32_t)Tcap + tm + (uint32_t)wave;
             const uint32_t fl = (uint32_t)lane * 16u;  // the lane's 16 bytes of a k-step's 1 KB
 #pragma unroll
             for (int k = 0; k < TPW; ++k)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
                     fr.b0[k][ks] = buf_load16(wr_s, (t0 + k * WAVES) * (16u * G * 2u) + fl + ks * 1024u);
-            if constexpr (L1) {
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    fr.b1[ks] = buf_load16(wr_s, t1 * (16u * G * 2u) + fl + ks * 1024u);
-            }
 #pragma unroll
             for (int k = 0; k < TPW; ++k)
                 fr.fo[k] = (int)buf_load4(fr_s, ((t0 + k * WAVES) * 16u + (uint32_t)col) * 4u);
@@ -292,41 +295,44 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
                 c[mt] = v;
             }
         };
-        // Tiles of group g_lo + i beyond the pipeline's (layer-0 tiles >=
-        // kStagedTiles, layer-1 tiles >= L1W), loaded and added at once by the
-        // wave that owns the layer-0 tile of the same index (t % WAVES): layer-0
-        // tiles past the pipeline's with their layer-1 pairs, and the layer-1
-        // tiles whose layer-0 pair is one of the wave's pipeline tiles (added one
-        // group later by the same wave).
+        // products c of a tile added at the lane's plan offset fo (both passes)
+        auto add_tile = [&](int fo, const f32x4 (&c)[MT]) __attribute__((always_inline)) {
+            const int o1 = pass1(fo);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                f32x4* q = reinterpret_cast<f32x4*>(accb + o1 + mt * 64 + colb);
+                *q = *q + c[mt];
+            }
+            if (any_lo(fo)) {
+                const int o2 = pass2(fo);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f32x4* q = reinterpret_cast<f32x4*>(accb + o2 + mt * 64 + colb);
+                    *q = *q + c[mt];
+                }
+            }
+        };
+        // Tiles of group g_lo + i beyond the pipeline's (>= kStagedTiles),
+        // loaded and added at once by the wave that owns the pipeline tile of
+        // the same index modulo WAVES.
         auto extra = [&](int i, u32x2 m, int buf) __attribute__((always_inline)) {
-            const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
-            const int n0 = tm - tb, n1 = te - tm;
+            const int tb = (int)(m[0] & 0xFFFF), te = (int)m[1];
             const int64_t gbase = (g_lo + __builtin_amdgcn_readfirstlane(i)) * Tcap;
             u32x4 a[MT][KS];
             read_a(buf, a);
-            auto one = [&](int t, bool l0, bool l1) __attribute__((always_inline)) {
-                // tiles are addressed from the group's first tile (all in range)
-                const rsrc_t wr = make_rsrc_u32(twt + gbase * 16 * G, (uint32_t)te * 16u * G * 2u);
-                const rsrc_t frr = make_rsrc_u32(tfeat + gbase * 16, (uint32_t)te * 16u * 4u);
-                u32x4 b0[KS], b1[KS];
+            // tiles are addressed from the group's first tile (all in range)
+            const rsrc_t wr = make_rsrc_u32(twt + gbase * 16 * G, (uint32_t)te * 16u * G * 2u);
+            const rsrc_t frr = make_rsrc_u32(tfeat + gbase * 16, (uint32_t)te * 16u * 4u);
+            for (int t = wave + kStagedTiles; t < te - tb; t += WAVES) {
+                u32x4 b0[KS];
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    b0[ks] = buf_load16(wr, l0 ? (uint32_t)((tb + t) * 16 * G + (ks * 64 + lane) * 8) * 2 : kOOB);
-                    b1[ks] = buf_load16(wr, l1 ? (uint32_t)((tm + t) * 16 * G + (ks * 64 + lane) * 8) * 2 : kOOB);
-                }
-                const int fo = (int)buf_load4(frr, (uint32_t)(((l0 ? tb : tm) + t) * 16 + col) * 4);
-                f32x4 c0[MT], c1[MT];
+                for (int ks = 0; ks < KS; ++ks)
+                    b0[ks] = buf_load16(wr, (uint32_t)((tb + t) * 16 * G + (ks * 64 + lane) * 8) * 2);
+                const int fo = (int)buf_load4(frr, (uint32_t)((tb + t) * 16 + col) * 4);
+                f32x4 c0[MT];
                 mma(a, b0, c0);
-                mma(a, b1, c1);
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    f32x4* p = reinterpret_cast<f32x4*>(accb + fo + mt * 64 + colb);
-                    *p = *p + (c0[mt] + c1[mt]);
-                }
-            };
-            for (int t = wave + kStagedTiles; t < n0; t += WAVES) one(t, true, t < n1);
-            for (int t = wave; t < kStagedTiles && t < n1; t += WAVES)
-                if (t >= L1W) one(t, false, true);
+                add_tile(fo, c0);
+            }
             // every load of this pass has been used; say so, so that later code
             // need not wait for them
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -338,7 +344,7 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
         u32x2 mu[DEPTH + 1];  // uniform metadata of groups i .. i+DEPTH
         f32x4 pd[TPW][MT];    // products of the previous group
         int fod[TPW];
-        int n0d = 0;          // uniform: layer-0 tiles of the previous group
+        int n0d = 0;          // uniform: tiles of the previous group
 #pragma unroll
         for (int k = 0; k < TPW; ++k) fod[k] = 0;
         {
@@ -371,41 +377,41 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
             yq[QN] = load_y(i + DEPTH + 1);
             mraw[QN] = load_meta(i + 2 * DEPTH + 1);
             const u32x2 m = mu[0];
-            const int tb = (int)(m[0] & 0xFFFF), tm = (int)(m[0] >> 16), te = (int)m[1];
-            // The previous group's partial rows are read, and this group's
-            // products computed, whether or not the wave has the tile (fod is
-            // always a valid row offset; a wave without the tile multiplies some
-            // other tile, and neither result is written): branches here would
-            // only add register initialisations.
+            const int tb = (int)(m[0] & 0xFFFF), te = (int)m[1];
+            // The previous group's partial rows (pass 1) are read, and this
+            // group's products computed, whether or not the wave has the tile
+            // (the offsets always name valid rows; a wave without the tile
+            // multiplies some other tile, and neither result is written):
+            // branches here would only add register initialisations.
             f32x4 old[TPW][MT];
 #pragma unroll
             for (int k = 0; k < TPW; ++k)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    old[k][mt] = *reinterpret_cast<const f32x4*>(accb + fod[k] + mt * 64 + colb);
+                    old[k][mt] = *reinterpret_cast<const f32x4*>(accb + pass1(fod[k]) + mt * 64 + colb);
             stage(i + 1, yq[Q], 1 - P);
             f32x4 pc[TPW][MT];
             u32x4 a[MT][KS];
             read_a(P, a);
 #pragma unroll
             for (int k = 0; k < TPW; ++k) mma(a, fq[Q].b0[k], pc[k]);
-            if constexpr (L1) {
-                if (wave < te - tm) {
-                    f32x4 c1[MT];
-                    mma(a, fq[Q].b1, c1);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) pc[0][mt] += c1[mt];
-                }
-            }
 #pragma unroll
             for (int k = 0; k < TPW; ++k) {
                 if (wave + k * WAVES < n0d) {  // uniform: the wave had tile k
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
-                        *reinterpret_cast<f32x4*>(accb + fod[k] + mt * 64 + colb) = old[k][mt] + pd[k][mt];
+                        *reinterpret_cast<f32x4*>(accb + pass1(fod[k]) + mt * 64 + colb) = old[k][mt] + pd[k][mt];
+                    if (any_lo(fod[k])) {  // the tile's lo rows, after their hi rows
+                        const int o2 = pass2(fod[k]);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            f32x4* q = reinterpret_cast<f32x4*>(accb + o2 + mt * 64 + colb);
+                            *q = *q + pd[k][mt];
+                        }
+                    }
                 }
             }
-            n0d = tm - tb;
+            n0d = te - tb;
 #pragma unroll
             for (int k = 0; k < TPW; ++k) {
                 fod[k] = fq[Q].fo[k];
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
             mu[DEPTH] = uniform_meta(mraw[Q]);
             __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
             __builtin_amdgcn_s_barrier();
-            if (tm - tb > kStagedTiles || te - tm > L1W) {  // uniform, rare
+            if (te - tb > kStagedTiles) {  // uniform, rare
                 extra(i, m, P);
                 __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
                 __builtin_amdgcn_s_barrier();
@@ -432,21 +438,12 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
             body(i + 5, std::integral_constant<int, 5>{});
         }
 #pragma unroll
-        for (int k = 0; k < TPW; ++k) {
-            if (wave + k * WAVES < n0d) {
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    f32x4* p = reinterpret_cast<f32x4*>(accb + fod[k] + mt * 64 + colb);
-                    *p = *p + pd[k][mt];
-                }
-            }
-        }
+        for (int k = 0; k < TPW; ++k)
+            if (wave + k * WAVES < n0d) add_tile(fod[k], pd[k]);
         // every load has been used (the last iterations' look-ahead loads are
         // out of range or unused)
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    };
-    if (wave < L1W) run(std::true_type{});
-    else run(std::false_type{});
+    }
     __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
     __syncthreads();
 

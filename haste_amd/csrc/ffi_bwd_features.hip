@@ -61,6 +61,26 @@ __device__ __forceinline__ int dup_free_index(int t, int p, int T0, int T1, int 
     for (int s = 0; s < p; ++s) n += T0 - dup_tiles_at(s, T1, nd);
     return n + t - dup_tiles_at(p, T1, nd);
 }
+// In-tile mode (the staged build's plan): a range's duplicated features come
+// first, feature k's two rows in tile k / 8 at positions 2(k % 8) and
+// 2(k % 8) + 1; single features fill the other slots position by position over
+// the tiles.  Tiles from in_first_free(p, nd) on have position p free.
+__device__ __forceinline__ int in_first_free(int p, int nd) {
+    return max(0, (nd - p / 2 + 7) / 8);
+}
+__device__ __forceinline__ void in_free_slot(int k, int T, int nd, int& t, int& p) {
+    for (p = 0; p < 15; ++p) {
+        const int fr = T - min(T, in_first_free(p, nd));
+        if (k < fr) break;
+        k -= fr;
+    }
+    t = in_first_free(p, nd) + k;
+}
+__device__ __forceinline__ int in_free_index(int t, int p, int T, int nd) {
+    int n = 0;
+    for (int q = 0; q < p; ++q) n += T - min(T, in_first_free(q, nd));
+    return n + t - in_first_free(p, nd);
+}
 __device__ __forceinline__ void dup_free_slot(int k, int T0, int T1, int nd, int& t, int& p) {
     for (p = 0; p < 15; ++p) {
         const int fr = T0 - dup_tiles_at(p, T1, nd);
@@ -72,7 +92,10 @@ __device__ __forceinline__ void dup_free_slot(int k, int T0, int T1, int nd, int
 
 // Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*2 + 0..1]
 // = (tb | tm << 16, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative
-// to g*Tcap); meta[(g*ndr + ndr-1)*2 + 1] is the group's tile count.  For tile row
+// to g*Tcap); meta[(g*ndr + ndr-1)*2 + 1] is the group's tile count.  In-tile
+// mode (in_tile != 0) has no layer 1 (tm = te): a duplicated feature's "lo" row
+// sits in the same tile as its "hi" row, one position after it, and its tfeat
+// entry carries bit 0 (row offsets are multiples of 16).  For tile row
 // (t, p): tfeat = byte offset of the feature's row in the main kernel's LDS
 // partial, (feature - r*Dc) * row_bytes, or (trash_row + p % kTrashRows) * row_bytes for
 // padding; tsrc = (start << 10) |
@@ -84,7 +107,7 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
                                                         int* __restrict__ perm,
                                                         int* __restrict__ meta, int F, int D,
                                                         int ndr, int Dc, int Tcap, int row_bytes,
-                                                        int trash_row) {
+                                                        int trash_row, int in_tile) {
     __shared__ int s_idx[256];
     __shared__ int s_flag[256];  // bit 0: first occurrence, bit 1: occurs more than once
     __shared__ int s_cnt[2][kMaxRanges];
@@ -132,9 +155,9 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         int t = 0;
         for (int rr = 0; rr < ndr; ++rr) {
             s_tile[rr][0] = t;
-            t += (s_cnt[0][rr] + 15) / 16;
+            t += (s_cnt[0][rr] + (in_tile ? s_cnt[1][rr] : 0) + 15) / 16;
             s_tile[rr][1] = t;
-            t += (s_cnt[1][rr] + 15) / 16;
+            if (!in_tile) t += (s_cnt[1][rr] + 15) / 16;
             s_tile[rr][2] = t;
         }
         s_ntiles = t;
@@ -146,7 +169,24 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         m[1] = s_tile[rr][2];
     }
     const int64_t tbase = g * Tcap;
-    if (tid < F && first) {
+    if (in_tile && tid < F && first) {
+        const int T = s_tile[r][1] - s_tile[r][0];
+        int t, p;
+        if (cnt > 1) {
+            t = pd / 8;
+            p = 2 * (pd % 8);
+        } else {
+            in_free_slot(pn, T, s_cnt[1][r], t, p);
+        }
+        const int64_t row0 = (tbase + s_tile[r][0] + t) * 16 + p;
+        tfeat[row0] = (f - r_lo) * row_bytes;
+        tsrc[row0] = (rank << 10) | (cnt << 1);
+        if (cnt > 1) {
+            tfeat[row0 + 1] = (f - r_lo) * row_bytes | 1;
+            tsrc[row0 + 1] = (rank << 10) | (cnt << 1) | 1;
+        }
+    }
+    if (!in_tile && tid < F && first) {
         const int T0 = s_tile[r][1] - s_tile[r][0], T1 = s_tile[r][2] - s_tile[r][1];
         // layer-0 slot: a duplicated feature takes the same (tile, position) as
         // its layer-1 row, so the main kernel can add the two products before
@@ -177,7 +217,10 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         const int nd = s_cnt[1][rr];
         const int T0 = s_tile[rr][1] - s_tile[rr][0], T1 = s_tile[rr][2] - s_tile[rr][1];
         bool used;
-        if (t >= s_tile[rr][1]) {
+        if (in_tile) {
+            const int tt = t - s_tile[rr][0];
+            used = tt < in_first_free(p, nd) || in_free_index(tt, p, T0, nd) < s_cnt[0][rr] - nd;
+        } else if (t >= s_tile[rr][1]) {
             used = p * T1 + (t - s_tile[rr][1]) < nd;
         } else {
             const int tt = t - s_tile[rr][0];
@@ -492,7 +535,7 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     if (!plan_ready) {
         bwdf_plan_kernel<<<pgrid, dim3(256), 0, st>>>(
             idx, tfeat, tsrc, perm, meta, (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap,
-            acc_stride((int)p.BT) * 4, (int)p.DCMAX);
+            acc_stride((int)p.BT) * 4, (int)p.DCMAX, (int)p.staged);
         HASTE_CHECK_LAUNCH(fn);
     }
     const bool gather = plan_ready != 2;
@@ -582,7 +625,7 @@ extern "C" int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace,
         idx, reinterpret_cast<int*>(base + p.tfeat_off), reinterpret_cast<int*>(base + p.tsrc_off),
         reinterpret_cast<int*>(base + p.perm_off), reinterpret_cast<int*>(base + p.meta_off),
         (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap, haste::acc_stride((int)p.BT) * 4,
-        (int)p.DCMAX);
+        (int)p.DCMAX, (int)p.staged);
     HASTE_CHECK_LAUNCH(fn);
     return HASTE_OK;
 }
