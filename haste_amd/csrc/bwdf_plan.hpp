@@ -55,12 +55,17 @@ __host__ __device__ constexpr int max_dc(int bt, int G, int rt) {
 }
 
 // The staged build (bwdf_staged.hpp): kStagedTiles W^T tiles of a group's
-// range in its pipeline, dealt over its waves, and a double-buffered LDS copy
-// of each group's dY tile of bt rows x G labels beside the partial.
+// range in its pipeline, dealt over its waves, and a ring of kStageBufs LDS
+// copies of the groups' dY tiles of bt rows x G labels beside the partial
+// (group i in buffer i % kStageBufs, staged two groups ahead).  Its plan is
+// made in pairs of groups (bwdf_plan_pair_kernel); bit 31 of meta word 0 of a
+// pair's second group says the pair could not be laid out as one.
 constexpr int kStagedTiles = 8;
 constexpr int kStagedWaves = 8;  // the model's wave count (pick_staged_bt)
+constexpr int kStageBufs = 4;
+constexpr uint32_t kMetaUnpaired = 0x80000000u;
 __host__ __device__ constexpr int staged_max_dc(int bt, int G) {
-    return (kLdsBytes - kLdsMisc - 2 * bt * 2 * G) / 4 / acc_stride(bt) - kTrashRows;
+    return (kLdsBytes - kLdsMisc - kStageBufs * bt * 2 * G) / 4 / acc_stride(bt) - kTrashRows;
 }
 
 // Probability that a range holds more than rt layer-0 tiles when its share of

@@ -7,8 +7,8 @@
 // CU), and an out-of-range buffer load costs as much as a real one.  So:
 //  - each group's dY tile [BT rows x G labels] is loaded once per workgroup,
 //    row-major (every thread one piece of PB bytes), and staged in LDS
-//    (two buffers; 16-byte chunks XOR-swizzled per row so that the operand
-//    reads of 16 rows hit distinct bank groups);
+//    (a ring of four buffers, two groups ahead; 16-byte chunks XOR-swizzled
+//    per row so that the operand reads of 16 rows hit distinct bank groups);
 //  - wave w owns W^T tile w of the range (16 positions): it loads that tile's
 //    operand fragments (chunk-major twt: one contiguous 1 KB per k-step) and
 //    the positions' partial-row offsets, reads the staged dY operands of all
@@ -17,8 +17,11 @@
 //    rows of the tile's features (one 16-byte read-modify-write per 16-row
 //    block).  Within a layer a group's features are distinct, so the waves of
 //    one group never touch the same partial word;
-//  - one barrier per group, after each wave's LDS operations have completed,
-//    orders the groups' partial updates and publishes the next staged tile.
+//  - a barrier, after each wave's LDS operations have completed, orders the
+//    groups' partial updates and publishes the staged tiles.  The plan lays
+//    out groups in pairs (2k, 2k+1) with every feature the two share in the
+//    tile of the same index -- one wave -- so the pair's updates need no
+//    barrier between them: one barrier per two groups.
 // A duplicated index's second ("lo") row sits in the same tile as its "hi"
 // row (the plan's in-tile mode: no layer-1 tiles, so no wave carries a second
 // tile in the pipeline), its partial-row offset marked by bit 0: the wave adds
@@ -136,7 +139,7 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
     constexpr int TPW = C::TPW;
     using Piece = typename PieceT<PW>::type;
     __shared__ __attribute__((aligned(16))) float acc[(C::DCMAX + kTrashRows) * AS];
-    __shared__ __attribute__((aligned(16))) char stg[2][STG];
+    __shared__ __attribute__((aligned(16))) char stg[kStageBufs][STG];
 
     const int64_t work = xcd_remap(blockIdx.x, (int64_t)S * ndr * nbt);
     if (work < 0) return;
@@ -351,17 +354,18 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
             u32x2 m0[DEPTH + 1];
 #pragma unroll
             for (int k = 0; k <= DEPTH; ++k) m0[k] = load_meta(k);
-            const Piece y0 = load_y(0);
+            const Piece y0 = load_y(0), y1 = load_y(1);
             for (int k = tid * 4; k < dn * AS; k += NTH * 4)
                 *reinterpret_cast<f32x4*>(&acc[k]) = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k <= DEPTH; ++k) mu[k] = uniform_meta(m0[k]);
             stage(0, y0, 0);
+            stage(1, y1, 1);
 #pragma unroll
             for (int k = 0; k < DEPTH; ++k) {
                 __builtin_amdgcn_sched_barrier(0);
                 load_frag(k, mu[k], fq[k % NS]);
-                yq[k % NS] = load_y(k + 1);
+                yq[k % NS] = load_y(k + 2);
                 mraw[k % NS] = load_meta(k + DEPTH + 1);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -371,10 +375,9 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
         auto body = [&](int i, auto kc) __attribute__((always_inline)) {
             constexpr int K = decltype(kc)::value;  // i % kGroupUnroll
             constexpr int Q = K % NS;               // slot of step i
-            constexpr int P = K % 2;                // staging buffer of group i
             constexpr int QN = (Q + DEPTH) % NS;    // slot of step i + DEPTH
             load_frag(i + DEPTH, mu[DEPTH], fq[QN]);
-            yq[QN] = load_y(i + DEPTH + 1);
+            yq[QN] = load_y(i + DEPTH + 2);
             mraw[QN] = load_meta(i + 2 * DEPTH + 1);
             const u32x2 m = mu[0];
             const int tb = (int)(m[0] & 0xFFFF), te = (int)m[1];
@@ -389,10 +392,10 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
                     old[k][mt] = *reinterpret_cast<const f32x4*>(accb + pass1(fod[k]) + mt * 64 + colb);
-            stage(i + 1, yq[Q], 1 - P);
+            stage(i + 2, yq[Q], (i + 2) & (kStageBufs - 1));
             f32x4 pc[TPW][MT];
             u32x4 a[MT][KS];
-            read_a(P, a);
+            read_a(i & (kStageBufs - 1), a);
 #pragma unroll
             for (int k = 0; k < TPW; ++k) mma(a, fq[Q].b0[k], pc[k]);
 #pragma unroll
@@ -421,10 +424,19 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
 #pragma unroll
             for (int k = 0; k < DEPTH; ++k) mu[k] = mu[k + 1];
             mu[DEPTH] = uniform_meta(mraw[Q]);
-            __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
-            __builtin_amdgcn_s_barrier();
-            if (te - tb > kStagedTiles) {  // uniform, rare
-                extra(i, m, P);
+            // The barrier orders this iteration's partial updates (group
+            // i-1's) before the next one's (group i's) and publishes the
+            // staged tile of group i+2, read two iterations later.  After an
+            // odd iteration whose group the plan paired with the one before
+            // (every feature they share in one wave's tile) neither needs it:
+            // the next barrier, one iteration later, publishes that tile.
+            const bool more = te - tb > kStagedTiles;  // uniform, rare
+            if (K % 2 == 0 || (m[0] & kMetaUnpaired) || more) {
+                __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
+                __builtin_amdgcn_s_barrier();
+            }
+            if (more) {
+                extra(i, m, i & (kStageBufs - 1));
                 __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
                 __builtin_amdgcn_s_barrier();
             }

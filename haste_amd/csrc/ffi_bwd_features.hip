@@ -92,10 +92,11 @@ __device__ __forceinline__ void dup_free_slot(int k, int T0, int T1, int nd, int
 
 // Tiles of group g start at tile g*Tcap.  For range r, meta[(g*ndr + r)*2 + 0..1]
 // = (tb | tm << 16, te): layer-0 tiles [tb, tm), layer-1 tiles [tm, te) (relative
-// to g*Tcap); meta[(g*ndr + ndr-1)*2 + 1] is the group's tile count.  In-tile
-// mode (in_tile != 0) has no layer 1 (tm = te): a duplicated feature's "lo" row
-// sits in the same tile as its "hi" row, one position after it, and its tfeat
-// entry carries bit 0 (row offsets are multiples of 16).  For tile row
+// to g*Tcap); meta[(g*ndr + ndr-1)*2 + 1] is the group's tile count.  The
+// staged build's plan is made in the in-tile mode instead (plan_in_tile,
+// bwdf_plan_pair_kernel): no layer 1 (tm = te); a duplicated feature's "lo"
+// row sits in the same tile as its "hi" row, one position after it, and its
+// tfeat entry carries bit 0 (row offsets are multiples of 16).  For tile row
 // (t, p): tfeat = byte offset of the feature's row in the main kernel's LDS
 // partial, (feature - r*Dc) * row_bytes, or (trash_row + p % kTrashRows) * row_bytes for
 // padding; tsrc = (start << 10) |
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
                                                         int* __restrict__ perm,
                                                         int* __restrict__ meta, int F, int D,
                                                         int ndr, int Dc, int Tcap, int row_bytes,
-                                                        int trash_row, int in_tile) {
+                                                        int trash_row) {
     __shared__ int s_idx[256];
     __shared__ int s_flag[256];  // bit 0: first occurrence, bit 1: occurs more than once
     __shared__ int s_cnt[2][kMaxRanges];
@@ -155,9 +156,9 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         int t = 0;
         for (int rr = 0; rr < ndr; ++rr) {
             s_tile[rr][0] = t;
-            t += (s_cnt[0][rr] + (in_tile ? s_cnt[1][rr] : 0) + 15) / 16;
+            t += (s_cnt[0][rr] + 15) / 16;
             s_tile[rr][1] = t;
-            if (!in_tile) t += (s_cnt[1][rr] + 15) / 16;
+            t += (s_cnt[1][rr] + 15) / 16;
             s_tile[rr][2] = t;
         }
         s_ntiles = t;
@@ -169,24 +170,7 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         m[1] = s_tile[rr][2];
     }
     const int64_t tbase = g * Tcap;
-    if (in_tile && tid < F && first) {
-        const int T = s_tile[r][1] - s_tile[r][0];
-        int t, p;
-        if (cnt > 1) {
-            t = pd / 8;
-            p = 2 * (pd % 8);
-        } else {
-            in_free_slot(pn, T, s_cnt[1][r], t, p);
-        }
-        const int64_t row0 = (tbase + s_tile[r][0] + t) * 16 + p;
-        tfeat[row0] = (f - r_lo) * row_bytes;
-        tsrc[row0] = (rank << 10) | (cnt << 1);
-        if (cnt > 1) {
-            tfeat[row0 + 1] = (f - r_lo) * row_bytes | 1;
-            tsrc[row0 + 1] = (rank << 10) | (cnt << 1) | 1;
-        }
-    }
-    if (!in_tile && tid < F && first) {
+    if (tid < F && first) {
         const int T0 = s_tile[r][1] - s_tile[r][0], T1 = s_tile[r][2] - s_tile[r][1];
         // layer-0 slot: a duplicated feature takes the same (tile, position) as
         // its layer-1 row, so the main kernel can add the two products before
@@ -217,10 +201,7 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         const int nd = s_cnt[1][rr];
         const int T0 = s_tile[rr][1] - s_tile[rr][0], T1 = s_tile[rr][2] - s_tile[rr][1];
         bool used;
-        if (in_tile) {
-            const int tt = t - s_tile[rr][0];
-            used = tt < in_first_free(p, nd) || in_free_index(tt, p, T0, nd) < s_cnt[0][rr] - nd;
-        } else if (t >= s_tile[rr][1]) {
+        if (t >= s_tile[rr][1]) {
             used = p * T1 + (t - s_tile[rr][1]) < nd;
         } else {
             const int tt = t - s_tile[rr][0];
@@ -231,6 +212,301 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
         tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
         tsrc[(tbase + t) * 16 + p] = 0;
     }
+}
+
+// ---------------------------------------------------------- pair plan ------
+// The staged build's plan (in-tile mode, see bwdf_plan_kernel) made for two
+// groups at a time, a pair (2k, 2k+1): group 2k is laid out as
+// bwdf_plan_kernel lays it out; group 2k+1 with every feature it shares with
+// group 2k (in the same range) in the tile of the same index, so the wave
+// that owns that tile adds both groups' products of the feature and the
+// staged kernel needs no barrier between the two groups' partial updates.
+// Where that does not fit (shared rows over 16 in a tile, or more tiles than
+// the layout tracks or the workspace holds), group 2k+1 is laid out on its own
+// and bit 31 of its meta word 0 (every range) tells the kernel to keep the
+// barrier.
+constexpr int kPairRanges = 8;     // ranges the pinned layout handles (else: unpaired)
+constexpr int kPairRangeTiles = 24;  // tiles of a range it tracks
+
+// One slot of a group's index row, as the plan sees it (thread tid = slot).
+struct PlanSlot {
+    int f, rank, cnt, r, r_lo, pn, pd;
+    bool first;
+};
+
+// The analysis of group g's index row by the workgroup's 256 threads: the
+// clamped indices in s_idx, first-occurrence / duplicated flags in s_flag,
+// perm, the per-range counts of distinct (s_c[0]) and duplicated (s_c[1])
+// features, and the thread's slot.  s_c must be zero on entry.
+__device__ __forceinline__ PlanSlot plan_analyse(const int32_t* __restrict__ idx, int64_t g, int F,
+                                                 int D, int Dc, int* s_idx, int* s_flag,
+                                                 int (*s_c)[kMaxRanges], int* __restrict__ perm) {
+    const int tid = threadIdx.x;
+    PlanSlot ps{0, 0, 0, 0, 0, 0, 0, false};
+    if (tid < F) s_idx[tid] = min(max(idx[g * F + tid], 0), D - 1);
+    __syncthreads();
+    if (tid < F) {
+        ps.f = s_idx[tid];
+        int before = 0;
+        for (int k = 0; k < F; ++k) {
+            const int v = s_idx[k];
+            ps.rank += v < ps.f;
+            before += (v == ps.f) & (k < tid);
+            ps.cnt += v == ps.f;
+        }
+        ps.rank += before;
+        ps.first = before == 0;
+        perm[g * F + ps.rank] = tid;
+        s_flag[tid] = (ps.first ? 1 : 0) | (ps.cnt > 1 ? 2 : 0);
+    }
+    __syncthreads();
+    ps.r = ps.f / Dc;
+    ps.r_lo = ps.r * Dc;
+    const int key = (((ps.f - ps.r_lo) & 15) << 16) | (ps.f - ps.r_lo);
+    if (tid < F && ps.first) {
+        for (int k = 0; k < F; ++k) {
+            const int v = s_idx[k], fl = s_flag[k];
+            const int kk = (((v - ps.r_lo) & 15) << 16) | (v - ps.r_lo);
+            const bool in = (fl & 1) && v >= ps.r_lo && v < ps.r_lo + Dc && kk < key;
+            ps.pn += in && !(fl & 2);
+            ps.pd += in && (fl & 2);
+        }
+        atomicAdd(&s_c[0][ps.r], 1);
+        if (ps.cnt > 1) atomicAdd(&s_c[1][ps.r], 1);
+    }
+    __syncthreads();
+    return ps;
+}
+
+// The in-tile layout of one group (the staged build's plan): tiles per
+// range, meta (tm = te, bit 31 of word 0 = flag), the rows of the thread's
+// feature and the padding rows.  *t_rel receives the tile of the thread's
+// feature relative to its range's first.
+__device__ __forceinline__ void plan_in_tile(const PlanSlot& ps, int64_t g, int F, int ndr, int Tcap,
+                                             int row_bytes, int trash_row, uint32_t flag,
+                                             int (*s_c)[kMaxRanges], int* s_toff,
+                                             int* __restrict__ tfeat, int* __restrict__ tsrc,
+                                             int* __restrict__ meta, int* t_rel) {
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        int t = 0;
+        for (int rr = 0; rr < ndr; ++rr) {
+            s_toff[rr] = t;
+            t += (s_c[0][rr] + s_c[1][rr] + 15) / 16;
+        }
+        s_toff[ndr] = t;
+    }
+    __syncthreads();
+    for (int rr = tid; rr < ndr; rr += 256) {
+        int* m = meta + (g * ndr + rr) * kMetaStride;
+        m[0] = (int)((uint32_t)s_toff[rr] | ((uint32_t)s_toff[rr + 1] << 16) | flag);
+        m[1] = s_toff[rr + 1];
+    }
+    const int64_t tbase = g * Tcap;
+    if (tid < F && ps.first) {
+        const int T = s_toff[ps.r + 1] - s_toff[ps.r];
+        int t, p;
+        if (ps.cnt > 1) {
+            t = ps.pd / 8;
+            p = 2 * (ps.pd % 8);
+        } else {
+            in_free_slot(ps.pn, T, s_c[1][ps.r], t, p);
+        }
+        *t_rel = t;
+        const int64_t row0 = (tbase + s_toff[ps.r] + t) * 16 + p;
+        tfeat[row0] = (ps.f - ps.r_lo) * row_bytes;
+        tsrc[row0] = (ps.rank << 10) | (ps.cnt << 1);
+        if (ps.cnt > 1) {
+            tfeat[row0 + 1] = (ps.f - ps.r_lo) * row_bytes | 1;
+            tsrc[row0 + 1] = (ps.rank << 10) | (ps.cnt << 1) | 1;
+        }
+    }
+    const int nslots = s_toff[ndr] * 16;
+    for (int i = tid; i < nslots; i += 256) {
+        const int t = i / 16, p = i % 16;
+        int rr = 0;
+        while (t >= s_toff[rr + 1]) ++rr;  // empty ranges are skipped
+        const int nd = s_c[1][rr];
+        const int tt = t - s_toff[rr];
+        const bool used = tt < in_first_free(p, nd) ||
+                          in_free_index(tt, p, s_toff[rr + 1] - s_toff[rr], nd) < s_c[0][rr] - nd;
+        if (used) continue;
+        tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
+        tsrc[(tbase + t) * 16 + p] = 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void bwdf_plan_pair_kernel(const int32_t* __restrict__ idx,
+                                                             int* __restrict__ tfeat,
+                                                             int* __restrict__ tsrc,
+                                                             int* __restrict__ perm,
+                                                             int* __restrict__ meta, int F, int D,
+                                                             int ndr, int Dc, int Tcap,
+                                                             int row_bytes, int trash_row,
+                                                             int64_t Gc) {
+    __shared__ int s_idx[2][256];
+    __shared__ int s_flag[2][256];
+    __shared__ int s_c[2][2][kMaxRanges];
+    __shared__ int s_toff[kMaxRanges + 1];
+    __shared__ int s_atile[256];                              // group A: tile of the slot's feature
+    __shared__ int s_pos[kPairRanges][kPairRangeTiles];       // group B: rows used per tile
+    __shared__ int s_need[kPairRanges][kPairRangeTiles];      // group B: pinned rows per tile
+    __shared__ int s_rs[kPairRanges][kPairRangeTiles];        // group B: pinned single features per tile
+    __shared__ short s_bt[256], s_bp[256];                   // group B: tile, position of the slot's rows
+    __shared__ short s_ord[kPairRanges][256];                 // group B: single features by residue key
+    __shared__ int s_nt[kPairRanges];                         // group B: tiles per range
+    __shared__ int s_fail;
+    const int tid = threadIdx.x;
+    const int64_t gA = 2 * (int64_t)blockIdx.x, gB = gA + 1;
+    for (int i = tid; i < 4 * kMaxRanges; i += 256) (&s_c[0][0][0])[i] = 0;
+    if (tid == 0) s_fail = ndr > kPairRanges;
+    __syncthreads();
+
+    // group A, and the tile of each of its features
+    const PlanSlot pa = plan_analyse(idx, gA, F, D, Dc, s_idx[0], s_flag[0], s_c[0], perm);
+    int ta = -1;
+    plan_in_tile(pa, gA, F, ndr, Tcap, row_bytes, trash_row, 0u, s_c[0], s_toff, tfeat, tsrc, meta,
+                 &ta);
+    if (tid < F) s_atile[tid] = pa.first ? ta : -1;
+    if (gB >= Gc) return;  // (uniform)
+    __syncthreads();
+
+    // group B: each feature shared with A pinned to A's tile for it
+    const PlanSlot pb = plan_analyse(idx, gB, F, D, Dc, s_idx[1], s_flag[1], s_c[1], perm);
+    int pin = -1;
+    if (tid < F && pb.first) {
+        for (int k = 0; k < F; ++k)
+            if (s_idx[0][k] == pb.f && s_atile[k] >= 0) pin = s_atile[k];
+    }
+    s_bt[tid] = (short)pin;  // the pin, until the layout below replaces it
+    if (tid < F && pb.first && pb.cnt == 1 && pb.r < kPairRanges) s_ord[pb.r][pb.pn] = (short)tid;
+    __syncthreads();
+    // the pinned layout, one thread per range: pinned duplicated features,
+    // unpinned duplicated ones (two rows at an even position of a tile that
+    // keeps room for its pinned single features), pinned singles, then the
+    // other singles in residue-key order, dealt over the tiles in turn (so
+    // that a tile's rows spread over the LDS banks)
+    if (tid < ndr && !s_fail) {
+        const int r = tid;
+        const int c0 = s_c[1][0][r], nd = s_c[1][1][r];
+        int* pos = s_pos[r];
+        int* need = s_need[r];
+        int* rs = s_rs[r];
+        for (int t = 0; t < kPairRangeTiles; ++t) pos[t] = need[t] = rs[t] = 0;
+        int nt = (c0 + nd + 15) / 16;
+        bool ok = nt <= kPairRangeTiles;
+        for (int k = 0; k < F && ok; ++k) {
+            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r) continue;
+            const int pt = s_bt[k];
+            if (pt < 0) continue;
+            if (pt >= kPairRangeTiles) { ok = false; break; }
+            need[pt] += (s_flag[1][k] & 2) ? 2 : 1;
+            if (!(s_flag[1][k] & 2)) ++rs[pt];
+            nt = max(nt, pt + 1);
+        }
+        for (int t = 0; t < kPairRangeTiles && ok; ++t) ok = need[t] <= 16;
+        // 1. pinned duplicated features
+        for (int k = 0; k < F && ok; ++k) {
+            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r || !(s_flag[1][k] & 2) || s_bt[k] < 0) continue;
+            const int t = s_bt[k];
+            s_bp[k] = (short)pos[t];
+            pos[t] += 2;
+        }
+        // 2. unpinned duplicated features
+        for (int k = 0; k < F && ok; ++k) {
+            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r || !(s_flag[1][k] & 2) || s_bt[k] >= 0) continue;
+            int t = 0;
+            while (t < nt && pos[t] + 2 + rs[t] > 16) ++t;
+            if (t == nt) {
+                if (nt == kPairRangeTiles) { ok = false; break; }
+                ++nt;
+            }
+            s_bt[k] = (short)(t | 0x4000);  // placed (bit 14: unpinned)
+            s_bp[k] = (short)pos[t];
+            pos[t] += 2;
+        }
+        // 3. pinned single features
+        for (int k = 0; k < F && ok; ++k) {
+            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r || (s_flag[1][k] & 2) || s_bt[k] < 0) continue;
+            const int t = s_bt[k];
+            s_bp[k] = (short)pos[t]++;
+        }
+        // 4. the other single features
+        int cur = 0;
+        for (int j = 0; j < c0 - nd && ok; ++j) {
+            const int k = s_ord[r][j];
+            if (s_bt[k] >= 0) continue;  // pinned
+            int tries = 0;
+            while (tries < nt && pos[cur] >= 16) {
+                cur = cur + 1 == nt ? 0 : cur + 1;
+                ++tries;
+            }
+            if (tries == nt) {
+                if (nt == kPairRangeTiles) { ok = false; break; }
+                cur = nt++;
+            }
+            s_bt[k] = (short)(cur | 0x4000);
+            s_bp[k] = (short)pos[cur]++;
+            cur = cur + 1 == nt ? 0 : cur + 1;
+        }
+        s_nt[r] = nt;
+        if (!ok) atomicOr(&s_fail, 1);
+    }
+    __syncthreads();
+    if (tid == 0 && !s_fail) {
+        int t = 0;
+        for (int rr = 0; rr < ndr; ++rr) {
+            s_toff[rr] = t;
+            t += s_nt[rr];
+        }
+        s_toff[ndr] = t;
+        if (t > Tcap) s_fail = 1;
+    }
+    __syncthreads();
+    if (s_fail) {  // (uniform) group B on its own, the barrier kept
+        int tb = -1;
+        plan_in_tile(pb, gB, F, ndr, Tcap, row_bytes, trash_row, kMetaUnpaired, s_c[1], s_toff,
+                     tfeat, tsrc, meta, &tb);
+        return;
+    }
+    for (int rr = tid; rr < ndr; rr += 256) {
+        int* m = meta + (gB * ndr + rr) * kMetaStride;
+        m[0] = s_toff[rr] | (s_toff[rr + 1] << 16);
+        m[1] = s_toff[rr + 1];
+    }
+    const int64_t tbase = gB * Tcap;
+    if (tid < F && pb.first) {
+        const int t = s_bt[tid] & 0x3FFF, p = s_bp[tid];
+        const int64_t row0 = (tbase + s_toff[pb.r] + t) * 16 + p;
+        tfeat[row0] = (pb.f - pb.r_lo) * row_bytes;
+        tsrc[row0] = (pb.rank << 10) | (pb.cnt << 1);
+        if (pb.cnt > 1) {
+            tfeat[row0 + 1] = (pb.f - pb.r_lo) * row_bytes | 1;
+            tsrc[row0 + 1] = (pb.rank << 10) | (pb.cnt << 1) | 1;
+        }
+    }
+    const int nslots = s_toff[ndr] * 16;
+    for (int i = tid; i < nslots; i += 256) {
+        const int t = i / 16, p = i % 16;
+        int rr = 0;
+        while (t >= s_toff[rr + 1]) ++rr;
+        if (p < s_pos[rr][t - s_toff[rr]]) continue;
+        tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
+        tsrc[(tbase + t) * 16 + p] = 0;
+    }
+}
+
+// The plan of p: the staged build's in pairs of groups, the others per group.
+void launch_plan(const int32_t* idx, int* tfeat, int* tsrc, int* perm, int* meta, int64_t F,
+                 int64_t D, const BwdFPlan& p, hipStream_t st) {
+    if (p.staged)
+        bwdf_plan_pair_kernel<<<dim3((unsigned)ceil_div(p.Gc, (int64_t)2)), dim3(256), 0, st>>>(
+            idx, tfeat, tsrc, perm, meta, (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap,
+            acc_stride((int)p.BT) * 4, (int)p.DCMAX, p.Gc);
+    else
+        bwdf_plan_kernel<<<dim3((unsigned)p.Gc), dim3(256), 0, st>>>(
+            idx, tfeat, tsrc, perm, meta, (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap,
+            acc_stride((int)p.BT) * 4, (int)p.DCMAX);
 }
 
 // ------------------------------------------------------------- gather ------
@@ -533,9 +809,7 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     auto* y = static_cast<const uint16_t*>(dY);
     const dim3 pgrid((unsigned)p.Gc);
     if (!plan_ready) {
-        bwdf_plan_kernel<<<pgrid, dim3(256), 0, st>>>(
-            idx, tfeat, tsrc, perm, meta, (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap,
-            acc_stride((int)p.BT) * 4, (int)p.DCMAX, (int)p.staged);
+        launch_plan(idx, tfeat, tsrc, perm, meta, F, D, p, st);
         HASTE_CHECK_LAUNCH(fn);
     }
     const bool gather = plan_ready != 2;
@@ -620,12 +894,11 @@ extern "C" int haste_ffi_bwd_features_plan(const int32_t* idx, void* workspace,
     if (rc != HASTE_OK) return rc;
     HASTE_CHECK_ARG(idx != nullptr, "%s: null pointer", fn);
     char* base = static_cast<char*>(workspace);
-    haste::bwdf_plan_kernel<<<dim3((unsigned)p.Gc), dim3(256), 0,
-                              static_cast<hipStream_t>(stream)>>>(
-        idx, reinterpret_cast<int*>(base + p.tfeat_off), reinterpret_cast<int*>(base + p.tsrc_off),
-        reinterpret_cast<int*>(base + p.perm_off), reinterpret_cast<int*>(base + p.meta_off),
-        (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap, haste::acc_stride((int)p.BT) * 4,
-        (int)p.DCMAX, (int)p.staged);
+    haste::launch_plan(idx, reinterpret_cast<int*>(base + p.tfeat_off),
+                       reinterpret_cast<int*>(base + p.tsrc_off),
+                       reinterpret_cast<int*>(base + p.perm_off),
+                       reinterpret_cast<int*>(base + p.meta_off), F, D, p,
+                       static_cast<hipStream_t>(stream));
     HASTE_CHECK_LAUNCH(fn);
     return HASTE_OK;
 }
