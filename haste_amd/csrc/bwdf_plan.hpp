@@ -62,7 +62,7 @@ __host__ __device__ constexpr int max_dc(int bt, int G, int rt) {
 // pair's second group says the pair could not be laid out as one.
 constexpr int kStagedTiles = 8;
 constexpr int kStagedWaves = 8;  // the model's wave count (pick_staged_bt)
-constexpr int kStageBufs = 4;
+constexpr int kStageBufs = 6;    // kGroupUnroll: a group's buffer is its unrolled step
 constexpr uint32_t kMetaUnpaired = 0x80000000u;
 __host__ __device__ constexpr int staged_max_dc(int bt, int G) {
     return (kLdsBytes - kLdsMisc - kStageBufs * bt * 2 * G) / 4 / acc_stride(bt) - kTrashRows;

@@ -7,7 +7,7 @@
 // CU), and an out-of-range buffer load costs as much as a real one.  So:
 //  - each group's dY tile [BT rows x G labels] is loaded once per workgroup,
 //    row-major (every thread one piece of PB bytes), and staged in LDS
-//    (a ring of four buffers, two groups ahead; 16-byte chunks XOR-swizzled
+//    (a ring of six buffers, two groups ahead; 16-byte chunks XOR-swizzled
 //    per row so that the operand reads of 16 rows hit distinct bank groups);
 //  - wave w owns W^T tile w of the range (16 positions): it loads that tile's
 //    operand fragments (chunk-major twt: one contiguous 1 KB per k-step) and
@@ -61,7 +61,7 @@ struct StagedCfg {
     static_assert(G >= 32, "staged build: G >= 32");
     static_assert(TPW * W == kStagedTiles, "tiles per wave");
     static_assert(PB == 4 || PB == 8 || PB == 16 || PB == 32, "dY piece");
-    static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0, "unroll");
+    static_assert(kGroupUnroll % NS == 0 && kGroupUnroll % 2 == 0 && kGroupUnroll % kStageBufs == 0, "unroll");
     static_assert(DCMAX > 0, "LDS budget");
 };
 
@@ -392,10 +392,10 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
                     old[k][mt] = *reinterpret_cast<const f32x4*>(accb + pass1(fod[k]) + mt * 64 + colb);
-            stage(i + 2, yq[Q], (i + 2) & (kStageBufs - 1));
+            stage(i + 2, yq[Q], (K + 2) % kStageBufs);
             f32x4 pc[TPW][MT];
             u32x4 a[MT][KS];
-            read_a(i & (kStageBufs - 1), a);
+            read_a(K % kStageBufs, a);
 #pragma unroll
             for (int k = 0; k < TPW; ++k) mma(a, fq[Q].b0[k], pc[k]);
 #pragma unroll
@@ -436,7 +436,7 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
                 __builtin_amdgcn_s_barrier();
             }
             if (more) {
-                extra(i, m, i & (kStageBufs - 1));
+                extra(i, m, K % kStageBufs);
                 __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
                 __builtin_amdgcn_s_barrier();
             }
