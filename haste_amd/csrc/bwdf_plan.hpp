@@ -57,12 +57,18 @@ __host__ __device__ constexpr int max_dc(int bt, int G, int rt) {
 // The staged build (bwdf_staged.hpp): kStagedTiles W^T tiles of a group's
 // range in its pipeline, dealt over its waves, and a ring of kStageBufs LDS
 // copies of the groups' dY tiles of bt rows x G labels beside the partial
-// (group i in buffer i % kStageBufs, staged two groups ahead).  Its plan is
-// made in pairs of groups (bwdf_plan_pair_kernel); bit 31 of meta word 0 of a
-// pair's second group says the pair could not be laid out as one.
+// (group i in buffer i % kStageBufs, staged kPlanWindow groups ahead).  Its
+// plan is made in windows of kPlanWindow groups (bwdf_plan_window_kernel) that
+// need no barrier between their partial updates; bit 31 of a group's meta
+// word 0 says it could not be laid out as part of its window.
 constexpr int kStagedTiles = 8;
 constexpr int kStagedWaves = 8;  // the model's wave count (pick_staged_bt)
 constexpr int kStageBufs = 6;    // kGroupUnroll: a group's buffer is its unrolled step
+#ifndef HASTE_PLAN_WINDOW
+#define HASTE_PLAN_WINDOW 3
+#endif
+constexpr int kPlanWindow = HASTE_PLAN_WINDOW;
+static_assert(kGroupUnroll % kPlanWindow == 0 && 2 * kPlanWindow <= kStageBufs, "plan window");
 constexpr uint32_t kMetaUnpaired = 0x80000000u;
 __host__ __device__ constexpr int staged_max_dc(int bt, int G) {
     return (kLdsBytes - kLdsMisc - kStageBufs * bt * 2 * G) / 4 / acc_stride(bt) - kTrashRows;

@@ -7,7 +7,7 @@
 // CU), and an out-of-range buffer load costs as much as a real one.  So:
 //  - each group's dY tile [BT rows x G labels] is loaded once per workgroup,
 //    row-major (every thread one piece of PB bytes), and staged in LDS
-//    (a ring of six buffers, two groups ahead; 16-byte chunks XOR-swizzled
+//    (a ring of six buffers, filled a plan window ahead; 16-byte chunks XOR-swizzled
 //    per row so that the operand reads of 16 rows hit distinct bank groups);
 //  - wave w owns W^T tile w of the range (16 positions): it loads that tile's
 //    operand fragments (chunk-major twt: one contiguous 1 KB per k-step) and
@@ -19,9 +19,9 @@
 //    one group never touch the same partial word;
 //  - a barrier, after each wave's LDS operations have completed, orders the
 //    groups' partial updates and publishes the staged tiles.  The plan lays
-//    out groups in pairs (2k, 2k+1) with every feature the two share in the
-//    tile of the same index -- one wave -- so the pair's updates need no
-//    barrier between them: one barrier per two groups.
+//    out windows of kPlanWindow consecutive groups with every feature they
+//    share in the tile of the same index -- one wave -- so the window's
+//    updates need no barrier between them: one barrier per window.
 // A duplicated index's second ("lo") row sits in the same tile as its "hi"
 // row (the plan's in-tile mode: no layer-1 tiles, so no wave carries a second
 // tile in the pipeline), its partial-row offset marked by bit 0: the wave adds
@@ -354,18 +354,20 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
             u32x2 m0[DEPTH + 1];
 #pragma unroll
             for (int k = 0; k <= DEPTH; ++k) m0[k] = load_meta(k);
-            const Piece y0 = load_y(0), y1 = load_y(1);
+            Piece y0[kPlanWindow];
+#pragma unroll
+            for (int k = 0; k < kPlanWindow; ++k) y0[k] = load_y(k);
             for (int k = tid * 4; k < dn * AS; k += NTH * 4)
                 *reinterpret_cast<f32x4*>(&acc[k]) = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int k = 0; k <= DEPTH; ++k) mu[k] = uniform_meta(m0[k]);
-            stage(0, y0, 0);
-            stage(1, y1, 1);
+#pragma unroll
+            for (int k = 0; k < kPlanWindow; ++k) stage(k, y0[k], k);
 #pragma unroll
             for (int k = 0; k < DEPTH; ++k) {
                 __builtin_amdgcn_sched_barrier(0);
                 load_frag(k, mu[k], fq[k % NS]);
-                yq[k % NS] = load_y(k + 2);
+                yq[k % NS] = load_y(k + kPlanWindow);
                 mraw[k % NS] = load_meta(k + DEPTH + 1);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -377,7 +379,7 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
             constexpr int Q = K % NS;               // slot of step i
             constexpr int QN = (Q + DEPTH) % NS;    // slot of step i + DEPTH
             load_frag(i + DEPTH, mu[DEPTH], fq[QN]);
-            yq[QN] = load_y(i + DEPTH + 2);
+            yq[QN] = load_y(i + DEPTH + kPlanWindow);
             mraw[QN] = load_meta(i + 2 * DEPTH + 1);
             const u32x2 m = mu[0];
             const int tb = (int)(m[0] & 0xFFFF), te = (int)m[1];
@@ -392,7 +394,7 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
                     old[k][mt] = *reinterpret_cast<const f32x4*>(accb + pass1(fod[k]) + mt * 64 + colb);
-            stage(i + 2, yq[Q], (K + 2) % kStageBufs);
+            stage(i + kPlanWindow, yq[Q], (K + kPlanWindow) % kStageBufs);
             f32x4 pc[TPW][MT];
             u32x4 a[MT][KS];
             read_a(K % kStageBufs, a);
@@ -426,12 +428,13 @@ __global__ __launch_bounds__(64 * W, 1) void bwdf_staged_kernel(
             mu[DEPTH] = uniform_meta(mraw[Q]);
             // The barrier orders this iteration's partial updates (group
             // i-1's) before the next one's (group i's) and publishes the
-            // staged tile of group i+2, read two iterations later.  After an
-            // odd iteration whose group the plan paired with the one before
-            // (every feature they share in one wave's tile) neither needs it:
-            // the next barrier, one iteration later, publishes that tile.
+            // staged tiles.  Within a plan window (every feature its groups
+            // share in one wave's tile) the updates need none: it runs after
+            // the iteration of a window's first group, and of a group the
+            // plan could not lay out with its window; a tile staged
+            // kPlanWindow groups ahead is published by one of them in time.
             const bool more = te - tb > kStagedTiles;  // uniform, rare
-            if (K % 2 == 0 || (m[0] & kMetaUnpaired) || more) {
+            if (K % kPlanWindow == 0 || (m[0] & kMetaUnpaired) || more) {
                 __builtin_amdgcn_s_waitcnt(wait_lgkmcnt(0));
                 __builtin_amdgcn_s_barrier();
             }

@@ -214,17 +214,17 @@ __global__ __launch_bounds__(256) void bwdf_plan_kernel(const int32_t* __restric
     }
 }
 
-// ---------------------------------------------------------- pair plan ------
-// The staged build's plan (in-tile mode, see bwdf_plan_kernel) made for two
-// groups at a time, a pair (2k, 2k+1): group 2k is laid out as
-// bwdf_plan_kernel lays it out; group 2k+1 with every feature it shares with
-// group 2k (in the same range) in the tile of the same index, so the wave
-// that owns that tile adds both groups' products of the feature and the
-// staged kernel needs no barrier between the two groups' partial updates.
-// Where that does not fit (shared rows over 16 in a tile, or more tiles than
-// the layout tracks or the workspace holds), group 2k+1 is laid out on its own
-// and bit 31 of its meta word 0 (every range) tells the kernel to keep the
-// barrier.
+// -------------------------------------------------------- window plan ------
+// The staged build's plan (in-tile mode, see bwdf_plan_kernel) made for
+// kPlanWindow consecutive groups at a time: the window's first group is laid
+// out on its own; each later one with every feature it shares with the
+// window's earlier groups (in the same range) in the tile of the same index as
+// the latest of them, so the wave that owns that tile adds all of the
+// window's products of the feature and the staged kernel needs no barrier
+// between the window's partial updates.  Where that does not fit (pinned rows
+// over 16 in a tile, or more tiles than the layout tracks or the workspace
+// holds), the group is laid out on its own and bit 31 of its meta word 0
+// (every range) tells the kernel to keep the barrier before its update.
 constexpr int kPairRanges = 8;     // ranges the pinned layout handles (else: unpaired)
 constexpr int kPairRangeTiles = 24;  // tiles of a range it tracks
 
@@ -278,7 +278,7 @@ __device__ __forceinline__ PlanSlot plan_analyse(const int32_t* __restrict__ idx
     return ps;
 }
 
-// The in-tile layout of one group (the staged build's plan): tiles per
+// The in-tile layout of one group on its own (the staged build's plan): tiles per
 // range, meta (tm = te, bit 31 of word 0 = flag), the rows of the thread's
 // feature and the padding rows.  *t_rel receives the tile of the thread's
 // feature relative to its range's first.
@@ -336,171 +336,171 @@ __device__ __forceinline__ void plan_in_tile(const PlanSlot& ps, int64_t g, int 
     }
 }
 
-__global__ __launch_bounds__(256) void bwdf_plan_pair_kernel(const int32_t* __restrict__ idx,
-                                                             int* __restrict__ tfeat,
-                                                             int* __restrict__ tsrc,
-                                                             int* __restrict__ perm,
-                                                             int* __restrict__ meta, int F, int D,
-                                                             int ndr, int Dc, int Tcap,
-                                                             int row_bytes, int trash_row,
-                                                             int64_t Gc) {
-    __shared__ int s_idx[2][256];
-    __shared__ int s_flag[2][256];
-    __shared__ int s_c[2][2][kMaxRanges];
+__global__ __launch_bounds__(256) void bwdf_plan_window_kernel(const int32_t* __restrict__ idx,
+                                                               int* __restrict__ tfeat,
+                                                               int* __restrict__ tsrc,
+                                                               int* __restrict__ perm,
+                                                               int* __restrict__ meta, int F, int D,
+                                                               int ndr, int Dc, int Tcap,
+                                                               int row_bytes, int trash_row,
+                                                               int64_t Gc) {
+    __shared__ int s_idx[kPlanWindow][256];
+    __shared__ int s_flag[kPlanWindow][256];
+    __shared__ int s_ftile[kPlanWindow][256];                 // tile of the slot's feature (first occurrences)
+    __shared__ int s_c[2][kMaxRanges];
     __shared__ int s_toff[kMaxRanges + 1];
-    __shared__ int s_atile[256];                              // group A: tile of the slot's feature
-    __shared__ int s_pos[kPairRanges][kPairRangeTiles];       // group B: rows used per tile
-    __shared__ int s_need[kPairRanges][kPairRangeTiles];      // group B: pinned rows per tile
-    __shared__ int s_rs[kPairRanges][kPairRangeTiles];        // group B: pinned single features per tile
-    __shared__ short s_bt[256], s_bp[256];                   // group B: tile, position of the slot's rows
-    __shared__ short s_ord[kPairRanges][256];                 // group B: single features by residue key
-    __shared__ int s_nt[kPairRanges];                         // group B: tiles per range
+    __shared__ int s_pos[kPairRanges][kPairRangeTiles];       // rows used per tile
+    __shared__ int s_need[kPairRanges][kPairRangeTiles];      // pinned rows per tile
+    __shared__ int s_rs[kPairRanges][kPairRangeTiles];        // pinned single features per tile
+    __shared__ short s_bt[256], s_bp[256];                   // tile, position of the slot's rows
+    __shared__ short s_ord[kPairRanges][256];                 // single features by residue key
+    __shared__ int s_nt[kPairRanges];                         // tiles per range
     __shared__ int s_fail;
     const int tid = threadIdx.x;
-    const int64_t gA = 2 * (int64_t)blockIdx.x, gB = gA + 1;
-    for (int i = tid; i < 4 * kMaxRanges; i += 256) (&s_c[0][0][0])[i] = 0;
-    if (tid == 0) s_fail = ndr > kPairRanges;
-    __syncthreads();
-
-    // group A, and the tile of each of its features
-    const PlanSlot pa = plan_analyse(idx, gA, F, D, Dc, s_idx[0], s_flag[0], s_c[0], perm);
-    int ta = -1;
-    plan_in_tile(pa, gA, F, ndr, Tcap, row_bytes, trash_row, 0u, s_c[0], s_toff, tfeat, tsrc, meta,
-                 &ta);
-    if (tid < F) s_atile[tid] = pa.first ? ta : -1;
-    if (gB >= Gc) return;  // (uniform)
-    __syncthreads();
-
-    // group B: each feature shared with A pinned to A's tile for it
-    const PlanSlot pb = plan_analyse(idx, gB, F, D, Dc, s_idx[1], s_flag[1], s_c[1], perm);
-    int pin = -1;
-    if (tid < F && pb.first) {
-        for (int k = 0; k < F; ++k)
-            if (s_idx[0][k] == pb.f && s_atile[k] >= 0) pin = s_atile[k];
-    }
-    s_bt[tid] = (short)pin;  // the pin, until the layout below replaces it
-    if (tid < F && pb.first && pb.cnt == 1 && pb.r < kPairRanges) s_ord[pb.r][pb.pn] = (short)tid;
-    __syncthreads();
-    // the pinned layout, one thread per range: pinned duplicated features,
-    // unpinned duplicated ones (two rows at an even position of a tile that
-    // keeps room for its pinned single features), pinned singles, then the
-    // other singles in residue-key order, dealt over the tiles in turn (so
-    // that a tile's rows spread over the LDS banks)
-    if (tid < ndr && !s_fail) {
-        const int r = tid;
-        const int c0 = s_c[1][0][r], nd = s_c[1][1][r];
-        int* pos = s_pos[r];
-        int* need = s_need[r];
-        int* rs = s_rs[r];
-        for (int t = 0; t < kPairRangeTiles; ++t) pos[t] = need[t] = rs[t] = 0;
-        int nt = (c0 + nd + 15) / 16;
-        bool ok = nt <= kPairRangeTiles;
-        for (int k = 0; k < F && ok; ++k) {
-            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r) continue;
-            const int pt = s_bt[k];
-            if (pt < 0) continue;
-            if (pt >= kPairRangeTiles) { ok = false; break; }
-            need[pt] += (s_flag[1][k] & 2) ? 2 : 1;
-            if (!(s_flag[1][k] & 2)) ++rs[pt];
-            nt = max(nt, pt + 1);
+    for (int j = 0; j < kPlanWindow; ++j) {
+        const int64_t g = kPlanWindow * (int64_t)blockIdx.x + j;
+        if (g >= Gc) return;  // (uniform)
+        for (int i = tid; i < 2 * kMaxRanges; i += 256) (&s_c[0][0])[i] = 0;
+        if (tid == 0) s_fail = j == 0 || ndr > kPairRanges;
+        __syncthreads();
+        const PlanSlot ps = plan_analyse(idx, g, F, D, Dc, s_idx[j], s_flag[j], s_c, perm);
+        // each feature the window's earlier groups hold pinned to the tile of
+        // the latest of them that holds it
+        int pin = -1;
+        if (tid < F && ps.first) {
+            for (int jj = 0; jj < j; ++jj)
+                for (int k = 0; k < F; ++k)
+                    if (s_idx[jj][k] == ps.f && s_ftile[jj][k] >= 0) pin = s_ftile[jj][k];
         }
-        for (int t = 0; t < kPairRangeTiles && ok; ++t) ok = need[t] <= 16;
-        // 1. pinned duplicated features
-        for (int k = 0; k < F && ok; ++k) {
-            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r || !(s_flag[1][k] & 2) || s_bt[k] < 0) continue;
-            const int t = s_bt[k];
-            s_bp[k] = (short)pos[t];
-            pos[t] += 2;
-        }
-        // 2. unpinned duplicated features
-        for (int k = 0; k < F && ok; ++k) {
-            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r || !(s_flag[1][k] & 2) || s_bt[k] >= 0) continue;
-            int t = 0;
-            while (t < nt && pos[t] + 2 + rs[t] > 16) ++t;
-            if (t == nt) {
-                if (nt == kPairRangeTiles) { ok = false; break; }
-                ++nt;
+        s_bt[tid] = (short)pin;  // the pin, until the layout below replaces it
+        if (tid < F && ps.first && ps.cnt == 1 && ps.r < kPairRanges) s_ord[ps.r][ps.pn] = (short)tid;
+        __syncthreads();
+        // the pinned layout, one thread per range: pinned duplicated features,
+        // unpinned duplicated ones (two rows at an even position of a tile that
+        // keeps room for its pinned single features), pinned singles, then the
+        // other singles in residue-key order, dealt over the tiles in turn (so
+        // that a tile's rows spread over the LDS banks)
+        if (tid < ndr && !s_fail) {
+            const int r = tid;
+            const int c0 = s_c[0][r], nd = s_c[1][r];
+            int* pos = s_pos[r];
+            int* need = s_need[r];
+            int* rs = s_rs[r];
+            for (int t = 0; t < kPairRangeTiles; ++t) pos[t] = need[t] = rs[t] = 0;
+            int nt = (c0 + nd + 15) / 16;
+            bool ok = nt <= kPairRangeTiles;
+            for (int k = 0; k < F && ok; ++k) {
+                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r) continue;
+                const int pt = s_bt[k];
+                if (pt < 0) continue;
+                if (pt >= kPairRangeTiles) { ok = false; break; }
+                need[pt] += (s_flag[j][k] & 2) ? 2 : 1;
+                if (!(s_flag[j][k] & 2)) ++rs[pt];
+                nt = max(nt, pt + 1);
             }
-            s_bt[k] = (short)(t | 0x4000);  // placed (bit 14: unpinned)
-            s_bp[k] = (short)pos[t];
-            pos[t] += 2;
-        }
-        // 3. pinned single features
-        for (int k = 0; k < F && ok; ++k) {
-            if (!(s_flag[1][k] & 1) || s_idx[1][k] / Dc != r || (s_flag[1][k] & 2) || s_bt[k] < 0) continue;
-            const int t = s_bt[k];
-            s_bp[k] = (short)pos[t]++;
-        }
-        // 4. the other single features
-        int cur = 0;
-        for (int j = 0; j < c0 - nd && ok; ++j) {
-            const int k = s_ord[r][j];
-            if (s_bt[k] >= 0) continue;  // pinned
-            int tries = 0;
-            while (tries < nt && pos[cur] >= 16) {
+            for (int t = 0; t < kPairRangeTiles && ok; ++t) ok = need[t] <= 16;
+            // 1. pinned duplicated features
+            for (int k = 0; k < F && ok; ++k) {
+                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r || !(s_flag[j][k] & 2) || s_bt[k] < 0) continue;
+                const int t = s_bt[k];
+                s_bp[k] = (short)pos[t];
+                pos[t] += 2;
+            }
+            // 2. unpinned duplicated features
+            for (int k = 0; k < F && ok; ++k) {
+                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r || !(s_flag[j][k] & 2) || s_bt[k] >= 0) continue;
+                int t = 0;
+                while (t < nt && pos[t] + 2 + rs[t] > 16) ++t;
+                if (t == nt) {
+                    if (nt == kPairRangeTiles) { ok = false; break; }
+                    ++nt;
+                }
+                s_bt[k] = (short)(t | 0x4000);  // placed (bit 14: unpinned)
+                s_bp[k] = (short)pos[t];
+                pos[t] += 2;
+            }
+            // 3. pinned single features
+            for (int k = 0; k < F && ok; ++k) {
+                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r || (s_flag[j][k] & 2) || s_bt[k] < 0) continue;
+                const int t = s_bt[k];
+                s_bp[k] = (short)pos[t]++;
+            }
+            // 4. the other single features
+            int cur = 0;
+            for (int q = 0; q < c0 - nd && ok; ++q) {
+                const int k = s_ord[r][q];
+                if (s_bt[k] >= 0) continue;  // pinned
+                int tries = 0;
+                while (tries < nt && pos[cur] >= 16) {
+                    cur = cur + 1 == nt ? 0 : cur + 1;
+                    ++tries;
+                }
+                if (tries == nt) {
+                    if (nt == kPairRangeTiles) { ok = false; break; }
+                    cur = nt++;
+                }
+                s_bt[k] = (short)(cur | 0x4000);
+                s_bp[k] = (short)pos[cur]++;
                 cur = cur + 1 == nt ? 0 : cur + 1;
-                ++tries;
             }
-            if (tries == nt) {
-                if (nt == kPairRangeTiles) { ok = false; break; }
-                cur = nt++;
+            s_nt[r] = nt;
+            if (!ok) atomicOr(&s_fail, 1);
+        }
+        __syncthreads();
+        if (tid == 0 && !s_fail) {
+            int t = 0;
+            for (int rr = 0; rr < ndr; ++rr) {
+                s_toff[rr] = t;
+                t += s_nt[rr];
             }
-            s_bt[k] = (short)(cur | 0x4000);
-            s_bp[k] = (short)pos[cur]++;
-            cur = cur + 1 == nt ? 0 : cur + 1;
+            s_toff[ndr] = t;
+            if (t > Tcap) s_fail = 1;
         }
-        s_nt[r] = nt;
-        if (!ok) atomicOr(&s_fail, 1);
-    }
-    __syncthreads();
-    if (tid == 0 && !s_fail) {
-        int t = 0;
-        for (int rr = 0; rr < ndr; ++rr) {
-            s_toff[rr] = t;
-            t += s_nt[rr];
+        __syncthreads();
+        if (s_fail) {  // (uniform) laid out on its own; past the window's first, the barrier kept
+            int tr = -1;
+            plan_in_tile(ps, g, F, ndr, Tcap, row_bytes, trash_row, j == 0 ? 0u : kMetaUnpaired, s_c,
+                         s_toff, tfeat, tsrc, meta, &tr);
+            s_ftile[j][tid] = tid < F && ps.first ? tr : -1;
+            __syncthreads();
+            continue;
         }
-        s_toff[ndr] = t;
-        if (t > Tcap) s_fail = 1;
-    }
-    __syncthreads();
-    if (s_fail) {  // (uniform) group B on its own, the barrier kept
-        int tb = -1;
-        plan_in_tile(pb, gB, F, ndr, Tcap, row_bytes, trash_row, kMetaUnpaired, s_c[1], s_toff,
-                     tfeat, tsrc, meta, &tb);
-        return;
-    }
-    for (int rr = tid; rr < ndr; rr += 256) {
-        int* m = meta + (gB * ndr + rr) * kMetaStride;
-        m[0] = s_toff[rr] | (s_toff[rr + 1] << 16);
-        m[1] = s_toff[rr + 1];
-    }
-    const int64_t tbase = gB * Tcap;
-    if (tid < F && pb.first) {
-        const int t = s_bt[tid] & 0x3FFF, p = s_bp[tid];
-        const int64_t row0 = (tbase + s_toff[pb.r] + t) * 16 + p;
-        tfeat[row0] = (pb.f - pb.r_lo) * row_bytes;
-        tsrc[row0] = (pb.rank << 10) | (pb.cnt << 1);
-        if (pb.cnt > 1) {
-            tfeat[row0 + 1] = (pb.f - pb.r_lo) * row_bytes | 1;
-            tsrc[row0 + 1] = (pb.rank << 10) | (pb.cnt << 1) | 1;
+        for (int rr = tid; rr < ndr; rr += 256) {
+            int* m = meta + (g * ndr + rr) * kMetaStride;
+            m[0] = s_toff[rr] | (s_toff[rr + 1] << 16);
+            m[1] = s_toff[rr + 1];
         }
-    }
-    const int nslots = s_toff[ndr] * 16;
-    for (int i = tid; i < nslots; i += 256) {
-        const int t = i / 16, p = i % 16;
-        int rr = 0;
-        while (t >= s_toff[rr + 1]) ++rr;
-        if (p < s_pos[rr][t - s_toff[rr]]) continue;
-        tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
-        tsrc[(tbase + t) * 16 + p] = 0;
+        const int64_t tbase = g * Tcap;
+        s_ftile[j][tid] = -1;
+        if (tid < F && ps.first) {
+            const int t = s_bt[tid] & 0x3FFF, p = s_bp[tid];
+            s_ftile[j][tid] = t;
+            const int64_t row0 = (tbase + s_toff[ps.r] + t) * 16 + p;
+            tfeat[row0] = (ps.f - ps.r_lo) * row_bytes;
+            tsrc[row0] = (ps.rank << 10) | (ps.cnt << 1);
+            if (ps.cnt > 1) {
+                tfeat[row0 + 1] = (ps.f - ps.r_lo) * row_bytes | 1;
+                tsrc[row0 + 1] = (ps.rank << 10) | (ps.cnt << 1) | 1;
+            }
+        }
+        const int nslots = s_toff[ndr] * 16;
+        for (int i = tid; i < nslots; i += 256) {
+            const int t = i / 16, p = i % 16;
+            int rr = 0;
+            while (t >= s_toff[rr + 1]) ++rr;
+            if (p < s_pos[rr][t - s_toff[rr]]) continue;
+            tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
+            tsrc[(tbase + t) * 16 + p] = 0;
+        }
+        __syncthreads();
     }
 }
 
-// The plan of p: the staged build's in pairs of groups, the others per group.
+// The plan of p: the staged build's in windows of groups, the others per group.
 void launch_plan(const int32_t* idx, int* tfeat, int* tsrc, int* perm, int* meta, int64_t F,
                  int64_t D, const BwdFPlan& p, hipStream_t st) {
     if (p.staged)
-        bwdf_plan_pair_kernel<<<dim3((unsigned)ceil_div(p.Gc, (int64_t)2)), dim3(256), 0, st>>>(
+        bwdf_plan_window_kernel<<<dim3((unsigned)ceil_div(p.Gc, (int64_t)kPlanWindow)), dim3(256), 0, st>>>(
             idx, tfeat, tsrc, perm, meta, (int)F, (int)D, (int)p.ndr, (int)p.Dc, (int)p.Tcap,
             acc_stride((int)p.BT) * 4, (int)p.DCMAX, p.Gc);
     else
