@@ -43,9 +43,9 @@ STAGED_CASES = [
     (37, 768, 2000, 32, 16, "random"), (37, 1500, 2000, 32, 256, "dups"),
     (37, 300, 2000, 32, 16, "dups"), (37, 1500, 2000, 32, 16, "random"),
     (37, 768, 2000, 64, 16, "dups"), (37, 4096, 2000, 64, 16, "random"),
-    (37, 300, 2000, 64, 16, "random"), (37, 1500, 2000, 64, 16, "dups"),
+    (37, 300, 2000, 64, 16, "random"), (37, 1000, 2000, 64, 16, "dups"),
     (37, 768, 2000, 128, 16, "random"), (37, 1500, 2000, 128, 16, "dups"),
-    (37, 300, 2000, 128, 16, "dups"),
+    (37, 200, 2000, 128, 16, "dups"),
 ]
 
 
