@@ -235,47 +235,73 @@ struct PlanSlot {
 };
 
 // The analysis of group g's index row by the workgroup's 256 threads: the
-// clamped indices in s_idx, first-occurrence / duplicated flags in s_flag,
-// perm, the per-range counts of distinct (s_c[0]) and duplicated (s_c[1])
-// features, and the thread's slot.  s_c must be zero on entry.
+// clamped indices in s_idx (padded to a multiple of 4 slots), first-occurrence /
+// duplicated flags in s_flag, perm, the per-range counts of distinct (s_c[0])
+// and duplicated (s_c[1]) features, and the thread's slot (pn / pd left 0, see
+// plan_keys).  s_c must be zero on entry.
 __device__ __forceinline__ PlanSlot plan_analyse(const int32_t* __restrict__ idx, int64_t g, int F,
                                                  int D, int Dc, int* s_idx, int* s_flag,
                                                  int (*s_c)[kMaxRanges], int* __restrict__ perm) {
     const int tid = threadIdx.x;
+    const int F4 = (F + 3) & ~3;  // the rows are scanned 4 slots per 16-byte read
     PlanSlot ps{0, 0, 0, 0, 0, 0, 0, false};
     if (tid < F) s_idx[tid] = min(max(idx[g * F + tid], 0), D - 1);
+    else if (tid < F4) s_idx[tid] = INT_MAX;  // padding: matches and precedes no index
     __syncthreads();
+    const int4* idx4 = reinterpret_cast<const int4*>(s_idx);
     if (tid < F) {
         ps.f = s_idx[tid];
         int before = 0;
-        for (int k = 0; k < F; ++k) {
-            const int v = s_idx[k];
-            ps.rank += v < ps.f;
-            before += (v == ps.f) & (k < tid);
-            ps.cnt += v == ps.f;
+#pragma unroll 4
+        for (int k4 = 0; k4 < F4 / 4; ++k4) {
+            const int4 v = idx4[k4];
+            const int k = 4 * k4;
+            ps.rank += (v.x < ps.f) + (v.y < ps.f) + (v.z < ps.f) + (v.w < ps.f);
+            before += ((v.x == ps.f) & (k < tid)) + ((v.y == ps.f) & (k + 1 < tid)) +
+                      ((v.z == ps.f) & (k + 2 < tid)) + ((v.w == ps.f) & (k + 3 < tid));
+            ps.cnt += (v.x == ps.f) + (v.y == ps.f) + (v.z == ps.f) + (v.w == ps.f);
         }
         ps.rank += before;
         ps.first = before == 0;
         perm[g * F + ps.rank] = tid;
         s_flag[tid] = (ps.first ? 1 : 0) | (ps.cnt > 1 ? 2 : 0);
+    } else if (tid < F4) {
+        s_flag[tid] = 0;
     }
     __syncthreads();
     ps.r = ps.f / Dc;
     ps.r_lo = ps.r * Dc;
-    const int key = (((ps.f - ps.r_lo) & 15) << 16) | (ps.f - ps.r_lo);
     if (tid < F && ps.first) {
-        for (int k = 0; k < F; ++k) {
-            const int v = s_idx[k], fl = s_flag[k];
-            const int kk = (((v - ps.r_lo) & 15) << 16) | (v - ps.r_lo);
-            const bool in = (fl & 1) && v >= ps.r_lo && v < ps.r_lo + Dc && kk < key;
-            ps.pn += in && !(fl & 2);
-            ps.pd += in && (fl & 2);
-        }
         atomicAdd(&s_c[0][ps.r], 1);
         if (ps.cnt > 1) atomicAdd(&s_c[1][ps.r], 1);
     }
     __syncthreads();
     return ps;
+}
+
+// ps.pn / ps.pd of a first occurrence (the single / duplicated features of its
+// range with a smaller residue key), which plan_in_tile places by.
+__device__ __forceinline__ void plan_keys(PlanSlot& ps, int F, int Dc, const int* s_idx,
+                                          const int* s_flag) {
+    if (!(threadIdx.x < F && ps.first)) return;
+    const int F4 = (F + 3) & ~3;
+    const int key = (((ps.f - ps.r_lo) & 15) << 16) | (ps.f - ps.r_lo);
+    const int4* idx4 = reinterpret_cast<const int4*>(s_idx);
+    const int4* flag4 = reinterpret_cast<const int4*>(s_flag);
+    auto count = [&](int v, int fl) {
+        const int kk = (((v - ps.r_lo) & 15) << 16) | (v - ps.r_lo);
+        const bool in = (fl & 1) && v >= ps.r_lo && v < ps.r_lo + Dc && kk < key;
+        ps.pn += in && !(fl & 2);
+        ps.pd += in && (fl & 2);
+    };
+#pragma unroll 4
+    for (int k4 = 0; k4 < F4 / 4; ++k4) {
+        const int4 v = idx4[k4], fl = flag4[k4];
+        count(v.x, fl.x);
+        count(v.y, fl.y);
+        count(v.z, fl.z);
+        count(v.w, fl.w);
+    }
 }
 
 // The in-tile layout of one group on its own (the staged build's plan): tiles per
@@ -336,6 +362,66 @@ __device__ __forceinline__ void plan_in_tile(const PlanSlot& ps, int64_t g, int 
     }
 }
 
+// The tile table of one range for the pinned layout, made by one thread from the
+// pinned rows per tile: unpinned duplicated features fill the tiles in order
+// (first fit: a tile takes floor((16 - pinned rows) / 2) of them, appended
+// tiles 8), pinned singles follow a tile's duplicated rows, and the other
+// singles are dealt over the tiles in turn, round k giving one row to every tile
+// with at least k free rows (appended tiles take 16 in order).  Writes the
+// range's tile count to *nt (over kPairRangeTiles: the pinned layout fails).
+struct PairTables {
+    int cb[kPairRanges][kPairRangeTiles];    // first unpinned-dup ordinal of the tile
+    int ce[kPairRanges][kPairRangeTiles];    // one past its last
+    int base[kPairRanges][kPairRangeTiles];  // rows of the tile's duplicated features
+    int fr[kPairRanges][kPairRangeTiles];    // rows free for the dealt singles
+    int S[kPairRanges][17];                  // dealt singles in rounds 1..k
+    int nt1[kPairRanges];                    // tiles before the dealt singles' appended ones
+};
+
+__device__ __forceinline__ void pair_range_table(int r, int c0, int nd, int maxpin,
+                                                 const int* __restrict__ pd, const int* __restrict__ rs,
+                                                 PairTables& tb, int* nt) {
+    int npd = 0, nrs = 0, need_ok = 1;
+    int p2[kPairRangeTiles], q1[kPairRangeTiles];
+#pragma unroll
+    for (int t = 0; t < kPairRangeTiles; ++t) {
+        p2[t] = 2 * pd[t];
+        q1[t] = rs[t];
+        npd += pd[t];
+        nrs += rs[t];
+        need_ok &= p2[t] + q1[t] <= 16;
+    }
+    const int nt0 = max((c0 + nd + 15) / 16, maxpin + 1);
+    const int M = nd - npd, U = (c0 - nd) - nrs;
+    int C = 0, nt1 = nt0;
+#pragma unroll
+    for (int t = 0; t < kPairRangeTiles; ++t) {
+        const int cap = t < nt0 ? (16 - p2[t] - q1[t]) / 2 : 8;
+        const int u = min(max(M - C, 0), cap);
+        if (t >= nt0 && u > 0) nt1 = t + 1;
+        tb.cb[r][t] = C;
+        tb.ce[r][t] = C + cap;
+        C += cap;
+        p2[t] += 2 * u;                                  // rows of duplicated features
+        tb.base[r][t] = p2[t];
+        q1[t] = t < nt1 ? 16 - p2[t] - q1[t] : 0;        // free rows (after nt1 is final below)
+    }
+    bool ok = need_ok && nt0 <= kPairRangeTiles && M <= C;
+    int S = 0;
+    tb.S[r][0] = 0;
+#pragma unroll
+    for (int k = 1; k <= 16; ++k) {
+#pragma unroll
+        for (int t = 0; t < kPairRangeTiles; ++t) S += (t < nt1 && q1[t] >= k) ? 1 : 0;
+        tb.S[r][k] = S;
+    }
+#pragma unroll
+    for (int t = 0; t < kPairRangeTiles; ++t) tb.fr[r][t] = t < nt1 ? q1[t] : 0;
+    tb.nt1[r] = nt1;
+    const int nt2 = nt1 + (U > S ? (U - S + 15) / 16 : 0);
+    *nt = ok ? nt2 : kPairRangeTiles + 1;
+}
+
 __global__ __launch_bounds__(256) void bwdf_plan_window_kernel(const int32_t* __restrict__ idx,
                                                                int* __restrict__ tfeat,
                                                                int* __restrict__ tsrc,
@@ -344,16 +430,17 @@ __global__ __launch_bounds__(256) void bwdf_plan_window_kernel(const int32_t* __
                                                                int ndr, int Dc, int Tcap,
                                                                int row_bytes, int trash_row,
                                                                int64_t Gc) {
-    __shared__ int s_idx[kPlanWindow][256];
-    __shared__ int s_flag[kPlanWindow][256];
-    __shared__ int s_ftile[kPlanWindow][256];                 // tile of the slot's feature (first occurrences)
+    __shared__ __align__(16) int s_idx[kPlanWindow][256];
+    __shared__ __align__(16) int s_flag[kPlanWindow][256];
+    __shared__ __align__(16) int s_ftile[kPlanWindow][256];   // tile of the slot's feature (first occurrences)
     __shared__ int s_c[2][kMaxRanges];
     __shared__ int s_toff[kMaxRanges + 1];
-    __shared__ int s_pos[kPairRanges][kPairRangeTiles];       // rows used per tile
-    __shared__ int s_need[kPairRanges][kPairRangeTiles];      // pinned rows per tile
+    __shared__ int s_pd[kPairRanges][kPairRangeTiles];        // pinned duplicated features per tile
     __shared__ int s_rs[kPairRanges][kPairRangeTiles];        // pinned single features per tile
-    __shared__ short s_bt[256], s_bp[256];                   // tile, position of the slot's rows
-    __shared__ short s_ord[kPairRanges][256];                 // single features by residue key
+    __shared__ int s_used[kPairRanges][kPairRangeTiles];      // rows used per tile
+    __shared__ int s_maxpin[kPairRanges];
+    __shared__ __align__(16) short s_pin[256];                // the slot's pinned tile, or -1
+    __shared__ PairTables s_tb;
     __shared__ int s_nt[kPairRanges];                         // tiles per range
     __shared__ int s_fail;
     const int tid = threadIdx.x;
@@ -361,90 +448,76 @@ __global__ __launch_bounds__(256) void bwdf_plan_window_kernel(const int32_t* __
         const int64_t g = kPlanWindow * (int64_t)blockIdx.x + j;
         if (g >= Gc) return;  // (uniform)
         for (int i = tid; i < 2 * kMaxRanges; i += 256) (&s_c[0][0])[i] = 0;
+        for (int i = tid; i < kPairRanges * kPairRangeTiles; i += 256) {
+            (&s_pd[0][0])[i] = 0;
+            (&s_rs[0][0])[i] = 0;
+            (&s_used[0][0])[i] = 0;
+        }
+        if (tid < kPairRanges) s_maxpin[tid] = -1;
         if (tid == 0) s_fail = j == 0 || ndr > kPairRanges;
         __syncthreads();
-        const PlanSlot ps = plan_analyse(idx, g, F, D, Dc, s_idx[j], s_flag[j], s_c, perm);
+        PlanSlot ps = plan_analyse(idx, g, F, D, Dc, s_idx[j], s_flag[j], s_c, perm);
+        const bool mine = tid < F && ps.first;
+        const bool dup = ps.cnt > 1;
         // each feature the window's earlier groups hold pinned to the tile of
         // the latest of them that holds it
         int pin = -1;
-        if (tid < F && ps.first) {
-            for (int jj = 0; jj < j; ++jj)
-                for (int k = 0; k < F; ++k)
-                    if (s_idx[jj][k] == ps.f && s_ftile[jj][k] >= 0) pin = s_ftile[jj][k];
+        if (mine) {
+            const int F4 = (F + 3) & ~3;
+            for (int jj = j - 1; jj >= 0 && pin < 0; --jj) {
+                const int4* v4 = reinterpret_cast<const int4*>(s_idx[jj]);
+                const int4* t4 = reinterpret_cast<const int4*>(s_ftile[jj]);
+#pragma unroll 4
+                for (int k4 = 0; k4 < F4 / 4; ++k4) {
+                    const int4 v = v4[k4], t = t4[k4];
+                    pin = max(pin, v.x == ps.f ? t.x : -1);  // one slot of a group holds the tile
+                    pin = max(pin, v.y == ps.f ? t.y : -1);
+                    pin = max(pin, v.z == ps.f ? t.z : -1);
+                    pin = max(pin, v.w == ps.f ? t.w : -1);
+                }
+            }
         }
-        s_bt[tid] = (short)pin;  // the pin, until the layout below replaces it
-        if (tid < F && ps.first && ps.cnt == 1 && ps.r < kPairRanges) s_ord[ps.r][ps.pn] = (short)tid;
+        s_pin[tid] = (short)pin;
+        if (mine && pin >= 0 && !s_fail) {
+            if (pin >= kPairRangeTiles) {
+                atomicOr(&s_fail, 1);
+            } else {
+                atomicAdd(dup ? &s_pd[ps.r][pin] : &s_rs[ps.r][pin], 1);
+                atomicMax(&s_maxpin[ps.r], pin);
+            }
+        }
         __syncthreads();
-        // the pinned layout, one thread per range: pinned duplicated features,
-        // unpinned duplicated ones (two rows at an even position of a tile that
-        // keeps room for its pinned single features), pinned singles, then the
-        // other singles in residue-key order, dealt over the tiles in turn (so
-        // that a tile's rows spread over the LDS banks)
+        // the slot's rank in its class: pinned rows by slot among their tile's,
+        // unpinned duplicated features by slot, unpinned singles by residue key
+        int rank = 0;
+        if (mine && !s_fail) {
+            const int key = (((ps.f - ps.r_lo) & 15) << 16) | (ps.f - ps.r_lo);
+            const bool by_key = pin < 0 && !dup;
+            auto count = [&](int k, int v, int fl, int pk) {
+                const int kk = (((v - ps.r_lo) & 15) << 16) | (v - ps.r_lo);
+                const bool same = (fl & 1) && v >= ps.r_lo && v < ps.r_lo + Dc &&
+                                  ((fl & 2) != 0) == dup && pk == pin;
+                rank += same && (by_key ? kk < key : k < tid);
+            };
+            const int4* v4 = reinterpret_cast<const int4*>(s_idx[j]);
+            const int4* f4 = reinterpret_cast<const int4*>(s_flag[j]);
+            const short4* p4 = reinterpret_cast<const short4*>(s_pin);
+            const int F4 = (F + 3) & ~3;
+#pragma unroll 4
+            for (int k4 = 0; k4 < F4 / 4; ++k4) {
+                const int4 v = v4[k4], fl = f4[k4];
+                const short4 pk = p4[k4];
+                count(4 * k4, v.x, fl.x, pk.x);
+                count(4 * k4 + 1, v.y, fl.y, pk.y);
+                count(4 * k4 + 2, v.z, fl.z, pk.z);
+                count(4 * k4 + 3, v.w, fl.w, pk.w);
+            }
+        }
         if (tid < ndr && !s_fail) {
-            const int r = tid;
-            const int c0 = s_c[0][r], nd = s_c[1][r];
-            int* pos = s_pos[r];
-            int* need = s_need[r];
-            int* rs = s_rs[r];
-            for (int t = 0; t < kPairRangeTiles; ++t) pos[t] = need[t] = rs[t] = 0;
-            int nt = (c0 + nd + 15) / 16;
-            bool ok = nt <= kPairRangeTiles;
-            for (int k = 0; k < F && ok; ++k) {
-                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r) continue;
-                const int pt = s_bt[k];
-                if (pt < 0) continue;
-                if (pt >= kPairRangeTiles) { ok = false; break; }
-                need[pt] += (s_flag[j][k] & 2) ? 2 : 1;
-                if (!(s_flag[j][k] & 2)) ++rs[pt];
-                nt = max(nt, pt + 1);
-            }
-            for (int t = 0; t < kPairRangeTiles && ok; ++t) ok = need[t] <= 16;
-            // 1. pinned duplicated features
-            for (int k = 0; k < F && ok; ++k) {
-                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r || !(s_flag[j][k] & 2) || s_bt[k] < 0) continue;
-                const int t = s_bt[k];
-                s_bp[k] = (short)pos[t];
-                pos[t] += 2;
-            }
-            // 2. unpinned duplicated features
-            for (int k = 0; k < F && ok; ++k) {
-                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r || !(s_flag[j][k] & 2) || s_bt[k] >= 0) continue;
-                int t = 0;
-                while (t < nt && pos[t] + 2 + rs[t] > 16) ++t;
-                if (t == nt) {
-                    if (nt == kPairRangeTiles) { ok = false; break; }
-                    ++nt;
-                }
-                s_bt[k] = (short)(t | 0x4000);  // placed (bit 14: unpinned)
-                s_bp[k] = (short)pos[t];
-                pos[t] += 2;
-            }
-            // 3. pinned single features
-            for (int k = 0; k < F && ok; ++k) {
-                if (!(s_flag[j][k] & 1) || s_idx[j][k] / Dc != r || (s_flag[j][k] & 2) || s_bt[k] < 0) continue;
-                const int t = s_bt[k];
-                s_bp[k] = (short)pos[t]++;
-            }
-            // 4. the other single features
-            int cur = 0;
-            for (int q = 0; q < c0 - nd && ok; ++q) {
-                const int k = s_ord[r][q];
-                if (s_bt[k] >= 0) continue;  // pinned
-                int tries = 0;
-                while (tries < nt && pos[cur] >= 16) {
-                    cur = cur + 1 == nt ? 0 : cur + 1;
-                    ++tries;
-                }
-                if (tries == nt) {
-                    if (nt == kPairRangeTiles) { ok = false; break; }
-                    cur = nt++;
-                }
-                s_bt[k] = (short)(cur | 0x4000);
-                s_bp[k] = (short)pos[cur]++;
-                cur = cur + 1 == nt ? 0 : cur + 1;
-            }
-            s_nt[r] = nt;
-            if (!ok) atomicOr(&s_fail, 1);
+            int nt;
+            pair_range_table(tid, s_c[0][tid], s_c[1][tid], s_maxpin[tid], s_pd[tid], s_rs[tid], s_tb, &nt);
+            s_nt[tid] = nt;
+            if (nt > kPairRangeTiles) atomicOr(&s_fail, 1);
         }
         __syncthreads();
         if (tid == 0 && !s_fail) {
@@ -459,9 +532,10 @@ __global__ __launch_bounds__(256) void bwdf_plan_window_kernel(const int32_t* __
         __syncthreads();
         if (s_fail) {  // (uniform) laid out on its own; past the window's first, the barrier kept
             int tr = -1;
+            plan_keys(ps, F, Dc, s_idx[j], s_flag[j]);
             plan_in_tile(ps, g, F, ndr, Tcap, row_bytes, trash_row, j == 0 ? 0u : kMetaUnpaired, s_c,
                          s_toff, tfeat, tsrc, meta, &tr);
-            s_ftile[j][tid] = tid < F && ps.first ? tr : -1;
+            s_ftile[j][tid] = mine ? tr : -1;
             __syncthreads();
             continue;
         }
@@ -472,23 +546,50 @@ __global__ __launch_bounds__(256) void bwdf_plan_window_kernel(const int32_t* __
         }
         const int64_t tbase = g * Tcap;
         s_ftile[j][tid] = -1;
-        if (tid < F && ps.first) {
-            const int t = s_bt[tid] & 0x3FFF, p = s_bp[tid];
+        if (mine) {
+            const int r = ps.r;
+            int t, p;
+            if (pin >= 0) {
+                t = pin;
+                p = dup ? 2 * rank : s_tb.base[r][t] + rank;
+            } else if (dup) {
+                t = 0;
+                while (rank >= s_tb.ce[r][t]) ++t;  // rank < the range's unpinned dups <= ce[nt-1]
+                p = s_pd[r][t] * 2 + 2 * (rank - s_tb.cb[r][t]);
+            } else if (rank < s_tb.S[r][16]) {
+                int k = 1;
+                while (rank >= s_tb.S[r][k]) ++k;
+                int i = rank - s_tb.S[r][k - 1];
+                t = 0;
+                for (;; ++t) {
+                    if (s_tb.fr[r][t] >= k) {
+                        if (i == 0) break;
+                        --i;
+                    }
+                }
+                p = 16 - s_tb.fr[r][t] + (k - 1);
+            } else {
+                const int q = rank - s_tb.S[r][16];
+                t = s_tb.nt1[r] + q / 16;
+                p = q % 16;
+            }
+            atomicAdd(&s_used[r][t], dup ? 2 : 1);
             s_ftile[j][tid] = t;
-            const int64_t row0 = (tbase + s_toff[ps.r] + t) * 16 + p;
+            const int64_t row0 = (tbase + s_toff[r] + t) * 16 + p;
             tfeat[row0] = (ps.f - ps.r_lo) * row_bytes;
             tsrc[row0] = (ps.rank << 10) | (ps.cnt << 1);
-            if (ps.cnt > 1) {
+            if (dup) {
                 tfeat[row0 + 1] = (ps.f - ps.r_lo) * row_bytes | 1;
                 tsrc[row0 + 1] = (ps.rank << 10) | (ps.cnt << 1) | 1;
             }
         }
+        __syncthreads();
         const int nslots = s_toff[ndr] * 16;
         for (int i = tid; i < nslots; i += 256) {
             const int t = i / 16, p = i % 16;
             int rr = 0;
             while (t >= s_toff[rr + 1]) ++rr;
-            if (p < s_pos[rr][t - s_toff[rr]]) continue;
+            if (p < s_used[rr][t - s_toff[rr]]) continue;
             tfeat[(tbase + t) * 16 + p] = (trash_row + (p & (kTrashRows - 1))) * row_bytes;
             tsrc[(tbase + t) * 16 + p] = 0;
         }
