@@ -102,6 +102,47 @@ def test_zero_grad_matches_torch_optimizer():
                 assert torch.equal(a.grad, b.grad) and not a.grad.requires_grad
 
 
+def test_step_hooks_match_torch_optimizer():
+    """SRSgd.step runs without torch's profiler wrapper but keeps its hook
+    semantics: global then per-optimizer pre-hooks (which may replace the
+    arguments), then per-optimizer then global post-hooks, each given the
+    optimizer and (optimizer, closure) as args; the closure's loss is returned.
+    torch.optim.SGD, which torch wraps, is the yardstick (fp32 parameters take
+    SRSgd's torch path, so this runs on the CPU)."""
+    from torch.optim.optimizer import (register_optimizer_step_post_hook,
+                                       register_optimizer_step_pre_hook)
+
+    def run(make):
+        calls = []
+        p = torch.nn.Parameter(torch.ones(3))
+        p.grad = torch.full((3,), 2.0)
+        opt = make([p])
+        opt.register_step_pre_hook(lambda o, a, k: calls.append(("pre", o is opt, len(a))))
+        opt.register_step_post_hook(lambda o, a, k: calls.append(("post", o is opt, len(a))))
+
+        def swap_closure(o, a, k):
+            if o is opt:
+                calls.append(("swap",))
+                return (a[0], lambda: torch.tensor(7.0)), k
+
+        handles = [register_optimizer_step_pre_hook(lambda o, a, k: calls.append(("gpre", o is opt))),
+                   register_optimizer_step_pre_hook(swap_closure),
+                   register_optimizer_step_post_hook(lambda o, a, k: calls.append(("gpost", o is opt)))]
+        try:
+            loss = opt.step(lambda: torch.tensor(1.0))
+        finally:
+            for h in handles:
+                h.remove()
+        return calls, loss, p.detach().clone()
+
+    mine = run(lambda ps: SRSgd(ps, lr=0.5, momentum=0.0))
+    ref = run(lambda ps: torch.optim.SGD(ps, lr=0.5))
+    assert mine[0] == ref[0]
+    assert float(mine[1]) == float(ref[1]) == 7.0
+    assert torch.equal(mine[2], ref[2])
+    assert type(SRSgd([torch.nn.Parameter(torch.ones(1))])).step is SRSgd.__dict__["step"]
+
+
 @pytest.mark.gpu
 def test_resume_is_bit_identical(dev):
     """Train, checkpoint layer + optimizer, keep training; a fresh layer and
