@@ -30,6 +30,15 @@ def make_case(B, D, O, G, F, seed=0, dtype=torch.bfloat16, idx_mode="perm"):
         idx = torch.stack([torch.randperm(D, generator=g)[:F] for _ in range(Gc)]).to(torch.int32)
     else:
         idx = torch.randint(0, D, (Gc, F), generator=g, dtype=torch.int32)
+    if idx_mode in ("shared", "same"):
+        # consecutive groups share most features (a random walk replacing 30 % of
+        # a row's slots per group), or all of them: the staged build's window
+        # plan keeps a shared feature on one wave across a window of groups
+        for i in range(1, Gc):
+            idx[i] = idx[i - 1]
+            if idx_mode == "shared":
+                m = torch.rand(F, generator=g) < 0.3
+                idx[i, m] = torch.randint(0, D, (int(m.sum()),), generator=g, dtype=torch.int32)
     if idx_mode == "dups":
         idx[0, :] = 5                                  # one index for the whole group
         if Gc > 1:
@@ -114,8 +123,15 @@ def test_backward_features(dev, B, D, O, G, F, mode):
 # every (G, BT, RT) case under the LDS-ring build (1) and, where it exists
 # (G = 32, 64), the direct build (2); every staged (G, BT) case and the ring
 # cases with G >= 32 under the staged build (3)
+# Index rows shared between consecutive groups, under the staged build: one or
+# several feature ranges, duplicates within a row (D < F), F = 256, and more
+# ranges than the window plan pins (every group then laid out on its own).
+WINDOW_CASES = [(96, 300, 20000, 64, 128, "shared", 3), (64, 768, 20000, 128, 256, "shared", 3),
+                (64, 1500, 20000, 32, 64, "shared", 3), (64, 9000, 20000, 64, 128, "shared", 3),
+                (64, 200, 6000, 64, 64, "same", 3), (48, 100, 9000, 128, 128, "shared", 3)]
 BUILD_CASES = ([c + (1,) for c in RING_CASES] + [c + (2,) for c in RING_CASES if c[3] in (32, 64)]
-               + [c + (3,) for c in STAGED_CASES] + [c + (3,) for c in RING_CASES if c[3] >= 32])
+               + [c + (3,) for c in STAGED_CASES] + [c + (3,) for c in RING_CASES if c[3] >= 32]
+               + WINDOW_CASES)
 
 
 @pytest.mark.parametrize("B,D,O,G,F,mode,build", BUILD_CASES)
