@@ -170,7 +170,8 @@ def test_sgd_multi_matches_per_tensor_oracle(dev, use_mom):
             assert np.array_equal(m.cpu().numpy().view(np.uint32), ref_m.view(np.uint32)), n
 
 
-@pytest.mark.parametrize("B,D,ldt", [(512, 768, 512), (50, 300, 64), (1, 7, 8), (130, 64, 192)])
+@pytest.mark.parametrize("B,D,ldt", [(512, 768, 512), (50, 300, 64), (1, 7, 8), (130, 64, 192),
+                                     (33, 65, 40), (100, 200, 104), (64, 4096, 64)])
 def test_transpose_features(dev, B, D, ldt):
     x = torch.randn(B, D + 3).to(torch.bfloat16)
     xd = x.to(dev)[:, :D] if D % 8 else x.to(dev)[:, :D].contiguous()
