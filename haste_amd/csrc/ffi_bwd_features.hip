@@ -627,96 +627,8 @@ struct GatherSgd {
     int gb_dtype;
 };
 
-template <int GD>
-__device__ __forceinline__ void grad8(const void* g, int64_t i, float out[8]) {
-    if constexpr (GD == HASTE_DTYPE_F32) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(g) + i);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(g) + i + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { out[e] = a[e]; out[4 + e] = b[e]; }
-    } else {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(g) + i);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t lo = v[q] & 0xFFFFu, hi = v[q] >> 16;
-            out[2 * q] = GD == HASTE_DTYPE_BF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-            out[2 * q + 1] = GD == HASTE_DTYPE_BF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
-        }
-    }
-}
-
-// One workgroup per group: W_g is staged in LDS ([label][slot], row stride
-// F + 2 halves so the 8 label rows a wave reads at once sit in distinct banks),
-// then each thread writes 8 labels (16 bytes) of one tile row.  SGD: the
-// staged rows are W_g after the SGD step (GatherSgd), which is also written
-// back to W (16-bit weights, bf16 only).
-template <typename T, int G, bool SGD>
-__global__ __launch_bounds__(256) void bwdf_gather_kernel(const uint16_t* __restrict__ W,
-                                                          const int* __restrict__ tsrc,
-                                                          const int* __restrict__ perm,
-                                                          const int* __restrict__ meta,
-                                                          uint16_t* __restrict__ twt, int F,
-                                                          int64_t O, int ndr, int Tcap,
-                                                          GatherSgd sg) {
-    __shared__ uint32_t s_w[G * 129];  // G rows of (F + 2) halves, F <= 256
-    __shared__ int s_perm[256];
-    const int64_t g = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int ldw = F / 2 + 1;  // row stride in 32-bit words
-    for (int it = tid; it < G * (F / 8); it += 256) {
-        const int l = it / (F / 8), j0 = (it % (F / 8)) * 8;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (g * G + l < O) {
-            const int64_t e = (g * G + l) * F + j0;
-            v = *reinterpret_cast<const u32x4*>(W + e);
-            if constexpr (SGD) {
-                float gv[8], mv[8];
-                if (sg.g_dtype == HASTE_DTYPE_F32) grad8<HASTE_DTYPE_F32>(sg.g, e, gv);
-                else if (sg.g_dtype == HASTE_DTYPE_BF16) grad8<HASTE_DTYPE_BF16>(sg.g, e, gv);
-                else grad8<HASTE_DTYPE_F16>(sg.g, e, gv);
-                if (sg.use_mom) {
-                    const f32x4 m0 = *reinterpret_cast<const f32x4*>(sg.m + e);
-                    const f32x4 m1 = *reinterpret_cast<const f32x4*>(sg.m + e + 4);
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) { mv[k] = m0[k]; mv[4 + k] = m1[k]; }
-                }
-                uint32_t ob[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const uint32_t wb = (k & 1) ? (v[k >> 1] >> 16) : (v[k >> 1] & 0xFFFFu);
-                    ob[k] = sgd_one(bf16_bits_to_f32(wb), gv[k], &mv[k], sg.use_mom, sg.lr, sg.wd,
-                                    sg.mu, sg.do_sr, (uint64_t)(e + k), sg.k0, sg.k1);
-                }
-                v = u32x4{ob[0] | (ob[1] << 16), ob[2] | (ob[3] << 16), ob[4] | (ob[5] << 16),
-                          ob[6] | (ob[7] << 16)};
-                *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(W) + e) = v;
-                if (sg.use_mom) {
-                    *reinterpret_cast<f32x4*>(sg.m + e) = f32x4{mv[0], mv[1], mv[2], mv[3]};
-                    *reinterpret_cast<f32x4*>(sg.m + e + 4) = f32x4{mv[4], mv[5], mv[6], mv[7]};
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) s_w[l * ldw + j0 / 2 + q] = v[q];
-    }
-    if (tid < F) s_perm[tid] = perm[g * F + tid];
-    const int nrows = meta[(g * ndr + ndr - 1) * kMetaStride + 1] * 16;
-    __syncthreads();
-    auto wv = [&](int l, int slot) -> uint32_t {
-        const uint32_t w2 = s_w[l * ldw + (slot >> 1)];
-        return (slot & 1) ? (w2 >> 16) : (w2 & 0xFFFFu);
-    };
-    constexpr int CH = G / 8;  // 16-byte chunks per row
-    // chunk it in twt storage order (consecutive threads write consecutive 16 bytes)
-    for (int it = tid; it < nrows * CH; it += 256) {
-        const int row = twt_row_of(it, G), lc = twt_chunk_of(it, G) * 8;
-        const u32x4 v = wt_chunk<T>(tsrc[(g * Tcap) * 16 + row], s_perm, wv, lc);
-        *reinterpret_cast<u32x4*>(twt + twt_elem((g * Tcap) * 16 + row, lc, G)) = v;
-    }
-}
-
 // haste_sgd_sr_step_wt: the SGD step of GatherSgd on W, then W^T of the updated
-// weights as bwdf_gather_kernel writes it.  A workgroup takes kWtLabels labels
+// weights as bwdf_gather_block_kernel writes it.  A workgroup takes kWtLabels labels
 // (W rows) of one group: it updates those rows, stages them in LDS and writes
 // their two 16-byte chunks of every W^T row of the group's tiles (the tiles are
 // chunk-major, so a label block's chunks are contiguous runs of 512 bytes).
@@ -833,6 +745,62 @@ __global__ __launch_bounds__(256) void sgd_wt_kernel(uint16_t* __restrict__ W,
     }
 }
 
+// W^T of the current weights, in the label blocks of sgd_wt_kernel (no update):
+// a workgroup loads kWtLabels rows of one group (8 KB of LDS at F = 256, so
+// many workgroups share a CU and the loads of one overlap the stores of
+// another) and writes their chunks of every W^T row of the group's tiles.
+template <typename T, int G>
+__global__ __launch_bounds__(256) void bwdf_gather_block_kernel(const uint16_t* __restrict__ W,
+                                                                const int* __restrict__ tsrc,
+                                                                const int* __restrict__ perm,
+                                                                const int* __restrict__ meta,
+                                                                uint16_t* __restrict__ twt, int F,
+                                                                int64_t O, int ndr, int Tcap) {
+    constexpr int NB = G / kWtLabels;  // workgroups per group
+    __shared__ uint32_t s_w[kWtLabels * 129];  // kWtLabels rows of (F + 2) halves
+    __shared__ int s_perm[256];
+    const int64_t g = blockIdx.x / NB;
+    const int h = (int)(blockIdx.x % NB);
+    const int tid = threadIdx.x;
+    const int ldw = F / 2 + 1;
+    const int cpr = F / 8;  // chunks per row
+    const int64_t l0 = g * G + h * kWtLabels;
+    const int rows = (int)max<int64_t>(0, min<int64_t>(kWtLabels, O - l0));
+    const int nch = rows * cpr;
+    const rsrc_t rw = make_rsrc_u32(W + l0 * F, (uint32_t)(rows * F * 2));
+    if (tid < F) s_perm[tid] = perm[g * F + tid];
+    u32x4 wv[kWtBatch];
+#pragma unroll
+    for (int b = 0; b < kWtBatch; ++b) {
+        const int it = b * 256 + tid;
+        wv[b] = buf_load16(rw, it < nch ? (uint32_t)it * 16u : kOOB);  // rows >= O read zeros
+    }
+#pragma unroll
+    for (int b = 0; b < kWtBatch; ++b) {
+        const int it = b * 256 + tid;
+        if (b * 256 >= kWtLabels * cpr) break;  // uniform: F <= 128 fills one pass
+        const int l = it / cpr, j0 = (it % cpr) * 8;
+        if (l < kWtLabels) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s_w[l * ldw + j0 / 2 + q] = wv[b][q];
+        }
+    }
+    const int nrows = meta[(g * ndr + ndr - 1) * kMetaStride + 1] * 16;
+    __syncthreads();
+    const int lb = h * kWtLabels;
+    auto wvf = [&](int l, int slot) -> uint32_t {
+        const uint32_t w2 = s_w[(l - lb) * ldw + (slot >> 1)];
+        return (slot & 1) ? (w2 >> 16) : (w2 & 0xFFFFu);
+    };
+    // per tile of 16 rows: chunk 2h of its rows, then chunk 2h + 1 (32 chunks, 512 bytes)
+    for (int it = tid; it < nrows * 2; it += 256) {
+        const int row = (it >> 5) * 16 + (it & 15);
+        const int lc = lb + ((it >> 4) & 1) * 8;
+        const u32x4 v = wt_chunk<T>(tsrc[(g * Tcap) * 16 + row], s_perm, wvf, lc);
+        *reinterpret_cast<u32x4*>(twt + twt_elem((g * Tcap) * 16 + row, lc, G)) = v;
+    }
+}
+
 // ------------------------------------------------------------- reduce ------
 // Both reduce kernels read the partials as 16-byte rows of 4 batch columns
 // (Bp is a multiple of 64, so every such read is in bounds and aligned).
@@ -908,7 +876,7 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     float* ws = reinterpret_cast<float*>(base + p.prep_bytes);
     auto* w = static_cast<const uint16_t*>(W);
     auto* y = static_cast<const uint16_t*>(dY);
-    const dim3 pgrid((unsigned)p.Gc);
+    const dim3 ggrid((unsigned)(p.Gc * (G / kWtLabels)));  // label blocks of the W^T gather
     if (!plan_ready) {
         launch_plan(idx, tfeat, tsrc, perm, meta, F, D, p, st);
         HASTE_CHECK_LAUNCH(fn);
@@ -919,8 +887,8 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
     case GG:                                                                                    \
         if (dtype == HASTE_DTYPE_BF16) {                                                        \
             if (gather) {                                                                       \
-                bwdf_gather_kernel<BF16, GG, false><<<pgrid, dim3(256), 0, st>>>(               \
-                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, GatherSgd{}); \
+                bwdf_gather_block_kernel<BF16, GG><<<ggrid, dim3(256), 0, st>>>( \
+                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap); \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
             rc = p.staged ? bwdf_run_staged(dtype, G, ya, tfeat, meta, twt, y, lddy, ws, p, B, D, O, st) \
@@ -928,8 +896,8 @@ int run_partials(const char* fn, const int32_t* idx, const void* W, const void* 
                       : run_main<BF16, GG, false>(tfeat, meta, twt, y, lddy, ws, p, B, D, F, O, st); \
         } else {                                                                                \
             if (gather) {                                                                       \
-                bwdf_gather_kernel<F16, GG, false><<<pgrid, dim3(256), 0, st>>>(                \
-                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap, GatherSgd{}); \
+                bwdf_gather_block_kernel<F16, GG><<<ggrid, dim3(256), 0, st>>>( \
+                    w, tsrc, perm, meta, twt, (int)F, O, (int)p.ndr, (int)p.Tcap); \
                 HASTE_CHECK_LAUNCH(fn);                                                         \
             }                                                                                   \
             rc = p.staged ? bwdf_run_staged(dtype, G, ya, tfeat, meta, twt, y, lddy, ws, p, B, D, O, st) \
